@@ -1,0 +1,265 @@
+/*
+ * sglang_lite_amd.h -- C ABI of the MI355X (gfx950) FP8 MoE expert path and
+ * FP8 KV pack of DeepSeek-V4-Flash.
+ *
+ * Every entry point:
+ *   - takes raw device pointers, int64 sizes/strides (in elements unless a
+ *     name ends in _bytes) and the HIP stream to launch on as the last
+ *     argument (NULL = the null stream);
+ *   - never allocates, frees or keeps a pointer after it returns; outputs and
+ *     workspaces are allocated by the caller;
+ *   - returns SGL_OK (0) or a negative sgl_status and never throws; the
+ *     message of the last failure on the calling thread is sgl_last_error();
+ *   - launches asynchronously and never reads routing data on the host, so a
+ *     whole MoE layer can be captured into a HIP graph.
+ *
+ * Each declaration names the reference (ParaTensor/sglang-lite) interface it
+ * replaces as file:line.
+ */
+#ifndef SGLANG_LITE_AMD_H_
+#define SGLANG_LITE_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SGL_ABI_VERSION 1
+
+typedef void* sgl_stream_t; /* hipStream_t */
+
+enum sgl_status {
+  SGL_OK = 0,
+  SGL_ERR_INVALID_ARG = -1, /* shape / stride / alignment / dtype the caller got wrong */
+  SGL_ERR_UNSUPPORTED = -2, /* valid request this build does not implement */
+  SGL_ERR_HIP = -3,         /* HIP runtime or launch failure */
+  SGL_ERR_WORKSPACE = -4    /* workspace too small */
+};
+
+/* Element dtypes of floating inputs / outputs. */
+enum sgl_dtype { SGL_BF16 = 0, SGL_F16 = 1, SGL_F32 = 2 };
+
+/*
+ * 1xG activation scale formulas.  amax is the group's max |x| in fp32.
+ *   SGL_SCALE_TORCH_FP32   sf = max(amax,1e-4) / 448;  q = e4m3(x * (1/sf))
+ *       deep_gemm_sm120/utils/math.py:25-37 per_token_cast_to_fp8(use_ue8m0=False)
+ *   SGL_SCALE_TORCH_UE8M0  sf = ceil_to_ue8m0(max(amax,1e-4) / 448);  q as above
+ *       deep_gemm_sm120/utils/math.py:13-16,25-37 (use_ue8m0=True)
+ *   SGL_SCALE_TILELANG_FP32 s = max(amax,1e-4) * fp32(1/448);  q = e4m3(clamp(x / s, +-448))
+ *       deepseek_infer/kernel.py:79,83,93-96 (round_scale=False)
+ *   SGL_SCALE_TILELANG_UE8M0 s = 2^ceil_log2(max(amax,1e-4) * fp32(1/448)); q as above
+ *       deepseek_infer/kernel.py:22-37,79-81,93-96 (round_scale=True)
+ *   SGL_SCALE_KV_UE8M0     s = 2^ceil(log2(max(max(amax,1e-12)*(1/448), 2^-30))); q as above
+ *       engine/dsv4_kv_pack.py:78-101 _torch_fp8_ue8m0_quant
+ * e4m3 is OCP e4m3fn with round-to-nearest-even (torch's float8_e4m3fn cast).
+ */
+enum sgl_scale_mode {
+  SGL_SCALE_TORCH_FP32 = 0,
+  SGL_SCALE_TORCH_UE8M0 = 1,
+  SGL_SCALE_TILELANG_FP32 = 2,
+  SGL_SCALE_TILELANG_UE8M0 = 3,
+  SGL_SCALE_KV_UE8M0 = 4
+};
+
+/* Router score functions: deepseek_infer/model.py:566-571. */
+enum sgl_score_func { SGL_SCORE_SOFTMAX = 0, SGL_SCORE_SIGMOID = 1, SGL_SCORE_SQRTSOFTPLUS = 2 };
+
+/* KV row layouts.
+ *   SGL_KV_LAYOUT_A  engine/dsv4_kv_pack.py:3-37: 512-dim row = 448 NoPE dims as
+ *                    e4m3 in blocks of 64 + 64 RoPE dims bf16; 584 B per row:
+ *                    [0:448) e4m3 | [448:576) rope bf16 | [576:583) 7 x e8m0 | [583] 0.
+ *   SGL_KV_LAYOUT_B  576-dim row = 512-dim latent as e4m3 with 4 fp32 per-128
+ *                    scales (SGL_SCALE_TORCH_FP32) + 64 RoPE dims bf16; 656 B per row:
+ *                    [0:512) e4m3 | [512:640) rope bf16 | [640:656) 4 x fp32 LE. */
+enum sgl_kv_layout { SGL_KV_LAYOUT_A = 0, SGL_KV_LAYOUT_B = 1 };
+
+/* Per-expert weight pointers of one MoE layer, stored in DEVICE memory as an
+ * array of E routed experts followed by the shared expert.  Weights are e4m3
+ * row-major [out, in] (deepseek_infer/model.py:138-142 FP8 Linear), scales
+ * fp32 [ceil(out/128), ceil(in/128)] row-major. */
+typedef struct sgl_expert_ptrs {
+  const void* w_gate;  /* w1: [I, H] */
+  const void* w_up;    /* w3: [I, H] */
+  const void* w_down;  /* w2: [H, I] */
+  const float* s_gate; /* [I/128, H/128] */
+  const float* s_up;   /* [I/128, H/128] */
+  const float* s_down; /* [H/128, I/128] */
+} sgl_expert_ptrs;
+
+/* ---------------------------------------------------------------- library */
+
+int sgl_abi_version(void);
+/* Message of the last failed call on this thread ("" if none). */
+const char* sgl_last_error(void);
+/* 1 when a gfx950 device is current and the kernels are loadable, else 0
+ * (and sgl_last_error() says why).  Mirrors the probe of
+ * engine/v4_deep_gemm.py:97-133 probe_deep_gemm_sm120. */
+int sgl_probe(void);
+
+/* ------------------------------------------------------ activation quant */
+
+/* Per-row 1 x group quantization of bf16 x [M, K] (K % group == 0,
+ * group in {32, 64, 128}).
+ * Replaces deepseek_infer/kernel.py:105-125 act_quant (and its TileLang
+ * kernel :40-102), deep_gemm_sm120/utils/math.py:25-37 per_token_cast_to_fp8.
+ *   y : e4m3 [M, K] with row stride ldy          (inplace == 0)
+ *       bf16 [M, K] quant-dequant of x, may alias x (inplace == 1; kernel.py:84-91)
+ *   s : scales [M, K/group] with row stride lds; fp32, or one e8m0 byte each
+ *       when scale_e8m0 != 0 (scale_dtype == torch.float8_e8m0fnu).
+ * Pointers must be 16-byte aligned and ldx, ldy multiples of 8. */
+int sgl_act_quant(const void* x, int64_t M, int64_t K, int64_t ldx, void* y, int64_t ldy,
+                  void* s, int64_t lds, int group, int scale_mode, int scale_e8m0, int inplace,
+                  sgl_stream_t stream);
+
+/* 128 x 128 block quantization of a weight w [N, K] (fp32 or bf16, row stride
+ * ldw) into e4m3 q [N, K] (row stride ldq) and fp32 scales s [ceil(N/128),
+ * ceil(K/128)] (row stride lds); ragged edge blocks behave as zero-padded.
+ * Replaces deep_gemm_sm120/utils/math.py:50-60 per_block_cast_to_fp8. */
+int sgl_weight_quant_128x128(const void* w, int dtype, int64_t N, int64_t K, int64_t ldw, void* q,
+                             int64_t ldq, float* s, int64_t lds, int use_ue8m0,
+                             sgl_stream_t stream);
+
+/* e8m0 bytes -> fp32 powers of two (n elements).  Replaces the scale cast of
+ * engine/v4_deep_gemm.py:136-141 scale_to_f32. */
+int sgl_e8m0_to_f32(const void* src, float* dst, int64_t n, sgl_stream_t stream);
+
+/* --------------------------------------------------------------- GEMMs */
+
+/* C[M, N] = sum_kb (A[:, kb] . B[:, kb]^T) * sa[m, kb] * sb[n/128, kb], fp32
+ * accumulation promoted once per 128-deep K block, output bf16 (out_dtype
+ * SGL_BF16) or fp32 (SGL_F32).  A e4m3 [M, K] contiguous, sa [M, K/128],
+ * B e4m3 [N, K] contiguous, sb [ceil(N/128), K/128]; each scale tensor is
+ * fp32, or one e8m0 byte per scale when its *_scale_e8m0 flag is set.
+ * K % 128 == 0, N % 16 == 0.
+ * Replaces deepseek_infer/kernel.py:257-273 fp8_gemm (kernel :203-254) and the
+ * call-site adapter engine/v4_deep_gemm.py:169-218 fp4_gemm_nt. */
+int sgl_fp8_gemm(const void* a, const void* sa, int a_scale_e8m0, const void* b, const void* sb,
+                 int b_scale_e8m0, void* c, int out_dtype, int64_t M, int64_t N, int64_t K,
+                 sgl_stream_t stream);
+
+/* ------------------------------------------------------------ MoE layer */
+
+/* Gate top-k from router logits [T, E] fp32 (E <= 512, k <= 16):
+ * scores = score_func(logits); selection on scores + bias (bias may be NULL);
+ * weights = scores gathered, renormalised unless softmax, times route_scale.
+ * ids int32 [T, k] in descending selection-score order (torch.topk order),
+ * weights fp32 [T, k].  Replaces deepseek_infer/model.py:565-584 Gate.forward
+ * after its router projection. */
+int sgl_moe_route_topk(const float* logits, int64_t T, int E, int k, int score_func,
+                       const float* bias, float route_scale, int32_t* ids, float* weights,
+                       sgl_stream_t stream);
+
+/* Stable counting sort of the T*k routing slots (slot = t*k + j) by expert id:
+ *   counts [E], offsets [E+1] (exclusive prefix sum, offsets[E] = T*k),
+ *   sorted_slot [T*k] (slot at each sorted position, token-ascending inside an
+ *   expert), slot_pos [T*k] (inverse permutation).
+ * Ids outside [0, E) are an error reported through counts (they are skipped
+ * and not placed).  Replaces the bincount / torch.where dispatch of
+ * deepseek_infer/model.py:634-640 and engine/v4_moe_fast.py:89-101. */
+int sgl_moe_permute(const int32_t* ids, int64_t T, int k, int E, int32_t* counts, int32_t* offsets,
+                    int32_t* sorted_slot, int32_t* slot_pos, sgl_stream_t stream);
+
+/* Grouped gate/up GEMM with the fused SwiGLU epilogue of one MoE layer.
+ * Rows are the routed slots in sorted order (row p reads token
+ * sorted_slot[p]/k of xq) followed, when has_shared, by T rows of the shared
+ * expert (row offsets[E]+t reads token t, weight 1).  For each row:
+ *   gate = bf16(A . w_gate^T), up = bf16(A . w_up^T)   (block-scaled FP8 GEMMs)
+ *   if swiglu_limit > 0: up = clamp(up, +-lim), gate = min(gate, lim)
+ *   h = bf16(silu(gate) * up * route_w[slot])
+ *   hq, hs = 1x128 quant of h with scale_mode (fp32 scales)
+ * xq e4m3 [T, H], xs fp32 [T, H/128], route_w fp32 [T*k] (slot-indexed),
+ * experts: device array of E (+1) sgl_expert_ptrs, hq e4m3 [rows, I],
+ * hs fp32 [rows, I/128], rows = T*k (+ T).  H % 128 == 0, I % 128 == 0.
+ * Replaces engine/v4_moe_fast.py:43-76 _expert_forward_fused up to w2's
+ * act_quant (and deepseek_infer/model.py:596-606 Expert.forward). */
+int sgl_moe_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I, int E, int k,
+                    const int32_t* offsets, const int32_t* sorted_slot, const float* route_w,
+                    const sgl_expert_ptrs* experts, int has_shared, float swiglu_limit,
+                    int scale_mode, void* hq, float* hs, sgl_stream_t stream);
+
+/* Grouped down GEMM: out[slot] = bf16(hq[row] . w_down[e]^T) for every row of
+ * sgl_moe_gate_up's row order; routed row p is written at output row
+ * sorted_slot[p] / k * (k + has_shared) + sorted_slot[p] % k and shared row t
+ * at t * (k + 1) + k, so the outputs of one token are contiguous.
+ * out bf16 [T * (k + has_shared), H].  Replaces the w2 projection of
+ * engine/v4_moe_fast.py:76 / deepseek_infer/model.py:606. */
+int sgl_moe_down(const void* hq, const float* hs, int64_t T, int64_t H, int64_t I, int E, int k,
+                 const int32_t* offsets, const int32_t* sorted_slot,
+                 const sgl_expert_ptrs* experts, int has_shared, void* out,
+                 sgl_stream_t stream);
+
+/* Unpermute-combine: y[t] = bf16( (sum over the token's k expert outputs in
+ * ascending expert-id order, fp32) + shared[t] ), matching the fp32
+ * accumulation order of engine/v4_moe_fast.py:86-106 (and
+ * deepseek_infer/model.py:633-644).  out as written by sgl_moe_down,
+ * ids int32 [T, k], y bf16 [T, H]. */
+int sgl_moe_combine(const void* out, const int32_t* ids, int64_t T, int k, int64_t H,
+                    int has_shared, void* y, sgl_stream_t stream);
+
+/* Bytes of workspace sgl_moe_forward needs (256-byte aligned sub-buffers). */
+size_t sgl_moe_workspace_size(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared);
+
+/* Whole routed+shared MoE layer from bf16 x [T, H] and a precomputed top-k
+ * (ids int32 [T, k], weights fp32 [T, k]): act quant -> permute -> gate/up
+ * -> down -> combine, y bf16 [T, H].  Replaces
+ * engine/v4_moe_fast.py:79-106 _moe_forward_activated_only after the gate. */
+int sgl_moe_forward(const void* x, int64_t T, int64_t H, int64_t I, int E, int k,
+                    const int32_t* ids, const float* weights, const sgl_expert_ptrs* experts,
+                    int has_shared, float swiglu_limit, int scale_mode, void* workspace,
+                    size_t workspace_bytes, void* y, sgl_stream_t stream);
+
+/* ------------------------------------------------------------- KV cache */
+
+/* Pack KV rows.  Layout A: kv [T, 512] (bf16 / f16 / f32, row stride ldkv)
+ * with scale_mode SGL_SCALE_KV_UE8M0 (the torch fallback,
+ * dsv4_kv_pack.py:78-101) or SGL_SCALE_TILELANG_UE8M0 (act_quant_fn
+ * injected, dsv4_kv_pack.py:58-61), out [T, 584] uint8; with paged != 0 the
+ * output is the footer-paged [ceil(T/page)*page*584] bytes of to_paged_hnd,
+ * zero-filled padding rows included.  Layout B: kv [T, 576], out [T, 656]
+ * (scale_mode ignored: SGL_SCALE_TORCH_FP32), paged must be 0.
+ * Replaces engine/dsv4_kv_pack.py:40-75 pack_dsv4_kv_bf16 (+ :104-146). */
+int sgl_kv_pack(const void* kv, int dtype, int64_t T, int64_t ldkv, int layout, int scale_mode,
+                int paged, int page_size, void* out, sgl_stream_t stream);
+
+/* Logical [T, 584] rows -> footer pages [ceil(T/page), page*584] (padding rows
+ * zero).  Replaces engine/dsv4_kv_pack.py:104-146 to_paged_hnd. */
+int sgl_kv_to_paged(const void* packed, int64_t T, int page_size, void* pages,
+                    sgl_stream_t stream);
+
+/* Gather-dequant for sparse MLA: out[q, i] = dequant(cache row idx[q, i]) as
+ * bf16, an index of -1 gives a zero row.  Layout A rows give 512 values
+ * (448 e4m3 * 2^(e8m0-127), 64 rope), layout B rows 576 (512 e4m3 * fp32
+ * scale rounded to bf16, 64 rope).  cache holds n_rows rows (paged: footer
+ * pages of page_size rows, layout A only).  idx int32 [nq, nsel],
+ * out bf16 [nq, nsel, 512 | 576].  Indices >= n_rows are an error: the row
+ * is zero-filled.  Semantics of engine/v4_sparse_torch.py:77-83 and
+ * deepseek_infer/kernel.py:322-325 applied to the packed cache consumed at
+ * engine/v4_sparse_mla.py:104-118. */
+int sgl_kv_gather_dequant(const void* cache, int layout, int paged, int page_size, int64_t n_rows,
+                          const int32_t* idx, int64_t nq, int64_t nsel, void* out,
+                          sgl_stream_t stream);
+
+/* Split concatenated top-k [BS, K] (int32, or int64 when idx_int64) into SWA
+ * columns [BS, min(window, K)] + lens and compressed columns [BS, K - swa]
+ * (valid entries shifted by -window) + lens, all int32.  Replaces
+ * engine/dsv4_kv_pack.py:149-175 split_swa_compress_indices. */
+int sgl_split_swa_compress_indices(const void* topk, int idx_int64, int64_t BS, int64_t K,
+                                   int64_t window, int32_t* swa, int32_t* swa_lens,
+                                   int32_t* comp, int32_t* comp_lens, sgl_stream_t stream);
+
+/* ------------------------------------------------- host-side self checks */
+
+/* The device numeric code compiled for the host, so the CPU test suite can
+ * check it without a GPU.  n elements each. */
+int sgl_host_f32_to_e4m3(const float* x, uint8_t* y, int64_t n);
+int sgl_host_e4m3_to_f32(const uint8_t* x, float* y, int64_t n);
+int sgl_host_group_scale(int scale_mode, const float* amax, float* scale, int64_t n);
+int sgl_host_quant_elem(int scale_mode, const float* x, const float* scale, uint8_t* y, int64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SGLANG_LITE_AMD_H_ */

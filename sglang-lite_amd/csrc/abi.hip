@@ -1,0 +1,99 @@
+// Library-level entry points: ABI version, last error, device probe and the
+// host-compiled copies of the numeric helpers used by the CPU test suite.
+#include <string.h>
+
+#include <mutex>
+
+#include "sgl_common.h"
+#include "sgl_numeric.h"
+
+namespace sgl {
+
+static thread_local char g_last_error[1024] = {0};
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+}
+
+int device_cu_count() {
+  static std::mutex mu;
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+}  // namespace sgl
+
+extern "C" {
+
+int sgl_abi_version(void) { return SGL_ABI_VERSION; }
+
+const char* sgl_last_error(void) { return sgl::g_last_error; }
+
+int sgl_probe(void) {
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0) {
+    sgl::set_error("no HIP device: %s", e != hipSuccess ? hipGetErrorString(e) : "count == 0");
+    return 0;
+  }
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    sgl::set_error("hipGetDevice failed");
+    return 0;
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+    sgl::set_error("hipGetDeviceProperties failed");
+    return 0;
+  }
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    sgl::set_error("device %d is %s; this library is built for gfx950 only", dev, prop.gcnArchName);
+    return 0;
+  }
+  return 1;
+}
+
+int sgl_host_f32_to_e4m3(const float* x, uint8_t* y, int64_t n) {
+  SGL_REQUIRE(x && y && n >= 0, "sgl_host_f32_to_e4m3: bad arguments");
+  for (int64_t i = 0; i < n; ++i) y[i] = sgl::f32_to_e4m3(x[i]);
+  return SGL_OK;
+}
+
+int sgl_host_e4m3_to_f32(const uint8_t* x, float* y, int64_t n) {
+  SGL_REQUIRE(x && y && n >= 0, "sgl_host_e4m3_to_f32: bad arguments");
+  for (int64_t i = 0; i < n; ++i) y[i] = sgl::e4m3_to_f32(x[i]);
+  return SGL_OK;
+}
+
+int sgl_host_group_scale(int scale_mode, const float* amax, float* scale, int64_t n) {
+  SGL_REQUIRE(amax && scale && n >= 0, "sgl_host_group_scale: bad arguments");
+  SGL_REQUIRE(scale_mode >= 0 && scale_mode <= 4, "sgl_host_group_scale: bad scale_mode %d",
+              scale_mode);
+  for (int64_t i = 0; i < n; ++i) scale[i] = sgl::group_scale(scale_mode, amax[i]);
+  return SGL_OK;
+}
+
+int sgl_host_quant_elem(int scale_mode, const float* x, const float* scale, uint8_t* y, int64_t n) {
+  SGL_REQUIRE(x && scale && y && n >= 0, "sgl_host_quant_elem: bad arguments");
+  SGL_REQUIRE(scale_mode >= 0 && scale_mode <= 4, "sgl_host_quant_elem: bad scale_mode %d",
+              scale_mode);
+  for (int64_t i = 0; i < n; ++i) {
+    float sf = scale[i];
+    y[i] = sgl::quant_elem(scale_mode, x[i], sf, 1.0f / sf);
+  }
+  return SGL_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,398 @@
+// FP8 KV row pack (layouts A and B), footer paging, sparse-MLA gather-dequant
+// and the SWA / compressed index split.
+//
+// All HBM-bound byte work: one wavefront per row, every lane moving 8 input
+// values (16 B for bf16) and 8 e4m3 bytes, group maxima by xor-shuffles inside
+// aligned lane groups (8 lanes = 64 values for layout A, 16 lanes = 128 values
+// for layout B), the group scales gathered into one lane for a single store.
+#include "sgl_common.h"
+#include "sgl_numeric.h"
+
+namespace sgl {
+namespace {
+
+constexpr int A_NOPE = 448, A_DIM = 512, A_ROW = 584, A_DATA = 576;
+constexpr int B_LAT = 512, B_DIM = 576, B_ROW = 656;
+
+template <int DT>
+__device__ __forceinline__ void load8(const uint8_t* row, int elem, float* f, uint4* raw) {
+  if constexpr (DT == SGL_F32) {
+    const float4 a = *reinterpret_cast<const float4*>(row + elem * 4);
+    const float4 b = *reinterpret_cast<const float4*>(row + elem * 4 + 16);
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    *raw = make_uint4(0, 0, 0, 0);
+  } else {
+    const uint4 v = *reinterpret_cast<const uint4*>(row + elem * 2);
+    *raw = v;
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (DT == SGL_BF16) {
+        f[2 * i] = bits_f32(w[i] << 16);
+        f[2 * i + 1] = bits_f32(w[i] & 0xFFFF0000u);
+      } else {
+        f[2 * i] = f16_to_f32((uint16_t)(w[i] & 0xFFFFu));
+        f[2 * i + 1] = f16_to_f32((uint16_t)(w[i] >> 16));
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ uint2 pack_q8(const uint8_t* q) {
+  return make_uint2((uint32_t)q[0] | ((uint32_t)q[1] << 8) | ((uint32_t)q[2] << 16) |
+                        ((uint32_t)q[3] << 24),
+                    (uint32_t)q[4] | ((uint32_t)q[5] << 8) | ((uint32_t)q[6] << 16) |
+                        ((uint32_t)q[7] << 24));
+}
+
+// Layout A: lanes 0..55 quantize 8 NoPE values each (7 groups of 64 = 8
+// lanes), lanes 56..63 carry the 128 RoPE bytes verbatim.  paged != 0 writes
+// the footer page layout of to_paged_hnd directly (data at l*576 inside the
+// page, scales at page*576 + l*8) and zero-fills padding rows.
+template <int DT>
+__global__ __launch_bounds__(256) void kv_pack_a_kernel(const uint8_t* __restrict__ kv, int64_t T,
+                                                        int64_t ld_bytes, int mode, int paged,
+                                                        int page, int64_t rows_total,
+                                                        uint8_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  for (int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); t < rows_total; t += nwaves) {
+    uint8_t* data;
+    uint8_t* foot;
+    if (paged) {
+      const int64_t pg = t / page, l = t - pg * page;
+      uint8_t* pbase = out + pg * (int64_t)page * A_ROW;
+      data = pbase + l * A_DATA;
+      foot = pbase + (int64_t)page * A_DATA + l * 8;
+    } else {
+      data = out + t * A_ROW;
+      foot = data + A_DATA;
+    }
+    if (t >= T) {  // padding row of the last page
+      if (lane < 72) *reinterpret_cast<uint2*>(data + lane * 8) = make_uint2(0, 0);
+      if (lane < 8) *reinterpret_cast<uint2*>(data + 512 + lane * 8) = make_uint2(0, 0);
+      if (lane == 0) *reinterpret_cast<uint2*>(foot) = make_uint2(0, 0);
+      continue;
+    }
+    const uint8_t* row = kv + t * ld_bytes;
+    float f[8];
+    uint4 raw;
+    load8<DT>(row, lane * 8, f, &raw);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf_(amax, fabsf(f[i]));
+#pragma unroll
+    for (int o = 4; o > 0; o >>= 1) amax = fmaxf_(amax, __shfl_xor(amax, o, 64));
+    const float sf = group_scale(mode, amax);
+    uint32_t sbyte = pow2_to_e8m0(sf);
+    if (lane < 56) {
+      uint8_t q[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) q[i] = quant_elem(mode, f[i], sf, 0.0f);
+      *reinterpret_cast<uint2*>(data + lane * 8) = pack_q8(q);
+    } else {
+      // rope bytes as given (bf16 / f16), 16 per lane at 448 + 16*(lane-56)
+      uint8_t* dst = data + A_NOPE + (lane - 56) * 16;
+      *reinterpret_cast<uint2*>(dst) = make_uint2(raw.x, raw.y);
+      *reinterpret_cast<uint2*>(dst + 8) = make_uint2(raw.z, raw.w);
+    }
+    // 7 scale bytes + zero pad -> one 8-byte store by lane 0
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int g = 0; g < 7; ++g) {
+      const uint32_t b = (uint32_t)__shfl((int)sbyte, g * 8, 64) & 0xFFu;
+      if (g < 4)
+        lo |= b << (8 * g);
+      else
+        hi |= b << (8 * (g - 4));
+    }
+    if (lane == 0) *reinterpret_cast<uint2*>(foot) = make_uint2(lo, hi);
+  }
+}
+
+// Layout B: 64 lanes x 8 latent values (4 groups of 128 = 16 lanes each),
+// then lanes 0..7 copy the 128 RoPE bytes; 4 fp32 scales stored by lane 0.
+template <int DT>
+__global__ __launch_bounds__(256) void kv_pack_b_kernel(const uint8_t* __restrict__ kv, int64_t T,
+                                                        int64_t ld_bytes,
+                                                        uint8_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  constexpr int ES = DT == SGL_F32 ? 4 : 2;
+  for (int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); t < T; t += nwaves) {
+    const uint8_t* row = kv + t * ld_bytes;
+    uint8_t* o = out + t * B_ROW;
+    float f[8];
+    uint4 raw;
+    load8<DT>(row, lane * 8, f, &raw);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf_(amax, fabsf(f[i]));
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) amax = fmaxf_(amax, __shfl_xor(amax, off, 64));
+    const float sf = group_scale(SCALE_TORCH_FP32, amax);
+    const float inv = 1.0f / sf;
+    uint8_t q[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = quant_elem(SCALE_TORCH_FP32, f[i], sf, inv);
+    *reinterpret_cast<uint2*>(o + lane * 8) = pack_q8(q);
+    if (lane < 8) {
+      if constexpr (DT == SGL_F32) {
+        // fp32 input: rope stored as bf16 (RNE) so the row stays 656 B
+        float r[8];
+        uint4 unused;
+        load8<DT>(row, B_LAT + lane * 8, r, &unused);
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          w[i] = (uint32_t)f32_to_bf16(r[2 * i]) | ((uint32_t)f32_to_bf16(r[2 * i + 1]) << 16);
+        *reinterpret_cast<uint4*>(o + B_LAT + lane * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+      } else {
+        const uint4 v = *reinterpret_cast<const uint4*>(row + (B_LAT + lane * 8) * ES);
+        *reinterpret_cast<uint4*>(o + B_LAT + lane * 16) = v;
+      }
+    }
+    const float s0 = __shfl(sf, 0, 64), s1 = __shfl(sf, 16, 64), s2 = __shfl(sf, 32, 64),
+                s3 = __shfl(sf, 48, 64);
+    if (lane == 0) *reinterpret_cast<float4*>(o + 640) = make_float4(s0, s1, s2, s3);
+  }
+}
+
+__global__ __launch_bounds__(256) void kv_to_paged_kernel(const uint8_t* __restrict__ packed,
+                                                          int64_t T, int page, int64_t rows_total,
+                                                          uint8_t* __restrict__ pages) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  for (int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); t < rows_total; t += nwaves) {
+    const int64_t pg = t / page, l = t - pg * page;
+    uint8_t* pbase = pages + pg * (int64_t)page * A_ROW;
+    // 73 eight-byte words per row: 72 data words, 1 footer word
+    for (int w = lane; w < 73; w += 64) {
+      const uint2 v = t < T ? *reinterpret_cast<const uint2*>(packed + t * A_ROW + w * 8)
+                            : make_uint2(0, 0);
+      uint8_t* dst = w < 72 ? pbase + l * A_DATA + w * 8 : pbase + (int64_t)page * A_DATA + l * 8;
+      *reinterpret_cast<uint2*>(dst) = v;
+    }
+  }
+}
+
+// One wavefront per gathered row.  Layout A: out 512 bf16 = 448 dequantized
+// (e4m3 * 2^(e8m0-127), exact in bf16) + 64 rope; layout B: out 576 bf16 =
+// 512 bf16(e4m3 * fp32 scale) + 64 rope.
+template <int LAYOUT>
+__global__ __launch_bounds__(256) void kv_gather_kernel(const uint8_t* __restrict__ cache,
+                                                        int paged, int page, int64_t n_rows,
+                                                        const int32_t* __restrict__ idx,
+                                                        int64_t total, uint16_t* __restrict__ out) {
+  constexpr int ODIM = LAYOUT == SGL_KV_LAYOUT_A ? A_DIM : B_DIM;
+  const int lane = threadIdx.x & 63;
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < total; r += nwaves) {
+    const int32_t id = idx[r];
+    uint16_t* o = out + r * ODIM;
+    if (id < 0 || id >= n_rows) {
+      const uint4 z = make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4*>(o + lane * 8) = z;
+      if (LAYOUT == SGL_KV_LAYOUT_B && lane < 8) *reinterpret_cast<uint4*>(o + 512 + lane * 8) = z;
+      continue;
+    }
+    if constexpr (LAYOUT == SGL_KV_LAYOUT_A) {
+      const uint8_t* data;
+      const uint8_t* foot;
+      if (paged) {
+        const int64_t pg = id / page, l = id - pg * page;
+        const uint8_t* pbase = cache + pg * (int64_t)page * A_ROW;
+        data = pbase + l * A_DATA;
+        foot = pbase + (int64_t)page * A_DATA + l * 8;
+      } else {
+        data = cache + (int64_t)id * A_ROW;
+        foot = data + A_DATA;
+      }
+      if (lane < 56) {
+        const uint2 qv = *reinterpret_cast<const uint2*>(data + lane * 8);
+        const uint32_t sb = foot[lane >> 3];
+        const uint8_t q[8] = {(uint8_t)qv.x, (uint8_t)(qv.x >> 8), (uint8_t)(qv.x >> 16),
+                              (uint8_t)(qv.x >> 24), (uint8_t)qv.y, (uint8_t)(qv.y >> 8),
+                              (uint8_t)(qv.y >> 16), (uint8_t)(qv.y >> 24)};
+        const float s = sb == 0xFFu ? bits_f32(0x7FC00000u)
+                                    : (sb == 0 ? bits_f32(0x00400000u) : bits_f32(sb << 23));
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          w[i] = (uint32_t)f32_to_bf16(e4m3_to_f32(q[2 * i]) * s) |
+                 ((uint32_t)f32_to_bf16(e4m3_to_f32(q[2 * i + 1]) * s) << 16);
+        *reinterpret_cast<uint4*>(o + lane * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+      } else {
+        const uint8_t* src = data + A_NOPE + (lane - 56) * 16;
+        const uint2 a = *reinterpret_cast<const uint2*>(src);
+        const uint2 b = *reinterpret_cast<const uint2*>(src + 8);
+        *reinterpret_cast<uint4*>(o + lane * 8) = make_uint4(a.x, a.y, b.x, b.y);
+      }
+    } else {
+      const uint8_t* row = cache + (int64_t)id * B_ROW;
+      const uint2 qv = *reinterpret_cast<const uint2*>(row + lane * 8);
+      const float s = *reinterpret_cast<const float*>(row + 640 + (lane >> 4) * 4);
+      const uint8_t q[8] = {(uint8_t)qv.x, (uint8_t)(qv.x >> 8), (uint8_t)(qv.x >> 16),
+                            (uint8_t)(qv.x >> 24), (uint8_t)qv.y, (uint8_t)(qv.y >> 8),
+                            (uint8_t)(qv.y >> 16), (uint8_t)(qv.y >> 24)};
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = (uint32_t)f32_to_bf16(e4m3_to_f32(q[2 * i]) * s) |
+               ((uint32_t)f32_to_bf16(e4m3_to_f32(q[2 * i + 1]) * s) << 16);
+      *reinterpret_cast<uint4*>(o + lane * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+      if (lane < 8)
+        *reinterpret_cast<uint4*>(o + 512 + lane * 8) =
+            *reinterpret_cast<const uint4*>(row + B_LAT + lane * 16);
+    }
+  }
+}
+
+template <typename IT>
+__global__ __launch_bounds__(256) void split_indices_kernel(const IT* __restrict__ topk, int64_t BS,
+                                                            int64_t K, int64_t window,
+                                                            int32_t* __restrict__ swa,
+                                                            int32_t* __restrict__ swa_lens,
+                                                            int32_t* __restrict__ comp,
+                                                            int32_t* __restrict__ comp_lens) {
+  const int lane = threadIdx.x & 63;
+  const int64_t swa_k = window < K ? window : K;
+  const int64_t comp_k = K - swa_k;
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  for (int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); b < BS; b += nwaves) {
+    int n_swa = 0, n_comp = 0;
+    for (int64_t c0 = 0; c0 < K; c0 += 64) {
+      const int64_t c = c0 + lane;
+      const bool in = c < K;
+      const int32_t v = in ? (int32_t)topk[b * K + c] : -1;
+      const bool valid = in && v >= 0;
+      const bool is_swa = c < swa_k;
+      if (in && is_swa) swa[b * swa_k + c] = v;
+      if (in && !is_swa) comp[b * comp_k + (c - swa_k)] = valid ? (int32_t)(v - window) : v;
+      n_swa += __popcll(__ballot(valid && is_swa));
+      n_comp += __popcll(__ballot(valid && !is_swa));
+    }
+    if (lane == 0) {
+      swa_lens[b] = n_swa;
+      comp_lens[b] = n_comp;
+    }
+  }
+}
+
+unsigned grid_for_rows(int64_t rows) {
+  int64_t blocks = ceil_div(rows, 4);
+  const int64_t cap = (int64_t)device_cu_count() * 32;
+  if (blocks > cap) blocks = cap;
+  return (unsigned)(blocks < 1 ? 1 : blocks);
+}
+
+}  // namespace
+}  // namespace sgl
+
+extern "C" {
+
+int sgl_kv_pack(const void* kv, int dtype, int64_t T, int64_t ldkv, int layout, int scale_mode,
+                int paged, int page_size, void* out, sgl_stream_t stream) {
+  SGL_REQUIRE(T >= 0, "kv_pack: negative T");
+  SGL_REQUIRE(dtype == SGL_BF16 || dtype == SGL_F16 || dtype == SGL_F32, "kv_pack: bad dtype");
+  SGL_REQUIRE(layout == SGL_KV_LAYOUT_A || layout == SGL_KV_LAYOUT_B, "kv_pack: bad layout");
+  hipStream_t st = (hipStream_t)stream;
+  const int es = dtype == SGL_F32 ? 4 : 2;
+  if (layout == SGL_KV_LAYOUT_A) {
+    SGL_REQUIRE(scale_mode == SGL_SCALE_KV_UE8M0 || scale_mode == SGL_SCALE_TILELANG_UE8M0,
+                "kv_pack: layout A needs a ue8m0 scale mode (got %d)", scale_mode);
+    SGL_REQUIRE(dtype != SGL_F32, "kv_pack: layout A stores the rope as 16-bit values; fp32 "
+                                  "input is not representable in the 584-byte row");
+    SGL_REQUIRE(ldkv >= 512, "kv_pack: layout A row stride %lld < 512", (long long)ldkv);
+    SGL_REQUIRE(!paged || page_size > 0, "kv_pack: page_size must be positive");
+    const int64_t rows = paged ? sgl::ceil_div(T, page_size) * page_size : T;
+    if (rows == 0) return SGL_OK;
+    SGL_REQUIRE(out && (T == 0 || kv), "kv_pack: null pointer");
+    SGL_REQUIRE(sgl::aligned(out, 8) && (T == 0 || (sgl::aligned(kv, 16) && (ldkv * es) % 16 == 0)),
+                "kv_pack: kv rows must be 16-byte aligned, out 8-byte aligned");
+    const unsigned g = sgl::grid_for_rows(rows);
+    if (dtype == SGL_BF16)
+      sgl::kv_pack_a_kernel<SGL_BF16><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
+                                                         scale_mode, paged, page_size, rows,
+                                                         (uint8_t*)out);
+    else
+      sgl::kv_pack_a_kernel<SGL_F16><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
+                                                        scale_mode, paged, page_size, rows,
+                                                        (uint8_t*)out);
+    return sgl::check_launch("kv_pack_a");
+  }
+  SGL_REQUIRE(!paged, "kv_pack: layout B has no paged form");
+  SGL_REQUIRE(ldkv >= 576, "kv_pack: layout B row stride %lld < 576", (long long)ldkv);
+  if (T == 0) return SGL_OK;
+  SGL_REQUIRE(kv && out, "kv_pack: null pointer");
+  SGL_REQUIRE(sgl::aligned(out, 16) && sgl::aligned(kv, 16) && (ldkv * es) % 16 == 0,
+              "kv_pack: layout B rows must be 16-byte aligned");
+  const unsigned g = sgl::grid_for_rows(T);
+  if (dtype == SGL_BF16)
+    sgl::kv_pack_b_kernel<SGL_BF16><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
+                                                       (uint8_t*)out);
+  else if (dtype == SGL_F16)
+    sgl::kv_pack_b_kernel<SGL_F16><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
+                                                      (uint8_t*)out);
+  else
+    sgl::kv_pack_b_kernel<SGL_F32><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
+                                                      (uint8_t*)out);
+  return sgl::check_launch("kv_pack_b");
+}
+
+int sgl_kv_to_paged(const void* packed, int64_t T, int page_size, void* pages,
+                    sgl_stream_t stream) {
+  SGL_REQUIRE(T >= 0 && page_size > 0, "kv_to_paged: bad T / page_size");
+  const int64_t rows = sgl::ceil_div(T, page_size) * page_size;
+  if (rows == 0) return SGL_OK;
+  SGL_REQUIRE(pages && (T == 0 || packed), "kv_to_paged: null pointer");
+  SGL_REQUIRE(sgl::aligned(pages, 8) && sgl::aligned(packed, 8), "kv_to_paged: misaligned");
+  sgl::kv_to_paged_kernel<<<sgl::grid_for_rows(rows), 256, 0, (hipStream_t)stream>>>(
+      (const uint8_t*)packed, T, page_size, rows, (uint8_t*)pages);
+  return sgl::check_launch("kv_to_paged");
+}
+
+int sgl_kv_gather_dequant(const void* cache, int layout, int paged, int page_size, int64_t n_rows,
+                          const int32_t* idx, int64_t nq, int64_t nsel, void* out,
+                          sgl_stream_t stream) {
+  SGL_REQUIRE(layout == SGL_KV_LAYOUT_A || layout == SGL_KV_LAYOUT_B, "kv_gather: bad layout");
+  SGL_REQUIRE(nq >= 0 && nsel >= 0 && n_rows >= 0, "kv_gather: negative size");
+  SGL_REQUIRE(!paged || (layout == SGL_KV_LAYOUT_A && page_size > 0),
+              "kv_gather: paged caches are layout A with a positive page_size");
+  const int64_t total = nq * nsel;
+  if (total == 0) return SGL_OK;
+  SGL_REQUIRE(idx && out && (n_rows == 0 || cache), "kv_gather: null pointer");
+  SGL_REQUIRE(sgl::aligned(out, 16) && sgl::aligned(cache, layout == SGL_KV_LAYOUT_B ? 16 : 8),
+              "kv_gather: misaligned cache/out");
+  const unsigned g = sgl::grid_for_rows(total);
+  hipStream_t st = (hipStream_t)stream;
+  if (layout == SGL_KV_LAYOUT_A)
+    sgl::kv_gather_kernel<SGL_KV_LAYOUT_A><<<g, 256, 0, st>>>(
+        (const uint8_t*)cache, paged, page_size, n_rows, idx, total, (uint16_t*)out);
+  else
+    sgl::kv_gather_kernel<SGL_KV_LAYOUT_B><<<g, 256, 0, st>>>(
+        (const uint8_t*)cache, 0, 1, n_rows, idx, total, (uint16_t*)out);
+  return sgl::check_launch("kv_gather_dequant");
+}
+
+int sgl_split_swa_compress_indices(const void* topk, int idx_int64, int64_t BS, int64_t K,
+                                   int64_t window, int32_t* swa, int32_t* swa_lens,
+                                   int32_t* comp, int32_t* comp_lens, sgl_stream_t stream) {
+  SGL_REQUIRE(BS >= 0 && K >= 0 && window >= 0, "split_indices: negative size");
+  if (BS == 0) return SGL_OK;
+  SGL_REQUIRE(swa_lens && comp_lens && (K == 0 || topk), "split_indices: null pointer");
+  const int64_t swa_k = window < K ? window : K;
+  SGL_REQUIRE((swa_k == 0 || swa) && (K - swa_k == 0 || comp), "split_indices: null pointer");
+  const unsigned g = sgl::grid_for_rows(BS);
+  hipStream_t st = (hipStream_t)stream;
+  if (idx_int64)
+    sgl::split_indices_kernel<int64_t><<<g, 256, 0, st>>>((const int64_t*)topk, BS, K, window, swa,
+                                                          swa_lens, comp, comp_lens);
+  else
+    sgl::split_indices_kernel<int32_t><<<g, 256, 0, st>>>((const int32_t*)topk, BS, K, window, swa,
+                                                          swa_lens, comp, comp_lens);
+  return sgl::check_launch("split_swa_compress_indices");
+}
+
+}  // extern "C"

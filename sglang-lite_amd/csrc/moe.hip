@@ -1,0 +1,468 @@
+// MoE dispatch around the grouped FP8 GEMMs: router top-k, the stable
+// token-to-expert permutation, the grouped gate/up and down entry points,
+// the ordered unpermute-combine, and the one-call layer.
+//
+// Reference semantics (deepseek_infer/model.py:629-644,
+// engine/v4_moe_fast.py:79-106): experts are visited in ascending id and
+// torch.where(indices == e) lists that expert's slots token-ascending, so the
+// permutation is a stable counting sort of slot = t*k + j by expert id; the
+// combine adds the bf16 expert outputs of a token into an fp32 zero in
+// ascending expert order, then adds the shared expert, then rounds to bf16.
+#include "sgl_gemm.h"
+#include "sgl_numeric.h"
+
+namespace sgl {
+namespace {
+
+constexpr int kMaxRouteE = 512;    // experts per token row in route_topk
+constexpr int kMaxPermE = 1024;    // experts in the permutation
+constexpr int kPermThreads = 1024; // one workgroup, 16 wavefronts
+constexpr int kPermWaves = kPermThreads / 64;
+
+// ------------------------------------------------------------ route top-k
+
+template <int EPL>
+__global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits, int64_t T,
+                                                         int E, int k, int score_func,
+                                                         const float* __restrict__ bias,
+                                                         float route_scale, int32_t* __restrict__ ids,
+                                                         float* __restrict__ weights) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float NEG_INF = -__builtin_huge_valf();
+  float lg[EPL], sc[EPL], sel[EPL];
+  bool ok[EPL];
+#pragma unroll
+  for (int q = 0; q < EPL; ++q) {
+    const int e = lane + 64 * q;
+    ok[q] = e < E;
+    lg[q] = ok[q] ? logits[t * E + e] : NEG_INF;
+  }
+  if (score_func == SGL_SCORE_SOFTMAX) {
+    float m = NEG_INF;
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) m = fmaxf_(m, lg[q]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf_(m, __shfl_xor(m, o, 64));
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) {
+      sc[q] = ok[q] ? expf(lg[q] - m) : 0.0f;
+      s += sc[q];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) sc[q] = sc[q] / s;
+  } else if (score_func == SGL_SCORE_SIGMOID) {
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) sc[q] = 1.0f / (1.0f + expf(-lg[q]));
+  } else {
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) {
+      const float x = lg[q];
+      sc[q] = sqrtf(x > 20.0f ? x : log1pf(expf(x)));
+    }
+  }
+  // Selection key: every score function is monotone in the logit, so without
+  // a bias the logits select exactly the experts torch.topk picks on the
+  // scores (barring exact score ties); with a bias the biased scores are used.
+#pragma unroll
+  for (int q = 0; q < EPL; ++q) {
+    const int e = lane + 64 * q;
+    sel[q] = !ok[q] ? NEG_INF : (bias ? sc[q] + bias[e] : lg[q]);
+  }
+  unsigned taken = 0u;
+  float wsum = 0.0f;
+  int my_e = 0;      // lane j keeps the j-th pick
+  float my_s = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    float bv = NEG_INF;
+    int be = 0x7FFFFFFF;
+    float bs = 0.0f;
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) {
+      const int e = lane + 64 * q;
+      const bool avail = ok[q] && !((taken >> q) & 1u);
+      if (avail && (be == 0x7FFFFFFF || sel[q] > bv || (sel[q] == bv && e < be))) {
+        bv = sel[q];
+        be = e;
+        bs = sc[q];
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oe = __shfl_xor(be, o, 64);
+      const float os = __shfl_xor(bs, o, 64);
+      if (oe != 0x7FFFFFFF && (be == 0x7FFFFFFF || ov > bv || (ov == bv && oe < be))) {
+        bv = ov;
+        be = oe;
+        bs = os;
+      }
+    }
+    if (be != 0x7FFFFFFF && (be & 63) == lane) taken |= 1u << (be >> 6);
+    if (lane == j) {
+      my_e = be;
+      my_s = bs;
+    }
+    wsum += bs;
+  }
+  if (lane < k) {
+    float w = my_s;
+    if (score_func != SGL_SCORE_SOFTMAX) w = w / wsum;
+    ids[t * k + lane] = my_e;
+    weights[t * k + lane] = w * route_scale;
+  }
+}
+
+// -------------------------------------------------------------- permute
+
+// One workgroup.  Pass 1 histograms the ids in LDS; an exclusive scan gives
+// the expert offsets.  Pass 2 walks the slots in order, 1024 per round: inside
+// a wavefront the lanes holding the same expert find each other with one
+// ballot per id bit (their rank = popcount of lower peers), per-wavefront
+// counts in LDS give the offset of each wavefront inside the round, and a
+// per-expert running base carries rounds forward, so equal ids keep slot order.
+__global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* __restrict__ ids,
+                                                               int64_t P, int E,
+                                                               int32_t* __restrict__ counts,
+                                                               int32_t* __restrict__ offsets,
+                                                               int32_t* __restrict__ sorted_slot,
+                                                               int32_t* __restrict__ slot_pos) {
+  __shared__ int cnt[kMaxPermE];
+  __shared__ int run[kMaxPermE];
+  __shared__ int wcnt[kPermWaves][kMaxPermE];
+  __shared__ int wsum[kPermWaves];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int e = tid; e < E; e += kPermThreads) {
+    cnt[e] = 0;
+    for (int w = 0; w < kPermWaves; ++w) wcnt[w][e] = 0;
+  }
+  __syncthreads();
+  for (int64_t i = tid; i < P; i += kPermThreads) {
+    const int e = ids[i];
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  // exclusive scan of cnt[0..E) (E <= 1024: one value per thread)
+  {
+    const int v = tid < E ? cnt[tid] : 0;
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += u;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < wave; ++w) base += wsum[w];
+    const int excl = base + incl - v;
+    if (tid < E) {
+      run[tid] = excl;
+      counts[tid] = v;
+      offsets[tid] = excl;
+    }
+    if (tid == E - 1) offsets[E] = excl + v;
+  }
+  __syncthreads();
+  const int nbits = E > 1 ? 32 - __clz(E - 1) : 0;
+  const unsigned long long lt_mask = (1ull << lane) - 1ull;
+  for (int64_t base = 0; base < P; base += kPermThreads) {
+    const int64_t i = base + tid;
+    const int e = i < P ? ids[i] : -1;
+    const bool valid = e >= 0 && e < E;
+    unsigned long long peers = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = valid && ((e >> b) & 1);
+      const unsigned long long m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    const int rank = __popcll(peers & lt_mask);
+    if (valid && rank == 0) wcnt[wave][e] = __popcll(peers);
+    __syncthreads();
+    if (valid) {
+      int pre = 0;
+      for (int w = 0; w < wave; ++w) pre += wcnt[w][e];
+      const int pos = run[e] + pre + rank;
+      sorted_slot[pos] = (int32_t)i;
+      slot_pos[i] = pos;
+    } else if (i < P) {
+      slot_pos[i] = -1;
+    }
+    __syncthreads();
+    for (int x = tid; x < E; x += kPermThreads) {
+      int s = 0;
+      for (int w = 0; w < kPermWaves; ++w) {
+        s += wcnt[w][x];
+        wcnt[w][x] = 0;
+      }
+      run[x] += s;
+    }
+    __syncthreads();
+  }
+}
+
+// -------------------------------------------------------------- combine
+
+// One workgroup per token: sum the token's k expert rows (bf16) into fp32 in
+// ascending expert id, add the shared row, round to bf16.  8 columns / thread.
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ out,
+                                                      const int32_t* __restrict__ ids, int64_t T,
+                                                      int k, int64_t H, int has_shared, int E,
+                                                      uint16_t* __restrict__ y) {
+  __shared__ int ord[16];
+  __shared__ int nvalid;
+  const int64_t t = blockIdx.x;
+  const int tid = threadIdx.x;
+  if (tid == 0) nvalid = 0;
+  __syncthreads();
+  if (tid < k) {
+    const int my = ids[t * k + tid];
+    if (my >= 0 && my < E) {
+      int rank = 0;
+      for (int j = 0; j < k; ++j) {
+        const int o = ids[t * k + j];
+        if (o < 0 || o >= E) continue;
+        if (o < my || (o == my && j < tid)) ++rank;
+      }
+      ord[rank] = tid;
+      atomicAdd(&nvalid, 1);
+    }
+  }
+  __syncthreads();
+  const int nv = nvalid;
+  const int stride_rows = k + has_shared;
+  const uint16_t* base = out + t * stride_rows * H;
+  for (int64_t col = (int64_t)tid * 8; col < H; col += 256 * 8) {
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+    for (int jj = 0; jj < nv; ++jj) {
+      const uint4 v = *reinterpret_cast<const uint4*>(base + (int64_t)ord[jj] * H + col);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += bits_f32(w[i] << 16);
+        acc[2 * i + 1] += bits_f32(w[i] & 0xFFFF0000u);
+      }
+    }
+    if (has_shared) {
+      const uint4 v = *reinterpret_cast<const uint4*>(base + (int64_t)k * H + col);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += bits_f32(w[i] << 16);
+        acc[2 * i + 1] += bits_f32(w[i] & 0xFFFF0000u);
+      }
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o[i] = (uint32_t)f32_to_bf16(acc[2 * i]) | ((uint32_t)f32_to_bf16(acc[2 * i + 1]) << 16);
+    *reinterpret_cast<uint4*>(y + t * H + col) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+struct MoeWorkspace {
+  uint8_t* xq;
+  float* xs;
+  int32_t* counts;
+  int32_t* offsets;
+  int32_t* sorted_slot;
+  int32_t* slot_pos;
+  uint8_t* hq;
+  float* hs;
+  uint16_t* out;
+  size_t bytes;
+};
+
+MoeWorkspace carve(void* base, int64_t T, int64_t H, int64_t I, int E, int k, int has_shared) {
+  MoeWorkspace w = {};
+  const int64_t P = T * k;
+  const int64_t rows = P + (has_shared ? T : 0);
+  uint8_t* p = reinterpret_cast<uint8_t*>(base);
+  int64_t off = 0;
+  auto take = [&](int64_t n) {
+    uint8_t* q = p ? p + off : nullptr;
+    off += align256(n);
+    return q;
+  };
+  w.xq = take(T * H);
+  w.xs = reinterpret_cast<float*>(take(T * (H / 128) * 4));
+  w.counts = reinterpret_cast<int32_t*>(take((int64_t)E * 4));
+  w.offsets = reinterpret_cast<int32_t*>(take((int64_t)(E + 1) * 4));
+  w.sorted_slot = reinterpret_cast<int32_t*>(take(P * 4));
+  w.slot_pos = reinterpret_cast<int32_t*>(take(P * 4));
+  w.hq = take(rows * I);
+  w.hs = reinterpret_cast<float*>(take(rows * (I / 128) * 4));
+  w.out = reinterpret_cast<uint16_t*>(take(T * (k + has_shared) * H * 2));
+  w.bytes = (size_t)off;
+  return w;
+}
+
+int check_moe_shapes(const char* what, int64_t T, int64_t H, int64_t I, int E, int k) {
+  SGL_REQUIRE(T >= 0 && H > 0 && I > 0, "%s: bad shape T=%lld H=%lld I=%lld", what, (long long)T,
+              (long long)H, (long long)I);
+  SGL_REQUIRE(H % 128 == 0 && I % 128 == 0, "%s: H and I must be multiples of 128", what);
+  SGL_REQUIRE(E >= 1 && E <= kMaxPermE, "%s: E=%d not in [1, %d]", what, E, kMaxPermE);
+  SGL_REQUIRE(k >= 1 && k <= 16 && k <= E, "%s: k=%d not in [1, min(16, E)]", what, k);
+  SGL_REQUIRE(T * k < 0x7FFFFFFF && T * (k + 1) * H < ((int64_t)1 << 46), "%s: too many tokens",
+              what);
+  return SGL_OK;
+}
+
+}  // namespace
+}  // namespace sgl
+
+extern "C" {
+
+int sgl_moe_route_topk(const float* logits, int64_t T, int E, int k, int score_func,
+                       const float* bias, float route_scale, int32_t* ids, float* weights,
+                       sgl_stream_t stream) {
+  SGL_REQUIRE(T >= 0, "route_topk: negative T");
+  SGL_REQUIRE(E >= 1 && E <= sgl::kMaxRouteE, "route_topk: E=%d not in [1, %d]", E,
+              sgl::kMaxRouteE);
+  SGL_REQUIRE(k >= 1 && k <= 16 && k <= E, "route_topk: k=%d not in [1, min(16, E)]", k);
+  SGL_REQUIRE(score_func >= 0 && score_func <= 2, "route_topk: bad score_func %d", score_func);
+  if (T == 0) return SGL_OK;
+  SGL_REQUIRE(logits && ids && weights, "route_topk: null pointer");
+  const unsigned blocks = (unsigned)sgl::ceil_div(T, 4);
+  hipStream_t st = (hipStream_t)stream;
+  const int epl = (E + 63) / 64;
+#define SGL_ROUTE(n)                                                                               \
+  case n:                                                                                          \
+    sgl::route_topk_kernel<n><<<blocks, 256, 0, st>>>(logits, T, E, k, score_func, bias,           \
+                                                      route_scale, ids, weights);                  \
+    break;
+  switch (epl) {
+    SGL_ROUTE(1) SGL_ROUTE(2) SGL_ROUTE(3) SGL_ROUTE(4) SGL_ROUTE(5) SGL_ROUTE(6) SGL_ROUTE(7)
+    default:
+      sgl::route_topk_kernel<8><<<blocks, 256, 0, st>>>(logits, T, E, k, score_func, bias,
+                                                        route_scale, ids, weights);
+  }
+#undef SGL_ROUTE
+  return sgl::check_launch("route_topk");
+}
+
+int sgl_moe_permute(const int32_t* ids, int64_t T, int k, int E, int32_t* counts, int32_t* offsets,
+                    int32_t* sorted_slot, int32_t* slot_pos, sgl_stream_t stream) {
+  SGL_REQUIRE(T >= 0 && k >= 1, "moe_permute: bad T=%lld k=%d", (long long)T, k);
+  SGL_REQUIRE(E >= 1 && E <= sgl::kMaxPermE, "moe_permute: E=%d not in [1, %d]", E,
+              sgl::kMaxPermE);
+  SGL_REQUIRE(T * k < 0x7FFFFFFF, "moe_permute: T*k too large");
+  SGL_REQUIRE(counts && offsets && (T == 0 || (ids && sorted_slot && slot_pos)),
+              "moe_permute: null pointer");
+  sgl::permute_kernel<<<1, sgl::kPermThreads, 0, (hipStream_t)stream>>>(
+      ids, T * k, E, counts, offsets, sorted_slot, slot_pos);
+  return sgl::check_launch("moe_permute");
+}
+
+int sgl_moe_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I, int E, int k,
+                    const int32_t* offsets, const int32_t* sorted_slot, const float* route_w,
+                    const sgl_expert_ptrs* experts, int has_shared, float swiglu_limit,
+                    int scale_mode, void* hq, float* hs, sgl_stream_t stream) {
+  int rc = sgl::check_moe_shapes("moe_gate_up", T, H, I, E, k);
+  if (rc) return rc;
+  SGL_REQUIRE(scale_mode >= 0 && scale_mode <= 3, "moe_gate_up: bad scale_mode %d", scale_mode);
+  if (T == 0) return SGL_OK;
+  SGL_REQUIRE(xq && xs && offsets && sorted_slot && experts && hq && hs,
+              "moe_gate_up: null pointer");
+  SGL_REQUIRE(sgl::aligned(xq, 16) && sgl::aligned(hq, 8), "moe_gate_up: xq/hq misaligned");
+  sgl::GemmArgs g = {};
+  g.a = (const uint8_t*)xq;
+  g.sa = xs;
+  g.experts = experts;
+  g.offsets = offsets;
+  g.sorted_slot = sorted_slot;
+  g.route_w = route_w;
+  g.E = E;
+  g.k = k;
+  g.has_shared = has_shared ? 1 : 0;
+  g.T = T;
+  g.N = I;
+  g.K = H;
+  g.hq = (uint8_t*)hq;
+  g.hs = hs;
+  g.swiglu_limit = swiglu_limit;
+  g.scale_mode = scale_mode;
+  return sgl::launch_gemm(sgl::KIND_GATE_UP, g, T * k / E, (hipStream_t)stream);
+}
+
+int sgl_moe_down(const void* hq, const float* hs, int64_t T, int64_t H, int64_t I, int E, int k,
+                 const int32_t* offsets, const int32_t* sorted_slot,
+                 const sgl_expert_ptrs* experts, int has_shared, void* out, sgl_stream_t stream) {
+  int rc = sgl::check_moe_shapes("moe_down", T, H, I, E, k);
+  if (rc) return rc;
+  if (T == 0) return SGL_OK;
+  SGL_REQUIRE(hq && hs && offsets && sorted_slot && experts && out, "moe_down: null pointer");
+  SGL_REQUIRE(sgl::aligned(hq, 16), "moe_down: hq misaligned");
+  sgl::GemmArgs g = {};
+  g.a = (const uint8_t*)hq;
+  g.sa = hs;
+  g.experts = experts;
+  g.offsets = offsets;
+  g.sorted_slot = sorted_slot;
+  g.E = E;
+  g.k = k;
+  g.has_shared = has_shared ? 1 : 0;
+  g.T = T;
+  g.N = H;
+  g.K = I;
+  g.c = out;
+  return sgl::launch_gemm(sgl::KIND_DOWN, g, T * k / E, (hipStream_t)stream);
+}
+
+int sgl_moe_combine(const void* out, const int32_t* ids, int64_t T, int k, int64_t H,
+                    int has_shared, void* y, sgl_stream_t stream) {
+  SGL_REQUIRE(T >= 0 && k >= 1 && k <= 16 && H > 0 && H % 8 == 0, "moe_combine: bad shape");
+  if (T == 0) return SGL_OK;
+  SGL_REQUIRE(out && ids && y, "moe_combine: null pointer");
+  SGL_REQUIRE(sgl::aligned(out, 16) && sgl::aligned(y, 16), "moe_combine: out/y misaligned");
+  sgl::combine_kernel<<<(unsigned)T, 256, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)out, ids, T, k, H, has_shared ? 1 : 0, 0x7FFFFFFF, (uint16_t*)y);
+  return sgl::check_launch("moe_combine");
+}
+
+size_t sgl_moe_workspace_size(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared) {
+  if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
+  return sgl::carve(nullptr, T, H, I, E, k, has_shared ? 1 : 0).bytes;
+}
+
+int sgl_moe_forward(const void* x, int64_t T, int64_t H, int64_t I, int E, int k,
+                    const int32_t* ids, const float* weights, const sgl_expert_ptrs* experts,
+                    int has_shared, float swiglu_limit, int scale_mode, void* workspace,
+                    size_t workspace_bytes, void* y, sgl_stream_t stream) {
+  int rc = sgl::check_moe_shapes("moe_forward", T, H, I, E, k);
+  if (rc) return rc;
+  SGL_REQUIRE(scale_mode >= 0 && scale_mode <= 3, "moe_forward: bad scale_mode %d", scale_mode);
+  if (T == 0) return SGL_OK;
+  SGL_REQUIRE(x && ids && weights && experts && workspace && y, "moe_forward: null pointer");
+  has_shared = has_shared ? 1 : 0;
+  const sgl::MoeWorkspace w = sgl::carve(workspace, T, H, I, E, k, has_shared);
+  if (workspace_bytes < w.bytes) {
+    sgl::set_error("moe_forward: workspace %zu bytes < %zu needed", workspace_bytes, w.bytes);
+    return SGL_ERR_WORKSPACE;
+  }
+  SGL_REQUIRE(sgl::aligned(workspace, 256), "moe_forward: workspace must be 256-byte aligned");
+  if ((rc = sgl_act_quant(x, T, H, H, w.xq, H, w.xs, H / 128, 128, scale_mode, 0, 0, stream)))
+    return rc;
+  if ((rc = sgl_moe_permute(ids, T, k, E, w.counts, w.offsets, w.sorted_slot, w.slot_pos, stream)))
+    return rc;
+  if ((rc = sgl_moe_gate_up(w.xq, w.xs, T, H, I, E, k, w.offsets, w.sorted_slot, weights, experts,
+                            has_shared, swiglu_limit, scale_mode, w.hq, w.hs, stream)))
+    return rc;
+  if ((rc = sgl_moe_down(w.hq, w.hs, T, H, I, E, k, w.offsets, w.sorted_slot, experts, has_shared,
+                         w.out, stream)))
+    return rc;
+  hipStream_t st = (hipStream_t)stream;
+  sgl::combine_kernel<<<(unsigned)T, 256, 0, st>>>(w.out, ids, T, k, H, has_shared, E,
+                                                    (uint16_t*)y);
+  return sgl::check_launch("moe_combine");
+}
+
+}  // extern "C"

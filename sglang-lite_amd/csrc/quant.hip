@@ -1,0 +1,247 @@
+// Activation (1 x G) and weight (128 x 128) FP8 quantization kernels.
+//
+// Both are HBM-bound: act_quant moves 2 B in + 1 B out per element plus one
+// scale per group.  One group of G bf16 values is owned by G/8 consecutive
+// lanes, each holding 8 values (one 16-byte load), so a 64-lane wavefront
+// covers 8 (G = 64) or 4 (G = 128) groups per iteration and the group's |x|
+// maximum needs log2(G/8) cross-lane steps.
+#include "sgl_common.h"
+#include "sgl_numeric.h"
+
+namespace sgl {
+namespace {
+
+__device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bits_f32(w[i] << 16);
+    f[2 * i + 1] = bits_f32(w[i] & 0xFFFF0000u);
+  }
+}
+
+template <int LPG>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = LPG / 2; o > 0; o >>= 1) v = fmaxf_(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+template <int GROUP, bool INPLACE>
+__global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restrict__ x, int64_t M,
+                                                        int64_t K, int64_t ldx, void* __restrict__ y,
+                                                        int64_t ldy, void* __restrict__ s,
+                                                        int64_t lds, int mode, int scale_e8m0) {
+  constexpr int LPG = GROUP / 8;
+  const int64_t gpr = K / GROUP;
+  const int64_t total = M * gpr;
+  const int sub = threadIdx.x % LPG;
+  const int64_t per_sweep = (int64_t)gridDim.x * blockDim.x / LPG;
+  for (int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / LPG; g < total;
+       g += per_sweep) {
+    const int64_t row = g / gpr;
+    const int64_t col = (g - row * gpr) * GROUP + sub * 8;
+    const uint4 v = *reinterpret_cast<const uint4*>(x + row * ldx + col);
+    float f[8];
+    unpack_bf16x8(v, f);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf_(amax, fabsf(f[i]));
+    amax = group_max<LPG>(amax);
+    const float sf = group_scale(mode, amax);
+    const float inv = 1.0f / sf;
+    uint8_t q[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = quant_elem(mode, f[i], sf, inv);
+    if (INPLACE) {
+      // quant-dequant back to bf16: bf16(fp32(e4m3) * s)
+      uint32_t o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t lo = f32_to_bf16(e4m3_to_f32(q[2 * i]) * sf);
+        uint32_t hi = f32_to_bf16(e4m3_to_f32(q[2 * i + 1]) * sf);
+        o[i] = lo | (hi << 16);
+      }
+      *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(y) + row * ldy + col) =
+          make_uint4(o[0], o[1], o[2], o[3]);
+    } else {
+      uint2 o;
+      o.x = (uint32_t)q[0] | ((uint32_t)q[1] << 8) | ((uint32_t)q[2] << 16) | ((uint32_t)q[3] << 24);
+      o.y = (uint32_t)q[4] | ((uint32_t)q[5] << 8) | ((uint32_t)q[6] << 16) | ((uint32_t)q[7] << 24);
+      *reinterpret_cast<uint2*>(reinterpret_cast<uint8_t*>(y) + row * ldy + col) = o;
+    }
+    if (sub == 0) {
+      const int64_t si = row * lds + col / GROUP;
+      if (scale_e8m0)
+        reinterpret_cast<uint8_t*>(s)[si] = pow2_to_e8m0(sf);
+      else
+        reinterpret_cast<float*>(s)[si] = sf;
+    }
+  }
+}
+
+// One 256-thread block per 128 x 128 weight block.  Thread t owns the 8
+// columns [8*(t%16), +8) of rows t/16 + 16*i, i < 8.
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float* f);
+template <>
+__device__ __forceinline__ void load8<float>(const float* p, float* f) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+  f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+template <>
+__device__ __forceinline__ void load8<uint16_t>(const uint16_t* p, float* f) {
+  unpack_bf16x8(*reinterpret_cast<const uint4*>(p), f);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void weight_quant_kernel(const T* __restrict__ w, int64_t N,
+                                                           int64_t K, int64_t ldw,
+                                                           uint8_t* __restrict__ q, int64_t ldq,
+                                                           float* __restrict__ s, int64_t lds,
+                                                           int use_ue8m0) {
+  __shared__ float red[4];
+  const int64_t bn = blockIdx.y, bk = blockIdx.x;
+  const int t = threadIdx.x;
+  const int64_t col = bk * 128 + (t % 16) * 8;
+  const bool col_ok = col < K;  // K % 8 == 0: a chunk is all in or all out
+  float v[8][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t row = bn * 128 + t / 16 + 16 * i;
+    if (col_ok && row < N) {
+      load8<T>(w + row * ldw + col, v[i]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[i][j] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf_(amax, fabsf(v[i][j]));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) amax = fmaxf_(amax, __shfl_xor(amax, o, 64));
+  if ((t & 63) == 0) red[t >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf_(fmaxf_(red[0], red[1]), fmaxf_(red[2], red[3]));
+  float sf = fmaxf_(amax, 1e-4f) / 448.0f;
+  if (use_ue8m0) sf = ceil_to_ue8m0(sf);
+  const float inv = 1.0f / sf;
+  if (t == 0) s[bn * lds + bk] = sf;
+  if (!col_ok) return;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t row = bn * 128 + t / 16 + 16 * i;
+    if (row >= N) continue;
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      lo |= (uint32_t)f32_to_e4m3(v[i][j] * inv) << (8 * j);
+      hi |= (uint32_t)f32_to_e4m3(v[i][j + 4] * inv) << (8 * j);
+    }
+    *reinterpret_cast<uint2*>(q + row * ldq + col) = make_uint2(lo, hi);
+  }
+}
+
+__global__ void e8m0_to_f32_kernel(const uint8_t* __restrict__ src, float* __restrict__ dst,
+                                   int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const uint32_t b = src[i];
+    // 0xFF is the e8m0 NaN code; 0 is 2^-127 (an fp32 subnormal)
+    dst[i] = b == 0xFFu ? bits_f32(0x7FC00000u) : (b == 0 ? bits_f32(0x00400000u) : bits_f32(b << 23));
+  }
+}
+
+template <int GROUP>
+int launch_act_quant(const void* x, int64_t M, int64_t K, int64_t ldx, void* y, int64_t ldy,
+                     void* s, int64_t lds, int mode, int scale_e8m0, int inplace,
+                     hipStream_t stream) {
+  const int64_t total_threads = M * (K / GROUP) * (GROUP / 8);
+  const int64_t max_blocks = (int64_t)device_cu_count() * 16;
+  int64_t blocks = ceil_div(total_threads, 256);
+  if (blocks > max_blocks) blocks = max_blocks;
+  if (blocks < 1) blocks = 1;
+  if (inplace)
+    act_quant_kernel<GROUP, true><<<(unsigned)blocks, 256, 0, stream>>>(
+        (const uint16_t*)x, M, K, ldx, y, ldy, s, lds, mode, scale_e8m0);
+  else
+    act_quant_kernel<GROUP, false><<<(unsigned)blocks, 256, 0, stream>>>(
+        (const uint16_t*)x, M, K, ldx, y, ldy, s, lds, mode, scale_e8m0);
+  return check_launch("act_quant");
+}
+
+}  // namespace
+}  // namespace sgl
+
+extern "C" {
+
+int sgl_act_quant(const void* x, int64_t M, int64_t K, int64_t ldx, void* y, int64_t ldy, void* s,
+                  int64_t lds, int group, int scale_mode, int scale_e8m0, int inplace,
+                  sgl_stream_t stream) {
+  SGL_REQUIRE(M >= 0 && K >= 0, "act_quant: negative shape M=%lld K=%lld", (long long)M,
+              (long long)K);
+  SGL_REQUIRE(group == 32 || group == 64 || group == 128, "act_quant: group %d not in {32,64,128}",
+              group);
+  SGL_REQUIRE(K % group == 0, "act_quant: K=%lld not divisible by group %d", (long long)K, group);
+  SGL_REQUIRE(scale_mode >= 0 && scale_mode <= 4, "act_quant: bad scale_mode %d", scale_mode);
+  SGL_REQUIRE(!scale_e8m0 || scale_mode == SGL_SCALE_TORCH_UE8M0 ||
+                  scale_mode == SGL_SCALE_TILELANG_UE8M0 || scale_mode == SGL_SCALE_KV_UE8M0,
+              "act_quant: e8m0 scale storage needs a power-of-two scale mode (got %d)", scale_mode);
+  if (M == 0 || K == 0) return SGL_OK;
+  SGL_REQUIRE(x && y && s, "act_quant: null pointer");
+  SGL_REQUIRE(ldx >= K && ldy >= K && lds >= K / group, "act_quant: row stride smaller than row");
+  SGL_REQUIRE(sgl::aligned(x, 16) && ldx % 8 == 0, "act_quant: x must be 16-byte aligned rows");
+  SGL_REQUIRE(sgl::aligned(y, inplace ? 16 : 8) && ldy % 8 == 0,
+              "act_quant: y must be aligned (16 B bf16 / 8 B e4m3) with ldy %% 8 == 0");
+  SGL_REQUIRE(scale_e8m0 || sgl::aligned(s, 4), "act_quant: fp32 scales must be 4-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  switch (group) {
+    case 32:
+      return sgl::launch_act_quant<32>(x, M, K, ldx, y, ldy, s, lds, scale_mode, scale_e8m0,
+                                       inplace, st);
+    case 64:
+      return sgl::launch_act_quant<64>(x, M, K, ldx, y, ldy, s, lds, scale_mode, scale_e8m0,
+                                       inplace, st);
+    default:
+      return sgl::launch_act_quant<128>(x, M, K, ldx, y, ldy, s, lds, scale_mode, scale_e8m0,
+                                        inplace, st);
+  }
+}
+
+int sgl_weight_quant_128x128(const void* w, int dtype, int64_t N, int64_t K, int64_t ldw, void* q,
+                             int64_t ldq, float* s, int64_t lds, int use_ue8m0,
+                             sgl_stream_t stream) {
+  SGL_REQUIRE(N >= 0 && K >= 0, "weight_quant: negative shape");
+  SGL_REQUIRE(dtype == SGL_F32 || dtype == SGL_BF16, "weight_quant: dtype must be f32 or bf16");
+  SGL_REQUIRE(K % 8 == 0, "weight_quant: K=%lld must be a multiple of 8", (long long)K);
+  if (N == 0 || K == 0) return SGL_OK;
+  SGL_REQUIRE(w && q && s, "weight_quant: null pointer");
+  SGL_REQUIRE(ldw >= K && ldq >= K && lds >= sgl::ceil_div(K, 128), "weight_quant: bad strides");
+  SGL_REQUIRE(sgl::aligned(w, 16) && ldw % 8 == 0 && sgl::aligned(q, 8) && ldq % 8 == 0,
+              "weight_quant: rows must be aligned (w 16 B, q 8 B)");
+  dim3 grid((unsigned)sgl::ceil_div(K, 128), (unsigned)sgl::ceil_div(N, 128));
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == SGL_F32)
+    sgl::weight_quant_kernel<float><<<grid, 256, 0, st>>>((const float*)w, N, K, ldw, (uint8_t*)q,
+                                                          ldq, s, lds, use_ue8m0);
+  else
+    sgl::weight_quant_kernel<uint16_t><<<grid, 256, 0, st>>>(
+        (const uint16_t*)w, N, K, ldw, (uint8_t*)q, ldq, s, lds, use_ue8m0);
+  return sgl::check_launch("weight_quant_128x128");
+}
+
+int sgl_e8m0_to_f32(const void* src, float* dst, int64_t n, sgl_stream_t stream) {
+  SGL_REQUIRE(n >= 0, "e8m0_to_f32: negative n");
+  if (n == 0) return SGL_OK;
+  SGL_REQUIRE(src && dst, "e8m0_to_f32: null pointer");
+  int64_t blocks = sgl::ceil_div(n, 256);
+  if (blocks > 4096) blocks = 4096;
+  sgl::e8m0_to_f32_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>((const uint8_t*)src,
+                                                                             dst, n);
+  return sgl::check_launch("e8m0_to_f32");
+}
+
+}  // extern "C"

@@ -1,0 +1,58 @@
+// Common plumbing for the C-ABI entry points: status codes, the thread-local
+// last-error message and launch checking.  Entry points never throw across
+// the ABI; they return a status and leave a message for sgl_last_error().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/sglang_lite_amd.h"
+
+namespace sgl {
+
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+
+inline int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return SGL_ERR_HIP;
+  }
+  return SGL_OK;
+}
+
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace sgl
+
+#define SGL_REQUIRE(cond, ...)          \
+  do {                                  \
+    if (!(cond)) {                      \
+      ::sgl::set_error(__VA_ARGS__);    \
+      return SGL_ERR_INVALID_ARG;       \
+    }                                   \
+  } while (0)
+
+#define SGL_REQUIRE_SUPPORTED(cond, ...) \
+  do {                                   \
+    if (!(cond)) {                       \
+      ::sgl::set_error(__VA_ARGS__);     \
+      return SGL_ERR_UNSUPPORTED;        \
+    }                                    \
+  } while (0)
+
+#define SGL_CHECK_HIP(expr)                                                       \
+  do {                                                                            \
+    hipError_t _e = (expr);                                                       \
+    if (_e != hipSuccess) {                                                       \
+      ::sgl::set_error("%s failed: %s", #expr, hipGetErrorString(_e));            \
+      return SGL_ERR_HIP;                                                         \
+    }                                                                             \
+  } while (0)

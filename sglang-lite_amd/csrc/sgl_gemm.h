@@ -1,0 +1,44 @@
+// Internal interface between the GEMM kernels (gemm.hip) and the MoE / dense
+// entry points.  Not part of the C ABI.
+#pragma once
+
+#include "sgl_common.h"
+
+namespace sgl {
+
+enum GemmKind : int { KIND_DENSE = 0, KIND_GATE_UP = 1, KIND_DOWN = 2 };
+
+// One launch of the block-scaled FP8 GEMM family.
+//   dense   : C[M, N] = A[M, K] . B[N, K]^T                       (fp8_gemm)
+//   gate_up : rows of the routed slots (+ shared rows), A gathered from the
+//             token-major quantized activations, B = w_gate | w_up of the
+//             row's expert, SwiGLU epilogue, 1x128 requant into hq / hs.
+//   down    : rows as gate_up, A = hq rows, B = w_down, bf16 rows scattered
+//             to the token-major output of sgl_moe_down.
+struct GemmArgs {
+  const uint8_t* a;   // dense: A [M, K]; gate_up: xq [T, K]; down: hq [rows, K]
+  const void* sa;     // row scales [*, K/128]
+  int sa_e8m0;        // sa holds e8m0 bytes instead of fp32
+  const uint8_t* b;   // dense only: B [N, K]
+  const void* sb;     // dense only: [ceil(N/128), K/128]
+  int sb_e8m0;
+  const sgl_expert_ptrs* experts;  // moe: device array [E (+1)]
+  const int32_t* offsets;          // moe: [E + 1]
+  const int32_t* sorted_slot;      // moe: [T * k]
+  const float* route_w;            // gate_up: [T * k] slot-indexed (may be null)
+  int E, k, has_shared;
+  int64_t T;
+  int64_t M, N, K;  // dense: M x N x K; gate_up: N = I, K = H; down: N = H, K = I
+  void* c;          // dense: [M, N]; down: [T * (k + has_shared), N]
+  int out_f32;      // dense output fp32 instead of bf16
+  uint8_t* hq;      // gate_up: [rows, N] e4m3
+  float* hs;        // gate_up: [rows, N/128]
+  float swiglu_limit;
+  int scale_mode;
+  int m_tiles;      // grid rows (upper bound of M tiles)
+  int n_tiles;      // tiles along N
+};
+
+int launch_gemm(int kind, GemmArgs& args, int64_t rows_hint, hipStream_t stream);
+
+}  // namespace sgl

@@ -1,0 +1,206 @@
+"""The FP8 MoE expert path on gfx950: routing, permutation, grouped GEMMs, combine.
+
+Every function launches HIP kernels of ``libsglang_lite_amd.so`` on torch's
+current stream; torch only allocates the buffers.  Nothing here reads routing
+data back to the host, so a layer can be captured into a HIP graph.
+
+Semantics follow the reference's official MoE (``deepseek_infer/model.py:
+546-644``) and its fast dispatch (``engine/v4_moe_fast.py:43-106``):
+
+* Gate: ``scores = score_func(logits)``, top-k on ``scores + bias``, weights =
+  gathered scores (renormalised unless softmax) times ``route_scale``.
+* Experts run only on the slots routed to them; the routing weight multiplies
+  ``silu(gate) * up`` before ``w2`` (model.py:603-606).
+* ``y = sum over the token's experts in ascending id (fp32) + shared(x)``,
+  rounded to bf16.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import List, Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+from .kernel import FP8, E8M0, e8m0_to_f32
+
+SCORE_FUNCS = {"softmax": _lib.SCORE_SOFTMAX, "sigmoid": _lib.SCORE_SIGMOID,
+               "sqrtsoftplus": _lib.SCORE_SQRTSOFTPLUS}
+
+
+def _f32_scale(s: torch.Tensor) -> torch.Tensor:
+    """fp32 view of a weight scale (e8m0 converted on the device once)."""
+    if s.dtype == torch.float32:
+        return s.contiguous()
+    if s.dtype == E8M0:
+        return e8m0_to_f32(s)
+    raise TypeError(f"weight scale must be float32 or float8_e8m0fnu, got {s.dtype}")
+
+
+@dataclass
+class ExpertTable:
+    """Device array of ``sgl_expert_ptrs`` (E routed experts, then the shared one).
+
+    Holds references to every tensor whose address is in the table so the
+    pointers stay valid for the table's lifetime.
+    """
+
+    ptrs: torch.Tensor          # int64 [E (+1), 6] on the device
+    E: int
+    H: int
+    I: int
+    has_shared: bool
+    keep: List[torch.Tensor] = field(default_factory=list)
+
+    @staticmethod
+    def build(experts: Sequence[Tuple[torch.Tensor, ...]],
+              shared: Optional[Tuple[torch.Tensor, ...]] = None) -> "ExpertTable":
+        """``experts``: per expert ``(w1, w3, w2, s1, s3, s2)`` with w1/w3 e4m3
+        [I, H], w2 e4m3 [H, I] and their 128x128 scales (fp32 or e8m0)."""
+        rows = list(experts) + ([shared] if shared is not None else [])
+        if not rows:
+            raise ValueError("ExpertTable needs at least one expert")
+        w1 = rows[0][0]
+        I, H = int(w1.shape[0]), int(w1.shape[1])
+        dev = w1.device
+        keep: List[torch.Tensor] = []
+        vals = []
+        for r in rows:
+            w1, w3, w2, s1, s3, s2 = r
+            for w, shape in ((w1, (I, H)), (w3, (I, H)), (w2, (H, I))):
+                if w.dtype != FP8 or tuple(w.shape) != shape or not w.is_contiguous():
+                    raise ValueError(f"expert weight must be contiguous e4m3 {shape}, got "
+                                     f"{w.dtype} {tuple(w.shape)}")
+                _lib.require_device(w, what="ExpertTable")
+            fs = [_f32_scale(s) for s in (s1, s3, s2)]
+            keep += [w1, w3, w2, *fs]
+            vals.append([w1.data_ptr(), w3.data_ptr(), w2.data_ptr(),
+                         fs[0].data_ptr(), fs[1].data_ptr(), fs[2].data_ptr()])
+        ptrs = torch.tensor(vals, dtype=torch.int64).to(dev)
+        return ExpertTable(ptrs, len(experts), H, I, shared is not None, keep)
+
+
+def route_topk(logits: torch.Tensor, k: int, score_func: str = "softmax",
+               bias: Optional[torch.Tensor] = None, route_scale: float = 1.0
+               ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Top-k routing from fp32 router logits [T, E] (model.py:565-584 after the
+    projection).  Returns ``(weights f32 [T, k], ids int32 [T, k])``."""
+    _lib.require_device(logits, bias, what="route_topk")
+    if logits.dtype != torch.float32 or logits.dim() != 2:
+        raise TypeError("route_topk: logits must be float32 [T, E]")
+    lg = logits.contiguous()
+    T, E = lg.shape
+    ids = torch.empty(T, k, dtype=torch.int32, device=lg.device)
+    w = torch.empty(T, k, dtype=torch.float32, device=lg.device)
+    b = None
+    if bias is not None:
+        b = bias.to(torch.float32).contiguous()
+    _lib.call("sgl_moe_route_topk", lg.data_ptr(), T, E, k, SCORE_FUNCS[score_func],
+              _lib.ptr(b), float(route_scale), ids.data_ptr(), w.data_ptr(), _lib.stream_of(lg))
+    return w, ids
+
+
+def _ids32(ids: torch.Tensor) -> torch.Tensor:
+    if ids.dtype == torch.int32:
+        return ids.contiguous()
+    if ids.dtype == torch.int64:
+        return ids.to(torch.int32).contiguous()
+    raise TypeError(f"expert ids must be int32/int64, got {ids.dtype}")
+
+
+def permute(ids: torch.Tensor, E: int):
+    """Stable counting sort of the slots (t*k+j) by expert id.
+
+    Returns ``(counts [E], offsets [E+1], sorted_slot [T*k], slot_pos [T*k])``, int32."""
+    _lib.require_device(ids, what="moe_permute")
+    ids = _ids32(ids)
+    T, k = ids.shape
+    dev = ids.device
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    sorted_slot = torch.empty(T * k, dtype=torch.int32, device=dev)
+    slot_pos = torch.empty(T * k, dtype=torch.int32, device=dev)
+    _lib.call("sgl_moe_permute", ids.data_ptr(), T, k, E, counts.data_ptr(), offsets.data_ptr(),
+              sorted_slot.data_ptr(), slot_pos.data_ptr(), _lib.stream_of(ids))
+    return counts, offsets, sorted_slot, slot_pos
+
+
+def gate_up(xq, xs, offsets, sorted_slot, route_w, table: ExpertTable, k: int,
+            swiglu_limit: float = 0.0, scale_mode: int = _lib.SCALE_TORCH_FP32):
+    """Grouped gate/up GEMM + SwiGLU + requant.  Returns ``(hq e4m3 [rows, I], hs f32 [rows, I/128])``."""
+    T, H = xq.shape
+    rows = T * k + (T if table.has_shared else 0)
+    hq = torch.empty(rows, table.I, dtype=FP8, device=xq.device)
+    hs = torch.empty(rows, table.I // 128, dtype=torch.float32, device=xq.device)
+    _lib.call("sgl_moe_gate_up", xq.data_ptr(), xs.data_ptr(), T, H, table.I, table.E, k,
+              offsets.data_ptr(), sorted_slot.data_ptr(), _lib.ptr(route_w), table.ptrs.data_ptr(),
+              int(table.has_shared), float(swiglu_limit), int(scale_mode), hq.data_ptr(),
+              hs.data_ptr(), _lib.stream_of(xq))
+    return hq, hs
+
+
+def down(hq, hs, offsets, sorted_slot, table: ExpertTable, T: int, k: int):
+    """Grouped down GEMM.  Returns bf16 [T, k (+1), H] (token-major expert rows)."""
+    kk = k + (1 if table.has_shared else 0)
+    out = torch.empty(T, kk, table.H, dtype=torch.bfloat16, device=hq.device)
+    _lib.call("sgl_moe_down", hq.data_ptr(), hs.data_ptr(), T, table.H, table.I, table.E, k,
+              offsets.data_ptr(), sorted_slot.data_ptr(), table.ptrs.data_ptr(),
+              int(table.has_shared), out.data_ptr(), _lib.stream_of(hq))
+    return out
+
+
+def combine(out: torch.Tensor, ids: torch.Tensor, has_shared: bool) -> torch.Tensor:
+    """Ordered fp32 combine of [T, k (+1), H] expert rows -> bf16 [T, H]."""
+    ids = _ids32(ids)
+    T, k = ids.shape
+    H = out.shape[-1]
+    y = torch.empty(T, H, dtype=torch.bfloat16, device=out.device)
+    _lib.call("sgl_moe_combine", out.data_ptr(), ids.data_ptr(), T, k, H, int(has_shared),
+              y.data_ptr(), _lib.stream_of(out))
+    return y
+
+
+class MoEWorkspace:
+    """Reusable device workspace for :func:`moe_forward` (grown on demand)."""
+
+    def __init__(self):
+        self.buf: Optional[torch.Tensor] = None
+
+    def get(self, nbytes: int, device) -> torch.Tensor:
+        if self.buf is None or self.buf.numel() < nbytes or self.buf.device != torch.device(device):
+            self.buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        return self.buf
+
+
+def moe_forward(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, table: ExpertTable,
+                swiglu_limit: float = 0.0, scale_mode: int = _lib.SCALE_TORCH_FP32,
+                workspace: Optional[MoEWorkspace] = None, out: Optional[torch.Tensor] = None
+                ) -> torch.Tensor:
+    """Routed + shared MoE layer on bf16 x [T, H] given top-k ``ids``/``weights``."""
+    _lib.require_device(x, ids, weights, what="moe_forward")
+    if x.dtype != torch.bfloat16 or x.dim() != 2:
+        raise TypeError("moe_forward: x must be bfloat16 [T, H]")
+    x = x.contiguous()
+    ids = _ids32(ids)
+    w = weights.to(torch.float32).contiguous() if weights.dtype != torch.float32 else weights.contiguous()
+    T, H = x.shape
+    k = ids.shape[1]
+    if H != table.H:
+        raise ValueError(f"moe_forward: x has H={H}, experts have H={table.H}")
+    lib = _lib.load()
+    nbytes = int(lib.sgl_moe_workspace_size(T, H, table.I, table.E, k, int(table.has_shared)))
+    ws = (workspace or MoEWorkspace()).get(nbytes, x.device)
+    y = out if out is not None else torch.empty(T, H, dtype=torch.bfloat16, device=x.device)
+    _lib.call("sgl_moe_forward", x.data_ptr(), T, H, table.I, table.E, k, ids.data_ptr(),
+              w.data_ptr(), table.ptrs.data_ptr(), int(table.has_shared), float(swiglu_limit),
+              int(scale_mode), ws.data_ptr(), ws.numel(), y.data_ptr(), _lib.stream_of(x))
+    return y
+
+
+def workspace_size(T: int, H: int, I: int, E: int, k: int, has_shared: bool) -> int:
+    return int(_lib.load().sgl_moe_workspace_size(T, H, I, E, k, int(has_shared)))
+
+
+__all__ = ["ExpertTable", "MoEWorkspace", "combine", "down", "gate_up", "moe_forward", "permute",
+           "route_topk", "workspace_size"]

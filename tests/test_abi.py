@@ -1,0 +1,148 @@
+"""The C-ABI library: loads on CPU, exports every declared symbol, and its
+host-compiled numeric core agrees with the oracle (no GPU compute here)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import quant as Q
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sglang_lite_amd.h")
+
+
+def _lib():
+    from sglang_lite_amd import _lib
+
+    return _lib.load()
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sgl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    from sglang_lite_amd import _lib
+
+    assert declared_symbols() == sorted(_lib.SIGNATURES), (
+        "ctypes signature table and include/sglang_lite_amd.h disagree")
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.sgl_abi_version() == 1
+
+
+def test_probe_without_gpu_reports_why():
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    lib = _lib()
+    assert lib.sgl_probe() == 0
+    assert lib.sgl_last_error()
+
+
+def _host(fn, *arrays, n):
+    lib = _lib()
+    args = [a.ctypes.data_as(ctypes.c_void_p) if isinstance(a, np.ndarray) else a for a in arrays]
+    assert getattr(lib, fn)(*args, n) == 0
+
+
+def test_host_e4m3_conversion_matches_oracle():
+    bits = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    rng = np.random.default_rng(0)
+    rand = rng.integers(0, 2**32, 2_000_000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    for x in (bits, rand):
+        x = np.ascontiguousarray(x)
+        y = np.zeros(x.size, np.uint8)
+        _host("sgl_host_f32_to_e4m3", x, y, n=x.size)
+        np.testing.assert_array_equal(y, Q.f32_to_e4m3(x))
+    codes = np.arange(256, dtype=np.uint8)
+    out = np.zeros(256, np.float32)
+    _host("sgl_host_e4m3_to_f32", codes, out, n=256)
+    ref = Q.e4m3_to_f32(codes)
+    ok = ~np.isnan(ref)
+    np.testing.assert_array_equal(out[ok], ref[ok])
+    assert np.all(np.isnan(out[~ok]))
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2, 3, 4])
+def test_host_group_scale_and_quant_match_oracle(mode):
+    rng = np.random.default_rng(10 + mode)
+    group = 64 if mode == 4 else 128
+    x = Q.bf16_round(rng.standard_normal((256, group * 2)).astype(np.float32) *
+                     np.exp(rng.uniform(-12, 6, (256, 1))).astype(np.float32))
+    x[0] = 0.0
+    q_ref, s_ref = Q.scale_mode_quant(x, mode, group)
+    amax = np.ascontiguousarray(np.abs(x.reshape(256, 2, group)).max(-1).ravel())
+    s = np.zeros_like(amax)
+    lib = _lib()
+    assert lib.sgl_host_group_scale(mode, amax.ctypes.data_as(ctypes.c_void_p),
+                                    s.ctypes.data_as(ctypes.c_void_p), amax.size) == 0
+    np.testing.assert_array_equal(s, s_ref.ravel())
+    xs = np.ascontiguousarray(x.ravel())
+    ss = np.ascontiguousarray(np.repeat(s, group))
+    q = np.zeros(xs.size, np.uint8)
+    assert lib.sgl_host_quant_elem(mode, xs.ctypes.data_as(ctypes.c_void_p),
+                                   ss.ctypes.data_as(ctypes.c_void_p),
+                                   q.ctypes.data_as(ctypes.c_void_p), xs.size) == 0
+    np.testing.assert_array_equal(q, q_ref.ravel())
+
+
+def test_kv_scale_host_matches_torch_log2_near_powers_of_two():
+    """fp32 amax values whose raw scale sits just above 2^k: the library follows
+    torch.log2 (correctly rounded), not the exponent+1 bit formula."""
+    ks = np.arange(-28, 10)
+    js = np.arange(0, 24)
+    target = (np.ldexp(1.0, ks)[:, None] * (1 + js[None, :] * 2.0**-23)).ravel()
+    amax = np.ascontiguousarray((target / float(Q.INV448)).astype(np.float32))
+    s = np.zeros_like(amax)
+    lib = _lib()
+    assert lib.sgl_host_group_scale(4, amax.ctypes.data_as(ctypes.c_void_p),
+                                    s.ctypes.data_as(ctypes.c_void_p), amax.size) == 0
+    raw = torch.from_numpy(amax).clamp(min=1e-12) * (1.0 / 448.0)
+    ref = torch.exp2(torch.ceil(torch.log2(raw.clamp(min=2**-30)))).numpy()
+    np.testing.assert_array_equal(s, ref)
+
+
+def test_invalid_arguments_map_to_value_error_without_launch():
+    from sglang_lite_amd import _lib as L
+
+    lib = _lib()
+    rc = lib.sgl_act_quant(None, 4, 100, 100, None, 100, None, 1, 128, 0, 0, 0, None)
+    assert rc == L.SGL_ERR_INVALID_ARG
+    assert "divisible" in L.last_error()
+    with pytest.raises(ValueError, match="group"):
+        L.call("sgl_act_quant", None, 4, 128, 128, None, 128, None, 1, 96, 0, 0, 0, None)
+    rc = lib.sgl_fp8_gemm(None, None, 0, None, None, 0, None, 0, 4, 100, 256, None)
+    assert rc == L.SGL_ERR_INVALID_ARG and "multiple of 16" in L.last_error()
+    rc = lib.sgl_moe_permute(None, 4, 2, 5000, None, None, None, None, None)
+    assert rc == L.SGL_ERR_INVALID_ARG
+    assert lib.sgl_moe_workspace_size(8192, 4096, 2048, 256, 8, 1) > 8192 * 4096
+
+
+def test_product_refuses_cpu_tensors():
+    from sglang_lite_amd import dsv4_kv_pack as KVP
+    from sglang_lite_amd import kernel as K
+
+    x = torch.zeros(4, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        K.act_quant(x)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        KVP.pack_dsv4_kv_bf16(torch.zeros(2, 512, dtype=torch.bfloat16))
+    # argument errors keep the reference's exception types (dsv4_kv_pack.py:50-53)
+    with pytest.raises(ValueError):
+        KVP.pack_dsv4_kv_bf16(torch.zeros(2, 500, dtype=torch.bfloat16))
+    with pytest.raises(TypeError):
+        KVP.pack_dsv4_kv_bf16(torch.zeros(2, 512, dtype=torch.int32))
+    with pytest.raises(AssertionError):
+        K.act_quant(torch.zeros(2, 100, dtype=torch.bfloat16))

@@ -1,0 +1,161 @@
+"""FP8 KV pack / paging / gather-dequant / index split on the GPU: bit-exact
+against the oracle, plus the reference's own KV tests run on the device
+(tests/test_dsv4_kv_pack.py:16-65, tests/test_v4_dual_pool.py:57-75)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_values, u8
+from oracle import kv as OK
+from oracle import quant as Q
+
+pytestmark = pytest.mark.gpu
+
+
+def _kv(rng, T, dim, dtype):
+    x = bf16_values(rng, (T, dim))
+    t = torch.from_numpy(x).to(dtype)
+    return t.float().numpy(), t
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("mode", [4, 3])
+@pytest.mark.parametrize("T", [1, 70, 4096])
+def test_pack_layout_a_bit_exact(gpu, dtype, mode, T):
+    from sglang_lite_amd import dsv4_kv_pack as KVP
+
+    rng = np.random.default_rng(T + mode)
+    xv, xt = _kv(rng, T, 512, dtype)
+    if T > 2:
+        xt[1, :64] = 0.0
+        xv[1, :64] = 0.0
+    rope = xt[:, 448:].contiguous().view(torch.uint8).numpy()
+    ref = OK.pack_layout_a(xv, rope, mode)
+    d = xt.to(gpu)
+    out = KVP.pack_dsv4_kv_bf16(d, act_quant_fn=None if mode == 4 else (lambda *a: None))
+    np.testing.assert_array_equal(out.cpu().numpy(), ref)
+    pages = KVP.pack_dsv4_kv_paged(d, 64, act_quant_fn=None if mode == 4 else (lambda *a: None))
+    np.testing.assert_array_equal(pages.cpu().numpy(), OK.to_paged_hnd(ref, 64))
+    pages2 = KVP.to_paged_hnd(out, 64)
+    np.testing.assert_array_equal(pages2.cpu().numpy(), OK.to_paged_hnd(ref, 64))
+
+
+def test_reference_pack_shape_and_rope_bytes(gpu):
+    """tests/test_dsv4_kv_pack.py:16-25 on the device."""
+    from sglang_lite_amd.dsv4_kv_pack import DSV4_PACKED_BYTES, pack_dsv4_kv_bf16
+
+    kv = torch.randn(3, 512, dtype=torch.bfloat16)
+    kv[:, 448:] = torch.arange(64, dtype=torch.bfloat16)
+    packed = pack_dsv4_kv_bf16(kv.to(gpu)).cpu()
+    assert packed.shape == (3, DSV4_PACKED_BYTES)
+    assert packed.dtype == torch.uint8
+    rope_u8 = kv[:, 448:].contiguous().view(torch.uint8).view(3, 128)
+    assert torch.equal(packed[:, 448:576], rope_u8)
+    assert (packed[:, 583] == 0).all()
+
+
+def test_reference_paging(gpu):
+    """tests/test_dsv4_kv_pack.py:28-54 on the device."""
+    from sglang_lite_amd.dsv4_kv_pack import (DSV4_DATA_BYTES, DSV4_PACKED_BYTES, DSV4_PAGE_SIZE,
+                                              DSV4_SCALE_STRIDE, to_paged_hnd)
+
+    pages = to_paged_hnd(torch.zeros(10, DSV4_PACKED_BYTES, dtype=torch.uint8, device=gpu),
+                         page_size=DSV4_PAGE_SIZE)
+    assert pages.shape == (1, 1, DSV4_PAGE_SIZE, DSV4_PACKED_BYTES)
+    packed = torch.arange(70 * DSV4_PACKED_BYTES, dtype=torch.int64).to(torch.uint8)
+    packed = packed.view(70, DSV4_PACKED_BYTES).clone()
+    packed[0, :DSV4_DATA_BYTES] = 11
+    packed[0, DSV4_DATA_BYTES:] = 22
+    packed[1, :DSV4_DATA_BYTES] = 33
+    packed[1, DSV4_DATA_BYTES:] = 44
+    pages = to_paged_hnd(packed.to(gpu), page_size=DSV4_PAGE_SIZE).cpu()
+    flat = pages.view(2, -1)[0]
+    assert (flat[0:DSV4_DATA_BYTES] == 11).all()
+    assert (flat[DSV4_DATA_BYTES: 2 * DSV4_DATA_BYTES] == 33).all()
+    scale0 = DSV4_PAGE_SIZE * DSV4_DATA_BYTES
+    assert (flat[scale0: scale0 + DSV4_SCALE_STRIDE] == 22).all()
+    assert (flat[scale0 + DSV4_SCALE_STRIDE: scale0 + 2 * DSV4_SCALE_STRIDE] == 44).all()
+    # page round trip is byte-identical (tests/test_v4_dual_pool.py:57-75)
+    np.testing.assert_array_equal(OK.unpage(pages.numpy(), 64)[:70], packed.numpy())
+    assert not OK.unpage(pages.numpy(), 64)[70:].any()
+
+
+def test_reference_split_indices(gpu):
+    """tests/test_dsv4_kv_pack.py:56-65 on the device, plus random int64 input."""
+    from sglang_lite_amd.dsv4_kv_pack import split_swa_compress_indices
+
+    topk = torch.tensor([[[0, 1, 2, -1, 4, 5]]], dtype=torch.int32, device=gpu)
+    swa, swa_l, comp, comp_l = split_swa_compress_indices(topk, window_size=4)
+    assert swa.shape == (1, 4)
+    assert int(swa_l[0]) == 3
+    assert torch.equal(comp[0].cpu(), torch.tensor([0, 1], dtype=torch.int32))
+    assert int(comp_l[0]) == 2
+    rng = np.random.default_rng(0)
+    for (b, s, k, win) in [(2, 3, 200, 128), (4, 1, 100, 128), (1, 5, 640, 128), (3, 2, 0, 4)]:
+        t = rng.integers(-1, 70000, (b, s, k)).astype(np.int64)
+        ref = OK.split_swa_compress_indices(t, win)
+        got = split_swa_compress_indices(torch.from_numpy(t).to(gpu), win)
+        for r, g in zip(ref, got):
+            np.testing.assert_array_equal(g.cpu().numpy(), r)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_pack_layout_b_bit_exact(gpu, dtype):
+    from sglang_lite_amd import dsv4_kv_pack as KVP
+
+    rng = np.random.default_rng(21)
+    T = 333
+    xv, xt = _kv(rng, T, 576, dtype)
+    if dtype == torch.float32:
+        rope = xt[:, 512:].to(torch.bfloat16).contiguous().view(torch.uint8).numpy()
+    else:
+        rope = xt[:, 512:].contiguous().view(torch.uint8).numpy()
+    ref = OK.pack_layout_b(xv[:, :512], rope)
+    out = KVP.pack_kv_latent_rope(xt.to(gpu))
+    np.testing.assert_array_equal(out.cpu().numpy(), ref)
+
+
+def test_gather_dequant_bit_exact(gpu):
+    from sglang_lite_amd import dsv4_kv_pack as KVP
+
+    rng = np.random.default_rng(22)
+    T = 1000
+    xv, xt = _kv(rng, T, 512, torch.bfloat16)
+    rope = xt[:, 448:].contiguous().view(torch.uint8).numpy()
+    rows_a = OK.pack_layout_a(xv, rope, 4)
+    idx = rng.integers(0, T, (8, 300)).astype(np.int32)
+    idx[:, -5:] = -1
+    idx[0, :3] = [0, T - 1, -1]
+    ref = OK.gather_dequant(rows_a, idx, "A")
+    d_rows = torch.from_numpy(rows_a).to(gpu)
+    d_idx = torch.from_numpy(idx).to(gpu)
+    got = KVP.gather_dequant(d_rows, d_idx, layout="A").float().cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+    pages = KVP.to_paged_hnd(d_rows, 64)
+    got_p = KVP.gather_dequant(pages, d_idx, layout="A", page_size=64).float().cpu().numpy()
+    np.testing.assert_array_equal(got_p.view(np.uint32), ref.view(np.uint32))
+    # layout B
+    xb, xbt = _kv(rng, T, 576, torch.bfloat16)
+    rows_b = OK.pack_layout_b(xb[:, :512], xbt[:, 512:].contiguous().view(torch.uint8).numpy())
+    ref_b = OK.gather_dequant(rows_b, idx, "B")
+    got_b = KVP.gather_dequant(torch.from_numpy(rows_b).to(gpu), d_idx, layout="B")
+    np.testing.assert_array_equal(got_b.float().cpu().numpy().view(np.uint32), ref_b.view(np.uint32))
+
+
+def test_layout_a_dequant_equals_qat_inplace(gpu):
+    """Layout A gather = the official QAT quant-dequant (kernel.py:84-91) of the
+    NoPE part with the injected act_quant formula."""
+    from sglang_lite_amd import dsv4_kv_pack as KVP
+
+    rng = np.random.default_rng(23)
+    xv, xt = _kv(rng, 200, 512, torch.bfloat16)
+    d = xt.to(gpu)
+    rows = KVP.pack_dsv4_kv_bf16(d, act_quant_fn=lambda *a: None)
+    idx = torch.arange(200, dtype=torch.int32, device=gpu)[None]
+    deq = KVP.gather_dequant(rows, idx, layout="A")[0].float().cpu().numpy()
+    qat, _ = Q.act_quant_inplace_tilelang(xv[:, :448], 64, round_scale=True)
+    np.testing.assert_array_equal(deq[:, :448], qat)
+    np.testing.assert_array_equal(deq[:, 448:], xv[:, 448:])

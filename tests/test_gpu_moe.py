@@ -1,0 +1,207 @@
+"""MoE path on the GPU vs the oracle: routing and permutation bit-exact, expert
+outputs within the GEMM tolerance, combine bit-exact given the expert rows."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (assert_gemm_close, bf16_values, f32, to_dev_bf16, to_dev_f32, to_dev_fp8,
+                     u8)
+from oracle import moe as OM
+from oracle import quant as Q
+
+pytestmark = pytest.mark.gpu
+
+
+def zipf_logits(rng, T, E, s=1.1):
+    """Router logits whose top-k load follows Zipf(s) over a random expert ranking."""
+    p = np.arange(1, E + 1, dtype=np.float64) ** -s
+    p /= p.sum()
+    perm = rng.permutation(E)
+    logp = np.log(p)[np.argsort(perm)]
+    g = rng.gumbel(size=(T, E))
+    return (logp[None, :] + g).astype(np.float32)
+
+
+def logits_without_near_ties(rng, T, E, k, score_func="softmax", bias=None, min_gap=1e-6,
+                             scale=2.0):
+    """N(0, scale) router logits, redrawing every row whose k-th and (k+1)-th
+    selection values are closer than ``min_gap`` (torch.topk's tie order is
+    unspecified, so test data carries no ties)."""
+    lg = (rng.standard_normal((T, E)) * scale).astype(np.float32)
+    for _ in range(100):
+        bad = [t for t in range(T) if OM.topk_margin(lg[t:t + 1], k, score_func, bias) < min_gap]
+        if not bad:
+            return lg
+        lg[bad] = (rng.standard_normal((len(bad), E)) * scale).astype(np.float32)
+    raise AssertionError("could not draw tie-free logits")
+
+
+def table_from(experts, shared, dev):
+    from sglang_lite_amd import moe as M
+
+    def ent(e):
+        return (to_dev_fp8(e["w1"], dev), to_dev_fp8(e["w3"], dev), to_dev_fp8(e["w2"], dev),
+                to_dev_f32(e["s1"], dev), to_dev_f32(e["s3"], dev), to_dev_f32(e["s2"], dev))
+
+    return M.ExpertTable.build([ent(e) for e in experts], ent(shared) if shared else None)
+
+
+@pytest.mark.parametrize("score_func,use_bias", [("softmax", False), ("sigmoid", True),
+                                                 ("sqrtsoftplus", True), ("sqrtsoftplus", False)])
+@pytest.mark.parametrize("T,E,k", [(1, 8, 2), (512, 256, 8), (300, 64, 6)])
+def test_route_topk(gpu, score_func, use_bias, T, E, k):
+    from sglang_lite_amd import moe as M
+
+    rng = np.random.default_rng(T + E + k)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32) if use_bias else None
+    logits = logits_without_near_ties(rng, T, E, k, score_func, bias)
+    assert OM.topk_margin(logits, k, score_func, bias) >= 1e-6
+    w_ref, ids_ref = OM.route_topk(logits, k, score_func, bias, route_scale=1.5)
+    w, ids = M.route_topk(to_dev_f32(logits, gpu), k, score_func,
+                          to_dev_f32(bias, gpu) if use_bias else None, route_scale=1.5)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_allclose(w.cpu().numpy(), w_ref, rtol=2e-6, atol=1e-7)
+
+
+def test_route_topk_matches_torch_topk(gpu):
+    """Library routine pin: torch.topk on torch.softmax scores (CPU)."""
+    from sglang_lite_amd import moe as M
+
+    rng = np.random.default_rng(3)
+    logits = zipf_logits(rng, 256, 256)
+    assert OM.topk_margin(logits, 8) >= 1e-7, "test data has a near-tie"
+    t = torch.from_numpy(logits)
+    scores = t.softmax(dim=-1)
+    ref_idx = scores.topk(8, dim=-1)[1]
+    ref_w = scores.gather(1, ref_idx)
+    w, ids = M.route_topk(t.to(gpu), 8)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ref_idx.numpy())
+    np.testing.assert_allclose(w.cpu().numpy(), ref_w.numpy(), rtol=2e-6)
+
+
+@pytest.mark.parametrize("T,k,E,kind", [(1, 1, 1, "uniform"), (64, 8, 256, "zipf"),
+                                        (512, 8, 256, "zipf"), (8192, 8, 256, "uniform"),
+                                        (1000, 6, 1024, "uniform"), (333, 2, 8, "one")])
+def test_permute_bit_exact(gpu, T, k, E, kind):
+    from sglang_lite_amd import moe as M
+
+    rng = np.random.default_rng(T * k)
+    if kind == "zipf":
+        ids = np.argsort(-zipf_logits(rng, T, E), axis=1)[:, :k]
+    elif kind == "one":
+        ids = np.zeros((T, k), np.int64)
+        ids[:, 1:] = rng.integers(1, E, (T, k - 1))
+    else:
+        ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]) if k <= E else None
+    ref = OM.permute(ids, E)
+    if T * k <= 4096:
+        np.testing.assert_array_equal(ref["sorted_slot"], OM.permute_bruteforce(ids, E))
+    counts, offsets, sorted_slot, slot_pos = M.permute(torch.from_numpy(ids).to(gpu), E)
+    np.testing.assert_array_equal(counts.cpu().numpy(), ref["counts"])
+    np.testing.assert_array_equal(offsets.cpu().numpy(), ref["offsets"])
+    np.testing.assert_array_equal(sorted_slot.cpu().numpy(), ref["sorted_slot"])
+    np.testing.assert_array_equal(slot_pos.cpu().numpy(), ref["slot_pos"])
+
+
+def _moe_case(rng, T, H, I, E, k, shared=True, zipf=False):
+    x = bf16_values(rng, (T, H))
+    logits = zipf_logits(rng, T, E) if zipf else logits_without_near_ties(rng, T, E, k)
+    w, ids = OM.route_topk(logits, k)
+    experts = [OM.make_expert(rng, H, I) for _ in range(E)]
+    sh = OM.make_expert(rng, H, I) if shared else None
+    return x, logits, w, ids, experts, sh
+
+
+def test_moe_stages_tiny(gpu):
+    """Config 1 shapes, stage by stage."""
+    from sglang_lite_amd import kernel as K
+    from sglang_lite_amd import moe as M
+
+    rng = np.random.default_rng(1)
+    T, H, I, E, k = 32, 256, 128, 8, 2
+    x, logits, w, ids, experts, sh = _moe_case(rng, T, H, I, E, k)
+    table = table_from(experts, sh, gpu)
+    xd = to_dev_bf16(x, gpu)
+    idd = torch.from_numpy(ids).to(gpu)
+    wd = to_dev_f32(w, gpu)
+    xq, xs = K.act_quant(xd)
+    counts, offsets, sorted_slot, _ = M.permute(idd, E)
+    hq, hs = M.gate_up(xq, xs, offsets, sorted_slot, wd.reshape(-1), table, k)
+    out = M.down(hq, hs, offsets, sorted_slot, table, T, k)
+    y = M.combine(out, idd, True)
+    torch.cuda.synchronize()
+    perm = OM.permute(ids, E)
+    hq_n, hs_n, out_n = u8(hq), hs.cpu().numpy(), f32(out)
+    # per expert: the dequantized h rows and the expert outputs
+    for e in range(E):
+        rows = perm["sorted_slot"][perm["offsets"][e]:perm["offsets"][e + 1]]
+        if rows.size == 0:
+            continue
+        tok, top = rows // k, rows % k
+        tr = {}
+        ref_out = OM.expert_forward(x[tok], experts[e], w[tok, top][:, None], trace=tr)
+        p0, p1 = perm["offsets"][e], perm["offsets"][e + 1]
+        h_dev = Q.dequant_rows(hq_n[p0:p1], hs_n[p0:p1])
+        assert_gemm_close(h_dev, Q.dequant_rows(tr["hq"], tr["hs"]), f"h expert {e}")
+        assert_gemm_close(out_n[tok, top], ref_out, f"out expert {e}")
+    tr = {}
+    ref_sh = OM.expert_forward(x, sh, None, trace=tr)
+    assert_gemm_close(out_n[:, k], ref_sh, "shared")
+    # combine is exact given the device's expert rows
+    order = np.argsort(ids, axis=1, kind="stable")
+    acc = np.zeros((T, H), np.float32)
+    for jj in range(k):
+        acc = (acc + np.take_along_axis(out_n[:, :k], order[:, jj][:, None, None], 1)[:, 0]).astype(np.float32)
+    acc = (acc + out_n[:, k]).astype(np.float32)
+    np.testing.assert_array_equal(f32(y).view(np.uint32), Q.bf16_round(acc).view(np.uint32))
+    # the whole layer against the oracle
+    y_ref = OM.moe_forward(x, ids, w, experts, sh)
+    assert_gemm_close(f32(y), y_ref, "moe tiny")
+
+
+@pytest.mark.parametrize("T,H,I,E,k,shared,lim,zipf", [
+    (32, 256, 128, 8, 2, True, 0.0, False),
+    (100, 512, 256, 16, 4, True, 10.0, False),
+    (64, 1024, 512, 32, 8, True, 0.0, True),
+    (7, 512, 384, 5, 3, False, 0.5, False),
+])
+def test_moe_forward_matches_oracle(gpu, T, H, I, E, k, shared, lim, zipf):
+    from sglang_lite_amd import moe as M
+
+    rng = np.random.default_rng(T * H + E)
+    x, logits, w, ids, experts, sh = _moe_case(rng, T, H, I, E, k, shared, zipf)
+    table = table_from(experts, sh, gpu)
+    y = M.moe_forward(to_dev_bf16(x, gpu), torch.from_numpy(ids).to(gpu), to_dev_f32(w, gpu),
+                      table, swiglu_limit=lim)
+    y_ref = OM.moe_forward(x, ids, w, experts, sh, swiglu_limit=lim)
+    assert_gemm_close(f32(y), y_ref, f"moe T={T} H={H} I={I} E={E} k={k}")
+
+
+def test_moe_forward_big_rows_tile_path(gpu):
+    """Enough rows per expert (>= 64) to take the 128-row tile configuration."""
+    from sglang_lite_amd import moe as M
+
+    rng = np.random.default_rng(5)
+    T, H, I, E, k = 512, 512, 256, 8, 2
+    x, logits, w, ids, experts, sh = _moe_case(rng, T, H, I, E, k)
+    table = table_from(experts, sh, gpu)
+    y = M.moe_forward(to_dev_bf16(x, gpu), torch.from_numpy(ids).to(gpu), to_dev_f32(w, gpu), table)
+    y_ref = OM.moe_forward(x, ids, w, experts, sh)
+    assert_gemm_close(f32(y), y_ref, "moe big tiles")
+
+
+def test_moe_forward_deterministic_and_repeatable(gpu):
+    from sglang_lite_amd import moe as M
+
+    rng = np.random.default_rng(9)
+    T, H, I, E, k = 200, 512, 256, 16, 4
+    x, logits, w, ids, experts, sh = _moe_case(rng, T, H, I, E, k)
+    table = table_from(experts, sh, gpu)
+    args = (to_dev_bf16(x, gpu), torch.from_numpy(ids).to(gpu), to_dev_f32(w, gpu), table)
+    ws = M.MoEWorkspace()
+    y1 = u8(M.moe_forward(*args, workspace=ws))
+    y2 = u8(M.moe_forward(*args, workspace=ws))
+    np.testing.assert_array_equal(y1, y2)
