@@ -1,0 +1,417 @@
+#!/usr/bin/env python3
+"""Benchmark: the FP8 MoE layer (DeepSeek-V4-Flash expert shapes) on one MI355X.
+
+Headline workload (one "step"): MoE prefill of T=8192 bf16 tokens, hidden 4096,
+expert intermediate 2048, 256 routed experts top-8 (softmax over uniform N(0,1)
+router logits) + 1 shared expert, FP8 e4m3 weights with fp32 128x128 scales:
+route -> 1x128 act quant -> permute -> grouped gate/up (+SiLU*mul*w, requant)
+-> grouped down -> ordered combine.  Inputs and weights are resident in HBM
+before the timed region.  Also measured (reported under "extra"): the decode
+configs (T = 64/256/512, Zipf(1.1) expert load), the dense FP8 GEMM
+(M = 16..4096, N = 4096, K = 7168), and the FP8 KV pack (65536 rows, 656-byte
+layout) + sparse-MLA gather-dequant (128 queries x 2048 rows).
+
+Prints ONE JSON line.  ``--gpus N`` with N > 1 exits: this build runs on one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "sglang-lite_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "FP8 MoE layer tokens/s + % FP8 MFMA peak (prefill) / % HBM BW (decode), 1 GPU"
+PEAK_FP8_TFLOPS = 5000.0   # MI355X dense FP8 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+H, I, E, K_TOP = 4096, 2048, 256, 8
+SCALE_BYTES_PER_EXPERT = 4 * (2 * (I // 128) * (H // 128) + (H // 128) * (I // 128))  # 6144
+W_BYTES_PER_EXPERT = 3 * H * I
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-extra", action="store_true", help="headline prefill line only")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-kernels", action="store_true",
+                    help="run only the prefill stages (plus a 256 MiB copy for counter "
+                         "calibration) for rocprofv3 --pmc runs; prints no JSON")
+    return ap.parse_args()
+
+
+# ------------------------------------------------------------------ weights
+
+
+def make_weights(torch, M, dev, seed=4):
+    """256 routed + 1 shared FP8 experts: N(0, 0.02) fp32 drawn on the GPU from a
+    seeded generator, quantized 128x128 by the library's weight-quant kernel."""
+    from sglang_lite_amd import kernel as K
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    n = E + 1
+    w13 = torch.empty(n, 2, I, H, dtype=torch.float8_e4m3fn, device=dev)
+    s13 = torch.empty(n, 2, I // 128, H // 128, dtype=torch.float32, device=dev)
+    w2 = torch.empty(n, H, I, dtype=torch.float8_e4m3fn, device=dev)
+    s2 = torch.empty(n, H // 128, I // 128, dtype=torch.float32, device=dev)
+    for e in range(n):
+        for j in range(2):
+            q, s = K.per_block_cast_to_fp8(torch.randn(I, H, generator=g, device=dev) * 0.02, False)
+            w13[e, j].copy_(q)
+            s13[e, j].copy_(s)
+        q, s = K.per_block_cast_to_fp8(torch.randn(H, I, generator=g, device=dev) * 0.02, False)
+        w2[e].copy_(q)
+        s2[e].copy_(s)
+    experts = [(w13[e, 0], w13[e, 1], w2[e], s13[e, 0], s13[e, 1], s2[e]) for e in range(E)]
+    shared = (w13[E, 0], w13[E, 1], w2[E], s13[E, 0], s13[E, 1], s2[E])
+    table = M.ExpertTable.build(experts, shared)
+    return table, (w13, s13, w2, s2)
+
+
+def zipf_logits(torch, T, seed, s=1.1):
+    g = torch.Generator().manual_seed(seed)
+    p = torch.arange(1, E + 1, dtype=torch.float64) ** -s
+    p /= p.sum()
+    perm = torch.randperm(E, generator=g)
+    logp = torch.log(p)[torch.argsort(perm)]
+    u = torch.rand(T, E, generator=g, dtype=torch.float64).clamp_min(1e-300)
+    gumbel = -torch.log(-torch.log(u))
+    return (logp[None, :] + gumbel).float()
+
+
+# ------------------------------------------------------------------- timing
+
+
+def time_steps(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def event_avg_ms(torch, fn, iters, flush=None):
+    """Average duration of fn on torch's current stream (the stream the
+    library launches on), timed with HIP events, optional cache flush between."""
+    tot = 0.0
+    for _ in range(iters):
+        if flush is not None:
+            flush()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        b.synchronize()
+        tot += a.elapsed_time(b)
+    return tot / iters
+
+
+class Prefill:
+    """The staged prefill pipeline with events around each stage."""
+
+    def __init__(self, torch, M, K, table, T, dev, seed):
+        self.torch, self.M, self.K, self.table, self.T = torch, M, K, table, T
+        g = torch.Generator().manual_seed(seed)
+        self.x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+        self.logits = torch.randn(T, E, generator=g).to(dev)
+        self.ws = M.MoEWorkspace()
+        self.y = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+
+    def step(self):
+        w, ids = self.M.route_topk(self.logits, K_TOP)
+        self.M.moe_forward(self.x, ids, w, self.table, workspace=self.ws, out=self.y)
+        return ids
+
+    def staged(self, iters):
+        torch, M, K = self.torch, self.M, self.K
+        names = ["route", "act_quant", "permute", "gate_up", "down", "combine"]
+        tot = {n: 0.0 for n in names}
+        for _ in range(iters):
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+            ev[0].record()
+            w, ids = M.route_topk(self.logits, K_TOP)
+            ev[1].record()
+            xq, xs = K.act_quant(self.x)
+            ev[2].record()
+            _, offsets, sorted_slot, _ = M.permute(ids, E)
+            ev[3].record()
+            hq, hs = M.gate_up(xq, xs, offsets, sorted_slot, w.reshape(-1), self.table, K_TOP)
+            ev[4].record()
+            out = M.down(hq, hs, offsets, sorted_slot, self.table, self.T, K_TOP)
+            ev[5].record()
+            M.combine(out, ids, True)
+            ev[6].record()
+            ev[6].synchronize()
+            for i, n in enumerate(names):
+                tot[n] += ev[i].elapsed_time(ev[i + 1])
+        return {n: v / iters for n, v in tot.items()}
+
+
+def moe_flops(rows):
+    return rows * 6.0 * H * I  # gate+up (4HI) + down (2HI) per routed/shared row
+
+
+def read_traffic(kernel_tag):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary, if present."""
+    path = os.path.join(ROOT, "profiles", f"{kernel_tag}_pmc.txt")
+    if not os.path.isfile(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1].split()[0])
+    return None
+
+
+# ------------------------------------------------------------- cpu baseline
+
+
+def cpu_baseline(torch, table, weights, pre, budget_s=20.0):
+    """The oracle (numpy restatement of the reference MoE path) timed on the
+    host on a bounded sample of the same prefill workload and extrapolated to
+    the whole layer by row count."""
+    import numpy as np
+
+    from oracle import moe as OM
+
+    w13, s13, w2, s2 = weights
+    torch.cuda.synchronize()
+    w, ids = pre.M.route_topk(pre.logits, K_TOP)
+    ids_np = ids.cpu().numpy()
+    w_np = w.cpu().numpy()
+    x_np = pre.x.float().cpu().numpy()
+
+    def expert_np(e):
+        return {"w1": w13[e, 0].view(torch.uint8).cpu().numpy(),
+                "w3": w13[e, 1].view(torch.uint8).cpu().numpy(),
+                "w2": w2[e].view(torch.uint8).cpu().numpy(),
+                "s1": s13[e, 0].cpu().numpy(), "s3": s13[e, 1].cpu().numpy(),
+                "s2": s2[e].cpu().numpy()}
+
+    rows_done, t_spent, experts_done = 0, 0.0, 0
+    for e in range(E):
+        tok, top = np.nonzero(ids_np == e)
+        if tok.size == 0:
+            continue
+        ex = expert_np(e)
+        t0 = time.perf_counter()
+        OM.expert_forward(x_np[tok], ex, w_np[tok, top][:, None])
+        t_spent += time.perf_counter() - t0
+        rows_done += tok.size
+        experts_done += 1
+        if t_spent > budget_s:
+            break
+    # time per routed row -> whole layer (routed rows T*k plus T shared rows)
+    total_rows = pre.T * K_TOP + pre.T
+    t_layer = t_spent / rows_done * total_rows
+    return {
+        "value": round(pre.T / t_layer, 3),
+        "unit": "tokens/s",
+        "cores": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)),
+        "kind": "port",
+        "sample": (f"oracle expert_forward (numpy, dequantize-to-fp32, float64 BLAS) on the rows of "
+                   f"{experts_done} routed experts ({rows_done} rows) of the T=8192 prefill, "
+                   f"{t_spent:.1f} s, extrapolated by row count to {total_rows} rows"),
+        "host_cpu": platform.processor() or platform.machine(),
+        "os_cpu_count": os.cpu_count(),
+    }
+
+
+# --------------------------------------------------------------------- main
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+
+    import sglang_lite_amd
+    from sglang_lite_amd import dsv4_kv_pack as KVP
+    from sglang_lite_amd import kernel as K
+    from sglang_lite_amd import moe as M
+
+    info = sglang_lite_amd.probe()
+    if not info["ok"]:
+        raise SystemExit(f"sglang_lite_amd probe failed: {info}")
+    dev = torch.device("cuda:0")
+    log("generating FP8 expert weights on the device")
+    table, weights = make_weights(torch, M, dev)
+    T = 8192
+    pre = Prefill(torch, M, K, table, T, dev, seed=4)
+
+    if args.profile_kernels:
+        for _ in range(3):
+            pre.step()
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("profile-kernels run done")
+        return
+
+    log(f"prefill T={T}: warmup {args.warmup}, timed {args.steps}")
+    ms = time_steps(torch, pre.step, args.steps, args.warmup)
+    stages = pre.staged(max(3, min(args.steps, 10)))
+    rows = T * K_TOP + T
+    flops = moe_flops(rows)
+    gu_flops = rows * 4.0 * H * I
+    gu_ms = stages["gate_up"]
+    n_experts_touched = E
+    layer_bytes = (n_experts_touched + 1) * (W_BYTES_PER_EXPERT + SCALE_BYTES_PER_EXPERT) + \
+        4 * T * H + 4 * T * E
+    tok_s = T / (ms / 1e3)
+    traffic = read_traffic("moe_gate_up_prefill")
+    result = {
+        "metric": METRIC,
+        "value": round(tok_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3",
+        "data": "synthetic (seeded N(0,1) bf16 activations and router logits; N(0,0.02) weights "
+                "drawn on the GPU and quantized 128x128)",
+        "config": {"workload": "moe_prefill_T8192_H4096_I2048_E256_top8_shared1",
+                   "tokens": T, "hidden": H, "expert_inter": I, "experts": E, "topk": K_TOP,
+                   "shared_experts": 1, "router": "softmax over N(0,1) logits",
+                   "parallelism": "none (1 GPU)"},
+        "layer": {"tflops": round(flops / (ms / 1e3) / 1e12, 2),
+                  "mfma_frac": round(flops / (ms / 1e3) / 1e12 / PEAK_FP8_TFLOPS, 4),
+                  "hbm_gbs_algorithmic": round(layer_bytes / (ms / 1e3) / 1e9, 1),
+                  "hbm_frac": round(layer_bytes / (ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+                  "stages_ms": {k_: round(v, 4) for k_, v in stages.items()}},
+        "roofline": {"kernel": "gemm_fp8_kernel<gate_up> (grouped gate/up + SwiGLU + requant)",
+                     "bound": "mfma", "achieved": round(gu_flops / (gu_ms / 1e3) / 1e12, 2),
+                     "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(gu_flops / (gu_ms / 1e3) / 1e12 / PEAK_FP8_TFLOPS, 4),
+                     "traffic": traffic,
+                     "flops_per_launch": gu_flops, "avg_launch_ms": round(gu_ms, 4)},
+    }
+    log(f"prefill {ms:.3f} ms/step -> {tok_s:.0f} tok/s; stages {stages}")
+
+    if not args.no_extra:
+        extra = {}
+        # ---- decode configs
+        dec = []
+        for Td, seed in ((64, 31), (256, 32), (512, 33)):
+            logits = zipf_logits(torch, Td, seed).to(dev)
+            xd = torch.randn(Td, H, generator=torch.Generator().manual_seed(seed)).to(
+                torch.bfloat16).to(dev)
+            ws = M.MoEWorkspace()
+            yd = torch.empty(Td, H, dtype=torch.bfloat16, device=dev)
+
+            def dstep():
+                w, ids = M.route_topk(logits, K_TOP)
+                M.moe_forward(xd, ids, w, table, workspace=ws, out=yd)
+
+            msd = time_steps(torch, dstep, max(args.steps, 10), args.warmup)
+            _, ids = M.route_topk(logits, K_TOP)
+            touched = int(torch.unique(ids).numel())
+            by = (touched + 1) * (W_BYTES_PER_EXPERT + SCALE_BYTES_PER_EXPERT) + 4 * Td * H + \
+                4 * Td * E
+            dec.append({"tokens": Td, "ms": round(msd, 4), "tokens_per_s": round(Td / msd * 1e3, 1),
+                        "experts_touched": touched, "bytes": by,
+                        "gbs": round(by / msd / 1e6, 1),
+                        "hbm_frac": round(by / msd / 1e6 / PEAK_HBM_GBS, 4)})
+            log(f"decode T={Td}: {msd:.3f} ms, touched {touched}, {by / msd / 1e6:.0f} GB/s")
+        extra["decode"] = dec
+        # ---- dense GEMM
+        flush_buf = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+
+        def flush():
+            flush_buf.zero_()
+
+        gw = torch.Generator(device=dev).manual_seed(2)
+        bq, bs = K.per_block_cast_to_fp8(torch.randn(4096, 7168, generator=gw, device=dev) * 0.02,
+                                         False)
+        dense = []
+        prev = torch.get_default_dtype()
+        torch.set_default_dtype(torch.bfloat16)
+        try:
+            for Md in (16, 128, 1024, 4096):
+                a = torch.randn(Md, 7168, generator=gw, device=dev).to(torch.bfloat16)
+                aq, as_ = K.act_quant(a)
+                c = torch.empty(Md, 4096, dtype=torch.bfloat16, device=dev)
+                for _ in range(2):
+                    K.fp8_gemm(aq, as_, bq, bs, out=c)
+                msg = event_avg_ms(torch, lambda: K.fp8_gemm(aq, as_, bq, bs, out=c), 10, flush)
+                fl = 2.0 * Md * 4096 * 7168
+                byt = Md * 7168 + 4 * Md * 56 + 4096 * 7168 + 4 * 32 * 56 + 2 * Md * 4096
+                dense.append({"M": Md, "N": 4096, "K": 7168, "ms": round(msg, 5),
+                              "tflops": round(fl / msg / 1e9, 2),
+                              "mfma_frac": round(fl / msg / 1e9 / PEAK_FP8_TFLOPS, 4),
+                              "gbs": round(byt / msg / 1e6, 1),
+                              "hbm_frac": round(byt / msg / 1e6 / PEAK_HBM_GBS, 4)})
+                log(f"dense M={Md}: {msg * 1e3:.1f} us")
+                aqm = K.act_quant(a)
+                del aqm
+            # act_quant alone at the largest dense shape
+            a = torch.randn(4096, 7168, generator=gw, device=dev).to(torch.bfloat16)
+            msq = event_avg_ms(torch, lambda: K.act_quant(a), 10, flush)
+            qb = 3 * 4096 * 7168 + 4 * 4096 * 56
+            extra["act_quant_4096x7168"] = {"ms": round(msq, 5), "gbs": round(qb / msq / 1e6, 1),
+                                            "hbm_frac": round(qb / msq / 1e6 / PEAK_HBM_GBS, 4)}
+        finally:
+            torch.set_default_dtype(prev)
+        extra["dense_gemm"] = dense
+        # ---- KV pack (layout B, 65536 rows) + gather-dequant (128 x 2048)
+        gk = torch.Generator().manual_seed(5)
+        kv = torch.randn(65536, 576, generator=gk).to(torch.bfloat16).to(dev)
+        packed = KVP.pack_kv_latent_rope(kv)
+        msp = event_avg_ms(torch, lambda: KVP.pack_kv_latent_rope(kv), 10, flush)
+        pb = 65536 * (1152 + 656)
+        idx = torch.stack([torch.randperm(65536, generator=gk)[:2048] for _ in range(128)]).to(
+            torch.int32).to(dev)
+        out = torch.empty(128, 2048, 576, dtype=torch.bfloat16, device=dev)
+        msg_ = event_avg_ms(torch, lambda: KVP.gather_dequant(packed, idx, layout="B", out=out),
+                            10, flush)
+        gb = 128 * 2048 * (656 + 1152)
+        kva = torch.randn(65536, 512, generator=gk).to(torch.bfloat16).to(dev)
+        msa = event_avg_ms(torch, lambda: KVP.pack_dsv4_kv_paged(kva, 64), 10, flush)
+        ab = 65536 * (1024 + 584)
+        extra["kv"] = {
+            "pack_layout_b_65536": {"ms": round(msp, 5), "gbs": round(pb / msp / 1e6, 1),
+                                    "hbm_frac": round(pb / msp / 1e6 / PEAK_HBM_GBS, 4)},
+            "gather_dequant_128x2048": {"ms": round(msg_, 5), "gbs": round(gb / msg_ / 1e6, 1),
+                                        "hbm_frac": round(gb / msg_ / 1e6 / PEAK_HBM_GBS, 4)},
+            "pack_layout_a_paged_65536": {"ms": round(msa, 5), "gbs": round(ab / msa / 1e6, 1),
+                                          "hbm_frac": round(ab / msa / 1e6 / PEAK_HBM_GBS, 4)},
+        }
+        log(f"kv pack {msp * 1e3:.1f} us, gather {msg_ * 1e3:.1f} us, pack A paged {msa * 1e3:.1f} us")
+        result["extra"] = extra
+
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle) on a bounded sample")
+        result["cpu_baseline"] = cpu_baseline(torch, table, weights, pre)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

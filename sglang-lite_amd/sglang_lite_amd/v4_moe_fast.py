@@ -1,0 +1,182 @@
+"""MoE / Expert forward replacements for the official DeepSeek-V4 graph on gfx950.
+
+Drop-in counterpart of ``engine/v4_moe_fast.py`` (``moe_fast_enabled`` :26-28,
+``_expert_forward_fused`` :43-76, ``_moe_forward_activated_only`` :79-106,
+``attach_v4_moe_fast`` :109-152).  Where the reference walks the activated
+experts on the host (``torch.unique(...).tolist()`` and one ``torch.where``
+per expert, both device->host syncs), the replacement runs the whole layer as
+five HIP launches with no host sync: 1x128 act quant, stable permutation,
+grouped gate/up (+SwiGLU, routing weight, requant), grouped down, ordered
+combine with the shared expert.  Results follow the reference's arithmetic:
+weight applied before ``w2``, fp32 sum over experts in ascending id, shared
+expert added last, bf16 out.
+
+Routing: the router projection stays ``F.linear(x.float(), W.float())`` as
+in ``Gate.forward`` (model.py:565; a plain fp32 library GEMM), then the HIP
+top-k kernel applies score function, bias, top-k, renormalisation and
+route_scale.  Hash-routed layers (model.py:576-577) keep the official gate.
+
+Env: ``SGLANG_LITE_V4_MOE_FAST=0`` keeps the official forwards (same switch as
+the reference).
+"""
+
+from __future__ import annotations
+
+import logging
+import os
+import sys
+from typing import Any, Optional
+
+import torch
+import torch.nn.functional as F
+
+from . import kernel as HK
+from . import moe as HM
+
+logger = logging.getLogger("sglang_lite_amd.v4_moe_fast")
+MARK = "_sglang_lite_moe_fast"
+
+
+def moe_fast_enabled() -> bool:
+    raw = os.environ.get("SGLANG_LITE_V4_MOE_FAST", "1").strip().lower()
+    return raw not in ("0", "false", "no", "off")
+
+
+def _official_model():
+    M = sys.modules.get("model")
+    if M is None:
+        raise RuntimeError("official DeepSeek-V4 'model' module is not loaded")
+    return M
+
+
+def _is_fp8(linear) -> bool:
+    w = getattr(linear, "weight", None)
+    return w is not None and w.dtype == torch.float8_e4m3fn and getattr(w, "scale", None) is not None
+
+
+def _expert_entry(expert):
+    return (expert.w1.weight.data, expert.w3.weight.data, expert.w2.weight.data,
+            expert.w1.weight.scale.data, expert.w3.weight.scale.data, expert.w2.weight.scale.data)
+
+
+def _scale_mode():
+    M = sys.modules.get("model")
+    return HK.scale_mode_for(getattr(M, "scale_fmt", None) if M is not None else None)
+
+
+def expert_table(moe) -> HM.ExpertTable:
+    """Device pointer table of a MoE module's experts + shared expert (cached)."""
+    tab = getattr(moe, "_sgl_table", None)
+    if tab is None:
+        experts = [_expert_entry(e) for e in moe.experts]
+        tab = HM.ExpertTable.build(experts, _expert_entry(moe.shared_experts))
+        moe._sgl_table = tab
+    return tab
+
+
+def _expert_forward_fused(self, x: torch.Tensor, weights: Optional[torch.Tensor] = None):
+    """Expert SwiGLU (model.py:596-606 / v4_moe_fast.py:43-76) for FP8 experts
+    as a one-expert grouped launch; other weight formats use the official forward."""
+    if not (_is_fp8(self.w1) and _is_fp8(self.w2) and _is_fp8(self.w3)):
+        return self._sgl_orig_forward(x, weights)  # bf16 experts: not this path
+    shape = x.shape
+    x2 = x.reshape(-1, shape[-1])
+    T = x2.shape[0]
+    tab = getattr(self, "_sgl_table", None)
+    if tab is None:
+        tab = HM.ExpertTable.build([_expert_entry(self)])
+        self._sgl_table = tab
+    ids = torch.zeros(T, 1, dtype=torch.int32, device=x.device)
+    if weights is None:
+        w = torch.ones(T, 1, dtype=torch.float32, device=x.device)
+    else:
+        w = weights.reshape(T, 1).to(torch.float32)
+    lim = float(getattr(self, "swiglu_limit", 0) or 0)
+    xb = x2 if x2.dtype == torch.bfloat16 else x2.to(torch.bfloat16)
+    y = HM.moe_forward(xb, ids, w, tab, swiglu_limit=lim, scale_mode=_scale_mode())
+    return y.to(x.dtype).view(*shape[:-1], y.shape[-1])
+
+
+def _gate_topk(gate, x: torch.Tensor, input_ids: torch.Tensor):
+    if getattr(gate, "hash", False):
+        return gate(x, input_ids.flatten())
+    logits = F.linear(x.float(), gate.weight.float())
+    weights, ids = HM.route_topk(logits, int(gate.topk), str(gate.score_func),
+                                 getattr(gate, "bias", None), float(gate.route_scale))
+    return weights, ids
+
+
+def _moe_forward_fused(self, x: torch.Tensor, input_ids: torch.Tensor):
+    """The whole MoE layer (v4_moe_fast.py:79-106) on the device, no host sync."""
+    M = sys.modules.get("model")
+    if (M is not None and getattr(M, "world_size", 1) > 1) or \
+            any(e is None for e in self.experts) or \
+            not all(_is_fp8(e.w1) for e in (self.experts[0], self.shared_experts)):
+        # expert-sharded ranks / non-FP8 experts are not this path
+        return self._sgl_orig_forward(x, input_ids)
+    shape = x.size()
+    x2 = x.view(-1, self.dim)
+    weights, ids = _gate_topk(self.gate, x2, input_ids)
+    lim = float(getattr(self.shared_experts, "swiglu_limit", 0) or 0)
+    xb = x2 if x2.dtype == torch.bfloat16 else x2.to(torch.bfloat16)
+    ws = getattr(self, "_sgl_ws", None)
+    if ws is None:
+        ws = HM.MoEWorkspace()
+        self._sgl_ws = ws
+    y = HM.moe_forward(xb, ids, weights, expert_table(self), swiglu_limit=lim,
+                       scale_mode=_scale_mode(), workspace=ws)
+    return y.type_as(x).view(shape)
+
+
+def attach_v4_moe_fast(model: Any) -> dict:
+    """Patch the official ``MoE.forward`` / ``Expert.forward`` (class level)
+    after a device probe.  Returns the reference's stats keys plus
+    ``backend`` and ``probe``; never raises."""
+    stats = {"enabled": False, "moe_class_patched": 0, "expert_class_patched": 0,
+             "moe_modules": 0, "expert_modules": 0, "backend": "official", "probe": None}
+    if not moe_fast_enabled():
+        return stats
+    import sglang_lite_amd
+
+    probe = sglang_lite_amd.probe()
+    stats["probe"] = probe
+    if not probe.get("ok"):
+        print(f"[sglang-lite-amd] MoE fast skipped (probe failed: {probe.get('error')})")
+        return stats
+    try:
+        M = _official_model()
+    except RuntimeError as e:
+        stats["error"] = str(e)
+        return stats
+    MoE, Expert = M.MoE, M.Expert
+    if getattr(MoE.forward, MARK, False) is not True:
+        MoE._sgl_orig_forward = MoE.forward
+        MoE.forward = _moe_forward_fused
+        setattr(MoE.forward, MARK, True)
+        stats["moe_class_patched"] = 1
+    if getattr(Expert.forward, MARK, False) is not True:
+        Expert._sgl_orig_forward = Expert.forward
+        Expert.forward = _expert_forward_fused
+        setattr(Expert.forward, MARK, True)
+        stats["expert_class_patched"] = 1
+    stats["moe_modules"] = sum(1 for m in model.modules() if isinstance(m, MoE))
+    stats["expert_modules"] = sum(1 for m in model.modules() if isinstance(m, Expert))
+    stats["enabled"] = True
+    stats["backend"] = "gfx950_hip"
+    print(f"[sglang-lite-amd] MoE fast armed (grouped FP8 MFMA, on-device dispatch); "
+          f"moe_modules={stats['moe_modules']} expert_modules={stats['expert_modules']}")
+    return stats
+
+
+def detach_v4_moe_fast() -> None:
+    M = sys.modules.get("model")
+    if M is None:
+        return
+    for cls in (M.MoE, M.Expert):
+        orig = cls.__dict__.get("_sgl_orig_forward")
+        if orig is not None:
+            cls.forward = orig
+            del cls._sgl_orig_forward
+
+
+__all__ = ["attach_v4_moe_fast", "detach_v4_moe_fast", "expert_table", "moe_fast_enabled"]

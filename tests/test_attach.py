@@ -1,0 +1,70 @@
+"""Attach / probe contract of the drop-in modules on CPU (no GPU compute):
+env switches, probe failure leaves the official functions untouched, error
+mapping; mirrors tests/test_v4_moe_fast.py:46-52 of the reference."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import fake_official
+
+
+@pytest.fixture
+def official():
+    M, K, saved = fake_official.install()
+    yield M, K
+    fake_official.uninstall(saved)
+
+
+def test_moe_fast_env_default_on(monkeypatch):
+    from sglang_lite_amd.v4_moe_fast import moe_fast_enabled
+
+    monkeypatch.delenv("SGLANG_LITE_V4_MOE_FAST", raising=False)
+    assert moe_fast_enabled() is True
+    monkeypatch.setenv("SGLANG_LITE_V4_MOE_FAST", "0")
+    assert moe_fast_enabled() is False
+
+
+def test_deep_gemm_env_switch(monkeypatch, official):
+    from sglang_lite_amd import v4_deep_gemm as D
+
+    monkeypatch.setenv("SGLANG_LITE_V4_DEEP_GEMM", "off")
+    st = D.attach_v4_deep_gemm(None)
+    assert st["backend"] == "disabled" and not st["patched"]
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="probe succeeds on a GPU")
+def test_failed_probe_leaves_official_functions(official):
+    from sglang_lite_amd import v4_deep_gemm as D
+    from sglang_lite_amd import v4_moe_fast as F
+
+    M, K = official
+    orig = (K.fp8_gemm, K.act_quant, M.MoE.forward, M.Expert.forward)
+    st = D.attach_v4_deep_gemm(None)
+    assert st["enabled"] is False and st["probe"]["ok"] is False
+    st2 = F.attach_v4_moe_fast(torch.nn.Module())
+    assert st2["enabled"] is False
+    assert (K.fp8_gemm, K.act_quant, M.MoE.forward, M.Expert.forward) == orig
+    assert D.is_armed() is False
+
+
+def test_fp4_path_is_reported_not_built():
+    from sglang_lite_amd import v4_deep_gemm as D
+
+    with pytest.raises(NotImplementedError):
+        D.fp4_gemm_nt(None, None, None, None)
+
+
+def test_scale_formula_switch(monkeypatch):
+    from sglang_lite_amd import _lib, kernel as K
+
+    monkeypatch.delenv("SGLANG_LITE_AMD_ACT_QUANT", raising=False)
+    assert K.scale_mode_for(None) == _lib.SCALE_TORCH_FP32
+    assert K.scale_mode_for("ue8m0") == _lib.SCALE_TORCH_UE8M0
+    monkeypatch.setenv("SGLANG_LITE_AMD_ACT_QUANT", "tilelang")
+    assert K.scale_mode_for(None) == _lib.SCALE_TILELANG_FP32
+    assert K.scale_mode_for("ue8m0") == _lib.SCALE_TILELANG_UE8M0
+    monkeypatch.setenv("SGLANG_LITE_AMD_ACT_QUANT", "bogus")
+    with pytest.raises(ValueError):
+        K.scale_mode_for(None)
