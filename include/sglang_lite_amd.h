@@ -129,15 +129,14 @@ int sgl_e8m0_to_f32(const void* src, float* dst, int64_t n, sgl_stream_t stream)
 
 /* C[M, N] = sum_kb (A[:, kb] . B[:, kb]^T) * sa[m, kb] * sb[n/128, kb], fp32
  * accumulation promoted once per 128-deep K block, output bf16 (out_dtype
- * SGL_BF16) or fp32 (SGL_F32).  A e4m3 [M, K] contiguous, sa [M, K/128],
- * B e4m3 [N, K] contiguous, sb [ceil(N/128), K/128]; each scale tensor is
- * fp32, or one e8m0 byte per scale when its *_scale_e8m0 flag is set.
- * K % 128 == 0, N % 16 == 0.
+ * SGL_BF16) or fp32 (SGL_F32).  A e4m3 [M, K] contiguous, sa fp32 [M, K/128]
+ * (e8m0 activation scales: convert with sgl_e8m0_to_f32 first), B e4m3 [N, K]
+ * contiguous, sb [ceil(N/128), K/128] fp32, or one e8m0 byte per scale when
+ * b_scale_e8m0 is set.  K % 128 == 0, N % 16 == 0, M*K and N*K < 2^31.
  * Replaces deepseek_infer/kernel.py:257-273 fp8_gemm (kernel :203-254) and the
  * call-site adapter engine/v4_deep_gemm.py:169-218 fp4_gemm_nt. */
-int sgl_fp8_gemm(const void* a, const void* sa, int a_scale_e8m0, const void* b, const void* sb,
-                 int b_scale_e8m0, void* c, int out_dtype, int64_t M, int64_t N, int64_t K,
-                 sgl_stream_t stream);
+int sgl_fp8_gemm(const void* a, const void* sa, const void* b, const void* sb, int b_scale_e8m0,
+                 void* c, int out_dtype, int64_t M, int64_t N, int64_t K, sgl_stream_t stream);
 
 /* ------------------------------------------------------------ MoE layer */
 

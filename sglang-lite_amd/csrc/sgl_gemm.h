@@ -17,8 +17,7 @@ enum GemmKind : int { KIND_DENSE = 0, KIND_GATE_UP = 1, KIND_DOWN = 2 };
 //             to the token-major output of sgl_moe_down.
 struct GemmArgs {
   const uint8_t* a;   // dense: A [M, K]; gate_up: xq [T, K]; down: hq [rows, K]
-  const void* sa;     // row scales [*, K/128]
-  int sa_e8m0;        // sa holds e8m0 bytes instead of fp32
+  const void* sa;     // fp32 row scales [*, K/128]
   const uint8_t* b;   // dense only: B [N, K]
   const void* sb;     // dense only: [ceil(N/128), K/128]
   int sb_e8m0;

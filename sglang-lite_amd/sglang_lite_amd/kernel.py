@@ -154,10 +154,12 @@ def fp8_gemm(
         out = a.new_empty(*a.size()[:-1], N, dtype=odt)
     else:
         assert out.is_contiguous() and out.dtype == odt and out.numel() == M * N
+    if _scale_flag(a_s, "fp8_gemm a_s"):
+        a_s = e8m0_to_f32(a_s)  # the kernel streams fp32 activation scales
     _lib.call(
         "sgl_fp8_gemm",
-        a.data_ptr(), a_s.data_ptr(), _scale_flag(a_s, "fp8_gemm a_s"),
-        b.data_ptr(), b_s.data_ptr(), _scale_flag(b_s, "fp8_gemm b_s"),
+        a.data_ptr(), a_s.data_ptr(), b.data_ptr(), b_s.data_ptr(),
+        _scale_flag(b_s, "fp8_gemm b_s"),
         out.data_ptr(), _lib.SGL_BF16 if odt == torch.bfloat16 else _lib.SGL_F32,
         M, N, K, _lib.stream_of(a),
     )
