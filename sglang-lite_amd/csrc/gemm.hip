@@ -11,9 +11,10 @@
 // Data movement: operand tiles go global -> LDS with global_load_lds_dwordx4
 // (each lane moves 16 bytes straight into LDS, no register staging) through
 // an NSTAGE-deep ring of LDS stages.  One 1 KB DMA instruction fills 8 rows x
-// 128 bytes of a stage; a row's 16-byte chunks are stored at chunk ^ (row & 7)
-// so the 8 lanes that read one chunk column of an MFMA operand hit distinct
-// banks, the swizzle being applied to the global address of each lane.  The
+// 128 bytes of a stage; a row's 16-byte chunks are stored at
+// chunk ^ ((row >> 1) & 7), so the 16 lanes that read one chunk column of an
+// MFMA operand (16 consecutive rows) cover all 16 sixteen-byte bank groups of
+// a 256-byte LDS line; the swizzle is applied to each lane's global address.  The
 // waits are explicit s_waitcnt vmcnt(n) counts plus a bare s_barrier, so
 // NSTAGE-1 stages of loads stay in flight while the MFMAs run.
 //
@@ -80,9 +81,11 @@ __device__ __forceinline__ float load_scale(const void* s, int64_t idx, int e8m0
 
 __device__ __forceinline__ float bf16r(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+
 __device__ __forceinline__ v8i read_frag(const uint8_t* tile, int row, int g4) {
-  const uint4 lo = *reinterpret_cast<const uint4*>(tile + row * 128 + (((2 * g4) ^ (row & 7)) << 4));
-  const uint4 hi = *reinterpret_cast<const uint4*>(tile + row * 128 + (((2 * g4 + 1) ^ (row & 7)) << 4));
+  const uint4 lo = *reinterpret_cast<const uint4*>(tile + row * 128 + (((2 * g4) ^ swz(row)) << 4));
+  const uint4 hi = *reinterpret_cast<const uint4*>(tile + row * 128 + (((2 * g4 + 1) ^ swz(row)) << 4));
   return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 }
 
@@ -296,13 +299,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
       if (c < BM / 8) {
         const int r = c * 8 + rr;
         const int s = sSrc[r] >= 0 ? sSrc[r] : src0;
-        voff[j] = (uint32_t)((int64_t)s * K + ((pc ^ (r & 7)) << 4));
+        voff[j] = (uint32_t)((int64_t)s * K + ((pc ^ swz(r)) << 4));
       } else {
         const int r = (c - BM / 8) * 8 + rr;
         const bool up_half = KIND == KIND_GATE_UP && r >= HALF;
         int64_t n = n0 + (up_half ? r - HALF : r);
         if (n >= N) n = n0;
-        voff[j] = (uint32_t)(n * K + ((pc ^ (r & 7)) << 4));
+        voff[j] = (uint32_t)(n * K + ((pc ^ swz(r)) << 4));
       }
     }
     const int sa_row = wave * C::SA_ROWS + (lane < C::SA_ROWS ? lane : 0);
@@ -372,18 +375,37 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
             sav[mi][r] = tS[(row / C::SA_ROWS) * 64 + (row % C::SA_ROWS)];
           }
         }
+        // software pipeline: B fragment nj+1 is read while the MFMAs of column
+        // block nj run, and block nj-1 is promoted after block nj's MFMAs
+        // are issued, so neither the LDS latency nor the MFMA latency sits
+        // in front of a dependent instruction
+        v8i bf[2];
+        v4f pr[2][TM];
+        bf[0] = read_frag(tB, tile_col(0) + r16, g4);
 #pragma unroll
         for (int nj = 0; nj < TN; ++nj) {
-          const v8i bf = read_frag(tB, tile_col(nj) + r16, g4);
-          const float sbv = (KIND == KIND_GATE_UP && nj >= TN / 2) ? sbv1 : sbv0;
+          if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB, tile_col(nj + 1) + r16, g4);
 #pragma unroll
-          for (int mi = 0; mi < TM; ++mi) {
-            const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[mi], bf, vzero, 0, 0,
-                                                                            0, 0, 0, 0);
+          for (int mi = 0; mi < TM; ++mi)
+            pr[nj & 1][mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                af[mi], bf[nj & 1], vzero, 0, 0, 0, 0, 0, 0);
+          if (nj > 0) {
+            const float sbv = (KIND == KIND_GATE_UP && nj - 1 >= TN / 2) ? sbv1 : sbv0;
+#pragma unroll
+            for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                acc[mi][nj - 1][r] =
+                    fmaf(pr[(nj - 1) & 1][mi][r], sav[mi][r] * sbv, acc[mi][nj - 1][r]);
+          }
+        }
+        {
+          const float sbv = (KIND == KIND_GATE_UP && TN - 1 >= TN / 2) ? sbv1 : sbv0;
+#pragma unroll
+          for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-              acc[mi][nj][r] = fmaf(p[r], sav[mi][r] * sbv, acc[mi][nj][r]);
-          }
+              acc[mi][TN - 1][r] = fmaf(pr[(TN - 1) & 1][mi][r], sav[mi][r] * sbv, acc[mi][TN - 1][r]);
         }
       }
     }
