@@ -11,10 +11,14 @@
 // Data movement: operand tiles go global -> LDS with global_load_lds_dwordx4
 // (each lane moves 16 bytes straight into LDS, no register staging) through
 // an NSTAGE-deep ring of LDS stages.  One 1 KB DMA instruction fills 8 rows x
-// 128 bytes of a stage; a row's 16-byte chunks are stored at
-// chunk ^ ((row >> 1) & 7), so the 16 lanes that read one chunk column of an
-// MFMA operand (16 consecutive rows) cover all 16 sixteen-byte bank groups of
-// a 256-byte LDS line; the swizzle is applied to each lane's global address.  The
+// 128 bytes of a stage; a row's 16-byte chunk c is stored at c ^ swz(row) with
+// swz(row) = (row & 6) | ((row >> 3) & 1).  A ds_read_b128 of an MFMA operand
+// has 16 lanes read one chunk column of 16 consecutive rows; with this swizzle
+// those reads are conflict-free on gfx950's 64-bank LDS (measured: 4 LDS
+// cycles per wavefront read, like a contiguous 1 KB read; the plain
+// (row >> 1) & 7 rotation measures 8, two-way conflicted).  The swizzle is
+// applied to each lane's global address, so the DMA keeps reading whole
+// 128-byte row segments.  The
 // waits are explicit s_waitcnt vmcnt(n) counts plus a bare s_barrier, so
 // NSTAGE-1 stages of loads stay in flight while the MFMAs run.
 //
@@ -81,7 +85,7 @@ __device__ __forceinline__ float load_scale(const void* s, int64_t idx, int e8m0
 
 __device__ __forceinline__ float bf16r(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
-__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ int swz(int row) { return (row & 6) | ((row >> 3) & 1); }
 
 __device__ __forceinline__ v8i read_frag(const uint8_t* tile, int row, int g4) {
   const uint4 lo = *reinterpret_cast<const uint4*>(tile + row * 128 + (((2 * g4) ^ swz(row)) << 4));
