@@ -125,6 +125,19 @@ int sgl_weight_quant_128x128(const void* w, int dtype, int64_t N, int64_t K, int
  * engine/v4_deep_gemm.py:136-141 scale_to_f32. */
 int sgl_e8m0_to_f32(const void* src, float* dst, int64_t n, sgl_stream_t stream);
 
+/* Device self-test; no counterpart in the reference.  The kernels convert
+ * fp32 to e4m3fn and bf16 with gfx950's v_cvt_pk_fp8_f32 / v_cvt_pk_bf16_f32
+ * plus a NaN fix-up, and e4m3 to fp32 with v_cvt_pk_f32_fp8; this compares
+ * those conversions with the bit-level
+ * software rules (round to nearest even, |x| > 464 -> NaN code, NaN keeps its
+ * sign; bf16 NaN -> 0x7FC0) for all 2^32 fp32 inputs and adds the mismatch
+ * counts to counts[5] (device memory, zeroed by the caller):
+ *   [0] e4m3 with fix-up, all inputs   [1] bf16 with fix-up, all inputs
+ *   [2] raw e4m3, non-NaN inputs       [3] raw bf16, non-NaN inputs
+ *   [4] e4m3 -> fp32 (v_cvt_pk_f32_fp8) over the 256 codes
+ * All five must stay 0. */
+int sgl_check_conversions(unsigned long long* counts, sgl_stream_t stream);
+
 /* --------------------------------------------------------------- GEMMs */
 
 /* C[M, N] = sum_kb (A[:, kb] . B[:, kb]^T) * sa[m, kb] * sb[n/128, kb], fp32

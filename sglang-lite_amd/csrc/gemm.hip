@@ -83,8 +83,6 @@ __device__ __forceinline__ float load_scale(const void* s, int64_t idx, int e8m0
   return reinterpret_cast<const float*>(s)[idx];
 }
 
-__device__ __forceinline__ float bf16r(float x) { return bf16_to_f32(f32_to_bf16(x)); }
-
 __device__ __forceinline__ int swz(int row) { return (row & 6) | ((row >> 3) & 1); }
 
 __device__ __forceinline__ v8i read_frag(const uint8_t* tile, int row, int g4) {
@@ -431,7 +429,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
             if (f32out)
               reinterpret_cast<float*>(smem)[row * BN + col] = v;
             else
-              reinterpret_cast<uint16_t*>(smem)[row * BN + col] = f32_to_bf16(v);
+              reinterpret_cast<uint16_t*>(smem)[row * BN + col] = bf16_bits_exact(v);
           }
       __syncthreads();
       const int chunks_per_row = BN * esz / 16;
@@ -447,6 +445,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
     } else {
       // ---- SwiGLU epilogue: h = bf16(w * silu(bf16(gate)) * bf16(up)), staged in
       // LDS as bf16 [BM][128], then 1x128 requant of each row (16 lanes per row).
+      // silu(g) = g / (1 + 2^(-g log2 e)) with the hardware exp2 and
+      // reciprocal (about 1 ulp each, far below the bf16 rounding of h).
       uint16_t* hbuf = reinterpret_cast<uint16_t*>(smem);
       const float lim = args.swiglu_limit;
 #pragma unroll
@@ -457,14 +457,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
           const float w = sW[row];
 #pragma unroll
           for (int j = 0; j < TN / 2; ++j) {
-            float gt = bf16r(acc[mi][j][r]);
-            float up = bf16r(acc[mi][j + TN / 2][r]);
+            float gt = bf16_round(acc[mi][j][r]);
+            float up = bf16_round(acc[mi][j + TN / 2][r]);
             if (lim > 0.0f) {
               up = clampf_(up, -lim, lim);
               gt = gt > lim ? lim : gt;
             }
-            const float silu = gt / (1.0f + expf(-gt));
-            hbuf[row * HALF + wn * HW + j * 16 + r16] = f32_to_bf16(w * (silu * up));
+            const float ex = __builtin_amdgcn_exp2f(gt * -1.4426950408889634f);
+            const float silu = gt * __builtin_amdgcn_rcpf(1.0f + ex);
+            hbuf[row * HALF + wn * HW + j * 16 + r16] = bf16_bits_exact(w * (silu * up));
           }
         }
       __syncthreads();
@@ -490,15 +491,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
         for (int o = LPR / 2; o > 0; o >>= 1) amax = fmaxf_(amax, __shfl_xor(amax, o, 64));
         if (row < rows) {
           const float sf = group_scale(args.scale_mode, amax);
-          const float inv = 1.0f / sf;
-          uint32_t lo = 0, hi = 0;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            lo |= (uint32_t)quant_elem(args.scale_mode, f[i], sf, inv) << (8 * i);
-            hi |= (uint32_t)quant_elem(args.scale_mode, f[i + 4], sf, inv) << (8 * i);
-          }
+          const uint2 qv = quant8_e4m3(args.scale_mode, f, sf);
           const int64_t p = row0 + row;
-          *reinterpret_cast<uint2*>(args.hq + p * N + n0 + sub * 8) = make_uint2(lo, hi);
+          *reinterpret_cast<uint2*>(args.hq + p * N + n0 + sub * 8) = qv;
           if (sub == 0) args.hs[p * NB + n0 / 128] = sf;
         }
       }

@@ -39,13 +39,6 @@ __device__ __forceinline__ void load8(const uint8_t* row, int elem, float* f, ui
   }
 }
 
-__device__ __forceinline__ uint2 pack_q8(const uint8_t* q) {
-  return make_uint2((uint32_t)q[0] | ((uint32_t)q[1] << 8) | ((uint32_t)q[2] << 16) |
-                        ((uint32_t)q[3] << 24),
-                    (uint32_t)q[4] | ((uint32_t)q[5] << 8) | ((uint32_t)q[6] << 16) |
-                        ((uint32_t)q[7] << 24));
-}
-
 // Layout A: lanes 0..55 quantize 8 NoPE values each (7 groups of 64 = 8
 // lanes), lanes 56..63 carry the 128 RoPE bytes verbatim.  paged != 0 writes
 // the footer page layout of to_paged_hnd directly (data at l*576 inside the
@@ -87,10 +80,7 @@ __global__ __launch_bounds__(256) void kv_pack_a_kernel(const uint8_t* __restric
     const float sf = group_scale(mode, amax);
     uint32_t sbyte = pow2_to_e8m0(sf);
     if (lane < 56) {
-      uint8_t q[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) q[i] = quant_elem(mode, f[i], sf, 0.0f);
-      *reinterpret_cast<uint2*>(data + lane * 8) = pack_q8(q);
+      *reinterpret_cast<uint2*>(data + lane * 8) = quant8_e4m3(mode, f, sf);
     } else {
       // rope bytes as given (bf16 / f16), 16 per lane at 448 + 16*(lane-56)
       uint8_t* dst = data + A_NOPE + (lane - 56) * 16;
@@ -132,11 +122,7 @@ __global__ __launch_bounds__(256) void kv_pack_b_kernel(const uint8_t* __restric
 #pragma unroll
     for (int off = 8; off > 0; off >>= 1) amax = fmaxf_(amax, __shfl_xor(amax, off, 64));
     const float sf = group_scale(SCALE_TORCH_FP32, amax);
-    const float inv = 1.0f / sf;
-    uint8_t q[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) q[i] = quant_elem(SCALE_TORCH_FP32, f[i], sf, inv);
-    *reinterpret_cast<uint2*>(o + lane * 8) = pack_q8(q);
+    *reinterpret_cast<uint2*>(o + lane * 8) = quant8_e4m3(SCALE_TORCH_FP32, f, sf);
     if (lane < 8) {
       if constexpr (DT == SGL_F32) {
         // fp32 input: rope stored as bf16 (RNE) so the row stays 656 B
@@ -145,8 +131,7 @@ __global__ __launch_bounds__(256) void kv_pack_b_kernel(const uint8_t* __restric
         load8<DT>(row, B_LAT + lane * 8, r, &unused);
         uint32_t w[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          w[i] = (uint32_t)f32_to_bf16(r[2 * i]) | ((uint32_t)f32_to_bf16(r[2 * i + 1]) << 16);
+        for (int i = 0; i < 4; ++i) w[i] = pk2_bf16_exact(r[2 * i], r[2 * i + 1]);
         *reinterpret_cast<uint4*>(o + B_LAT + lane * 16) = make_uint4(w[0], w[1], w[2], w[3]);
       } else {
         const uint4 v = *reinterpret_cast<const uint4*>(row + (B_LAT + lane * 8) * ES);
@@ -212,16 +197,14 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const uint8_t* __restric
       if (lane < 56) {
         const uint2 qv = *reinterpret_cast<const uint2*>(data + lane * 8);
         const uint32_t sb = foot[lane >> 3];
-        const uint8_t q[8] = {(uint8_t)qv.x, (uint8_t)(qv.x >> 8), (uint8_t)(qv.x >> 16),
-                              (uint8_t)(qv.x >> 24), (uint8_t)qv.y, (uint8_t)(qv.y >> 8),
-                              (uint8_t)(qv.y >> 16), (uint8_t)(qv.y >> 24)};
         const float s = sb == 0xFFu ? bits_f32(0x7FC00000u)
                                     : (sb == 0 ? bits_f32(0x00400000u) : bits_f32(sb << 23));
+        float d[8];
+        unpack4_e4m3(qv.x, d);
+        unpack4_e4m3(qv.y, d + 4);
         uint32_t w[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          w[i] = (uint32_t)f32_to_bf16(e4m3_to_f32(q[2 * i]) * s) |
-                 ((uint32_t)f32_to_bf16(e4m3_to_f32(q[2 * i + 1]) * s) << 16);
+        for (int i = 0; i < 4; ++i) w[i] = pk2_bf16_exact(d[2 * i] * s, d[2 * i + 1] * s);
         *reinterpret_cast<uint4*>(o + lane * 8) = make_uint4(w[0], w[1], w[2], w[3]);
       } else {
         const uint8_t* src = data + A_NOPE + (lane - 56) * 16;
@@ -233,14 +216,12 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const uint8_t* __restric
       const uint8_t* row = cache + (int64_t)id * B_ROW;
       const uint2 qv = *reinterpret_cast<const uint2*>(row + lane * 8);
       const float s = *reinterpret_cast<const float*>(row + 640 + (lane >> 4) * 4);
-      const uint8_t q[8] = {(uint8_t)qv.x, (uint8_t)(qv.x >> 8), (uint8_t)(qv.x >> 16),
-                            (uint8_t)(qv.x >> 24), (uint8_t)qv.y, (uint8_t)(qv.y >> 8),
-                            (uint8_t)(qv.y >> 16), (uint8_t)(qv.y >> 24)};
+      float d[8];
+      unpack4_e4m3(qv.x, d);
+      unpack4_e4m3(qv.y, d + 4);
       uint32_t w[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        w[i] = (uint32_t)f32_to_bf16(e4m3_to_f32(q[2 * i]) * s) |
-               ((uint32_t)f32_to_bf16(e4m3_to_f32(q[2 * i + 1]) * s) << 16);
+      for (int i = 0; i < 4; ++i) w[i] = pk2_bf16_exact(d[2 * i] * s, d[2 * i + 1] * s);
       *reinterpret_cast<uint4*>(o + lane * 8) = make_uint4(w[0], w[1], w[2], w[3]);
       if (lane < 8)
         *reinterpret_cast<uint4*>(o + 512 + lane * 8) =

@@ -49,26 +49,19 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
     for (int i = 0; i < 8; ++i) amax = fmaxf_(amax, fabsf(f[i]));
     amax = group_max<LPG>(amax);
     const float sf = group_scale(mode, amax);
-    const float inv = 1.0f / sf;
-    uint8_t q[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) q[i] = quant_elem(mode, f[i], sf, inv);
+    const uint2 qv = quant8_e4m3(mode, f, sf);
     if (INPLACE) {
       // quant-dequant back to bf16: bf16(fp32(e4m3) * s)
+      float d[8];
+      unpack4_e4m3(qv.x, d);
+      unpack4_e4m3(qv.y, d + 4);
       uint32_t o[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t lo = f32_to_bf16(e4m3_to_f32(q[2 * i]) * sf);
-        uint32_t hi = f32_to_bf16(e4m3_to_f32(q[2 * i + 1]) * sf);
-        o[i] = lo | (hi << 16);
-      }
+      for (int i = 0; i < 4; ++i) o[i] = pk2_bf16_exact(d[2 * i] * sf, d[2 * i + 1] * sf);
       *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(y) + row * ldy + col) =
           make_uint4(o[0], o[1], o[2], o[3]);
     } else {
-      uint2 o;
-      o.x = (uint32_t)q[0] | ((uint32_t)q[1] << 8) | ((uint32_t)q[2] << 16) | ((uint32_t)q[3] << 24);
-      o.y = (uint32_t)q[4] | ((uint32_t)q[5] << 8) | ((uint32_t)q[6] << 16) | ((uint32_t)q[7] << 24);
-      *reinterpret_cast<uint2*>(reinterpret_cast<uint8_t*>(y) + row * ldy + col) = o;
+      *reinterpret_cast<uint2*>(reinterpret_cast<uint8_t*>(y) + row * ldy + col) = qv;
     }
     if (sub == 0) {
       const int64_t si = row * lds + col / GROUP;
@@ -135,12 +128,8 @@ __global__ __launch_bounds__(256) void weight_quant_kernel(const T* __restrict__
   for (int i = 0; i < 8; ++i) {
     const int64_t row = bn * 128 + t / 16 + 16 * i;
     if (row >= N) continue;
-    uint32_t lo = 0, hi = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      lo |= (uint32_t)f32_to_e4m3(v[i][j] * inv) << (8 * j);
-      hi |= (uint32_t)f32_to_e4m3(v[i][j + 4] * inv) << (8 * j);
-    }
+    const uint32_t lo = pk4_e4m3_exact(v[i][0] * inv, v[i][1] * inv, v[i][2] * inv, v[i][3] * inv);
+    const uint32_t hi = pk4_e4m3_exact(v[i][4] * inv, v[i][5] * inv, v[i][6] * inv, v[i][7] * inv);
     *reinterpret_cast<uint2*>(q + row * ldq + col) = make_uint2(lo, hi);
   }
 }
@@ -153,6 +142,55 @@ __global__ void e8m0_to_f32_kernel(const uint8_t* __restrict__ src, float* __res
     // 0xFF is the e8m0 NaN code; 0 is 2^-127 (an fp32 subnormal)
     dst[i] = b == 0xFFu ? bits_f32(0x7FC00000u) : (b == 0 ? bits_f32(0x00400000u) : bits_f32(b << 23));
   }
+}
+
+// Self-check of the hardware conversions over every fp32 bit pattern: thread
+// t of a launch covers inputs start + 4t .. start + 4t + 3.
+//   counts[0]: pk4_e4m3_exact != f32_to_e4m3   (all inputs)
+//   counts[1]: pk2_bf16_exact != f32_to_bf16   (all inputs)
+//   counts[2]: pk4_e4m3 != f32_to_e4m3         (non-NaN inputs)
+//   counts[3]: pk2_bf16 != f32_to_bf16         (non-NaN inputs)
+//   counts[4]: unpack4_e4m3 != e4m3_to_f32      (256 codes; NaN code -> any NaN)
+__global__ void check_conversions_kernel(uint64_t start, unsigned long long* counts) {
+  const uint64_t u0 = start + ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  float x[4];
+  uint32_t sw8 = 0;
+  unsigned c[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[i] = bits_f32((uint32_t)(u0 + i));
+    sw8 |= (uint32_t)f32_to_e4m3(x[i]) << (8 * i);
+  }
+  const uint32_t hx = pk4_e4m3_exact(x[0], x[1], x[2], x[3]);
+  const uint32_t hr = pk4_e4m3(x[0], x[1], x[2], x[3]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t s8 = (sw8 >> (8 * i)) & 0xFFu;
+    c[0] += ((hx >> (8 * i)) & 0xFFu) != s8;
+    c[2] += (x[i] == x[i]) && ((hr >> (8 * i)) & 0xFFu) != s8;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i += 2) {
+    const uint32_t sw = (uint32_t)f32_to_bf16(x[i]) | ((uint32_t)f32_to_bf16(x[i + 1]) << 16);
+    const uint32_t ex = pk2_bf16_exact(x[i], x[i + 1]);
+    const uint32_t raw = pk2_bf16(x[i], x[i + 1]);
+    c[1] += (ex & 0xFFFFu) != (sw & 0xFFFFu);
+    c[1] += (ex >> 16) != (sw >> 16);
+    c[3] += (x[i] == x[i]) && (raw & 0xFFFFu) != (sw & 0xFFFFu);
+    c[3] += (x[i + 1] == x[i + 1]) && (raw >> 16) != (sw >> 16);
+  }
+  unsigned c4 = 0;
+  if (u0 < 1024) {  // the 256 e4m3 codes, one per thread of the first launch
+    const uint32_t code = (uint32_t)(u0 >> 2);
+    float hw[4];
+    unpack4_e4m3(code, hw);
+    const float ref = e4m3_to_f32((uint8_t)code);
+    c4 = ref != ref ? (hw[0] == hw[0]) : (f32_bits(hw[0]) != f32_bits(ref));
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (c[i]) atomicAdd(&counts[i], (unsigned long long)c[i]);
+  if (c4) atomicAdd(&counts[4], (unsigned long long)c4);
 }
 
 template <int GROUP>
@@ -242,6 +280,18 @@ int sgl_e8m0_to_f32(const void* src, float* dst, int64_t n, sgl_stream_t stream)
   sgl::e8m0_to_f32_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>((const uint8_t*)src,
                                                                              dst, n);
   return sgl::check_launch("e8m0_to_f32");
+}
+
+int sgl_check_conversions(unsigned long long* counts, sgl_stream_t stream) {
+  SGL_REQUIRE(counts, "check_conversions: null pointer");
+  const uint64_t per_launch = 1ull << 28;  // inputs per launch, 4 per thread
+  for (uint64_t start = 0; start < (1ull << 32); start += per_launch) {
+    sgl::check_conversions_kernel<<<(unsigned)(per_launch / 4 / 256), 256, 0, (hipStream_t)stream>>>(
+        start, counts);
+    const int rc = sgl::check_launch("check_conversions");
+    if (rc != SGL_OK) return rc;
+  }
+  return SGL_OK;
 }
 
 }  // extern "C"

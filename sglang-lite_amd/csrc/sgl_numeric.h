@@ -77,6 +77,49 @@ SGL_HD uint8_t f32_to_e4m3(float x) {
   return (uint8_t)(sign | (uint8_t)iq);
 }
 
+#if defined(__HIPCC__)
+// gfx950 conversion instructions.  v_cvt_pk_fp8_f32 (OCP e4m3fn, round to
+// nearest even, out of range -> NaN code) and v_cvt_pk_bf16_f32 (round to
+// nearest even) give exactly f32_to_e4m3 / f32_to_bf16 for every non-NaN fp32
+// input; sgl_check_conversions re-verifies that over all 2^32 inputs on the
+// device.  For NaN inputs the hardware e4m3 code can carry the other sign bit
+// and the bf16 result keeps payload bits; the *_exact forms restore the
+// software convention (NaN keeps its sign as S.1111.111; bf16 NaN is 0x7FC0).
+typedef float sgl_f2 __attribute__((ext_vector_type(2)));
+typedef __bf16 sgl_bf2 __attribute__((ext_vector_type(2)));
+
+// bytes {a, b, c, d} as e4m3fn, little-endian
+__device__ __forceinline__ uint32_t pk4_e4m3(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+__device__ __forceinline__ uint32_t pk4_e4m3_exact(float a, float b, float c, float d) {
+  const uint32_t signs = ((f32_bits(a) >> 24) & 0x80u) | ((f32_bits(b) >> 16) & 0x8000u) |
+                         ((f32_bits(c) >> 8) & 0x800000u) | (f32_bits(d) & 0x80000000u);
+  return (pk4_e4m3(a, b, c, d) & 0x7F7F7F7Fu) | signs;
+}
+// {lo, hi} as bf16, lo in the low half-word
+__device__ __forceinline__ uint32_t pk2_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(sgl_f2{lo, hi}, sgl_bf2));
+}
+__device__ __forceinline__ uint16_t bf16_bits(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
+__device__ __forceinline__ uint16_t bf16_bits_exact(float x) {
+  return x != x ? (uint16_t)0x7FC0 : bf16_bits(x);
+}
+__device__ __forceinline__ uint32_t pk2_bf16_exact(float lo, float hi) {
+  return (uint32_t)bf16_bits_exact(lo) | ((uint32_t)bf16_bits_exact(hi) << 16);
+}
+// four e4m3 bytes (little-endian) -> fp32, exact (v_cvt_pk_f32_fp8); the NaN
+// code gives a NaN
+__device__ __forceinline__ void unpack4_e4m3(uint32_t w, float* f) {
+  const sgl_f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const sgl_f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  f[0] = lo.x; f[1] = lo.y; f[2] = hi.x; f[3] = hi.y;
+}
+// fp32 value of the bf16 rounding of x (NaN stays NaN)
+__device__ __forceinline__ float bf16_round(float x) { return bits_f32((uint32_t)bf16_bits(x) << 16); }
+#endif
+
 // e4m3fn -> fp32 (exact).
 SGL_HD float e4m3_to_f32(uint8_t v) {
   const uint32_t sign = ((uint32_t)v & 0x80u) << 24;
@@ -172,5 +215,28 @@ SGL_HD uint8_t quant_elem(int mode, float x, float sf, float inv) {
   if (mode == SCALE_TORCH_FP32 || mode == SCALE_TORCH_UE8M0) return f32_to_e4m3(x * inv);
   return f32_to_e4m3(clampf_(x / sf, -448.0f, 448.0f));
 }
+
+#if defined(__HIPCC__)
+// Eight consecutive elements of one group -> e4m3 bytes (little-endian in
+// .x then .y), bit-identical to quant_elem for every mode.  ue8m0 scales are
+// powers of two (or Inf / NaN), so TileLang-ue8m0 and KV divisions equal the
+// product with the exact reciprocal; only TileLang-fp32 divides.
+__device__ __forceinline__ uint2 quant8_e4m3(int mode, const float* f, float sf) {
+  float y[8];
+  if (mode == SCALE_TILELANG_FP32) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = clampf_(f[i] / sf, -448.0f, 448.0f);
+  } else {
+    const float inv = 1.0f / sf;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = f[i] * inv;
+    if (mode != SCALE_TORCH_FP32 && mode != SCALE_TORCH_UE8M0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = clampf_(y[i], -448.0f, 448.0f);
+    }
+  }
+  return make_uint2(pk4_e4m3_exact(y[0], y[1], y[2], y[3]), pk4_e4m3_exact(y[4], y[5], y[6], y[7]));
+}
+#endif
 
 }  // namespace sgl

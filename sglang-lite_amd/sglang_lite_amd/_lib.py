@@ -48,6 +48,7 @@ SIGNATURES = {
     "sgl_act_quant": (c_int, [P, I64, I64, I64, P, I64, P, I64, c_int, c_int, c_int, c_int, P]),
     "sgl_weight_quant_128x128": (c_int, [P, c_int, I64, I64, I64, P, I64, P, I64, c_int, P]),
     "sgl_e8m0_to_f32": (c_int, [P, P, I64, P]),
+    "sgl_check_conversions": (c_int, [P, P]),
     "sgl_fp8_gemm": (c_int, [P, P, P, P, c_int, P, c_int, I64, I64, I64, P]),
     "sgl_moe_route_topk": (c_int, [P, I64, c_int, c_int, c_int, P, c_float, P, P, P]),
     "sgl_moe_permute": (c_int, [P, I64, c_int, c_int, P, P, P, P, P]),

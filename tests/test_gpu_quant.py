@@ -92,3 +92,15 @@ def test_e8m0_to_f32(gpu):
     ok = ~np.isnan(ref)
     np.testing.assert_array_equal(got[ok].view(np.uint32), ref[ok].view(np.uint32))
     assert np.all(np.isnan(got[~ok]))
+
+
+def test_hardware_conversions_match_software_rules_exhaustively(gpu):
+    """v_cvt_pk_fp8_f32 / v_cvt_pk_bf16_f32 (+ NaN fix-up), used by the GEMM
+    epilogues and the quant kernels, equal the bit-level rounding rules of
+    f32_to_e4m3 / f32_to_bf16 for all 2^32 fp32 inputs."""
+    from sglang_lite_amd import _lib
+
+    counts = torch.zeros(5, dtype=torch.int64, device=gpu)
+    _lib.call("sgl_check_conversions", counts.data_ptr(), _lib.stream_of(counts))
+    torch.cuda.synchronize()
+    assert counts.cpu().tolist() == [0, 0, 0, 0, 0]
