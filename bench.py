@@ -341,10 +341,15 @@ def main():
             log(f"decode T={Td}: {msd:.3f} ms, touched {touched}, {by / msd / 1e6:.0f} GB/s")
         extra["decode"] = dec
         # ---- dense GEMM
-        flush_buf = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+        # cold-cache timing: read 512 MiB between runs so neither L2 nor the
+        # memory-side cache holds the inputs.  A read, not a fill: a fill
+        # leaves 512 MiB of dirty lines whose write-back would land inside
+        # the next timed kernel.
+        flush_buf = torch.ones(128 << 20, dtype=torch.float32, device=dev)
+        flush_sink = torch.empty((), dtype=torch.float32, device=dev)
 
         def flush():
-            flush_buf.zero_()
+            torch.sum(flush_buf, dim=0, out=flush_sink)
 
         gw = torch.Generator(device=dev).manual_seed(2)
         bq, bs = K.per_block_cast_to_fp8(torch.randn(4096, 7168, generator=gw, device=dev) * 0.02,

@@ -13,6 +13,13 @@ namespace {
 
 constexpr int A_NOPE = 448, A_DIM = 512, A_ROW = 584, A_DATA = 576;
 constexpr int B_LAT = 512, B_DIM = 576, B_ROW = 656;
+#ifndef SGL_KV_ROWS
+#define SGL_KV_ROWS 1
+#endif
+#ifndef SGL_KV_BLOCKS_PER_CU
+#define SGL_KV_BLOCKS_PER_CU 32
+#endif
+constexpr int kKvRows = SGL_KV_ROWS;  // rows per wavefront step in the pack / gather kernels
 
 template <int DT>
 __device__ __forceinline__ void load8(const uint8_t* row, int elem, float* f, uint4* raw) {
@@ -42,105 +49,131 @@ __device__ __forceinline__ void load8(const uint8_t* row, int elem, float* f, ui
 // Layout A: lanes 0..55 quantize 8 NoPE values each (7 groups of 64 = 8
 // lanes), lanes 56..63 carry the 128 RoPE bytes verbatim.  paged != 0 writes
 // the footer page layout of to_paged_hnd directly (data at l*576 inside the
-// page, scales at page*576 + l*8) and zero-fills padding rows.
-template <int DT>
+// page, scales at page*576 + l*8) and zero-fills padding rows.  A wavefront
+// takes R consecutive rows per step and issues all their loads first, so R
+// rows of reads are in flight per wavefront.
+template <int DT, int R>
 __global__ __launch_bounds__(256) void kv_pack_a_kernel(const uint8_t* __restrict__ kv, int64_t T,
                                                         int64_t ld_bytes, int mode, int paged,
                                                         int page, int64_t rows_total,
                                                         uint8_t* __restrict__ out) {
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * 4;
-  for (int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); t < rows_total; t += nwaves) {
-    uint8_t* data;
-    uint8_t* foot;
-    if (paged) {
-      const int64_t pg = t / page, l = t - pg * page;
-      uint8_t* pbase = out + pg * (int64_t)page * A_ROW;
-      data = pbase + l * A_DATA;
-      foot = pbase + (int64_t)page * A_DATA + l * 8;
-    } else {
-      data = out + t * A_ROW;
-      foot = data + A_DATA;
-    }
-    if (t >= T) {  // padding row of the last page
-      if (lane < 72) *reinterpret_cast<uint2*>(data + lane * 8) = make_uint2(0, 0);
-      if (lane < 8) *reinterpret_cast<uint2*>(data + 512 + lane * 8) = make_uint2(0, 0);
-      if (lane == 0) *reinterpret_cast<uint2*>(foot) = make_uint2(0, 0);
-      continue;
-    }
-    const uint8_t* row = kv + t * ld_bytes;
-    float f[8];
-    uint4 raw;
-    load8<DT>(row, lane * 8, f, &raw);
-    float amax = 0.0f;
+  const int64_t w0 = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  for (int64_t tb = w0 * R; tb < rows_total; tb += nwaves * R) {
+    float f[R][8];
+    uint4 raw[R];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf_(amax, fabsf(f[i]));
+    for (int r = 0; r < R; ++r)
+      if (tb + r < T) load8<DT>(kv + (tb + r) * ld_bytes, lane * 8, f[r], &raw[r]);
 #pragma unroll
-    for (int o = 4; o > 0; o >>= 1) amax = fmaxf_(amax, __shfl_xor(amax, o, 64));
-    const float sf = group_scale(mode, amax);
-    uint32_t sbyte = pow2_to_e8m0(sf);
-    if (lane < 56) {
-      *reinterpret_cast<uint2*>(data + lane * 8) = quant8_e4m3(mode, f, sf);
-    } else {
-      // rope bytes as given (bf16 / f16), 16 per lane at 448 + 16*(lane-56)
-      uint8_t* dst = data + A_NOPE + (lane - 56) * 16;
-      *reinterpret_cast<uint2*>(dst) = make_uint2(raw.x, raw.y);
-      *reinterpret_cast<uint2*>(dst + 8) = make_uint2(raw.z, raw.w);
-    }
-    // 7 scale bytes + zero pad -> one 8-byte store by lane 0
-    uint32_t lo = 0, hi = 0;
+    for (int r = 0; r < R; ++r) {
+      const int64_t t = tb + r;
+      if (t >= rows_total) break;
+      uint8_t* data;
+      uint8_t* foot;
+      if (paged) {
+        const int64_t pg = t / page, l = t - pg * page;
+        uint8_t* pbase = out + pg * (int64_t)page * A_ROW;
+        data = pbase + l * A_DATA;
+        foot = pbase + (int64_t)page * A_DATA + l * 8;
+      } else {
+        data = out + t * A_ROW;
+        foot = data + A_DATA;
+      }
+      if (t >= T) {  // padding row of the last page
+        if (lane < 72) *reinterpret_cast<uint2*>(data + lane * 8) = make_uint2(0, 0);
+        if (lane < 8) *reinterpret_cast<uint2*>(data + 512 + lane * 8) = make_uint2(0, 0);
+        if (lane == 0) *reinterpret_cast<uint2*>(foot) = make_uint2(0, 0);
+        continue;
+      }
+      float amax = 0.0f;
 #pragma unroll
-    for (int g = 0; g < 7; ++g) {
-      const uint32_t b = (uint32_t)__shfl((int)sbyte, g * 8, 64) & 0xFFu;
-      if (g < 4)
-        lo |= b << (8 * g);
-      else
-        hi |= b << (8 * (g - 4));
+      for (int i = 0; i < 8; ++i) amax = fmaxf_(amax, fabsf(f[r][i]));
+#pragma unroll
+      for (int o = 4; o > 0; o >>= 1) amax = fmaxf_(amax, __shfl_xor(amax, o, 64));
+      const float sf = group_scale(mode, amax);
+      const uint32_t sbyte = pow2_to_e8m0(sf);
+      if (lane < 56) {
+        *reinterpret_cast<uint2*>(data + lane * 8) = quant8_e4m3(mode, f[r], sf);
+      } else {
+        // rope bytes as given (bf16 / f16), 16 per lane at 448 + 16*(lane-56)
+        uint8_t* dst = data + A_NOPE + (lane - 56) * 16;
+        *reinterpret_cast<uint2*>(dst) = make_uint2(raw[r].x, raw[r].y);
+        *reinterpret_cast<uint2*>(dst + 8) = make_uint2(raw[r].z, raw[r].w);
+      }
+      // 7 scale bytes + zero pad -> one 8-byte store by lane 0
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int g = 0; g < 7; ++g) {
+        const uint32_t b = (uint32_t)__shfl((int)sbyte, g * 8, 64) & 0xFFu;
+        if (g < 4)
+          lo |= b << (8 * g);
+        else
+          hi |= b << (8 * (g - 4));
+      }
+      if (lane == 0) *reinterpret_cast<uint2*>(foot) = make_uint2(lo, hi);
     }
-    if (lane == 0) *reinterpret_cast<uint2*>(foot) = make_uint2(lo, hi);
   }
 }
 
 // Layout B: 64 lanes x 8 latent values (4 groups of 128 = 16 lanes each),
 // then lanes 0..7 copy the 128 RoPE bytes; 4 fp32 scales stored by lane 0.
-template <int DT>
+// R consecutive rows per wavefront step, loads first.
+template <int DT, int R>
 __global__ __launch_bounds__(256) void kv_pack_b_kernel(const uint8_t* __restrict__ kv, int64_t T,
                                                         int64_t ld_bytes,
                                                         uint8_t* __restrict__ out) {
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * 4;
+  const int64_t w0 = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   constexpr int ES = DT == SGL_F32 ? 4 : 2;
-  for (int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); t < T; t += nwaves) {
-    const uint8_t* row = kv + t * ld_bytes;
-    uint8_t* o = out + t * B_ROW;
-    float f[8];
-    uint4 raw;
-    load8<DT>(row, lane * 8, f, &raw);
-    float amax = 0.0f;
+  for (int64_t tb = w0 * R; tb < T; tb += nwaves * R) {
+    float f[R][8];
+    uint4 raw[R];
+    float rf[R][8];  // fp32 input: the rope values of lanes 0..7
+    uint4 rope[R];   // 16-bit input: the rope bytes of lanes 0..7
 #pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf_(amax, fabsf(f[i]));
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) amax = fmaxf_(amax, __shfl_xor(amax, off, 64));
-    const float sf = group_scale(SCALE_TORCH_FP32, amax);
-    *reinterpret_cast<uint2*>(o + lane * 8) = quant8_e4m3(SCALE_TORCH_FP32, f, sf);
-    if (lane < 8) {
-      if constexpr (DT == SGL_F32) {
-        // fp32 input: rope stored as bf16 (RNE) so the row stays 656 B
-        float r[8];
-        uint4 unused;
-        load8<DT>(row, B_LAT + lane * 8, r, &unused);
-        uint32_t w[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = pk2_bf16_exact(r[2 * i], r[2 * i + 1]);
-        *reinterpret_cast<uint4*>(o + B_LAT + lane * 16) = make_uint4(w[0], w[1], w[2], w[3]);
-      } else {
-        const uint4 v = *reinterpret_cast<const uint4*>(row + (B_LAT + lane * 8) * ES);
-        *reinterpret_cast<uint4*>(o + B_LAT + lane * 16) = v;
+    for (int r = 0; r < R; ++r) {
+      if (tb + r >= T) break;
+      const uint8_t* row = kv + (tb + r) * ld_bytes;
+      load8<DT>(row, lane * 8, f[r], &raw[r]);
+      if (lane < 8) {
+        if constexpr (DT == SGL_F32) {
+          uint4 unused;
+          load8<DT>(row, B_LAT + lane * 8, rf[r], &unused);
+        } else {
+          rope[r] = *reinterpret_cast<const uint4*>(row + (B_LAT + lane * 8) * ES);
+        }
       }
     }
-    const float s0 = __shfl(sf, 0, 64), s1 = __shfl(sf, 16, 64), s2 = __shfl(sf, 32, 64),
-                s3 = __shfl(sf, 48, 64);
-    if (lane == 0) *reinterpret_cast<float4*>(o + 640) = make_float4(s0, s1, s2, s3);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t t = tb + r;
+      if (t >= T) break;
+      uint8_t* o = out + t * B_ROW;
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) amax = fmaxf_(amax, fabsf(f[r][i]));
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) amax = fmaxf_(amax, __shfl_xor(amax, off, 64));
+      const float sf = group_scale(SCALE_TORCH_FP32, amax);
+      *reinterpret_cast<uint2*>(o + lane * 8) = quant8_e4m3(SCALE_TORCH_FP32, f[r], sf);
+      if (lane < 8) {
+        if constexpr (DT == SGL_F32) {
+          // fp32 input: rope stored as bf16 (RNE) so the row stays 656 B
+          uint32_t w[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) w[i] = pk2_bf16_exact(rf[r][2 * i], rf[r][2 * i + 1]);
+          *reinterpret_cast<uint4*>(o + B_LAT + lane * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+          *reinterpret_cast<uint4*>(o + B_LAT + lane * 16) = rope[r];
+        }
+      }
+      const float s0 = __shfl(sf, 0, 64), s1 = __shfl(sf, 16, 64), s2 = __shfl(sf, 32, 64),
+                  s3 = __shfl(sf, 48, 64);
+      if (lane == 0) *reinterpret_cast<float4*>(o + 640) = make_float4(s0, s1, s2, s3);
+    }
   }
 }
 
@@ -162,10 +195,12 @@ __global__ __launch_bounds__(256) void kv_to_paged_kernel(const uint8_t* __restr
   }
 }
 
-// One wavefront per gathered row.  Layout A: out 512 bf16 = 448 dequantized
-// (e4m3 * 2^(e8m0-127), exact in bf16) + 64 rope; layout B: out 576 bf16 =
-// 512 bf16(e4m3 * fp32 scale) + 64 rope.
-template <int LAYOUT>
+// One wavefront per gathered row, R rows per step: the R indices come in
+// with one load, then every row's loads are issued before any is used.
+// Layout A: out 512 bf16 = 448 dequantized (e4m3 * 2^(e8m0-127), exact in
+// bf16) + 64 rope; layout B: out 576 bf16 = 512 bf16(e4m3 * fp32 scale) + 64
+// rope.  Indices outside [0, n_rows) give zero rows.
+template <int LAYOUT, int R>
 __global__ __launch_bounds__(256) void kv_gather_kernel(const uint8_t* __restrict__ cache,
                                                         int paged, int page, int64_t n_rows,
                                                         const int32_t* __restrict__ idx,
@@ -173,59 +208,75 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const uint8_t* __restric
   constexpr int ODIM = LAYOUT == SGL_KV_LAYOUT_A ? A_DIM : B_DIM;
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * 4;
-  for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < total; r += nwaves) {
-    const int32_t id = idx[r];
-    uint16_t* o = out + r * ODIM;
-    if (id < 0 || id >= n_rows) {
-      const uint4 z = make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4*>(o + lane * 8) = z;
-      if (LAYOUT == SGL_KV_LAYOUT_B && lane < 8) *reinterpret_cast<uint4*>(o + 512 + lane * 8) = z;
-      continue;
-    }
-    if constexpr (LAYOUT == SGL_KV_LAYOUT_A) {
-      const uint8_t* data;
-      const uint8_t* foot;
-      if (paged) {
-        const int64_t pg = id / page, l = id - pg * page;
-        const uint8_t* pbase = cache + pg * (int64_t)page * A_ROW;
-        data = pbase + l * A_DATA;
-        foot = pbase + (int64_t)page * A_DATA + l * 8;
+  const int64_t w0 = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  for (int64_t rb = w0 * R; rb < total; rb += nwaves * R) {
+    const int32_t my_id = (lane < R && rb + lane < total) ? idx[rb + lane] : -1;
+    int32_t id[R];
+    uint2 qv[R];
+    uint32_t sraw[R];  // layout A: the e8m0 byte; layout B: the fp32 scale bits
+    uint4 rope[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      id[r] = __builtin_amdgcn_readfirstlane(__shfl(my_id, r, 64));
+      if (id[r] < 0 || id[r] >= n_rows) continue;
+      if constexpr (LAYOUT == SGL_KV_LAYOUT_A) {
+        const uint8_t* data;
+        const uint8_t* foot;
+        if (paged) {
+          const int64_t pg = id[r] / page, l = id[r] - pg * page;
+          const uint8_t* pbase = cache + pg * (int64_t)page * A_ROW;
+          data = pbase + l * A_DATA;
+          foot = pbase + (int64_t)page * A_DATA + l * 8;
+        } else {
+          data = cache + (int64_t)id[r] * A_ROW;
+          foot = data + A_DATA;
+        }
+        if (lane < 56) {
+          qv[r] = *reinterpret_cast<const uint2*>(data + lane * 8);
+          sraw[r] = foot[lane >> 3];
+        } else {
+          const uint8_t* src = data + A_NOPE + (lane - 56) * 16;
+          const uint2 a = *reinterpret_cast<const uint2*>(src);
+          const uint2 b = *reinterpret_cast<const uint2*>(src + 8);
+          rope[r] = make_uint4(a.x, a.y, b.x, b.y);
+        }
       } else {
-        data = cache + (int64_t)id * A_ROW;
-        foot = data + A_DATA;
+        const uint8_t* row = cache + (int64_t)id[r] * B_ROW;
+        qv[r] = *reinterpret_cast<const uint2*>(row + lane * 8);
+        sraw[r] = *reinterpret_cast<const uint32_t*>(row + 640 + (lane >> 4) * 4);
+        if (lane < 8) rope[r] = *reinterpret_cast<const uint4*>(row + B_LAT + lane * 16);
       }
-      if (lane < 56) {
-        const uint2 qv = *reinterpret_cast<const uint2*>(data + lane * 8);
-        const uint32_t sb = foot[lane >> 3];
-        const float s = sb == 0xFFu ? bits_f32(0x7FC00000u)
-                                    : (sb == 0 ? bits_f32(0x00400000u) : bits_f32(sb << 23));
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (rb + r >= total) break;
+      uint16_t* o = out + (rb + r) * ODIM;
+      if (id[r] < 0 || id[r] >= n_rows) {
+        const uint4 z = make_uint4(0, 0, 0, 0);
+        *reinterpret_cast<uint4*>(o + lane * 8) = z;
+        if (LAYOUT == SGL_KV_LAYOUT_B && lane < 8) *reinterpret_cast<uint4*>(o + 512 + lane * 8) = z;
+        continue;
+      }
+      const bool deq = LAYOUT == SGL_KV_LAYOUT_B || lane < 56;
+      if (deq) {
+        float sc;
+        if constexpr (LAYOUT == SGL_KV_LAYOUT_A) {
+          const uint32_t sb = sraw[r];
+          sc = sb == 0xFFu ? bits_f32(0x7FC00000u) : (sb == 0 ? bits_f32(0x00400000u) : bits_f32(sb << 23));
+        } else {
+          sc = bits_f32(sraw[r]);
+        }
         float d[8];
-        unpack4_e4m3(qv.x, d);
-        unpack4_e4m3(qv.y, d + 4);
+        unpack4_e4m3(qv[r].x, d);
+        unpack4_e4m3(qv[r].y, d + 4);
         uint32_t w[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = pk2_bf16_exact(d[2 * i] * s, d[2 * i + 1] * s);
+        for (int i = 0; i < 4; ++i) w[i] = pk2_bf16_exact(d[2 * i] * sc, d[2 * i + 1] * sc);
         *reinterpret_cast<uint4*>(o + lane * 8) = make_uint4(w[0], w[1], w[2], w[3]);
       } else {
-        const uint8_t* src = data + A_NOPE + (lane - 56) * 16;
-        const uint2 a = *reinterpret_cast<const uint2*>(src);
-        const uint2 b = *reinterpret_cast<const uint2*>(src + 8);
-        *reinterpret_cast<uint4*>(o + lane * 8) = make_uint4(a.x, a.y, b.x, b.y);
+        *reinterpret_cast<uint4*>(o + lane * 8) = rope[r];
       }
-    } else {
-      const uint8_t* row = cache + (int64_t)id * B_ROW;
-      const uint2 qv = *reinterpret_cast<const uint2*>(row + lane * 8);
-      const float s = *reinterpret_cast<const float*>(row + 640 + (lane >> 4) * 4);
-      float d[8];
-      unpack4_e4m3(qv.x, d);
-      unpack4_e4m3(qv.y, d + 4);
-      uint32_t w[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) w[i] = pk2_bf16_exact(d[2 * i] * s, d[2 * i + 1] * s);
-      *reinterpret_cast<uint4*>(o + lane * 8) = make_uint4(w[0], w[1], w[2], w[3]);
-      if (lane < 8)
-        *reinterpret_cast<uint4*>(o + 512 + lane * 8) =
-            *reinterpret_cast<const uint4*>(row + B_LAT + lane * 16);
+      if (LAYOUT == SGL_KV_LAYOUT_B && lane < 8) *reinterpret_cast<uint4*>(o + 512 + lane * 8) = rope[r];
     }
   }
 }
@@ -261,9 +312,11 @@ __global__ __launch_bounds__(256) void split_indices_kernel(const IT* __restrict
   }
 }
 
-unsigned grid_for_rows(int64_t rows) {
-  int64_t blocks = ceil_div(rows, 4);
-  const int64_t cap = (int64_t)device_cu_count() * 32;
+// 4 wavefronts per block, rows_per_wave rows per wavefront step; at most
+// SGL_KV_BLOCKS_PER_CU blocks per CU, the rest loop.
+unsigned grid_for_rows(int64_t rows, int rows_per_wave = 1) {
+  int64_t blocks = ceil_div(rows, 4 * (int64_t)rows_per_wave);
+  const int64_t cap = (int64_t)device_cu_count() * SGL_KV_BLOCKS_PER_CU;
   if (blocks > cap) blocks = cap;
   return (unsigned)(blocks < 1 ? 1 : blocks);
 }
@@ -292,13 +345,13 @@ int sgl_kv_pack(const void* kv, int dtype, int64_t T, int64_t ldkv, int layout, 
     SGL_REQUIRE(out && (T == 0 || kv), "kv_pack: null pointer");
     SGL_REQUIRE(sgl::aligned(out, 8) && (T == 0 || (sgl::aligned(kv, 16) && (ldkv * es) % 16 == 0)),
                 "kv_pack: kv rows must be 16-byte aligned, out 8-byte aligned");
-    const unsigned g = sgl::grid_for_rows(rows);
+    const unsigned g = sgl::grid_for_rows(rows, sgl::kKvRows);
     if (dtype == SGL_BF16)
-      sgl::kv_pack_a_kernel<SGL_BF16><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
+      sgl::kv_pack_a_kernel<SGL_BF16, sgl::kKvRows><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
                                                          scale_mode, paged, page_size, rows,
                                                          (uint8_t*)out);
     else
-      sgl::kv_pack_a_kernel<SGL_F16><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
+      sgl::kv_pack_a_kernel<SGL_F16, sgl::kKvRows><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
                                                         scale_mode, paged, page_size, rows,
                                                         (uint8_t*)out);
     return sgl::check_launch("kv_pack_a");
@@ -309,15 +362,15 @@ int sgl_kv_pack(const void* kv, int dtype, int64_t T, int64_t ldkv, int layout, 
   SGL_REQUIRE(kv && out, "kv_pack: null pointer");
   SGL_REQUIRE(sgl::aligned(out, 16) && sgl::aligned(kv, 16) && (ldkv * es) % 16 == 0,
               "kv_pack: layout B rows must be 16-byte aligned");
-  const unsigned g = sgl::grid_for_rows(T);
+  const unsigned g = sgl::grid_for_rows(T, sgl::kKvRows);
   if (dtype == SGL_BF16)
-    sgl::kv_pack_b_kernel<SGL_BF16><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
+    sgl::kv_pack_b_kernel<SGL_BF16, sgl::kKvRows><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
                                                        (uint8_t*)out);
   else if (dtype == SGL_F16)
-    sgl::kv_pack_b_kernel<SGL_F16><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
+    sgl::kv_pack_b_kernel<SGL_F16, sgl::kKvRows><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
                                                       (uint8_t*)out);
   else
-    sgl::kv_pack_b_kernel<SGL_F32><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
+    sgl::kv_pack_b_kernel<SGL_F32, sgl::kKvRows><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
                                                       (uint8_t*)out);
   return sgl::check_launch("kv_pack_b");
 }
@@ -346,13 +399,13 @@ int sgl_kv_gather_dequant(const void* cache, int layout, int paged, int page_siz
   SGL_REQUIRE(idx && out && (n_rows == 0 || cache), "kv_gather: null pointer");
   SGL_REQUIRE(sgl::aligned(out, 16) && sgl::aligned(cache, layout == SGL_KV_LAYOUT_B ? 16 : 8),
               "kv_gather: misaligned cache/out");
-  const unsigned g = sgl::grid_for_rows(total);
+  const unsigned g = sgl::grid_for_rows(total, sgl::kKvRows);
   hipStream_t st = (hipStream_t)stream;
   if (layout == SGL_KV_LAYOUT_A)
-    sgl::kv_gather_kernel<SGL_KV_LAYOUT_A><<<g, 256, 0, st>>>(
+    sgl::kv_gather_kernel<SGL_KV_LAYOUT_A, sgl::kKvRows><<<g, 256, 0, st>>>(
         (const uint8_t*)cache, paged, page_size, n_rows, idx, total, (uint16_t*)out);
   else
-    sgl::kv_gather_kernel<SGL_KV_LAYOUT_B><<<g, 256, 0, st>>>(
+    sgl::kv_gather_kernel<SGL_KV_LAYOUT_B, sgl::kKvRows><<<g, 256, 0, st>>>(
         (const uint8_t*)cache, 0, 1, n_rows, idx, total, (uint16_t*)out);
   return sgl::check_launch("kv_gather_dequant");
 }

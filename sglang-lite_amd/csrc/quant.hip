@@ -8,6 +8,13 @@
 #include "sgl_common.h"
 #include "sgl_numeric.h"
 
+#ifndef SGL_AQ_ROWS
+#define SGL_AQ_ROWS 1
+#endif
+#ifndef SGL_AQ_BLOCKS_PER_CU
+#define SGL_AQ_BLOCKS_PER_CU 32
+#endif
+
 namespace sgl {
 namespace {
 
@@ -27,7 +34,9 @@ __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
-template <int GROUP, bool INPLACE>
+// R groups per thread and step (group g, g + sweep, ...), loads first, so R
+// 16-byte reads per lane are in flight.
+template <int GROUP, bool INPLACE, int R>
 __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restrict__ x, int64_t M,
                                                         int64_t K, int64_t ldx, void* __restrict__ y,
                                                         int64_t ldy, void* __restrict__ s,
@@ -36,39 +45,53 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
   const int64_t gpr = K / GROUP;
   const int64_t total = M * gpr;
   const int sub = threadIdx.x % LPG;
-  const int64_t per_sweep = (int64_t)gridDim.x * blockDim.x / LPG;
-  for (int64_t g = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / LPG; g < total;
-       g += per_sweep) {
-    const int64_t row = g / gpr;
-    const int64_t col = (g - row * gpr) * GROUP + sub * 8;
-    const uint4 v = *reinterpret_cast<const uint4*>(x + row * ldx + col);
-    float f[8];
-    unpack_bf16x8(v, f);
-    float amax = 0.0f;
+  const int64_t sweep = (int64_t)gridDim.x * blockDim.x / LPG;
+  for (int64_t gb = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / LPG; gb < total;
+       gb += sweep * R) {
+    uint4 v[R];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf_(amax, fabsf(f[i]));
-    amax = group_max<LPG>(amax);
-    const float sf = group_scale(mode, amax);
-    const uint2 qv = quant8_e4m3(mode, f, sf);
-    if (INPLACE) {
-      // quant-dequant back to bf16: bf16(fp32(e4m3) * s)
-      float d[8];
-      unpack4_e4m3(qv.x, d);
-      unpack4_e4m3(qv.y, d + 4);
-      uint32_t o[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = pk2_bf16_exact(d[2 * i] * sf, d[2 * i + 1] * sf);
-      *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(y) + row * ldy + col) =
-          make_uint4(o[0], o[1], o[2], o[3]);
-    } else {
-      *reinterpret_cast<uint2*>(reinterpret_cast<uint8_t*>(y) + row * ldy + col) = qv;
+    for (int r = 0; r < R; ++r) {
+      const int64_t g = gb + r * sweep;
+      if (g < total) {
+        const int64_t row = g / gpr;
+        const int64_t col = (g - row * gpr) * GROUP + sub * 8;
+        v[r] = *reinterpret_cast<const uint4*>(x + row * ldx + col);
+      }
     }
-    if (sub == 0) {
-      const int64_t si = row * lds + col / GROUP;
-      if (scale_e8m0)
-        reinterpret_cast<uint8_t*>(s)[si] = pow2_to_e8m0(sf);
-      else
-        reinterpret_cast<float*>(s)[si] = sf;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t g = gb + r * sweep;
+      if (g >= total) break;
+      const int64_t row = g / gpr;
+      const int64_t col = (g - row * gpr) * GROUP + sub * 8;
+      float f[8];
+      unpack_bf16x8(v[r], f);
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) amax = fmaxf_(amax, fabsf(f[i]));
+      amax = group_max<LPG>(amax);
+      const float sf = group_scale(mode, amax);
+      const uint2 qv = quant8_e4m3(mode, f, sf);
+      if (INPLACE) {
+        // quant-dequant back to bf16: bf16(fp32(e4m3) * s)
+        float d[8];
+        unpack4_e4m3(qv.x, d);
+        unpack4_e4m3(qv.y, d + 4);
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = pk2_bf16_exact(d[2 * i] * sf, d[2 * i + 1] * sf);
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(y) + row * ldy + col) =
+            make_uint4(o[0], o[1], o[2], o[3]);
+      } else {
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint8_t*>(y) + row * ldy + col) = qv;
+      }
+      if (sub == 0) {
+        const int64_t si = row * lds + col / GROUP;
+        if (scale_e8m0)
+          reinterpret_cast<uint8_t*>(s)[si] = pow2_to_e8m0(sf);
+        else
+          reinterpret_cast<float*>(s)[si] = sf;
+      }
     }
   }
 }
@@ -197,16 +220,17 @@ template <int GROUP>
 int launch_act_quant(const void* x, int64_t M, int64_t K, int64_t ldx, void* y, int64_t ldy,
                      void* s, int64_t lds, int mode, int scale_e8m0, int inplace,
                      hipStream_t stream) {
+  constexpr int R = SGL_AQ_ROWS;
   const int64_t total_threads = M * (K / GROUP) * (GROUP / 8);
-  const int64_t max_blocks = (int64_t)device_cu_count() * 16;
-  int64_t blocks = ceil_div(total_threads, 256);
+  const int64_t max_blocks = (int64_t)device_cu_count() * SGL_AQ_BLOCKS_PER_CU;
+  int64_t blocks = ceil_div(total_threads, 256 * R);
   if (blocks > max_blocks) blocks = max_blocks;
   if (blocks < 1) blocks = 1;
   if (inplace)
-    act_quant_kernel<GROUP, true><<<(unsigned)blocks, 256, 0, stream>>>(
+    act_quant_kernel<GROUP, true, R><<<(unsigned)blocks, 256, 0, stream>>>(
         (const uint16_t*)x, M, K, ldx, y, ldy, s, lds, mode, scale_e8m0);
   else
-    act_quant_kernel<GROUP, false><<<(unsigned)blocks, 256, 0, stream>>>(
+    act_quant_kernel<GROUP, false, R><<<(unsigned)blocks, 256, 0, stream>>>(
         (const uint16_t*)x, M, K, ldx, y, ldy, s, lds, mode, scale_e8m0);
   return check_launch("act_quant");
 }

@@ -200,8 +200,16 @@ SGL_HD float group_scale(int mode, float amax) {
       if (!(raw < 3.0e38f)) return raw;  // Inf / NaN pass through as the scale
       // ceil of the correctly rounded fp32 log2.  For fp32 inputs just above a
       // power of two this is not the exponent+1 of the bit formula: log2 of
-      // 2^k(1+tiny) rounds to exactly k.  Rounding the double-precision log2
-      // to fp32 gives the correctly rounded value.
+      // 2^k(1+tiny) rounds to exactly k.  raw = 2^k (1 + M 2^-23) is normal
+      // here (raw >= 2^-30); M == 0 gives k, and M > 64 gives k + 1 for every
+      // |k| <= 127 (log2(1 + 65 2^-23) > 2^-17 exceeds half the fp32 spacing
+      // at any such k), so only M in [1, 64] needs the double-precision log2,
+      // whose rounding to fp32 is the correctly rounded value.
+      const uint32_t u = f32_bits(raw);
+      const int k = (int)((u >> 23) & 0xFFu) - 127;
+      const uint32_t M = u & 0x7FFFFFu;
+      if (M == 0u) return pow2_f32(k);
+      if (M > 64u) return pow2_f32(k + 1);
       float l = (float)log2((double)raw);
       return pow2_f32((int)ceilf(l));
     }

@@ -114,6 +114,36 @@ def test_kv_scale_host_matches_torch_log2_near_powers_of_two():
     np.testing.assert_array_equal(s, ref)
 
 
+def test_kv_scale_mantissa_shortcut_premise():
+    """The KV ue8m0 scale skips the double log2 when the raw scale's mantissa
+    field M is 0 (-> 2^k) or above 64 (-> 2^(k+1)).  Pin the premise: for every
+    exponent the raw scale can have, M = 65 already rounds log2 above k (the
+    smallest such M, log2 is monotone), while small M can round to exactly k."""
+    ks = np.arange(-30, 128)
+    for M, expect_up in ((65, True), (1, None)):
+        raw = (np.ldexp(1.0, ks) * (1 + M * 2.0**-23)).astype(np.float32)
+        ceil_t = torch.ceil(torch.log2(torch.from_numpy(raw))).numpy().astype(np.int64)
+        ceil_d = np.ceil(np.log2(raw.astype(np.float64)).astype(np.float32)).astype(np.int64)
+        np.testing.assert_array_equal(ceil_t, ceil_d)
+        if expect_up:
+            np.testing.assert_array_equal(ceil_t, ks + 1)
+        else:
+            assert (ceil_t == ks).any()  # the hazard the double path exists for
+    # end to end through the library on amax values whose raw scale has
+    # M in [0, 70] or near the top, over the whole exponent range
+    ms = np.concatenate([np.arange(0, 71), [2**22, 2**23 - 1]])
+    raw = (np.ldexp(1.0, ks)[:, None] * (1 + ms[None, :] * 2.0**-23)).ravel()
+    amax = np.ascontiguousarray((raw / float(Q.INV448)).astype(np.float32))
+    amax = amax[np.isfinite(amax)]
+    s = np.zeros_like(amax)
+    lib = _lib()
+    assert lib.sgl_host_group_scale(4, amax.ctypes.data_as(ctypes.c_void_p),
+                                    s.ctypes.data_as(ctypes.c_void_p), amax.size) == 0
+    rawt = torch.from_numpy(amax).clamp(min=1e-12) * (1.0 / 448.0)
+    ref = torch.exp2(torch.ceil(torch.log2(rawt.clamp(min=2**-30)))).numpy()
+    np.testing.assert_array_equal(s, ref)
+
+
 def test_invalid_arguments_map_to_value_error_without_launch():
     from sglang_lite_amd import _lib as L
 
