@@ -85,9 +85,20 @@ __device__ __forceinline__ float load_scale(const void* s, int64_t idx, int e8m0
 
 __device__ __forceinline__ int swz(int row) { return (row & 6) | ((row >> 3) & 1); }
 
-__device__ __forceinline__ v8i read_frag(const uint8_t* tile, int row, int g4) {
-  const uint4 lo = *reinterpret_cast<const uint4*>(tile + row * 128 + (((2 * g4) ^ swz(row)) << 4));
-  const uint4 hi = *reinterpret_cast<const uint4*>(tile + row * 128 + (((2 * g4 + 1) ^ swz(row)) << 4));
+// Lane l's two 16-byte chunks of a 16-row operand block: row l % 16, logical
+// chunks 2 (l / 16) and 2 (l / 16) + 1.  Blocks start at multiples of 16 rows,
+// where the swizzle repeats, so the lane's byte offsets inside any block are
+// the same two numbers; the block's own offset (row0 * 128) is a constant.
+struct FragLane {
+  uint32_t lo, hi;
+};
+__device__ __forceinline__ FragLane frag_lane(int r16, int g4) {
+  return FragLane{(uint32_t)(r16 * 128 + (((2 * g4) ^ swz(r16)) << 4)),
+                  (uint32_t)(r16 * 128 + (((2 * g4 + 1) ^ swz(r16)) << 4))};
+}
+__device__ __forceinline__ v8i read_frag(const uint8_t* block, FragLane fl) {
+  const uint4 lo = *reinterpret_cast<const uint4*>(block + fl.lo);
+  const uint4 hi = *reinterpret_cast<const uint4*>(block + fl.hi);
   return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 }
 
@@ -102,16 +113,19 @@ struct Cfg {
   static constexpr int A_BYTES = BM * 128;
   static constexpr int B_BYTES = BN * 128;
   static constexpr int SA_ROWS = BM / NW;  // row scales each wavefront loads per stage
-  static constexpr int STAGE = A_BYTES + B_BYTES + NW * 256;
+  static constexpr int STAGE = A_BYTES + B_BYTES;  // one K block of A and B rows
+  static constexpr int SA_SLOT = NW * 256;           // one K block of row scales
   static constexpr int CHUNKS = (BM + BN) / 8;  // 1 KB DMA chunks per stage
   static constexpr int CPW = CHUNKS / NW;       // per wavefront
   static constexpr int LPS = CPW + 1;           // DMA instructions per wavefront per stage
-  static constexpr int SMEM = NSTAGE * STAGE;
+  static constexpr int NSA = NSTAGE;  // row-scale slots (a ring of their own)
+  static constexpr int RING = NSTAGE * STAGE;
+  static constexpr int SMEM = RING + NSA * SA_SLOT;
   static_assert(CHUNKS % NW == 0, "chunks must split evenly over wavefronts");
   static_assert(SA_ROWS >= 1 && SA_ROWS <= 64, "row scales per wavefront");
   static_assert(TM >= 1 && TN >= 1, "tile too small");
   static_assert(KIND != KIND_GATE_UP || (TN % 2 == 0 && HALF == 128), "gate_up needs 128 h columns");
-  static_assert(KIND == KIND_GATE_UP ? BM * HALF * 2 <= SMEM : BM * BN * 4 <= SMEM,
+  static_assert(KIND == KIND_GATE_UP ? BM * HALF * 2 <= RING : BM * BN * 4 <= RING,
                 "epilogue staging must fit in the stage ring");
   static_assert(NSTAGE >= 2 && NSTAGE <= 4, "stages");
 };
@@ -133,6 +147,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int g4 = lane >> 4, r16 = lane & 15;
+  const FragLane fl = frag_lane(r16, g4);
   const int64_t K = args.K, N = args.N;
   const int KB = (int)(K / 128);
   const int n_tiles = args.n_tiles;
@@ -316,17 +331,29 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
     const uint8_t* sa_base = uniform_ptr(args.sa);
     const uint32_t smem_lds = __builtin_amdgcn_readfirstlane(lds_u32(smem));
 
-    auto issue = [&](int kb) {
-      const uint32_t st = smem_lds + (uint32_t)((kb % NSTAGE) * C::STAGE);
+    // DMA K block kb into operand slot `slot` and row-scale slot `sa_slot`
+    // (defaults: the block's own slots kb % NSTAGE, kb % NSA)
+    auto issue = [&](int kb, int slot = -1, int sa_slot = -1) {
+      if (slot < 0) slot = kb % NSTAGE;
+      if (sa_slot < 0) sa_slot = kb % C::NSA;
+      const uint32_t st = smem_lds + (uint32_t)(slot * C::STAGE);
 #pragma unroll
       for (int j = 0; j < C::CPW; ++j) {
         const int c = wave + j * NW;
-        const bool isA = c < BM / 8;
-        const bool up_half = KIND == KIND_GATE_UP && !isA && (c - BM / 8) * 8 >= HALF;
+        bool isA, up_half;
+        if constexpr ((BM / 8) % NW == 0 && (HALF / 8) % NW == 0) {
+          // chunk j of every wavefront is of the same kind: decided at compile time
+          isA = j < (BM / 8) / NW;
+          up_half = KIND == KIND_GATE_UP && j >= (BM / 8 + HALF / 8) / NW;
+        } else {
+          isA = c < BM / 8;
+          up_half = KIND == KIND_GATE_UP && !isA && (c - BM / 8) * 8 >= HALF;
+        }
         const uint8_t* base = isA ? baseA : (up_half ? b1 : b0);
         dma16(base, voff[j] + (uint32_t)kb * 128u, st + (uint32_t)c * 1024u);
       }
-      dma4(sa_base, sa_off + (uint32_t)kb * 4u, st + C::A_BYTES + C::B_BYTES + wave * 256);
+      dma4(sa_base, sa_off + (uint32_t)kb * 4u,
+           smem_lds + (uint32_t)(C::RING + sa_slot * C::SA_SLOT + wave * 256));
     };
 
     v4f acc[TM][TN];
@@ -359,7 +386,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
       const uint8_t* stg = smem + (kb % NSTAGE) * C::STAGE;
       const uint8_t* tA = stg;
       const uint8_t* tB = stg + C::A_BYTES;
-      const float* tS = reinterpret_cast<const float*>(stg + C::A_BYTES + C::B_BYTES);
+      const float* tS = reinterpret_cast<const float*>(smem + C::RING + (kb % C::NSA) * C::SA_SLOT);
       const float sbv0 = sSb[wave_blk][kb];
       const float sbv1 = KIND == KIND_GATE_UP ? sSb[1][kb] : 0.0f;
 
@@ -370,7 +397,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
 #pragma unroll
         for (int mi = 0; mi < TM; ++mi) {
           const int rbase = (wm * TM + mi) * 16;
-          af[mi] = read_frag(tA, rbase + r16, g4);
+          af[mi] = read_frag(tA + rbase * 128, fl);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int row = rbase + 4 * g4 + r;
@@ -383,10 +410,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
         // in front of a dependent instruction
         v8i bf[2];
         v4f pr[2][TM];
-        bf[0] = read_frag(tB, tile_col(0) + r16, g4);
+        bf[0] = read_frag(tB + tile_col(0) * 128, fl);
 #pragma unroll
         for (int nj = 0; nj < TN; ++nj) {
-          if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB, tile_col(nj + 1) + r16, g4);
+          if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + tile_col(nj + 1) * 128, fl);
 #pragma unroll
           for (int mi = 0; mi < TM; ++mi)
             pr[nj & 1][mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
