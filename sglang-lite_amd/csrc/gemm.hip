@@ -542,15 +542,163 @@ int launch_cfg(GemmArgs& a, hipStream_t stream) {
   }
   const int64_t tiles = mt_bound * a.n_tiles;
   if (tiles == 0) return SGL_OK;
-  // persistent: one workgroup per CU (the LDS ring holds one per CU), a
-  // multiple of 8 so every XCD gets the same number of workgroups
-  int64_t wgs = device_cu_count();
+  // persistent: as many workgroups per CU as their LDS allows (the 160 KB
+  // of a CU), a multiple of 8 so every XCD gets the same number
+  using C = Cfg<KIND, BM, BN, WM, WN, NSTAGE>;
+  constexpr int kLdsPerCU = 160 * 1024;
+  constexpr int kExtra = (KIND == KIND_DENSE ? 4 : 4 * (kMaxGroups + 1)) + BM * 12 + 2 * kMaxKB * 4;
+  constexpr int per_cu = kLdsPerCU / (C::SMEM + kExtra) >= 2 ? 2 : 1;
+  int64_t wgs = (int64_t)device_cu_count() * per_cu;
   wgs = (wgs + 7) / 8 * 8;
   const int64_t need = (tiles + 7) / 8 * 8;
   if (need < wgs) wgs = need;
   a.m_tiles = (int)mt_bound;
   gemm_fp8_kernel<KIND, BM, BN, WM, WN, NSTAGE><<<(unsigned)wgs, 64 * WM * WN, 0, stream>>>(a);
   return check_launch("gemm_fp8");
+}
+
+// ---------------------------------------------------------------- skinny
+// Dense GEMM for small M (M <= 256): one workgroup per 16-column slab of B
+// and (16 TM)-row tile of A, split over K inside the workgroup.  Wavefront w
+// of the W (16, or 8 for the 64-row tile) takes K blocks w, w + W, ...; every lane loads its MFMA
+// operands straight from global memory (row l % 16, bytes [32 (l/16), +32) of
+// the block: two 16-byte loads per operand) one block ahead, promotes each
+// block partial with the row and weight scales staged in LDS, and the 16
+// partial tiles are summed through LDS at the end.  B, the weight stream, is
+// read once (per row tile); the grid holds N/16 x ceil(M / 16 TM) workgroups,
+// enough to keep every CU streaming where the 128 x 256 tiles leave most idle.
+#ifndef SGL_SKINNY_MAX_M
+#define SGL_SKINNY_MAX_M 64
+#endif
+// dense GEMMs up to this M take the skinny kernel (measured crossover with
+// the 64 x 128 tiles)
+constexpr int64_t kSkinnyMaxM = SGL_SKINNY_MAX_M;
+template <int TM>
+struct Skinny {
+  static constexpr int WAVES = TM >= 4 ? 8 : 16;  // 64-row tiles need the 256-VGPR budget
+};
+
+__device__ __forceinline__ v8i load_frag_global(const uint8_t* p) {
+  const uint4 lo = *reinterpret_cast<const uint4*>(p);
+  const uint4 hi = *reinterpret_cast<const uint4*>(p + 16);
+  return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+}
+
+template <int TM>
+__global__ __launch_bounds__(64 * Skinny<TM>::WAVES) void gemm_skinny_kernel(const GemmArgs args) {
+  constexpr int ROWS = 16 * TM;
+  constexpr int kSkinnyWaves = Skinny<TM>::WAVES;
+  __shared__ float sSa[ROWS][kMaxKB];
+  __shared__ float sSk[kMaxKB];
+  __shared__ float sRed[kSkinnyWaves][ROWS * 16];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g4 = lane >> 4, r16 = lane & 15;
+  const int64_t M = args.M, N = args.N, K = args.K;
+  const int KB = (int)(K / 128);
+  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const int64_t m0 = (int64_t)blockIdx.y * ROWS;
+
+  // operand rows of this lane (rows past M re-read row M-1; their outputs are dropped)
+  const uint8_t* arow[TM];
+#pragma unroll
+  for (int mi = 0; mi < TM; ++mi) {
+    int64_t row = m0 + 16 * mi + r16;
+    if (row > M - 1) row = M - 1;
+    arow[mi] = args.a + row * K + 32 * g4;
+  }
+  const uint8_t* brow = args.b + (n0 + r16) * K + 32 * g4;
+
+  // Scale loads are issued first and the first NB operand blocks right
+  // after, so waiting for the scales (to stage them in LDS) leaves the
+  // operand loads in flight: loads retire in issue order.
+  constexpr int SPT = (ROWS * kMaxKB + 64 * kSkinnyWaves - 1) / (64 * kSkinnyWaves);
+  const float* sa = reinterpret_cast<const float*>(args.sa);
+  float sv[SPT];
+#pragma unroll
+  for (int j = 0; j < SPT; ++j) {
+    const int i = tid + j * 64 * kSkinnyWaves;
+    const int r = i / KB, kb = i - r * KB;
+    const int64_t row = m0 + r;
+    sv[j] = (i < ROWS * KB && row < M) ? sa[row * KB + kb] : 0.0f;
+  }
+  float skv = 0.0f;
+  if (tid < KB) skv = load_scale(args.sb, (n0 / 128) * KB + tid, args.sb_e8m0);
+
+  constexpr int NB = 4;  // K blocks per wavefront whose loads are in flight together
+  v8i af[NB][TM], bf[NB];
+  auto load_chunk = [&](int base) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int kb = base + j * kSkinnyWaves;
+      if (kb < KB) {
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi) af[j][mi] = load_frag_global(arow[mi] + (int64_t)kb * 128);
+        bf[j] = load_frag_global(brow + (int64_t)kb * 128);
+      }
+    }
+  };
+  load_chunk(wave);
+
+#pragma unroll
+  for (int j = 0; j < SPT; ++j) {
+    const int i = tid + j * 64 * kSkinnyWaves;
+    if (i < ROWS * KB) sSa[i / KB][i - (i / KB) * KB] = sv[j];
+  }
+  if (tid < KB) sSk[tid] = skv;
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+
+  v4f acc[TM];
+#pragma unroll
+  for (int mi = 0; mi < TM; ++mi) acc[mi] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  const v4f vzero = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int base = wave; base < KB; base += NB * kSkinnyWaves) {
+    if (base != wave) load_chunk(base);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int kb = base + j * kSkinnyWaves;
+      if (kb < KB) {
+        const float sk = sSk[kb];
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi) {
+          const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[j][mi], bf[j], vzero, 0,
+                                                                         0, 0, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[mi][r] = fmaf(p[r], sSa[16 * mi + 4 * g4 + r][kb] * sk, acc[mi][r]);
+        }
+      }
+    }
+  }
+
+  // sum the 16 partial tiles; lane (g4, r16) holds rows 4 g4 + r, column r16
+#pragma unroll
+  for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sRed[wave][(16 * mi + 4 * g4 + r) * 16 + r16] = acc[mi][r];
+  __syncthreads();
+  for (int i = tid; i < ROWS * 16; i += 64 * kSkinnyWaves) {
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kSkinnyWaves; ++w) v += sRed[w][i];
+    const int64_t row = m0 + i / 16;
+    const int64_t col = n0 + (i & 15);
+    if (row < M) {
+      if (args.out_f32)
+        reinterpret_cast<float*>(args.c)[row * N + col] = v;
+      else
+        reinterpret_cast<uint16_t*>(args.c)[row * N + col] = bf16_bits_exact(v);
+    }
+  }
+}
+
+template <int TM>
+int launch_skinny(GemmArgs& a, hipStream_t stream) {
+  dim3 grid((unsigned)(a.N / 16), (unsigned)ceil_div(a.M, (int64_t)(16 * TM)));
+  gemm_skinny_kernel<TM><<<grid, 64 * Skinny<TM>::WAVES, 0, stream>>>(a);
+  return check_launch("gemm_fp8_skinny");
 }
 
 }  // namespace
@@ -563,8 +711,15 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
   const bool big = rows_hint >= 64;
   switch (kind) {
     case KIND_DENSE:
-      return big ? launch_cfg<KIND_DENSE, 128, 256, 2, 4, 3>(a, stream)
-                 : launch_cfg<KIND_DENSE, 32, 256, 1, 4, 4>(a, stream);
+      if (a.M <= kSkinnyMaxM) {
+        if (a.M <= 16) return launch_skinny<1>(a, stream);
+        if (a.M <= 32) return launch_skinny<2>(a, stream);
+        return launch_skinny<4>(a, stream);
+      }
+      // 128 x 256 tiles from M = 2048 up; below, 64 x 128 tiles (two
+      // workgroups per CU) so the grid still covers every CU
+      if (a.M <= 2048) return launch_cfg<KIND_DENSE, 64, 128, 2, 2, 3>(a, stream);
+      return launch_cfg<KIND_DENSE, 128, 256, 2, 4, 3>(a, stream);
     case KIND_GATE_UP:
       return big ? launch_cfg<KIND_GATE_UP, 128, 256, 2, 4, 3>(a, stream)
                  : launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 4>(a, stream);
