@@ -119,60 +119,22 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
 
 // -------------------------------------------------------------- permute
 
-// One workgroup.  Pass 1 histograms the ids in LDS; an exclusive scan gives
-// the expert offsets.  Pass 2 walks the slots in order, 1024 per round: inside
-// a wavefront the lanes holding the same expert find each other with one
-// ballot per id bit (their rank = popcount of lower peers), per-wavefront
-// counts in LDS give the offset of each wavefront inside the round, and a
-// per-expert running base carries rounds forward, so equal ids keep slot order.
-__global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* __restrict__ ids,
-                                                               int64_t P, int E,
-                                                               int32_t* __restrict__ counts,
-                                                               int32_t* __restrict__ offsets,
-                                                               int32_t* __restrict__ sorted_slot,
-                                                               int32_t* __restrict__ slot_pos) {
-  __shared__ int cnt[kMaxPermE];
-  __shared__ int run[kMaxPermE];
-  __shared__ int wcnt[kPermWaves][kMaxPermE];
-  __shared__ int wsum[kPermWaves];
+// Slot ranking shared by both permute forms: walk slots [lo, hi) in order,
+// kPermThreads per round.  Inside a wavefront the lanes holding the same
+// expert find each other with one ballot per id bit (their rank = popcount of
+// lower peers), per-wavefront counts in LDS give the offset of each wavefront
+// inside the round, and run[e] (the next free position of expert e) carries
+// rounds forward, so equal ids keep slot order.  Writes slot_pos, and
+// sorted_slot when it is non-null.
+__device__ void rank_slots(const int32_t* __restrict__ ids, int64_t lo, int64_t hi, int E,
+                           int* run, int (*wcnt)[kMaxPermE], int32_t* __restrict__ sorted_slot,
+                           int32_t* __restrict__ slot_pos) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int e = tid; e < E; e += kPermThreads) {
-    cnt[e] = 0;
-    for (int w = 0; w < kPermWaves; ++w) wcnt[w][e] = 0;
-  }
-  __syncthreads();
-  for (int64_t i = tid; i < P; i += kPermThreads) {
-    const int e = ids[i];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
-  }
-  __syncthreads();
-  // exclusive scan of cnt[0..E) (E <= 1024: one value per thread)
-  {
-    const int v = tid < E ? cnt[tid] : 0;
-    int incl = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int u = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += u;
-    }
-    if (lane == 63) wsum[wave] = incl;
-    __syncthreads();
-    int base = 0;
-    for (int w = 0; w < wave; ++w) base += wsum[w];
-    const int excl = base + incl - v;
-    if (tid < E) {
-      run[tid] = excl;
-      counts[tid] = v;
-      offsets[tid] = excl;
-    }
-    if (tid == E - 1) offsets[E] = excl + v;
-  }
-  __syncthreads();
   const int nbits = E > 1 ? 32 - __clz(E - 1) : 0;
   const unsigned long long lt_mask = (1ull << lane) - 1ull;
-  for (int64_t base = 0; base < P; base += kPermThreads) {
+  for (int64_t base = lo; base < hi; base += kPermThreads) {
     const int64_t i = base + tid;
-    const int e = i < P ? ids[i] : -1;
+    const int e = i < hi ? ids[i] : -1;
     const bool valid = e >= 0 && e < E;
     unsigned long long peers = __ballot(valid);
     for (int b = 0; b < nbits; ++b) {
@@ -187,21 +149,152 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* __
       int pre = 0;
       for (int w = 0; w < wave; ++w) pre += wcnt[w][e];
       const int pos = run[e] + pre + rank;
-      sorted_slot[pos] = (int32_t)i;
+      if (sorted_slot) sorted_slot[pos] = (int32_t)i;
       slot_pos[i] = pos;
-    } else if (i < P) {
+    } else if (i < hi) {
       slot_pos[i] = -1;
     }
     __syncthreads();
     for (int x = tid; x < E; x += kPermThreads) {
-      int s = 0;
+      int sum = 0;
       for (int w = 0; w < kPermWaves; ++w) {
-        s += wcnt[w][x];
+        sum += wcnt[w][x];
         wcnt[w][x] = 0;
       }
-      run[x] += s;
+      run[x] += sum;
     }
     __syncthreads();
+  }
+}
+
+// Exclusive scan of v over threads 0..E-1 of a kPermThreads workgroup (E <=
+// 1024: one value per thread); returns the thread's exclusive prefix.
+__device__ int block_exclusive_scan(int v, int* wsum) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += u;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += wsum[w];
+  return base + incl - v;
+}
+
+// Small inputs: one workgroup.  Pass 1 histograms the ids in LDS, an
+// exclusive scan gives the expert offsets, pass 2 ranks every slot.
+__global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* __restrict__ ids,
+                                                               int64_t P, int E,
+                                                               int32_t* __restrict__ counts,
+                                                               int32_t* __restrict__ offsets,
+                                                               int32_t* __restrict__ sorted_slot,
+                                                               int32_t* __restrict__ slot_pos) {
+  __shared__ int cnt[kMaxPermE];
+  __shared__ int run[kMaxPermE];
+  __shared__ int wcnt[kPermWaves][kMaxPermE];
+  __shared__ int wsum[kPermWaves];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += kPermThreads) {
+    cnt[e] = 0;
+    for (int w = 0; w < kPermWaves; ++w) wcnt[w][e] = 0;
+  }
+  __syncthreads();
+  for (int64_t i = tid; i < P; i += kPermThreads) {
+    const int e = ids[i];
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  {
+    const int v = tid < E ? cnt[tid] : 0;
+    const int excl = block_exclusive_scan(v, wsum);
+    if (tid < E) {
+      run[tid] = excl;
+      counts[tid] = v;
+      offsets[tid] = excl;
+    }
+    if (tid == E - 1) offsets[E] = excl + v;
+  }
+  __syncthreads();
+  rank_slots(ids, 0, P, E, run, wcnt, sorted_slot, slot_pos);
+}
+
+// Large inputs: chunks of kPermChunk slots, one workgroup each, in four
+// launches.  The per-chunk tables live in the outputs before the outputs are
+// final: (1) chunk histograms -> slot_pos[c*E + e]; (2) one workgroup sums
+// them into counts / offsets and writes each chunk's start position per
+// expert -> sorted_slot[c*E + e]; (3) each chunk ranks its slots from those
+// starts and writes slot_pos; (4) sorted_slot[slot_pos[i]] = i.  Needs
+// chunks * E <= P (checked by the caller).
+constexpr int kPermChunk = 4096;
+
+__global__ __launch_bounds__(kPermThreads) void permute_hist_kernel(const int32_t* __restrict__ ids,
+                                                                    int64_t P, int E,
+                                                                    int32_t* __restrict__ hist) {
+  __shared__ int cnt[kMaxPermE];
+  const int tid = threadIdx.x;
+  const int64_t lo = (int64_t)blockIdx.x * kPermChunk;
+  const int64_t hi = lo + kPermChunk < P ? lo + kPermChunk : P;
+  for (int e = tid; e < E; e += kPermThreads) cnt[e] = 0;
+  __syncthreads();
+  for (int64_t i = lo + tid; i < hi; i += kPermThreads) {
+    const int e = ids[i];
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += kPermThreads) hist[(int64_t)blockIdx.x * E + e] = cnt[e];
+}
+
+__global__ __launch_bounds__(kPermThreads) void permute_scan_kernel(const int32_t* __restrict__ hist,
+                                                                    int nchunks, int E,
+                                                                    int32_t* __restrict__ counts,
+                                                                    int32_t* __restrict__ offsets,
+                                                                    int32_t* __restrict__ starts) {
+  __shared__ int wsum[kPermWaves];
+  const int tid = threadIdx.x;
+  int v = 0;
+  if (tid < E)
+    for (int c = 0; c < nchunks; ++c) v += hist[(int64_t)c * E + tid];
+  const int excl = block_exclusive_scan(v, wsum);
+  if (tid < E) {
+    counts[tid] = v;
+    offsets[tid] = excl;
+    int run = excl;
+    for (int c = 0; c < nchunks; ++c) {
+      const int h = hist[(int64_t)c * E + tid];
+      starts[(int64_t)c * E + tid] = run;
+      run += h;
+    }
+  }
+  if (tid == E - 1) offsets[E] = excl + v;
+}
+
+__global__ __launch_bounds__(kPermThreads) void permute_rank_kernel(const int32_t* __restrict__ ids,
+                                                                    int64_t P, int E,
+                                                                    const int32_t* __restrict__ starts,
+                                                                    int32_t* __restrict__ slot_pos) {
+  __shared__ int run[kMaxPermE];
+  __shared__ int wcnt[kPermWaves][kMaxPermE];
+  const int tid = threadIdx.x;
+  const int64_t lo = (int64_t)blockIdx.x * kPermChunk;
+  const int64_t hi = lo + kPermChunk < P ? lo + kPermChunk : P;
+  for (int e = tid; e < E; e += kPermThreads) {
+    run[e] = starts[(int64_t)blockIdx.x * E + e];
+    for (int w = 0; w < kPermWaves; ++w) wcnt[w][e] = 0;
+  }
+  __syncthreads();
+  rank_slots(ids, lo, hi, E, run, wcnt, nullptr, slot_pos);
+}
+
+__global__ __launch_bounds__(256) void permute_scatter_kernel(const int32_t* __restrict__ slot_pos,
+                                                              int64_t P,
+                                                              int32_t* __restrict__ sorted_slot) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < P;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int32_t p = slot_pos[i];
+    if (p >= 0) sorted_slot[p] = (int32_t)i;
   }
 }
 
@@ -356,8 +449,22 @@ int sgl_moe_permute(const int32_t* ids, int64_t T, int k, int E, int32_t* counts
   SGL_REQUIRE(T * k < 0x7FFFFFFF, "moe_permute: T*k too large");
   SGL_REQUIRE(counts && offsets && (T == 0 || (ids && sorted_slot && slot_pos)),
               "moe_permute: null pointer");
-  sgl::permute_kernel<<<1, sgl::kPermThreads, 0, (hipStream_t)stream>>>(
-      ids, T * k, E, counts, offsets, sorted_slot, slot_pos);
+  const int64_t P = T * k;
+  const int64_t chunks = sgl::ceil_div(P, (int64_t)sgl::kPermChunk);
+  hipStream_t st = (hipStream_t)stream;
+  if (P < 4 * sgl::kPermChunk || chunks * E > P) {
+    sgl::permute_kernel<<<1, sgl::kPermThreads, 0, st>>>(ids, P, E, counts, offsets, sorted_slot,
+                                                         slot_pos);
+    return sgl::check_launch("moe_permute");
+  }
+  sgl::permute_hist_kernel<<<(unsigned)chunks, sgl::kPermThreads, 0, st>>>(ids, P, E, slot_pos);
+  sgl::permute_scan_kernel<<<1, sgl::kPermThreads, 0, st>>>(slot_pos, (int)chunks, E, counts,
+                                                            offsets, sorted_slot);
+  sgl::permute_rank_kernel<<<(unsigned)chunks, sgl::kPermThreads, 0, st>>>(ids, P, E, sorted_slot,
+                                                                           slot_pos);
+  int64_t sblocks = sgl::ceil_div(P, (int64_t)256);
+  if (sblocks > 4096) sblocks = 4096;
+  sgl::permute_scatter_kernel<<<(unsigned)sblocks, 256, 0, st>>>(slot_pos, P, sorted_slot);
   return sgl::check_launch("moe_permute");
 }
 

@@ -84,7 +84,9 @@ def test_route_topk_matches_torch_topk(gpu):
 
 @pytest.mark.parametrize("T,k,E,kind", [(1, 1, 1, "uniform"), (64, 8, 256, "zipf"),
                                         (512, 8, 256, "zipf"), (8192, 8, 256, "uniform"),
-                                        (1000, 6, 1024, "uniform"), (333, 2, 8, "one")])
+                                        (1000, 6, 1024, "uniform"), (333, 2, 8, "one"),
+                                        (4096, 8, 256, "zipf"), (2500, 8, 1024, "uniform"),
+                                        (16384, 8, 256, "one"), (2049, 8, 16, "uniform")])
 def test_permute_bit_exact(gpu, T, k, E, kind):
     from sglang_lite_amd import moe as M
 
