@@ -191,7 +191,22 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
   const int t_begin = xcd * per;
   const int t_end = min(t_begin + per, total);
 
-  for (int L = t_begin + slot; L < t_end; L += per_xcd) {
+  // Static order: slot s of an XCD takes tiles s, s + per_xcd, ...  With
+  // tile counters the workgroups of an XCD take the next tile when they
+  // finish one, so tiles that are adjacent in the order (the M tiles sharing
+  // a weight slice) start together even when tile costs differ.
+  __shared__ int sNext;
+  for (int iter = 0;; ++iter) {
+    int local;
+    if (args.tile_ctr) {
+      if (tid == 0) sNext = atomicAdd(&args.tile_ctr[xcd], 1);
+      __syncthreads();
+      local = __builtin_amdgcn_readfirstlane(sNext);
+    } else {
+      local = slot + iter * per_xcd;
+    }
+    const int L = t_begin + local;
+    if (L >= t_end) break;
     // ---- resolve the tile: group g, its M tile mt, N tile nt (M tiles adjacent)
     int e = 0, row0, rows, nt;
     if constexpr (KIND == KIND_DENSE) {

@@ -191,12 +191,14 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* __
                                                                int32_t* __restrict__ counts,
                                                                int32_t* __restrict__ offsets,
                                                                int32_t* __restrict__ sorted_slot,
-                                                               int32_t* __restrict__ slot_pos) {
+                                                               int32_t* __restrict__ slot_pos,
+                                                               int32_t* __restrict__ zero, int nzero) {
   __shared__ int cnt[kMaxPermE];
   __shared__ int run[kMaxPermE];
   __shared__ int wcnt[kPermWaves][kMaxPermE];
   __shared__ int wsum[kPermWaves];
   const int tid = threadIdx.x;
+  if (zero && tid < nzero) zero[tid] = 0;
   for (int e = tid; e < E; e += kPermThreads) {
     cnt[e] = 0;
     for (int w = 0; w < kPermWaves; ++w) wcnt[w][e] = 0;
@@ -251,9 +253,12 @@ __global__ __launch_bounds__(kPermThreads) void permute_scan_kernel(const int32_
                                                                     int nchunks, int E,
                                                                     int32_t* __restrict__ counts,
                                                                     int32_t* __restrict__ offsets,
-                                                                    int32_t* __restrict__ starts) {
+                                                                    int32_t* __restrict__ starts,
+                                                                    int32_t* __restrict__ zero,
+                                                                    int nzero) {
   __shared__ int wsum[kPermWaves];
   const int tid = threadIdx.x;
+  if (zero && tid < nzero) zero[tid] = 0;
   int v = 0;
   if (tid < E)
     for (int c = 0; c < nchunks; ++c) v += hist[(int64_t)c * E + tid];
@@ -370,6 +375,7 @@ struct MoeWorkspace {
   uint8_t* hq;
   float* hs;
   uint16_t* out;
+  int32_t* tile_ctr;  // [2][8] per-XCD tile counters of the gate/up and down GEMMs
   size_t bytes;
 };
 
@@ -393,6 +399,7 @@ MoeWorkspace carve(void* base, int64_t T, int64_t H, int64_t I, int E, int k, in
   w.hq = take(rows * I);
   w.hs = reinterpret_cast<float*>(take(rows * (I / 128) * 4));
   w.out = reinterpret_cast<uint16_t*>(take(T * (k + has_shared) * H * 2));
+  w.tile_ctr = reinterpret_cast<int32_t*>(take(16 * 4));
   w.bytes = (size_t)off;
   return w;
 }
@@ -406,6 +413,93 @@ int check_moe_shapes(const char* what, int64_t T, int64_t H, int64_t I, int E, i
   SGL_REQUIRE(T * k < 0x7FFFFFFF && T * (k + 1) * H < ((int64_t)1 << 46), "%s: too many tokens",
               what);
   return SGL_OK;
+}
+
+// Also zeroes zero[0, nzero) (nzero <= 1024) on the way, for the caller's
+// tile counters.
+int launch_permute(const int32_t* ids, int64_t T, int k, int E, int32_t* counts, int32_t* offsets,
+                   int32_t* sorted_slot, int32_t* slot_pos, int32_t* zero, int nzero,
+                   hipStream_t st) {
+  SGL_REQUIRE(T >= 0 && k >= 1, "moe_permute: bad T=%lld k=%d", (long long)T, k);
+  SGL_REQUIRE(E >= 1 && E <= kMaxPermE, "moe_permute: E=%d not in [1, %d]", E,
+              kMaxPermE);
+  SGL_REQUIRE(T * k < 0x7FFFFFFF, "moe_permute: T*k too large");
+  SGL_REQUIRE(counts && offsets && (T == 0 || (ids && sorted_slot && slot_pos)),
+              "moe_permute: null pointer");
+  const int64_t P = T * k;
+  const int64_t chunks = ceil_div(P, (int64_t)kPermChunk);
+  if (P < 4 * kPermChunk || chunks * E > P) {
+    permute_kernel<<<1, kPermThreads, 0, st>>>(ids, P, E, counts, offsets, sorted_slot, slot_pos,
+                                               zero, nzero);
+    return check_launch("moe_permute");
+  }
+  permute_hist_kernel<<<(unsigned)chunks, kPermThreads, 0, st>>>(ids, P, E, slot_pos);
+  permute_scan_kernel<<<1, kPermThreads, 0, st>>>(slot_pos, (int)chunks, E, counts, offsets,
+                                                       sorted_slot, zero, nzero);
+  permute_rank_kernel<<<(unsigned)chunks, kPermThreads, 0, st>>>(ids, P, E, sorted_slot,
+                                                                           slot_pos);
+  int64_t sblocks = ceil_div(P, (int64_t)256);
+  if (sblocks > 4096) sblocks = 4096;
+  permute_scatter_kernel<<<(unsigned)sblocks, 256, 0, st>>>(slot_pos, P, sorted_slot);
+  return check_launch("moe_permute");
+}
+
+int run_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I, int E, int k,
+                    const int32_t* offsets, const int32_t* sorted_slot, const float* route_w,
+                    const sgl_expert_ptrs* experts, int has_shared, float swiglu_limit,
+                    int scale_mode, void* hq, float* hs, int* tile_ctr, hipStream_t stream) {
+  int rc = check_moe_shapes("moe_gate_up", T, H, I, E, k);
+  if (rc) return rc;
+  SGL_REQUIRE(scale_mode >= 0 && scale_mode <= 3, "moe_gate_up: bad scale_mode %d", scale_mode);
+  if (T == 0) return SGL_OK;
+  SGL_REQUIRE(xq && xs && offsets && sorted_slot && experts && hq && hs,
+              "moe_gate_up: null pointer");
+  SGL_REQUIRE(aligned(xq, 16) && aligned(hq, 8), "moe_gate_up: xq/hq misaligned");
+  GemmArgs g = {};
+  g.a = (const uint8_t*)xq;
+  g.sa = xs;
+  g.experts = experts;
+  g.offsets = offsets;
+  g.sorted_slot = sorted_slot;
+  g.route_w = route_w;
+  g.E = E;
+  g.k = k;
+  g.has_shared = has_shared ? 1 : 0;
+  g.T = T;
+  g.N = I;
+  g.K = H;
+  g.hq = (uint8_t*)hq;
+  g.hs = hs;
+  g.swiglu_limit = swiglu_limit;
+  g.scale_mode = scale_mode;
+  g.tile_ctr = tile_ctr;
+  return launch_gemm(KIND_GATE_UP, g, T * k / E, stream);
+}
+
+int run_down(const void* hq, const float* hs, int64_t T, int64_t H, int64_t I, int E, int k,
+                 const int32_t* offsets, const int32_t* sorted_slot,
+                 const sgl_expert_ptrs* experts, int has_shared, void* out, int* tile_ctr,
+             hipStream_t stream) {
+  int rc = check_moe_shapes("moe_down", T, H, I, E, k);
+  if (rc) return rc;
+  if (T == 0) return SGL_OK;
+  SGL_REQUIRE(hq && hs && offsets && sorted_slot && experts && out, "moe_down: null pointer");
+  SGL_REQUIRE(aligned(hq, 16), "moe_down: hq misaligned");
+  GemmArgs g = {};
+  g.a = (const uint8_t*)hq;
+  g.sa = hs;
+  g.experts = experts;
+  g.offsets = offsets;
+  g.sorted_slot = sorted_slot;
+  g.E = E;
+  g.k = k;
+  g.has_shared = has_shared ? 1 : 0;
+  g.T = T;
+  g.N = H;
+  g.K = I;
+  g.c = out;
+  g.tile_ctr = tile_ctr;
+  return launch_gemm(KIND_DOWN, g, T * k / E, stream);
 }
 
 }  // namespace
@@ -443,84 +537,23 @@ int sgl_moe_route_topk(const float* logits, int64_t T, int E, int k, int score_f
 
 int sgl_moe_permute(const int32_t* ids, int64_t T, int k, int E, int32_t* counts, int32_t* offsets,
                     int32_t* sorted_slot, int32_t* slot_pos, sgl_stream_t stream) {
-  SGL_REQUIRE(T >= 0 && k >= 1, "moe_permute: bad T=%lld k=%d", (long long)T, k);
-  SGL_REQUIRE(E >= 1 && E <= sgl::kMaxPermE, "moe_permute: E=%d not in [1, %d]", E,
-              sgl::kMaxPermE);
-  SGL_REQUIRE(T * k < 0x7FFFFFFF, "moe_permute: T*k too large");
-  SGL_REQUIRE(counts && offsets && (T == 0 || (ids && sorted_slot && slot_pos)),
-              "moe_permute: null pointer");
-  const int64_t P = T * k;
-  const int64_t chunks = sgl::ceil_div(P, (int64_t)sgl::kPermChunk);
-  hipStream_t st = (hipStream_t)stream;
-  if (P < 4 * sgl::kPermChunk || chunks * E > P) {
-    sgl::permute_kernel<<<1, sgl::kPermThreads, 0, st>>>(ids, P, E, counts, offsets, sorted_slot,
-                                                         slot_pos);
-    return sgl::check_launch("moe_permute");
-  }
-  sgl::permute_hist_kernel<<<(unsigned)chunks, sgl::kPermThreads, 0, st>>>(ids, P, E, slot_pos);
-  sgl::permute_scan_kernel<<<1, sgl::kPermThreads, 0, st>>>(slot_pos, (int)chunks, E, counts,
-                                                            offsets, sorted_slot);
-  sgl::permute_rank_kernel<<<(unsigned)chunks, sgl::kPermThreads, 0, st>>>(ids, P, E, sorted_slot,
-                                                                           slot_pos);
-  int64_t sblocks = sgl::ceil_div(P, (int64_t)256);
-  if (sblocks > 4096) sblocks = 4096;
-  sgl::permute_scatter_kernel<<<(unsigned)sblocks, 256, 0, st>>>(slot_pos, P, sorted_slot);
-  return sgl::check_launch("moe_permute");
+  return sgl::launch_permute(ids, T, k, E, counts, offsets, sorted_slot, slot_pos, nullptr, 0,
+                             (hipStream_t)stream);
 }
 
 int sgl_moe_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I, int E, int k,
                     const int32_t* offsets, const int32_t* sorted_slot, const float* route_w,
                     const sgl_expert_ptrs* experts, int has_shared, float swiglu_limit,
                     int scale_mode, void* hq, float* hs, sgl_stream_t stream) {
-  int rc = sgl::check_moe_shapes("moe_gate_up", T, H, I, E, k);
-  if (rc) return rc;
-  SGL_REQUIRE(scale_mode >= 0 && scale_mode <= 3, "moe_gate_up: bad scale_mode %d", scale_mode);
-  if (T == 0) return SGL_OK;
-  SGL_REQUIRE(xq && xs && offsets && sorted_slot && experts && hq && hs,
-              "moe_gate_up: null pointer");
-  SGL_REQUIRE(sgl::aligned(xq, 16) && sgl::aligned(hq, 8), "moe_gate_up: xq/hq misaligned");
-  sgl::GemmArgs g = {};
-  g.a = (const uint8_t*)xq;
-  g.sa = xs;
-  g.experts = experts;
-  g.offsets = offsets;
-  g.sorted_slot = sorted_slot;
-  g.route_w = route_w;
-  g.E = E;
-  g.k = k;
-  g.has_shared = has_shared ? 1 : 0;
-  g.T = T;
-  g.N = I;
-  g.K = H;
-  g.hq = (uint8_t*)hq;
-  g.hs = hs;
-  g.swiglu_limit = swiglu_limit;
-  g.scale_mode = scale_mode;
-  return sgl::launch_gemm(sgl::KIND_GATE_UP, g, T * k / E, (hipStream_t)stream);
+  return sgl::run_gate_up(xq, xs, T, H, I, E, k, offsets, sorted_slot, route_w, experts, has_shared,
+                          swiglu_limit, scale_mode, hq, hs, nullptr, (hipStream_t)stream);
 }
 
 int sgl_moe_down(const void* hq, const float* hs, int64_t T, int64_t H, int64_t I, int E, int k,
                  const int32_t* offsets, const int32_t* sorted_slot,
                  const sgl_expert_ptrs* experts, int has_shared, void* out, sgl_stream_t stream) {
-  int rc = sgl::check_moe_shapes("moe_down", T, H, I, E, k);
-  if (rc) return rc;
-  if (T == 0) return SGL_OK;
-  SGL_REQUIRE(hq && hs && offsets && sorted_slot && experts && out, "moe_down: null pointer");
-  SGL_REQUIRE(sgl::aligned(hq, 16), "moe_down: hq misaligned");
-  sgl::GemmArgs g = {};
-  g.a = (const uint8_t*)hq;
-  g.sa = hs;
-  g.experts = experts;
-  g.offsets = offsets;
-  g.sorted_slot = sorted_slot;
-  g.E = E;
-  g.k = k;
-  g.has_shared = has_shared ? 1 : 0;
-  g.T = T;
-  g.N = H;
-  g.K = I;
-  g.c = out;
-  return sgl::launch_gemm(sgl::KIND_DOWN, g, T * k / E, (hipStream_t)stream);
+  return sgl::run_down(hq, hs, T, H, I, E, k, offsets, sorted_slot, experts, has_shared, out,
+                       nullptr, (hipStream_t)stream);
 }
 
 int sgl_moe_combine(const void* out, const int32_t* ids, int64_t T, int k, int64_t H,
@@ -557,15 +590,17 @@ int sgl_moe_forward(const void* x, int64_t T, int64_t H, int64_t I, int E, int k
   SGL_REQUIRE(sgl::aligned(workspace, 256), "moe_forward: workspace must be 256-byte aligned");
   if ((rc = sgl_act_quant(x, T, H, H, w.xq, H, w.xs, H / 128, 128, scale_mode, 0, 0, stream)))
     return rc;
-  if ((rc = sgl_moe_permute(ids, T, k, E, w.counts, w.offsets, w.sorted_slot, w.slot_pos, stream)))
-    return rc;
-  if ((rc = sgl_moe_gate_up(w.xq, w.xs, T, H, I, E, k, w.offsets, w.sorted_slot, weights, experts,
-                            has_shared, swiglu_limit, scale_mode, w.hq, w.hs, stream)))
-    return rc;
-  if ((rc = sgl_moe_down(w.hq, w.hs, T, H, I, E, k, w.offsets, w.sorted_slot, experts, has_shared,
-                         w.out, stream)))
-    return rc;
   hipStream_t st = (hipStream_t)stream;
+  // the permute also zeroes the GEMMs' tile counters
+  if ((rc = sgl::launch_permute(ids, T, k, E, w.counts, w.offsets, w.sorted_slot, w.slot_pos,
+                                w.tile_ctr, 16, st)))
+    return rc;
+  if ((rc = sgl::run_gate_up(w.xq, w.xs, T, H, I, E, k, w.offsets, w.sorted_slot, weights, experts,
+                             has_shared, swiglu_limit, scale_mode, w.hq, w.hs, w.tile_ctr, st)))
+    return rc;
+  if ((rc = sgl::run_down(w.hq, w.hs, T, H, I, E, k, w.offsets, w.sorted_slot, experts, has_shared,
+                          w.out, w.tile_ctr + 8, st)))
+    return rc;
   sgl::combine_kernel<<<(unsigned)T, 256, 0, st>>>(w.out, ids, T, k, H, has_shared, E,
                                                     (uint16_t*)y);
   return sgl::check_launch("moe_combine");

@@ -36,6 +36,7 @@ struct GemmArgs {
   int scale_mode;
   int m_tiles;      // grid rows (upper bound of M tiles)
   int n_tiles;      // tiles along N
+  int* tile_ctr;    // moe: 8 zeroed per-XCD tile counters -> dynamic tile order (null: static)
 };
 
 int launch_gemm(int kind, GemmArgs& args, int64_t rows_hint, hipStream_t stream);
