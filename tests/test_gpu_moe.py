@@ -207,3 +207,40 @@ def test_moe_forward_deterministic_and_repeatable(gpu):
     y1 = u8(M.moe_forward(*args, workspace=ws))
     y2 = u8(M.moe_forward(*args, workspace=ws))
     np.testing.assert_array_equal(y1, y2)
+
+
+def test_tiny_moe_golden_fixture(gpu):
+    """The committed tiny-MoE fixture (tests/golden/tiny_moe_seed1.npz):
+    routing, permutation and activation quant bit-exact against the stored
+    bytes; the requantized gate/up rows and the layer output within the GEMM
+    tolerance."""
+    import os
+    import sys
+
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+    import make_tiny_moe as G
+    from sglang_lite_amd import kernel as K
+    from sglang_lite_amd import moe as M
+
+    gold = dict(np.load(G.PATH))
+    inp = G.make_inputs()
+    assert bytes(gold["weights_sha256"]).decode() == G.weights_digest(inp)
+    table = table_from(inp["experts"], inp["shared"], gpu)
+    w, ids = M.route_topk(to_dev_f32(gold["logits"], gpu), G.K_TOP)
+    xd = to_dev_bf16(inp["x"], gpu)
+    xq, xs = K.act_quant(xd)
+    counts, offsets, sorted_slot, slot_pos = M.permute(ids, G.E)
+    hq, hs = M.gate_up(xq, xs, offsets, sorted_slot, w.reshape(-1), table, G.K_TOP)
+    y = M.moe_forward(xd, ids, w, table)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(ids.cpu().numpy().astype(np.int32), gold["ids"])
+    np.testing.assert_allclose(f32(w), gold["route_w"], rtol=1e-6, atol=1e-7)
+    for name, dev in (("counts", counts), ("offsets", offsets), ("sorted_slot", sorted_slot),
+                      ("slot_pos", slot_pos)):
+        np.testing.assert_array_equal(dev.cpu().numpy(), gold[name], err_msg=name)
+    np.testing.assert_array_equal(u8(xq), gold["xq"])
+    np.testing.assert_array_equal(f32(xs).view(np.uint32), gold["xs"].view(np.uint32))
+    assert_gemm_close(Q.dequant_rows(u8(hq), f32(hs)), Q.dequant_rows(gold["hq"], gold["hs"]),
+                      "golden h")
+    y_ref = (gold["y_bf16_bits"].astype(np.uint32) << 16).view(np.float32)
+    assert_gemm_close(f32(y), y_ref, "golden y")
