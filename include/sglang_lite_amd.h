@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 1
+#define SGL_ABI_VERSION 2
 
 typedef void* sgl_stream_t; /* hipStream_t */
 
@@ -75,17 +75,27 @@ enum sgl_score_func { SGL_SCORE_SOFTMAX = 0, SGL_SCORE_SIGMOID = 1, SGL_SCORE_SQ
  *                    [0:512) e4m3 | [512:640) rope bf16 | [640:656) 4 x fp32 LE. */
 enum sgl_kv_layout { SGL_KV_LAYOUT_A = 0, SGL_KV_LAYOUT_B = 1 };
 
+/* Weight formats of the routed experts of a MoE layer.
+ *   SGL_EXPERT_FP8_BLOCK128  e4m3 row-major [out, in] with fp32 scales
+ *       [ceil(out/128), ceil(in/128)] (deepseek_infer/model.py:138-142 FP8 Linear)
+ *   SGL_EXPERT_FP4_E2M1      packed e2m1 [out, in/2] (byte b of a row holds
+ *       element 2b in its low nibble, 2b+1 in its high nibble; torch
+ *       float4_e2m1fn_x2) with e8m0 scales [out, in/32], one per 32
+ *       consecutive inputs (deepseek_infer/model.py:129-137 FP4 Linear,
+ *       expert_dtype "fp4", model.py:623-624)
+ * The shared expert is always SGL_EXPERT_FP8_BLOCK128 (model.py:626). */
+enum sgl_expert_format { SGL_EXPERT_FP8_BLOCK128 = 0, SGL_EXPERT_FP4_E2M1 = 1 };
+
 /* Per-expert weight pointers of one MoE layer, stored in DEVICE memory as an
- * array of E routed experts followed by the shared expert.  Weights are e4m3
- * row-major [out, in] (deepseek_infer/model.py:138-142 FP8 Linear), scales
- * fp32 [ceil(out/128), ceil(in/128)] row-major. */
+ * array of E routed experts followed by the shared expert; weights and
+ * scales in the expert's sgl_expert_format. */
 typedef struct sgl_expert_ptrs {
-  const void* w_gate;  /* w1: [I, H] */
-  const void* w_up;    /* w3: [I, H] */
-  const void* w_down;  /* w2: [H, I] */
-  const float* s_gate; /* [I/128, H/128] */
-  const float* s_up;   /* [I/128, H/128] */
-  const float* s_down; /* [H/128, I/128] */
+  const void* w_gate; /* w1: [I, H] (fp4: [I, H/2]) */
+  const void* w_up;   /* w3: [I, H] (fp4: [I, H/2]) */
+  const void* w_down; /* w2: [H, I] (fp4: [H, I/2]) */
+  const void* s_gate; /* fp32 [I/128, H/128] (fp4: e8m0 [I, H/32]) */
+  const void* s_up;   /* fp32 [I/128, H/128] (fp4: e8m0 [I, H/32]) */
+  const void* s_down; /* fp32 [H/128, I/128] (fp4: e8m0 [H, I/32]) */
 } sgl_expert_ptrs;
 
 /* ---------------------------------------------------------------- library */
@@ -151,6 +161,28 @@ int sgl_check_conversions(unsigned long long* counts, sgl_stream_t stream);
 int sgl_fp8_gemm(const void* a, const void* sa, const void* b, const void* sb, int b_scale_e8m0,
                  void* c, int out_dtype, int64_t M, int64_t N, int64_t K, sgl_stream_t stream);
 
+/* C[M, N] = A_e4m3[M, K] . B_e2m1[N, K]^T with A scaled per (row, 128-deep K
+ * block) by sa and B per (row, 32-deep K block) by sb; fp32 accumulation,
+ * output bf16 (SGL_BF16) or fp32 (SGL_F32).  A e4m3 [M, K] contiguous, sa
+ * fp32 [M, K/128] (e8m0 activation scales: convert with sgl_e8m0_to_f32
+ * first), B packed e2m1 [N, K/2] (low nibble = even K), sb e8m0 [N, K/32].
+ * The weight scales are applied inside the MFMA; the row scales too when
+ * sa_pow2 != 0, which declares every sa entry a power of two (its mantissa
+ * bits are then ignored), else each 128-deep partial is promoted with sa in
+ * fp32.  K % 256 == 0, N % 16 == 0, M*K and N*K/2 < 2^31.
+ * Replaces deepseek_infer/kernel.py:519-536 fp4_gemm (kernel :441-516) and
+ * engine/v4_deep_gemm.py:169-218 fp4_gemm_nt (DeepGEMM fp8_fp4_gemm_nt). */
+int sgl_fp4_gemm(const void* a, const float* sa, int sa_pow2, const void* b, const void* sb,
+                 void* c, int out_dtype, int64_t M, int64_t N, int64_t K, sgl_stream_t stream);
+
+/* Lossless FP4 -> FP8 weight repack: per 128 x 128 block, s = (max of the
+ * block's 512 e8m0 scales) / 2^6 and q = e4m3(e2m1 * (scale / s)).  b packed
+ * e2m1 [N, K/2], sb e8m0 [N, K/32]; q e4m3 [N, K], s_out e8m0 [N/128, K/128].
+ * N % 128 == 0, K % 128 == 0.  Replaces deepseek_infer/convert.py:17-52
+ * cast_e2m1fn_to_e4m3fn (the convert.py --expert-dtype fp8 load step). */
+int sgl_fp4_to_fp8_weight(const void* b, const void* sb, int64_t N, int64_t K, void* q,
+                          void* s_out, sgl_stream_t stream);
+
 /* ------------------------------------------------------------ MoE layer */
 
 /* Gate top-k from router logits [T, E] fp32 (E <= 512, k <= 16):
@@ -182,25 +214,30 @@ int sgl_moe_permute(const int32_t* ids, int64_t T, int k, int E, int32_t* counts
  *   h = bf16(silu(gate) * up * route_w[slot])
  *   hq, hs = 1x128 quant of h with scale_mode (fp32 scales)
  * xq e4m3 [T, H], xs fp32 [T, H/128], route_w fp32 [T*k] (slot-indexed),
- * experts: device array of E (+1) sgl_expert_ptrs, hq e4m3 [rows, I],
- * hs fp32 [rows, I/128], rows = T*k (+ T).  H % 128 == 0, I % 128 == 0.
+ * experts: device array of E (+1) sgl_expert_ptrs, the routed ones in
+ * expert_format (sgl_expert_format), hq e4m3 [rows, I], hs fp32 [rows, I/128],
+ * rows = T*k (+ T).  H % 128 == 0, I % 128 == 0 (FP4: multiples of 256).
+ * With FP4 routed experts and a power-of-two scale_mode (*_UE8M0) the row
+ * scales xs must be powers of two (as act_quant makes them in that mode):
+ * they are applied as e8m0 exponents inside the MFMA.
  * Replaces engine/v4_moe_fast.py:43-76 _expert_forward_fused up to w2's
  * act_quant (and deepseek_infer/model.py:596-606 Expert.forward). */
 int sgl_moe_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I, int E, int k,
                     const int32_t* offsets, const int32_t* sorted_slot, const float* route_w,
-                    const sgl_expert_ptrs* experts, int has_shared, float swiglu_limit,
-                    int scale_mode, void* hq, float* hs, sgl_stream_t stream);
+                    const sgl_expert_ptrs* experts, int has_shared, int expert_format,
+                    float swiglu_limit, int scale_mode, void* hq, float* hs, sgl_stream_t stream);
 
 /* Grouped down GEMM: out[slot] = bf16(hq[row] . w_down[e]^T) for every row of
  * sgl_moe_gate_up's row order; routed row p is written at output row
  * sorted_slot[p] / k * (k + has_shared) + sorted_slot[p] % k and shared row t
  * at t * (k + 1) + k, so the outputs of one token are contiguous.
- * out bf16 [T * (k + has_shared), H].  Replaces the w2 projection of
- * engine/v4_moe_fast.py:76 / deepseek_infer/model.py:606. */
+ * out bf16 [T * (k + has_shared), H].  expert_format and scale_mode (the
+ * mode hs was made with) as for sgl_moe_gate_up.  Replaces the w2 projection
+ * of engine/v4_moe_fast.py:76 / deepseek_infer/model.py:606. */
 int sgl_moe_down(const void* hq, const float* hs, int64_t T, int64_t H, int64_t I, int E, int k,
                  const int32_t* offsets, const int32_t* sorted_slot,
-                 const sgl_expert_ptrs* experts, int has_shared, void* out,
-                 sgl_stream_t stream);
+                 const sgl_expert_ptrs* experts, int has_shared, int expert_format, int scale_mode,
+                 void* out, sgl_stream_t stream);
 
 /* Unpermute-combine: y[t] = bf16( (sum over the token's k expert outputs in
  * ascending expert-id order, fp32) + shared[t] ), matching the fp32
@@ -215,12 +252,13 @@ size_t sgl_moe_workspace_size(int64_t T, int64_t H, int64_t I, int E, int k, int
 
 /* Whole routed+shared MoE layer from bf16 x [T, H] and a precomputed top-k
  * (ids int32 [T, k], weights fp32 [T, k]): act quant -> permute -> gate/up
- * -> down -> combine, y bf16 [T, H].  Replaces
- * engine/v4_moe_fast.py:79-106 _moe_forward_activated_only after the gate. */
+ * -> down -> combine, y bf16 [T, H]; routed experts in expert_format.
+ * Replaces engine/v4_moe_fast.py:79-106 _moe_forward_activated_only after
+ * the gate. */
 int sgl_moe_forward(const void* x, int64_t T, int64_t H, int64_t I, int E, int k,
                     const int32_t* ids, const float* weights, const sgl_expert_ptrs* experts,
-                    int has_shared, float swiglu_limit, int scale_mode, void* workspace,
-                    size_t workspace_bytes, void* y, sgl_stream_t stream);
+                    int has_shared, int expert_format, float swiglu_limit, int scale_mode,
+                    void* workspace, size_t workspace_bytes, void* y, sgl_stream_t stream);
 
 /* ------------------------------------------------------------- KV cache */
 

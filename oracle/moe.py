@@ -9,6 +9,7 @@ from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 
+from . import fp4 as F4
 from . import quant as Q
 
 # --------------------------------------------------------------- routing
@@ -141,11 +142,14 @@ def expert_forward(x_bf16: np.ndarray, w: Dict[str, np.ndarray], weights: Option
     weights: one act_quant for gate and up, bf16 GEMM outputs upcast,
     clamp, silu(gate)*up, *weights, bf16, w2 (act_quant + fp8_gemm) -> bf16.
 
-    ``w`` holds ``w1, w3, w2`` (e4m3 uint8) and ``s1, s3, s2`` (fp32 block scales).
+    ``w`` holds ``w1, w3, w2`` (e4m3 uint8) and ``s1, s3, s2`` (fp32 block
+    scales), or with ``fmt == "fp4"`` packed e2m1 weights and e8m0 1x32 scales
+    (model.py:113-115: the same act_quant, then fp4_gemm).
     """
+    gemm = F4.fp4_gemm if w.get("fmt") == "fp4" else fp8_gemm
     xq, xs = Q.scale_mode_quant(x_bf16, mode, 128)
-    gate = fp8_gemm(xq, xs, w["w1"], w["s1"])
-    up = fp8_gemm(xq, xs, w["w3"], w["s3"])
+    gate = gemm(xq, xs, w["w1"], w["s1"])
+    up = gemm(xq, xs, w["w3"], w["s3"])
     if swiglu_limit > 0:
         lim = np.float32(swiglu_limit)
         up = np.clip(up, -lim, lim)
@@ -155,7 +159,7 @@ def expert_forward(x_bf16: np.ndarray, w: Dict[str, np.ndarray], weights: Option
         h = (np.asarray(weights, np.float32) * h).astype(np.float32)
     hb = Q.bf16_round(h)
     hq, hs = Q.scale_mode_quant(hb, mode, 128)
-    out = fp8_gemm(hq, hs, w["w2"], w["s2"])
+    out = gemm(hq, hs, w["w2"], w["s2"])
     if trace is not None:
         trace.update(xq=xq, xs=xs, gate=gate, up=up, h=hb, hq=hq, hs=hs, out=out)
     return out
@@ -212,6 +216,17 @@ def make_expert(rng: np.random.Generator, H: int, I: int, std: float = 0.02) -> 
     for name, shape in (("1", (I, H)), ("3", (I, H)), ("2", (H, I))):
         w = (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
         q, s = Q.per_block_cast_to_fp8(w)
+        out["w" + name] = q
+        out["s" + name] = s
+    return out
+
+
+def make_fp4_expert(rng: np.random.Generator, H: int, I: int, std: float = 0.02) -> Dict[str, np.ndarray]:
+    """Synthetic MXFP4 expert (the reference's routed-expert format,
+    model.py:129-137): N(0, std) weights -> packed e2m1 + e8m0 1x32 scales."""
+    out = {"fmt": "fp4"}
+    for name, shape in (("1", (I, H)), ("3", (I, H)), ("2", (H, I))):
+        q, s = F4.make_fp4_weight(rng, *shape, std=std)
         out["w" + name] = q
         out["s" + name] = s
     return out

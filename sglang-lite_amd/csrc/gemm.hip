@@ -96,13 +96,21 @@ __device__ __forceinline__ FragLane frag_lane(int r16, int g4) {
   return FragLane{(uint32_t)(r16 * 128 + (((2 * g4) ^ swz(r16)) << 4)),
                   (uint32_t)(r16 * 128 + (((2 * g4 + 1) ^ swz(r16)) << 4))};
 }
+// With a packed e2m1 B operand the MFMA pairs A's K differently: lane l
+// holds A bytes [16 (l/16), +16) and [64 + 16 (l/16), +16) of its row, i.e.
+// logical chunks l/16 and 4 + l/16 (B lane l holds K [32 (l/16), +32) of its
+// column as 16 packed bytes).
+__device__ __forceinline__ FragLane frag_lane_fp4a(int r16, int g4) {
+  return FragLane{(uint32_t)(r16 * 128 + ((g4 ^ swz(r16)) << 4)),
+                  (uint32_t)(r16 * 128 + (((4 + g4) ^ swz(r16)) << 4))};
+}
 __device__ __forceinline__ v8i read_frag(const uint8_t* block, FragLane fl) {
   const uint4 lo = *reinterpret_cast<const uint4*>(block + fl.lo);
   const uint4 hi = *reinterpret_cast<const uint4*>(block + fl.hi);
   return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 }
 
-template <int KIND, int BM, int BN, int WM, int WN, int NSTAGE>
+template <int KIND, int BM, int BN, int WM, int WN, int NSTAGE, int WF, bool SAHW>
 struct Cfg {
   static constexpr int NT = 64 * WM * WN;
   static constexpr int NW = WM * WN;
@@ -110,37 +118,47 @@ struct Cfg {
   static constexpr int TN = BN / (WN * 16);
   static constexpr int HALF = BN / 2;   // gate_up: gate columns, then the same up columns
   static constexpr int HW = HALF / WN;  // gate_up: h columns per wavefront
-  static constexpr int A_BYTES = BM * 128;
+  // 128-deep K steps per stage: a stage always holds 128-byte B rows, which
+  // is 128 K of e4m3 or 256 K of packed e2m1
+  static constexpr int KS = WF == WF_FP4 ? 2 : 1;
+  static constexpr int A_BYTES = BM * 128 * KS;  // KS sub-blocks of BM x 128 bytes
   static constexpr int B_BYTES = BN * 128;
+  static constexpr int SB_BYTES = WF == WF_FP4 ? BN * 8 : 0;  // e8m0 weight scales: 8 per column
+  static constexpr int SBI = SB_BYTES / (NW * 256);           // their dword DMAs per wavefront
   static constexpr int SA_ROWS = BM / NW;  // row scales each wavefront loads per stage
-  static constexpr int STAGE = A_BYTES + B_BYTES;  // one K block of A and B rows
-  static constexpr int SA_SLOT = NW * 256;           // one K block of row scales
-  static constexpr int CHUNKS = (BM + BN) / 8;  // 1 KB DMA chunks per stage
+  static constexpr int STAGE = A_BYTES + B_BYTES + SB_BYTES;
+  static constexpr int SA_SLOT = NW * 256;           // one stage of row scales
+  static constexpr int ACH = BM * KS / 8;            // 1 KB DMA chunks of A per stage
+  static constexpr int CHUNKS = ACH + BN / 8;        // ... of A and B
   static constexpr int CPW = CHUNKS / NW;       // per wavefront
-  static constexpr int LPS = CPW + 1;           // DMA instructions per wavefront per stage
+  static constexpr int LPS = CPW + 1 + SBI;     // DMA instructions per wavefront per stage
   static constexpr int NSA = NSTAGE;  // row-scale slots (a ring of their own)
   static constexpr int RING = NSTAGE * STAGE;
   static constexpr int SMEM = RING + NSA * SA_SLOT;
   static_assert(CHUNKS % NW == 0, "chunks must split evenly over wavefronts");
-  static_assert(SA_ROWS >= 1 && SA_ROWS <= 64, "row scales per wavefront");
+  static_assert(SA_ROWS >= 1 && SA_ROWS * KS <= 64, "row scales per wavefront");
+  static_assert(SB_BYTES % (NW * 256) == 0, "weight-scale DMAs must split evenly");
   static_assert(TM >= 1 && TN >= 1, "tile too small");
   static_assert(KIND != KIND_GATE_UP || (TN % 2 == 0 && HALF == 128), "gate_up needs 128 h columns");
   static_assert(KIND == KIND_GATE_UP ? BM * HALF * 2 <= RING : BM * BN * 4 <= RING,
                 "epilogue staging must fit in the stage ring");
   static_assert(NSTAGE >= 2 && NSTAGE <= 4, "stages");
+  static_assert(WF == WF_FP4 || !SAHW, "in-MFMA activation scales are an FP4-weight path");
 };
 
-template <int KIND, int BM, int BN, int WM, int WN, int NSTAGE>
+template <int KIND, int BM, int BN, int WM, int WN, int NSTAGE, int WF, bool SAHW>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs args) {
-  using C = Cfg<KIND, BM, BN, WM, WN, NSTAGE>;
+  using C = Cfg<KIND, BM, BN, WM, WN, NSTAGE, WF, SAHW>;
   constexpr int NT = C::NT, NW = C::NW, TM = C::TM, TN = C::TN, HALF = C::HALF, HW = C::HW;
+  constexpr int KS = C::KS;
+  constexpr bool FP4 = WF == WF_FP4;
 
   __shared__ __align__(16) uint8_t smem[C::SMEM];
   __shared__ int sTstart[KIND == KIND_DENSE ? 1 : kMaxGroups + 1];
   __shared__ int sSrc[BM];
   __shared__ int sDst[BM];
   __shared__ float sW[BM];
-  __shared__ float sSb[2][kMaxKB];  // the tile's weight scales per K block
+  __shared__ float sSb[2][FP4 ? 1 : kMaxKB];  // fp8: the tile's weight scales per K block
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -148,8 +166,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
   const int wm = wave / WN, wn = wave % WN;
   const int g4 = lane >> 4, r16 = lane & 15;
   const FragLane fl = frag_lane(r16, g4);
+  const FragLane fla = FP4 ? frag_lane_fp4a(r16, g4) : fl;
   const int64_t K = args.K, N = args.N;
+  const int64_t KROW = FP4 ? K / 2 : K;  // bytes per B row
   const int KB = (int)(K / 128);
+  const int NST = KB / KS;  // stages along K
   const int n_tiles = args.n_tiles;
 
   // ---- M-tile prefix over the expert groups (E routed, then the shared one)
@@ -264,12 +285,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
     // tiles span BN/128 scale blocks, one per wavefront column group
     // (TN*16 <= 128 columns), clamped for a ragged last tile
     const int64_t sb_blk = n0 / 128;
-    static_assert(KIND == KIND_GATE_UP || (TN * 16 <= 128 && 128 % (TN * 16) == 0 && BN <= 256),
+    static_assert(FP4 || KIND == KIND_GATE_UP ||
+                      (TN * 16 <= 128 && 128 % (TN * 16) == 0 && BN <= 256),
                   "a wavefront's columns must sit in one 128-column scale block");
     const int wave_blk = KIND == KIND_GATE_UP ? 0 : (wn * TN * 16) / 128;
-    // the tile's weight scales -> LDS (row 0: gate / first block, row 1: up /
-    // second block), so the K loop issues no vector loads besides the DMAs
-    for (int i = tid; i < 2 * KB; i += NT) {
+    // fp8: the tile's weight scales -> LDS (row 0: gate / first block, row 1:
+    // up / second block), so the K loop issues no vector loads besides the
+    // DMAs; fp4 weight scales travel with each stage
+    for (int i = tid; i < (FP4 ? 0 : 2 * KB); i += NT) {
       const int j = i / KB, kb = i - j * KB;
       float v;
       if constexpr (KIND == KIND_GATE_UP) {
@@ -301,7 +324,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
             if (args.route_w) w = args.route_w[sl];
           } else {
             src = p;
-            dst = t * (args.k + args.has_shared) + j;
+            dst = t * args.out_k + j;
           }
         } else {
           const int t = p - (int)shared_base;
@@ -310,7 +333,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
             dst = p;
           } else {
             src = p;
-            dst = t * (args.k + 1) + args.k;
+            dst = t * args.out_k + args.k;
           }
         }
       }
@@ -322,52 +345,79 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
 
     const int src0 = __builtin_amdgcn_readfirstlane(sSrc[0]);
 
-    // chunk c = wave + j * NW: A rows [8c, 8c+8) for c < BM/8, else B rows
+    // chunk c = wave + j * NW: for c < ACH, rows [8c', 8c'+8) of A's K
+    // sub-block c / (BM/8) (c' = c % (BM/8)); else B rows
     uint32_t voff[C::CPW];
 #pragma unroll
     for (int j = 0; j < C::CPW; ++j) {
       const int c = wave + j * NW;
       const int rr = lane >> 3, pc = lane & 7;
-      if (c < BM / 8) {
-        const int r = c * 8 + rr;
+      if (c < C::ACH) {
+        const int sub = c / (BM / 8);
+        const int r = (c - sub * (BM / 8)) * 8 + rr;
         const int s = sSrc[r] >= 0 ? sSrc[r] : src0;
-        voff[j] = (uint32_t)((int64_t)s * K + ((pc ^ swz(r)) << 4));
+        voff[j] = (uint32_t)((int64_t)s * K + sub * 128 + ((pc ^ swz(r)) << 4));
       } else {
-        const int r = (c - BM / 8) * 8 + rr;
+        const int r = (c - C::ACH) * 8 + rr;
         const bool up_half = KIND == KIND_GATE_UP && r >= HALF;
         int64_t n = n0 + (up_half ? r - HALF : r);
         if (n >= N) n = n0;
-        voff[j] = (uint32_t)(n * K + ((pc ^ swz(r)) << 4));
+        voff[j] = (uint32_t)(n * KROW + ((pc ^ swz(r)) << 4));
       }
     }
-    const int sa_row = wave * C::SA_ROWS + (lane < C::SA_ROWS ? lane : 0);
+    // row scales: lane l < KS * SA_ROWS loads row wave * SA_ROWS + l % SA_ROWS,
+    // K step l / SA_ROWS of the stage (the other lanes repeat lane 0's load)
+    const int sa_l = lane < KS * C::SA_ROWS ? lane : 0;
+    const int sa_row = wave * C::SA_ROWS + sa_l % C::SA_ROWS;
     const int sa_src = sSrc[sa_row] >= 0 ? sSrc[sa_row] : src0;
-    const uint32_t sa_off = (uint32_t)((int64_t)sa_src * KB * 4);
+    const uint32_t sa_off = (uint32_t)(((int64_t)sa_src * KB + sa_l / C::SA_ROWS) * 4);
     const uint8_t* sa_base = uniform_ptr(args.sa);
     const uint32_t smem_lds = __builtin_amdgcn_readfirstlane(lds_u32(smem));
+    // fp4 weight scales: dword d = (q NW + wave) 64 + lane of the stage's
+    // [BN][8] bytes is column d / 2, half d % 2 (32 columns per instruction,
+    // so a gate_up instruction is wholly gate or wholly up)
+    uint32_t sb_off[C::SBI > 0 ? C::SBI : 1];
+#pragma unroll
+    for (int q = 0; q < C::SBI; ++q) {
+      const int d = (q * NW + wave) * 64 + lane;
+      const int col = d >> 1;
+      const bool up_half = KIND == KIND_GATE_UP && col >= HALF;
+      int64_t n = n0 + (up_half ? col - HALF : col);
+      if (n >= N) n = n0;
+      sb_off[q] = (uint32_t)(n * (K / 32) + (d & 1) * 4);
+    }
+    const uint8_t* sbp0 = FP4 ? uniform_ptr(sb0) : nullptr;
+    const uint8_t* sbp1 = FP4 && KIND == KIND_GATE_UP ? uniform_ptr(sb1) : nullptr;
 
-    // DMA K block kb into operand slot `slot` and row-scale slot `sa_slot`
-    // (defaults: the block's own slots kb % NSTAGE, kb % NSA)
-    auto issue = [&](int kb, int slot = -1, int sa_slot = -1) {
-      if (slot < 0) slot = kb % NSTAGE;
-      if (sa_slot < 0) sa_slot = kb % C::NSA;
-      const uint32_t st = smem_lds + (uint32_t)(slot * C::STAGE);
+    // DMA stage st (K steps st*KS ...) into operand slot `slot` and
+    // row-scale slot `sa_slot` (defaults: st % NSTAGE, st % NSA)
+    auto issue = [&](int st, int slot = -1, int sa_slot = -1) {
+      if (slot < 0) slot = st % NSTAGE;
+      if (sa_slot < 0) sa_slot = st % C::NSA;
+      const uint32_t sl = smem_lds + (uint32_t)(slot * C::STAGE);
 #pragma unroll
       for (int j = 0; j < C::CPW; ++j) {
         const int c = wave + j * NW;
         bool isA, up_half;
-        if constexpr ((BM / 8) % NW == 0 && (HALF / 8) % NW == 0) {
+        if constexpr (C::ACH % NW == 0 && (HALF / 8) % NW == 0) {
           // chunk j of every wavefront is of the same kind: decided at compile time
-          isA = j < (BM / 8) / NW;
-          up_half = KIND == KIND_GATE_UP && j >= (BM / 8 + HALF / 8) / NW;
+          isA = j < C::ACH / NW;
+          up_half = KIND == KIND_GATE_UP && j >= (C::ACH + HALF / 8) / NW;
         } else {
-          isA = c < BM / 8;
-          up_half = KIND == KIND_GATE_UP && !isA && (c - BM / 8) * 8 >= HALF;
+          isA = c < C::ACH;
+          up_half = KIND == KIND_GATE_UP && !isA && (c - C::ACH) * 8 >= HALF;
         }
         const uint8_t* base = isA ? baseA : (up_half ? b1 : b0);
-        dma16(base, voff[j] + (uint32_t)kb * 128u, st + (uint32_t)c * 1024u);
+        const uint32_t koff = isA ? (uint32_t)st * (128u * KS) : (uint32_t)st * 128u;
+        dma16(base, voff[j] + koff, sl + (uint32_t)c * 1024u);
       }
-      dma4(sa_base, sa_off + (uint32_t)kb * 4u,
+#pragma unroll
+      for (int q = 0; q < C::SBI; ++q) {
+        const bool up_half = KIND == KIND_GATE_UP && (q * NW + wave) * 32 >= HALF;
+        dma4(up_half ? sbp1 : sbp0, sb_off[q] + (uint32_t)st * 8u,
+             sl + (uint32_t)(C::A_BYTES + C::B_BYTES + (q * NW + wave) * 256));
+      }
+      dma4(sa_base, sa_off + (uint32_t)st * (4u * KS),
            smem_lds + (uint32_t)(C::RING + sa_slot * C::SA_SLOT + wave * 256));
     };
 
@@ -387,69 +437,142 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
 
 #pragma unroll
     for (int s = 0; s < NSTAGE - 1; ++s)
-      if (s < KB) issue(s);
+      if (s < NST) issue(s);
 
-    for (int kb = 0; kb < KB; ++kb) {
-      // loads of stage kb are the oldest in flight: allow the younger ones
-      const int younger = min(NSTAGE - 2, KB - 1 - kb);
+    for (int st = 0; st < NST; ++st) {
+      // loads of stage st are the oldest in flight: allow the younger ones
+      const int younger = min(NSTAGE - 2, NST - 1 - st);
       if (younger >= 2) wait_vmcnt<2 * C::LPS>();
       else if (younger == 1) wait_vmcnt<C::LPS>();
       else wait_vmcnt<0>();
       __builtin_amdgcn_s_barrier();
-      if (kb + NSTAGE - 1 < KB) issue(kb + NSTAGE - 1);
+      if (st + NSTAGE - 1 < NST) issue(st + NSTAGE - 1);
 
-      const uint8_t* stg = smem + (kb % NSTAGE) * C::STAGE;
-      const uint8_t* tA = stg;
+      const uint8_t* stg = smem + (st % NSTAGE) * C::STAGE;
       const uint8_t* tB = stg + C::A_BYTES;
-      const float* tS = reinterpret_cast<const float*>(smem + C::RING + (kb % C::NSA) * C::SA_SLOT);
-      const float sbv0 = sSb[wave_blk][kb];
-      const float sbv1 = KIND == KIND_GATE_UP ? sSb[1][kb] : 0.0f;
+      const float* tS = reinterpret_cast<const float*>(smem + C::RING + (st % C::NSA) * C::SA_SLOT);
+      // row scale of tile row `row`, K step ks of the stage
+      auto row_scale = [&](int row, int ks) -> float {
+        return tS[(row / C::SA_ROWS) * 64 + ks * C::SA_ROWS + row % C::SA_ROWS];
+      };
 
       // a wavefront whose rows all lie past the tile's last row has no work
       if ((wm * TM) * 16 < rows) {
-        v8i af[TM];
-        float sav[TM][4];
 #pragma unroll
-        for (int mi = 0; mi < TM; ++mi) {
-          const int rbase = (wm * TM + mi) * 16;
-          af[mi] = read_frag(tA + rbase * 128, fl);
+        for (int ks = 0; ks < KS; ++ks) {
+          const uint8_t* tA = stg + ks * (BM * 128);
+          v8i af[TM];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int row = rbase + 4 * g4 + r;
-            sav[mi][r] = tS[(row / C::SA_ROWS) * 64 + (row % C::SA_ROWS)];
-          }
-        }
-        // software pipeline: B fragment nj+1 is read while the MFMAs of column
-        // block nj run, and block nj-1 is promoted after block nj's MFMAs
-        // are issued, so neither the LDS latency nor the MFMA latency sits
-        // in front of a dependent instruction
-        v8i bf[2];
-        v4f pr[2][TM];
-        bf[0] = read_frag(tB + tile_col(0) * 128, fl);
+          for (int mi = 0; mi < TM; ++mi) af[mi] = read_frag(tA + (wm * TM + mi) * 16 * 128, fla);
+          if constexpr (!FP4) {
+            const int kb = st;
+            const float sbv0 = sSb[wave_blk][kb];
+            const float sbv1 = KIND == KIND_GATE_UP ? sSb[1][kb] : 0.0f;
+            float sav[TM][4];
 #pragma unroll
-        for (int nj = 0; nj < TN; ++nj) {
-          if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + tile_col(nj + 1) * 128, fl);
+            for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
-          for (int mi = 0; mi < TM; ++mi)
-            pr[nj & 1][mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                af[mi], bf[nj & 1], vzero, 0, 0, 0, 0, 0, 0);
-          if (nj > 0) {
-            const float sbv = (KIND == KIND_GATE_UP && nj - 1 >= TN / 2) ? sbv1 : sbv0;
+              for (int r = 0; r < 4; ++r) sav[mi][r] = row_scale((wm * TM + mi) * 16 + 4 * g4 + r, 0);
+            // software pipeline: B fragment nj+1 is read while the MFMAs of
+            // column block nj run, and block nj-1 is promoted after block
+            // nj's MFMAs are issued, so neither the LDS latency nor the MFMA
+            // latency sits in front of a dependent instruction
+            v8i bf[2];
+            v4f pr[2][TM];
+            bf[0] = read_frag(tB + tile_col(0) * 128, fl);
+#pragma unroll
+            for (int nj = 0; nj < TN; ++nj) {
+              if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + tile_col(nj + 1) * 128, fl);
+#pragma unroll
+              for (int mi = 0; mi < TM; ++mi)
+                pr[nj & 1][mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                    af[mi], bf[nj & 1], vzero, 0, 0, 0, 0, 0, 0);
+              if (nj > 0) {
+                const float sbv = (KIND == KIND_GATE_UP && nj - 1 >= TN / 2) ? sbv1 : sbv0;
+#pragma unroll
+                for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+                  for (int r = 0; r < 4; ++r)
+                    acc[mi][nj - 1][r] =
+                        fmaf(pr[(nj - 1) & 1][mi][r], sav[mi][r] * sbv, acc[mi][nj - 1][r]);
+              }
+            }
+            const float sbv = (KIND == KIND_GATE_UP && TN - 1 >= TN / 2) ? sbv1 : sbv0;
 #pragma unroll
             for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
               for (int r = 0; r < 4; ++r)
-                acc[mi][nj - 1][r] =
-                    fmaf(pr[(nj - 1) & 1][mi][r], sav[mi][r] * sbv, acc[mi][nj - 1][r]);
+                acc[mi][TN - 1][r] = fmaf(pr[(TN - 1) & 1][mi][r], sav[mi][r] * sbv, acc[mi][TN - 1][r]);
+          } else {
+            // fp4 B: lane (r16, g4) of column block nj reads 16 bytes = K
+            // [32 g4, 32 g4 + 32) of the step from column tile_col(nj) + r16,
+            // and that column's e8m0 scale of the same 32-deep block
+            const uint32_t bl = (uint32_t)(r16 * 128 + (((4 * ks + g4) ^ swz(r16)) << 4));
+            const uint8_t* tSB = stg + C::A_BYTES + C::B_BYTES + ks * 4;
+            auto read_b = [&](int nj) -> v8i {
+              const uint4 v = *reinterpret_cast<const uint4*>(tB + tile_col(nj) * 128 + bl);
+              return v8i{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
+            };
+            auto read_sb = [&](int nj) -> int {
+              const uint32_t w = *reinterpret_cast<const uint32_t*>(tSB + (tile_col(nj) + r16) * 8);
+              return (int)(w >> (8 * g4));
+            };
+            v8i bf[2];
+            int sbb[2];
+            bf[0] = read_b(0);
+            sbb[0] = read_sb(0);
+            if constexpr (SAHW) {
+              // power-of-two row scales: e8m0 = the fp32 exponent field; both
+              // scales are applied inside the MFMA, which accumulates in place
+              int sae[TM];
+#pragma unroll
+              for (int mi = 0; mi < TM; ++mi)
+                sae[mi] = (int)(__float_as_uint(row_scale((wm * TM + mi) * 16 + r16, ks)) >> 23);
+#pragma unroll
+              for (int nj = 0; nj < TN; ++nj) {
+                if (nj + 1 < TN) {
+                  bf[(nj + 1) & 1] = read_b(nj + 1);
+                  sbb[(nj + 1) & 1] = read_sb(nj + 1);
+                }
+#pragma unroll
+                for (int mi = 0; mi < TM; ++mi)
+                  acc[mi][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                      af[mi], bf[nj & 1], acc[mi][nj], 0, 4, 0, sae[mi], 0, sbb[nj & 1]);
+              }
+            } else {
+              // fp32 row scales: the weight scales inside the MFMA, the row
+              // scale promoted once per 128-deep step as in the fp8 path
+              float sav[TM][4];
+#pragma unroll
+              for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sav[mi][r] = row_scale((wm * TM + mi) * 16 + 4 * g4 + r, ks);
+              v4f pr[2][TM];
+#pragma unroll
+              for (int nj = 0; nj < TN; ++nj) {
+                if (nj + 1 < TN) {
+                  bf[(nj + 1) & 1] = read_b(nj + 1);
+                  sbb[(nj + 1) & 1] = read_sb(nj + 1);
+                }
+#pragma unroll
+                for (int mi = 0; mi < TM; ++mi)
+                  pr[nj & 1][mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                      af[mi], bf[nj & 1], vzero, 0, 4, 0, 127, 0, sbb[nj & 1]);
+                if (nj > 0) {
+#pragma unroll
+                  for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                      acc[mi][nj - 1][r] = fmaf(pr[(nj - 1) & 1][mi][r], sav[mi][r], acc[mi][nj - 1][r]);
+                }
+              }
+#pragma unroll
+              for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                  acc[mi][TN - 1][r] = fmaf(pr[(TN - 1) & 1][mi][r], sav[mi][r], acc[mi][TN - 1][r]);
+            }
           }
-        }
-        {
-          const float sbv = (KIND == KIND_GATE_UP && TN - 1 >= TN / 2) ? sbv1 : sbv0;
-#pragma unroll
-          for (int mi = 0; mi < TM; ++mi)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              acc[mi][TN - 1][r] = fmaf(pr[(TN - 1) & 1][mi][r], sav[mi][r] * sbv, acc[mi][TN - 1][r]);
         }
       }
     }
@@ -544,7 +667,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
   }
 }
 
-template <int KIND, int BM, int BN, int WM, int WN, int NSTAGE>
+template <int KIND, int BM, int BN, int WM, int WN, int NSTAGE, int WF = WF_FP8, bool SAHW = false>
 int launch_cfg(GemmArgs& a, hipStream_t stream) {
   const int64_t half = KIND == KIND_GATE_UP ? BN / 2 : BN;
   a.n_tiles = (int)ceil_div(a.N, half);
@@ -552,23 +675,25 @@ int launch_cfg(GemmArgs& a, hipStream_t stream) {
   if constexpr (KIND == KIND_DENSE) {
     mt_bound = ceil_div(a.M, BM);
   } else {
-    const int64_t P = a.T * a.k;
+    const int64_t P = a.E > 0 ? a.T * a.k : 0;
     mt_bound = P / BM + (P < a.E ? P : a.E) + (a.has_shared ? ceil_div(a.T, BM) : 0);
   }
   const int64_t tiles = mt_bound * a.n_tiles;
   if (tiles == 0) return SGL_OK;
   // persistent: as many workgroups per CU as their LDS allows (the 160 KB
   // of a CU), a multiple of 8 so every XCD gets the same number
-  using C = Cfg<KIND, BM, BN, WM, WN, NSTAGE>;
+  using C = Cfg<KIND, BM, BN, WM, WN, NSTAGE, WF, SAHW>;
   constexpr int kLdsPerCU = 160 * 1024;
-  constexpr int kExtra = (KIND == KIND_DENSE ? 4 : 4 * (kMaxGroups + 1)) + BM * 12 + 2 * kMaxKB * 4;
+  constexpr int kExtra = (KIND == KIND_DENSE ? 4 : 4 * (kMaxGroups + 1)) + BM * 12 +
+                         2 * (WF == WF_FP4 ? 1 : kMaxKB) * 4;
+  static_assert(C::SMEM + kExtra <= kLdsPerCU, "tile configuration exceeds the LDS of a CU");
   constexpr int per_cu = kLdsPerCU / (C::SMEM + kExtra) >= 2 ? 2 : 1;
   int64_t wgs = (int64_t)device_cu_count() * per_cu;
   wgs = (wgs + 7) / 8 * 8;
   const int64_t need = (tiles + 7) / 8 * 8;
   if (need < wgs) wgs = need;
   a.m_tiles = (int)mt_bound;
-  gemm_fp8_kernel<KIND, BM, BN, WM, WN, NSTAGE><<<(unsigned)wgs, 64 * WM * WN, 0, stream>>>(a);
+  gemm_fp8_kernel<KIND, BM, BN, WM, WN, NSTAGE, WF, SAHW><<<(unsigned)wgs, 64 * WM * WN, 0, stream>>>(a);
   return check_launch("gemm_fp8");
 }
 
@@ -599,12 +724,14 @@ __device__ __forceinline__ v8i load_frag_global(const uint8_t* p) {
   return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 }
 
-template <int TM>
+template <int TM, int WF, bool SAHW>
 __global__ __launch_bounds__(64 * Skinny<TM>::WAVES) void gemm_skinny_kernel(const GemmArgs args) {
   constexpr int ROWS = 16 * TM;
   constexpr int kSkinnyWaves = Skinny<TM>::WAVES;
+  constexpr bool FP4 = WF == WF_FP4;
   __shared__ float sSa[ROWS][kMaxKB];
-  __shared__ float sSk[kMaxKB];
+  __shared__ float sSk[FP4 ? 1 : kMaxKB];             // fp8: the slab's weight scale per K block
+  __shared__ uint32_t sSb4[FP4 ? 16 : 1][kMaxKB];     // fp4: 4 e8m0 scales per column and K block
   __shared__ float sRed[kSkinnyWaves][ROWS * 16];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -615,15 +742,18 @@ __global__ __launch_bounds__(64 * Skinny<TM>::WAVES) void gemm_skinny_kernel(con
   const int64_t n0 = (int64_t)blockIdx.x * 16;
   const int64_t m0 = (int64_t)blockIdx.y * ROWS;
 
-  // operand rows of this lane (rows past M re-read row M-1; their outputs are dropped)
+  // operand rows of this lane (rows past M re-read row M-1; their outputs are
+  // dropped).  fp8: A and B bytes [32 g4, +32) of each K block; fp4: A bytes
+  // [16 g4, +16) and [64 + 16 g4, +16), B packed bytes [16 g4, +16).
   const uint8_t* arow[TM];
 #pragma unroll
   for (int mi = 0; mi < TM; ++mi) {
     int64_t row = m0 + 16 * mi + r16;
     if (row > M - 1) row = M - 1;
-    arow[mi] = args.a + row * K + 32 * g4;
+    arow[mi] = args.a + row * K + (FP4 ? 16 : 32) * g4;
   }
-  const uint8_t* brow = args.b + (n0 + r16) * K + 32 * g4;
+  const int64_t KROW = FP4 ? K / 2 : K;
+  const uint8_t* brow = args.b + (n0 + r16) * KROW + (FP4 ? 16 : 32) * g4;
 
   // Scale loads are issued first and the first NB operand blocks right
   // after, so waiting for the scales (to stage them in LDS) leaves the
@@ -639,7 +769,20 @@ __global__ __launch_bounds__(64 * Skinny<TM>::WAVES) void gemm_skinny_kernel(con
     sv[j] = (i < ROWS * KB && row < M) ? sa[row * KB + kb] : 0.0f;
   }
   float skv = 0.0f;
-  if (tid < KB) skv = load_scale(args.sb, (n0 / 128) * KB + tid, args.sb_e8m0);
+  constexpr int BPT = FP4 ? (16 * kMaxKB + 64 * kSkinnyWaves - 1) / (64 * kSkinnyWaves) : 1;
+  uint32_t sbw[BPT];
+  if constexpr (FP4) {
+    // dword kb of column c holds the e8m0 scales of its four 32-deep blocks
+    const uint32_t* sb = reinterpret_cast<const uint32_t*>(args.sb);
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      const int i = tid + j * 64 * kSkinnyWaves;
+      const int c = i / KB, kb = i - c * KB;
+      sbw[j] = i < 16 * KB ? sb[(n0 + c) * KB + kb] : 0u;
+    }
+  } else {
+    if (tid < KB) skv = load_scale(args.sb, (n0 / 128) * KB + tid, args.sb_e8m0);
+  }
 
   constexpr int NB = 4;  // K blocks per wavefront whose loads are in flight together
   v8i af[NB][TM], bf[NB];
@@ -648,9 +791,20 @@ __global__ __launch_bounds__(64 * Skinny<TM>::WAVES) void gemm_skinny_kernel(con
     for (int j = 0; j < NB; ++j) {
       const int kb = base + j * kSkinnyWaves;
       if (kb < KB) {
+        if constexpr (FP4) {
 #pragma unroll
-        for (int mi = 0; mi < TM; ++mi) af[j][mi] = load_frag_global(arow[mi] + (int64_t)kb * 128);
-        bf[j] = load_frag_global(brow + (int64_t)kb * 128);
+          for (int mi = 0; mi < TM; ++mi) {
+            const uint4 lo = *reinterpret_cast<const uint4*>(arow[mi] + (int64_t)kb * 128);
+            const uint4 hi = *reinterpret_cast<const uint4*>(arow[mi] + (int64_t)kb * 128 + 64);
+            af[j][mi] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+          }
+          const uint4 v = *reinterpret_cast<const uint4*>(brow + (int64_t)kb * 64);
+          bf[j] = v8i{(int)v.x, (int)v.y, (int)v.z, (int)v.w, 0, 0, 0, 0};
+        } else {
+#pragma unroll
+          for (int mi = 0; mi < TM; ++mi) af[j][mi] = load_frag_global(arow[mi] + (int64_t)kb * 128);
+          bf[j] = load_frag_global(brow + (int64_t)kb * 128);
+        }
       }
     }
   };
@@ -661,7 +815,15 @@ __global__ __launch_bounds__(64 * Skinny<TM>::WAVES) void gemm_skinny_kernel(con
     const int i = tid + j * 64 * kSkinnyWaves;
     if (i < ROWS * KB) sSa[i / KB][i - (i / KB) * KB] = sv[j];
   }
-  if (tid < KB) sSk[tid] = skv;
+  if constexpr (FP4) {
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      const int i = tid + j * 64 * kSkinnyWaves;
+      if (i < 16 * KB) sSb4[i / KB][i - (i / KB) * KB] = sbw[j];
+    }
+  } else {
+    if (tid < KB) sSk[tid] = skv;
+  }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
 
@@ -675,20 +837,37 @@ __global__ __launch_bounds__(64 * Skinny<TM>::WAVES) void gemm_skinny_kernel(con
     for (int j = 0; j < NB; ++j) {
       const int kb = base + j * kSkinnyWaves;
       if (kb < KB) {
-        const float sk = sSk[kb];
+        if constexpr (FP4) {
+          const int sbb = (int)(sSb4[r16][kb] >> (8 * g4));
 #pragma unroll
-        for (int mi = 0; mi < TM; ++mi) {
-          const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[j][mi], bf[j], vzero, 0,
-                                                                         0, 0, 0, 0, 0);
+          for (int mi = 0; mi < TM; ++mi) {
+            if constexpr (SAHW) {
+              const int sae = (int)(__float_as_uint(sSa[16 * mi + r16][kb]) >> 23);
+              acc[mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[j][mi], bf[j], acc[mi], 0, 4,
+                                                                        0, sae, 0, sbb);
+            } else {
+              const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[j][mi], bf[j], vzero, 0,
+                                                                             4, 0, 127, 0, sbb);
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            acc[mi][r] = fmaf(p[r], sSa[16 * mi + 4 * g4 + r][kb] * sk, acc[mi][r]);
+              for (int r = 0; r < 4; ++r) acc[mi][r] = fmaf(p[r], sSa[16 * mi + 4 * g4 + r][kb], acc[mi][r]);
+            }
+          }
+        } else {
+          const float sk = sSk[kb];
+#pragma unroll
+          for (int mi = 0; mi < TM; ++mi) {
+            const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[j][mi], bf[j], vzero, 0,
+                                                                           0, 0, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              acc[mi][r] = fmaf(p[r], sSa[16 * mi + 4 * g4 + r][kb] * sk, acc[mi][r]);
+          }
         }
       }
     }
   }
 
-  // sum the 16 partial tiles; lane (g4, r16) holds rows 4 g4 + r, column r16
+  // sum the partial tiles; lane (g4, r16) holds rows 4 g4 + r, column r16
 #pragma unroll
   for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
@@ -709,19 +888,51 @@ __global__ __launch_bounds__(64 * Skinny<TM>::WAVES) void gemm_skinny_kernel(con
   }
 }
 
-template <int TM>
+template <int TM, int WF = WF_FP8, bool SAHW = false>
 int launch_skinny(GemmArgs& a, hipStream_t stream) {
   dim3 grid((unsigned)(a.N / 16), (unsigned)ceil_div(a.M, (int64_t)(16 * TM)));
-  gemm_skinny_kernel<TM><<<grid, 64 * Skinny<TM>::WAVES, 0, stream>>>(a);
-  return check_launch("gemm_fp8_skinny");
+  gemm_skinny_kernel<TM, WF, SAHW><<<grid, 64 * Skinny<TM>::WAVES, 0, stream>>>(a);
+  return check_launch(WF == WF_FP4 ? "gemm_fp4_skinny" : "gemm_fp8_skinny");
 }
 
 }  // namespace
+
+// FP4 weights: a stage is 256 deep, so two stages fill what three fp8
+// stages of the same tile would (the 128 x 256 tiles run one workgroup per
+// CU with one stage in flight while the other is computed)
+template <bool SAHW>
+int launch_fp4(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
+  const bool big = rows_hint >= 64;
+  switch (kind) {
+    case KIND_DENSE:
+      if (a.M <= kSkinnyMaxM) {
+        if (a.M <= 16) return launch_skinny<1, WF_FP4, SAHW>(a, stream);
+        if (a.M <= 32) return launch_skinny<2, WF_FP4, SAHW>(a, stream);
+        return launch_skinny<4, WF_FP4, SAHW>(a, stream);
+      }
+      if (a.M <= 2048) return launch_cfg<KIND_DENSE, 64, 128, 2, 2, 2, WF_FP4, SAHW>(a, stream);
+      return launch_cfg<KIND_DENSE, 128, 256, 2, 4, 2, WF_FP4, SAHW>(a, stream);
+    case KIND_GATE_UP:
+      return big ? launch_cfg<KIND_GATE_UP, 128, 256, 2, 4, 2, WF_FP4, SAHW>(a, stream)
+                 : launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 3, WF_FP4, SAHW>(a, stream);
+    default:
+      return big ? launch_cfg<KIND_DOWN, 128, 256, 2, 4, 2, WF_FP4, SAHW>(a, stream)
+                 : launch_cfg<KIND_DOWN, 32, 256, 1, 4, 3, WF_FP4, SAHW>(a, stream);
+  }
+}
 
 int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
   if (a.K > 128 * kMaxKB) {
     set_error("gemm: K=%lld above the supported %d", (long long)a.K, 128 * kMaxKB);
     return SGL_ERR_UNSUPPORTED;
+  }
+  if (a.wfmt == WF_FP4) {
+    if (a.K % 256 != 0) {
+      set_error("gemm: FP4 weights need K=%lld to be a multiple of 256", (long long)a.K);
+      return SGL_ERR_INVALID_ARG;
+    }
+    return a.sa_pow2 ? launch_fp4<true>(kind, a, rows_hint, stream)
+                     : launch_fp4<false>(kind, a, rows_hint, stream);
   }
   const bool big = rows_hint >= 64;
   switch (kind) {
@@ -767,6 +978,35 @@ extern "C" int sgl_fp8_gemm(const void* a, const void* sa, const void* b, const 
   g.b = (const uint8_t*)b;
   g.sb = sb;
   g.sb_e8m0 = b_scale_e8m0;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.c = c;
+  g.out_f32 = out_dtype == SGL_F32;
+  return sgl::launch_gemm(sgl::KIND_DENSE, g, M, (hipStream_t)stream);
+}
+
+extern "C" int sgl_fp4_gemm(const void* a, const float* sa, int sa_pow2, const void* b,
+                            const void* sb, void* c, int out_dtype, int64_t M, int64_t N,
+                            int64_t K, sgl_stream_t stream) {
+  SGL_REQUIRE(M >= 0 && N >= 0 && K >= 0, "fp4_gemm: negative shape");
+  SGL_REQUIRE(out_dtype == SGL_BF16 || out_dtype == SGL_F32, "fp4_gemm: out_dtype must be bf16/f32");
+  SGL_REQUIRE(K % 256 == 0, "fp4_gemm: K=%lld must be a multiple of 256", (long long)K);
+  SGL_REQUIRE(N % 16 == 0, "fp4_gemm: N=%lld must be a multiple of 16", (long long)N);
+  if (M == 0 || N == 0) return SGL_OK;
+  SGL_REQUIRE(a && sa && b && sb && c, "fp4_gemm: null pointer");
+  SGL_REQUIRE(M * K < ((int64_t)1 << 31) && N * K / 2 < ((int64_t)1 << 31),
+              "fp4_gemm: operands above 2 GiB are not supported");
+  SGL_REQUIRE(sgl::aligned(a, 16) && sgl::aligned(b, 16) && sgl::aligned(c, 16),
+              "fp4_gemm: A, B and C must be 16-byte aligned");
+  SGL_REQUIRE(sgl::aligned(sa, 4) && sgl::aligned(sb, 4), "fp4_gemm: sa and sb must be 4-byte aligned");
+  sgl::GemmArgs g = {};
+  g.a = (const uint8_t*)a;
+  g.sa = sa;
+  g.b = (const uint8_t*)b;
+  g.sb = sb;
+  g.wfmt = sgl::WF_FP4;
+  g.sa_pow2 = sa_pow2 ? 1 : 0;
   g.M = M;
   g.N = N;
   g.K = K;

@@ -375,9 +375,12 @@ struct MoeWorkspace {
   uint8_t* hq;
   float* hs;
   uint16_t* out;
-  int32_t* tile_ctr;  // [2][8] per-XCD tile counters of the gate/up and down GEMMs
+  int32_t* tile_ctr;  // [4][8] per-XCD tile counters of the gate/up and down GEMMs
+                      // (routed + shared, or one launch each)
   size_t bytes;
 };
+
+constexpr int kTileCtrs = 32;
 
 MoeWorkspace carve(void* base, int64_t T, int64_t H, int64_t I, int E, int k, int has_shared) {
   MoeWorkspace w = {};
@@ -399,15 +402,20 @@ MoeWorkspace carve(void* base, int64_t T, int64_t H, int64_t I, int E, int k, in
   w.hq = take(rows * I);
   w.hs = reinterpret_cast<float*>(take(rows * (I / 128) * 4));
   w.out = reinterpret_cast<uint16_t*>(take(T * (k + has_shared) * H * 2));
-  w.tile_ctr = reinterpret_cast<int32_t*>(take(16 * 4));
+  w.tile_ctr = reinterpret_cast<int32_t*>(take(kTileCtrs * 4));
   w.bytes = (size_t)off;
   return w;
 }
 
-int check_moe_shapes(const char* what, int64_t T, int64_t H, int64_t I, int E, int k) {
+int check_moe_shapes(const char* what, int64_t T, int64_t H, int64_t I, int E, int k,
+                     int expert_format) {
   SGL_REQUIRE(T >= 0 && H > 0 && I > 0, "%s: bad shape T=%lld H=%lld I=%lld", what, (long long)T,
               (long long)H, (long long)I);
   SGL_REQUIRE(H % 128 == 0 && I % 128 == 0, "%s: H and I must be multiples of 128", what);
+  SGL_REQUIRE(expert_format == SGL_EXPERT_FP8_BLOCK128 || expert_format == SGL_EXPERT_FP4_E2M1,
+              "%s: bad expert_format %d", what, expert_format);
+  SGL_REQUIRE(expert_format != SGL_EXPERT_FP4_E2M1 || (H % 256 == 0 && I % 256 == 0),
+              "%s: FP4 experts need H and I multiples of 256", what);
   SGL_REQUIRE(E >= 1 && E <= kMaxPermE, "%s: E=%d not in [1, %d]", what, E, kMaxPermE);
   SGL_REQUIRE(k >= 1 && k <= 16 && k <= E, "%s: k=%d not in [1, min(16, E)]", what, k);
   SGL_REQUIRE(T * k < 0x7FFFFFFF && T * (k + 1) * H < ((int64_t)1 << 46), "%s: too many tokens",
@@ -444,17 +452,28 @@ int launch_permute(const int32_t* ids, int64_t T, int k, int E, int32_t* counts,
   return check_launch("moe_permute");
 }
 
+bool pow2_scale_mode(int scale_mode) {
+  return scale_mode == SGL_SCALE_TORCH_UE8M0 || scale_mode == SGL_SCALE_TILELANG_UE8M0;
+}
+
+// The routed experts in `expert_format`; the shared expert (experts[E]) is
+// always FP8 128 x 128 (deepseek_infer/model.py:623-626 builds it without the
+// routed experts' dtype).  FP4 routed experts run in a launch of their own,
+// followed by the shared expert's FP8 launch over the rows from offsets[E].
+// tile_ctr: 16 zeroed counters (or null) for the two launches.
 int run_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I, int E, int k,
-                    const int32_t* offsets, const int32_t* sorted_slot, const float* route_w,
-                    const sgl_expert_ptrs* experts, int has_shared, float swiglu_limit,
-                    int scale_mode, void* hq, float* hs, int* tile_ctr, hipStream_t stream) {
-  int rc = check_moe_shapes("moe_gate_up", T, H, I, E, k);
+                const int32_t* offsets, const int32_t* sorted_slot, const float* route_w,
+                const sgl_expert_ptrs* experts, int has_shared, int expert_format,
+                float swiglu_limit, int scale_mode, void* hq, float* hs, int* tile_ctr,
+                hipStream_t stream) {
+  int rc = check_moe_shapes("moe_gate_up", T, H, I, E, k, expert_format);
   if (rc) return rc;
   SGL_REQUIRE(scale_mode >= 0 && scale_mode <= 3, "moe_gate_up: bad scale_mode %d", scale_mode);
   if (T == 0) return SGL_OK;
   SGL_REQUIRE(xq && xs && offsets && sorted_slot && experts && hq && hs,
               "moe_gate_up: null pointer");
   SGL_REQUIRE(aligned(xq, 16) && aligned(hq, 8), "moe_gate_up: xq/hq misaligned");
+  const bool split = expert_format == SGL_EXPERT_FP4_E2M1;
   GemmArgs g = {};
   g.a = (const uint8_t*)xq;
   g.sa = xs;
@@ -464,7 +483,8 @@ int run_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I
   g.route_w = route_w;
   g.E = E;
   g.k = k;
-  g.has_shared = has_shared ? 1 : 0;
+  g.has_shared = has_shared && !split ? 1 : 0;
+  g.out_k = k + (has_shared ? 1 : 0);
   g.T = T;
   g.N = I;
   g.K = H;
@@ -472,19 +492,31 @@ int run_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I
   g.hs = hs;
   g.swiglu_limit = swiglu_limit;
   g.scale_mode = scale_mode;
+  g.wfmt = split ? WF_FP4 : WF_FP8;
+  g.sa_pow2 = pow2_scale_mode(scale_mode);
   g.tile_ctr = tile_ctr;
-  return launch_gemm(KIND_GATE_UP, g, T * k / E, stream);
+  if ((rc = launch_gemm(KIND_GATE_UP, g, T * k / E, stream)) || !split || !has_shared) return rc;
+  GemmArgs sh = g;  // the shared expert: one group whose rows start at offsets[E]
+  sh.E = 0;
+  sh.offsets = offsets + E;
+  sh.experts = experts + E;
+  sh.has_shared = 1;
+  sh.wfmt = WF_FP8;
+  sh.sa_pow2 = 0;
+  sh.tile_ctr = tile_ctr ? tile_ctr + 8 : nullptr;
+  return launch_gemm(KIND_GATE_UP, sh, T, stream);
 }
 
 int run_down(const void* hq, const float* hs, int64_t T, int64_t H, int64_t I, int E, int k,
-                 const int32_t* offsets, const int32_t* sorted_slot,
-                 const sgl_expert_ptrs* experts, int has_shared, void* out, int* tile_ctr,
+             const int32_t* offsets, const int32_t* sorted_slot, const sgl_expert_ptrs* experts,
+             int has_shared, int expert_format, int scale_mode, void* out, int* tile_ctr,
              hipStream_t stream) {
-  int rc = check_moe_shapes("moe_down", T, H, I, E, k);
+  int rc = check_moe_shapes("moe_down", T, H, I, E, k, expert_format);
   if (rc) return rc;
   if (T == 0) return SGL_OK;
   SGL_REQUIRE(hq && hs && offsets && sorted_slot && experts && out, "moe_down: null pointer");
   SGL_REQUIRE(aligned(hq, 16), "moe_down: hq misaligned");
+  const bool split = expert_format == SGL_EXPERT_FP4_E2M1;
   GemmArgs g = {};
   g.a = (const uint8_t*)hq;
   g.sa = hs;
@@ -493,13 +525,25 @@ int run_down(const void* hq, const float* hs, int64_t T, int64_t H, int64_t I, i
   g.sorted_slot = sorted_slot;
   g.E = E;
   g.k = k;
-  g.has_shared = has_shared ? 1 : 0;
+  g.has_shared = has_shared && !split ? 1 : 0;
+  g.out_k = k + (has_shared ? 1 : 0);
   g.T = T;
   g.N = H;
   g.K = I;
   g.c = out;
+  g.wfmt = split ? WF_FP4 : WF_FP8;
+  g.sa_pow2 = pow2_scale_mode(scale_mode);
   g.tile_ctr = tile_ctr;
-  return launch_gemm(KIND_DOWN, g, T * k / E, stream);
+  if ((rc = launch_gemm(KIND_DOWN, g, T * k / E, stream)) || !split || !has_shared) return rc;
+  GemmArgs sh = g;
+  sh.E = 0;
+  sh.offsets = offsets + E;
+  sh.experts = experts + E;
+  sh.has_shared = 1;
+  sh.wfmt = WF_FP8;
+  sh.sa_pow2 = 0;
+  sh.tile_ctr = tile_ctr ? tile_ctr + 8 : nullptr;
+  return launch_gemm(KIND_DOWN, sh, T, stream);
 }
 
 }  // namespace
@@ -543,17 +587,19 @@ int sgl_moe_permute(const int32_t* ids, int64_t T, int k, int E, int32_t* counts
 
 int sgl_moe_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I, int E, int k,
                     const int32_t* offsets, const int32_t* sorted_slot, const float* route_w,
-                    const sgl_expert_ptrs* experts, int has_shared, float swiglu_limit,
-                    int scale_mode, void* hq, float* hs, sgl_stream_t stream) {
+                    const sgl_expert_ptrs* experts, int has_shared, int expert_format,
+                    float swiglu_limit, int scale_mode, void* hq, float* hs, sgl_stream_t stream) {
   return sgl::run_gate_up(xq, xs, T, H, I, E, k, offsets, sorted_slot, route_w, experts, has_shared,
-                          swiglu_limit, scale_mode, hq, hs, nullptr, (hipStream_t)stream);
+                          expert_format, swiglu_limit, scale_mode, hq, hs, nullptr,
+                          (hipStream_t)stream);
 }
 
 int sgl_moe_down(const void* hq, const float* hs, int64_t T, int64_t H, int64_t I, int E, int k,
                  const int32_t* offsets, const int32_t* sorted_slot,
-                 const sgl_expert_ptrs* experts, int has_shared, void* out, sgl_stream_t stream) {
-  return sgl::run_down(hq, hs, T, H, I, E, k, offsets, sorted_slot, experts, has_shared, out,
-                       nullptr, (hipStream_t)stream);
+                 const sgl_expert_ptrs* experts, int has_shared, int expert_format, int scale_mode,
+                 void* out, sgl_stream_t stream) {
+  return sgl::run_down(hq, hs, T, H, I, E, k, offsets, sorted_slot, experts, has_shared,
+                       expert_format, scale_mode, out, nullptr, (hipStream_t)stream);
 }
 
 int sgl_moe_combine(const void* out, const int32_t* ids, int64_t T, int k, int64_t H,
@@ -574,9 +620,9 @@ size_t sgl_moe_workspace_size(int64_t T, int64_t H, int64_t I, int E, int k, int
 
 int sgl_moe_forward(const void* x, int64_t T, int64_t H, int64_t I, int E, int k,
                     const int32_t* ids, const float* weights, const sgl_expert_ptrs* experts,
-                    int has_shared, float swiglu_limit, int scale_mode, void* workspace,
-                    size_t workspace_bytes, void* y, sgl_stream_t stream) {
-  int rc = sgl::check_moe_shapes("moe_forward", T, H, I, E, k);
+                    int has_shared, int expert_format, float swiglu_limit, int scale_mode,
+                    void* workspace, size_t workspace_bytes, void* y, sgl_stream_t stream) {
+  int rc = sgl::check_moe_shapes("moe_forward", T, H, I, E, k, expert_format);
   if (rc) return rc;
   SGL_REQUIRE(scale_mode >= 0 && scale_mode <= 3, "moe_forward: bad scale_mode %d", scale_mode);
   if (T == 0) return SGL_OK;
@@ -593,13 +639,14 @@ int sgl_moe_forward(const void* x, int64_t T, int64_t H, int64_t I, int E, int k
   hipStream_t st = (hipStream_t)stream;
   // the permute also zeroes the GEMMs' tile counters
   if ((rc = sgl::launch_permute(ids, T, k, E, w.counts, w.offsets, w.sorted_slot, w.slot_pos,
-                                w.tile_ctr, 16, st)))
+                                w.tile_ctr, sgl::kTileCtrs, st)))
     return rc;
   if ((rc = sgl::run_gate_up(w.xq, w.xs, T, H, I, E, k, w.offsets, w.sorted_slot, weights, experts,
-                             has_shared, swiglu_limit, scale_mode, w.hq, w.hs, w.tile_ctr, st)))
+                             has_shared, expert_format, swiglu_limit, scale_mode, w.hq, w.hs,
+                             w.tile_ctr, st)))
     return rc;
   if ((rc = sgl::run_down(w.hq, w.hs, T, H, I, E, k, w.offsets, w.sorted_slot, experts, has_shared,
-                          w.out, w.tile_ctr + 8, st)))
+                          expert_format, scale_mode, w.out, w.tile_ctr + 16, st)))
     return rc;
   sgl::combine_kernel<<<(unsigned)T, 256, 0, st>>>(w.out, ids, T, k, H, has_shared, E,
                                                     (uint16_t*)y);

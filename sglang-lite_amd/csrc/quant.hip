@@ -167,6 +167,70 @@ __global__ void e8m0_to_f32_kernel(const uint8_t* __restrict__ src, float* __res
   }
 }
 
+// e2m1 code -> fp32: sign bit 3, exponent bits 2..1 (bias 1), mantissa bit 0
+// (0, 0.5, 1, 1.5, 2, 3, 4, 6 and their negatives)
+__device__ __forceinline__ float e2m1_value(uint32_t c) {
+  const uint32_t e = (c >> 1) & 3u, m = c & 1u;
+  const float mag = e == 0 ? 0.5f * (float)m : ldexpf(1.0f + 0.5f * (float)m, (int)e - 1);
+  return (c & 8u) ? -mag : mag;
+}
+
+// Lossless FP4 -> FP8 weight repack (deepseek_infer/convert.py:17-52), one
+// workgroup per 128 x 128 block.  Thread t covers row t/2 of the block and
+// its 64 elements [64 (t%2), +64): 32 packed bytes under two e8m0 scales.
+__global__ __launch_bounds__(256) void fp4_to_fp8_weight_kernel(
+    const uint8_t* __restrict__ b, const uint8_t* __restrict__ sb, int64_t K,
+    uint8_t* __restrict__ q, uint8_t* __restrict__ s_out) {
+  __shared__ uint32_t sMax[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t kb = blockIdx.x, nb = blockIdx.y;
+  const int r = tid >> 1, hf = tid & 1;
+  const int64_t n = nb * 128 + r;
+  const uint8_t* sp = sb + n * (K / 32) + kb * 4 + hf * 2;
+  const uint32_t s0 = sp[0], s1 = sp[1];
+  // the block's largest scale; 0xFF (NaN) is also the largest byte, and a
+  // NaN scale makes the whole block NaN as torch's amax does
+  uint32_t m = s0 > s1 ? s0 : s1;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t v = (uint32_t)__shfl_xor((int)m, o, 64);
+    m = v > m ? v : m;
+  }
+  if (lane == 0) sMax[wave] = m;
+  __syncthreads();
+  uint32_t smax = sMax[0];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) smax = sMax[w] > smax ? sMax[w] : smax;
+  const bool nan = smax == 0xFFu;
+  // s = smax / 2^6 (clamped at the smallest e8m0, 2^-127)
+  const int sbyte = smax >= 6 ? (int)smax - 6 : 0;
+  if (tid == 0) s_out[nb * (K / 128) + kb] = nan ? 0xFF : (uint8_t)sbyte;
+
+  const uint8_t* bp = b + n * (K / 2) + kb * 64 + hf * 32;
+  uint8_t* qp = q + n * K + kb * 128 + hf * 64;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {  // packed bytes [16 h, 16 h + 16): elements under scale s_h
+    const uint4 v = *reinterpret_cast<const uint4*>(bp + 16 * h);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    const int off = (int)(h ? s1 : s0) - sbyte;  // scale / s = 2^off, off <= 6
+    uint32_t o[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float f[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t byte = (w[i] >> (8 * j)) & 0xFFu;
+        f[2 * j] = ldexpf(e2m1_value(byte & 0xFu), off);
+        f[2 * j + 1] = ldexpf(e2m1_value(byte >> 4), off);
+      }
+      o[2 * i] = nan ? 0x7F7F7F7Fu : pk4_e4m3_exact(f[0], f[1], f[2], f[3]);
+      o[2 * i + 1] = nan ? 0x7F7F7F7Fu : pk4_e4m3_exact(f[4], f[5], f[6], f[7]);
+    }
+    *reinterpret_cast<uint4*>(qp + 32 * h) = make_uint4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<uint4*>(qp + 32 * h + 16) = make_uint4(o[4], o[5], o[6], o[7]);
+  }
+}
+
 // Self-check of the hardware conversions over every fp32 bit pattern: thread
 // t of a launch covers inputs start + 4t .. start + 4t + 3.
 //   counts[0]: pk4_e4m3_exact != f32_to_e4m3   (all inputs)
@@ -304,6 +368,21 @@ int sgl_e8m0_to_f32(const void* src, float* dst, int64_t n, sgl_stream_t stream)
   sgl::e8m0_to_f32_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>((const uint8_t*)src,
                                                                              dst, n);
   return sgl::check_launch("e8m0_to_f32");
+}
+
+int sgl_fp4_to_fp8_weight(const void* b, const void* sb, int64_t N, int64_t K, void* q,
+                          void* s_out, sgl_stream_t stream) {
+  SGL_REQUIRE(N >= 0 && K >= 0 && N % 128 == 0 && K % 128 == 0,
+              "fp4_to_fp8_weight: N=%lld and K=%lld must be multiples of 128", (long long)N,
+              (long long)K);
+  if (N == 0 || K == 0) return SGL_OK;
+  SGL_REQUIRE(b && sb && q && s_out, "fp4_to_fp8_weight: null pointer");
+  SGL_REQUIRE(sgl::aligned(b, 16) && sgl::aligned(q, 16), "fp4_to_fp8_weight: b and q must be 16-byte aligned");
+  SGL_REQUIRE(N / 128 <= 65535, "fp4_to_fp8_weight: N too large");
+  dim3 grid((unsigned)(K / 128), (unsigned)(N / 128));
+  sgl::fp4_to_fp8_weight_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(
+      (const uint8_t*)b, (const uint8_t*)sb, K, (uint8_t*)q, (uint8_t*)s_out);
+  return sgl::check_launch("fp4_to_fp8_weight");
 }
 
 int sgl_check_conversions(unsigned long long* counts, sgl_stream_t stream) {

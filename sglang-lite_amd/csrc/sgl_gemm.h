@@ -8,6 +8,11 @@ namespace sgl {
 
 enum GemmKind : int { KIND_DENSE = 0, KIND_GATE_UP = 1, KIND_DOWN = 2 };
 
+// Weight formats: e4m3 with one scale per 128 x 128 block (fp32, or e8m0 for
+// dense sb_e8m0), or packed e2m1 (low nibble = even K) with one e8m0 scale
+// per row and 32-deep K block.
+enum WeightFmt : int { WF_FP8 = 0, WF_FP4 = 1 };
+
 // One launch of the block-scaled FP8 GEMM family.
 //   dense   : C[M, N] = A[M, K] . B[N, K]^T                       (fp8_gemm)
 //   gate_up : rows of the routed slots (+ shared rows), A gathered from the
@@ -19,15 +24,18 @@ struct GemmArgs {
   const uint8_t* a;   // dense: A [M, K]; gate_up: xq [T, K]; down: hq [rows, K]
   const void* sa;     // fp32 row scales [*, K/128]
   const uint8_t* b;   // dense only: B [N, K]
-  const void* sb;     // dense only: [ceil(N/128), K/128]
+  const void* sb;     // dense only: fp8 [ceil(N/128), K/128]; fp4 e8m0 [N, K/32]
   int sb_e8m0;
+  int wfmt;           // WeightFmt of B (moe: of every expert in the launch)
+  int sa_pow2;        // activation scales are powers of two: applied inside the MFMA
   const sgl_expert_ptrs* experts;  // moe: device array [E (+1)]
   const int32_t* offsets;          // moe: [E + 1]
   const int32_t* sorted_slot;      // moe: [T * k]
   const float* route_w;            // gate_up: [T * k] slot-indexed (may be null)
-  int E, k, has_shared;
+  int E, k, has_shared;  // has_shared: the launch includes the shared expert's rows
+  int out_k;             // down: output rows per token (k + the layer's shared expert)
   int64_t T;
-  int64_t M, N, K;  // dense: M x N x K; gate_up: N = I, K = H; down: N = H, K = I
+  int64_t M, N, K;  // dense: M x N x K; gate_up: N = I, K = H; down: N = H, K = I (logical K)
   void* c;          // dense: [M, N]; down: [T * (k + has_shared), N]
   int out_f32;      // dense output fp32 instead of bf16
   uint8_t* hq;      // gate_up: [rows, N] e4m3

@@ -16,7 +16,7 @@ from typing import Optional
 LIB_DIR = Path(__file__).resolve().parent / "lib"
 LIB_PATH = LIB_DIR / "libsglang_lite_amd.so"
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 SGL_OK = 0
 SGL_ERR_INVALID_ARG = -1
@@ -36,6 +36,8 @@ SCALE_KV_UE8M0 = 4
 SCORE_SOFTMAX, SCORE_SIGMOID, SCORE_SQRTSOFTPLUS = 0, 1, 2
 # sgl_kv_layout
 KV_LAYOUT_A, KV_LAYOUT_B = 0, 1
+# sgl_expert_format
+EXPERT_FP8_BLOCK128, EXPERT_FP4_E2M1 = 0, 1
 
 P = c_void_p
 I64 = c_int64
@@ -50,18 +52,22 @@ SIGNATURES = {
     "sgl_e8m0_to_f32": (c_int, [P, P, I64, P]),
     "sgl_check_conversions": (c_int, [P, P]),
     "sgl_fp8_gemm": (c_int, [P, P, P, P, c_int, P, c_int, I64, I64, I64, P]),
+    "sgl_fp4_gemm": (c_int, [P, P, c_int, P, P, P, c_int, I64, I64, I64, P]),
+    "sgl_fp4_to_fp8_weight": (c_int, [P, P, I64, I64, P, P, P]),
     "sgl_moe_route_topk": (c_int, [P, I64, c_int, c_int, c_int, P, c_float, P, P, P]),
     "sgl_moe_permute": (c_int, [P, I64, c_int, c_int, P, P, P, P, P]),
     "sgl_moe_gate_up": (
         c_int,
-        [P, P, I64, I64, I64, c_int, c_int, P, P, P, P, c_int, c_float, c_int, P, P, P],
+        [P, P, I64, I64, I64, c_int, c_int, P, P, P, P, c_int, c_int, c_float, c_int, P, P, P],
     ),
-    "sgl_moe_down": (c_int, [P, P, I64, I64, I64, c_int, c_int, P, P, P, c_int, P, P]),
+    "sgl_moe_down": (
+        c_int, [P, P, I64, I64, I64, c_int, c_int, P, P, P, c_int, c_int, c_int, P, P]
+    ),
     "sgl_moe_combine": (c_int, [P, P, I64, c_int, I64, c_int, P, P]),
     "sgl_moe_workspace_size": (c_size_t, [I64, I64, I64, c_int, c_int, c_int]),
     "sgl_moe_forward": (
         c_int,
-        [P, I64, I64, I64, c_int, c_int, P, P, P, c_int, c_float, c_int, P, c_size_t, P, P],
+        [P, I64, I64, I64, c_int, c_int, P, P, P, c_int, c_int, c_float, c_int, P, c_size_t, P, P],
     ),
     "sgl_kv_pack": (c_int, [P, c_int, I64, I64, c_int, c_int, c_int, c_int, P, P]),
     "sgl_kv_to_paged": (c_int, [P, I64, c_int, P, P]),

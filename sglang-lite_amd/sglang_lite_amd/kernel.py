@@ -2,7 +2,8 @@
 
 Same names, arguments, return values and assertions as
 ``engine/vendor/deepseek_infer/kernel.py`` (``act_quant`` :105-125,
-``fp8_gemm`` :257-273), plus the DeepGEMM quant helpers
+``fp8_gemm`` :257-273, ``fp4_gemm`` :519-536), the FP4 -> FP8 weight repack of
+``deepseek_infer/convert.py:17-52``, plus the DeepGEMM quant helpers
 (``deep_gemm_sm120/utils/math.py:25-37,50-60``) the synthetic weights use.
 Every op runs a hand-written HIP kernel from ``libsglang_lite_amd.so``; CPU
 tensors are refused.
@@ -26,6 +27,7 @@ from . import _lib
 
 FP8 = torch.float8_e4m3fn
 E8M0 = torch.float8_e8m0fnu
+FP4 = torch.float4_e2m1fn_x2  # two e2m1 codes per byte, low nibble = even K
 
 
 def act_quant_formula() -> str:
@@ -166,10 +168,98 @@ def fp8_gemm(
     return out
 
 
+def fp4_bytes(b: torch.Tensor) -> torch.Tensor:
+    """Packed e2m1 weight [N, K/2] (float4_e2m1fn_x2, or its int8 / uint8 view
+    as convert.py stores it) as a uint8 view."""
+    if b.dtype not in (FP4, torch.int8, torch.uint8):
+        raise TypeError(f"FP4 weight must be float4_e2m1fn_x2 / int8 / uint8, got {b.dtype}")
+    return b.view(torch.uint8)
+
+
+def fp4_weight_scale(s: torch.Tensor) -> torch.Tensor:
+    """e8m0 [N, K/32] weight scales (fp32 powers of two are cast to e8m0)."""
+    if s.dtype == E8M0:
+        return s.contiguous()
+    if s.dtype == torch.float32:
+        return s.contiguous().to(E8M0)
+    raise TypeError(f"FP4 weight scales must be float8_e8m0fnu or float32, got {s.dtype}")
+
+
+def fp4_gemm(
+    a: torch.Tensor,
+    a_s: torch.Tensor,
+    b: torch.Tensor,
+    b_s: torch.Tensor,
+    scale_dtype: torch.dtype = torch.float32,
+    *,
+    out: Optional[torch.Tensor] = None,
+    a_scale_pow2: Optional[bool] = None,
+) -> torch.Tensor:
+    """C[M,N] = A_fp8[M,K] @ B_fp4[N,K]^T (deepseek_infer/kernel.py:519-536).
+
+    A has one scale per 128 K (fp32 or e8m0), B one e8m0 scale per 32 K and is
+    stored as [N, K//2] float4_e2m1fn_x2 (2 FP4 values per byte, packed along
+    K).  Output dtype is torch's default dtype (bf16 or fp32).  With e8m0
+    activation scales (or ``a_scale_pow2=True`` for fp32 powers of two) both
+    scales are applied inside the MFMA; otherwise each 128-deep partial is
+    promoted with the fp32 activation scale.  K % 256 == 0."""
+    del scale_dtype
+    assert a.is_contiguous() and b.is_contiguous(), "Input tensors must be contiguous"
+    assert a_s.is_contiguous() and b_s.is_contiguous(), "Scaling factor tensors must be contiguous"
+    _lib.require_device(a, a_s, b, b_s, what="fp4_gemm")
+    if a.dtype != FP8:
+        raise TypeError(f"fp4_gemm: activations must be float8_e4m3fn, got {a.dtype}")
+    bq = fp4_bytes(b)
+    K = a.size(-1)
+    M = a.numel() // K
+    N = b.size(0)
+    if bq.dim() != 2 or bq.size(1) * 2 != K:
+        raise ValueError(f"fp4_gemm: weight must be [N, K/2] = [{N}, {K // 2}], got {tuple(b.shape)}")
+    odt = torch.get_default_dtype()
+    if odt not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"fp4_gemm: default dtype must be bfloat16 or float32, got {odt}")
+    if out is None:
+        out = a.new_empty(*a.size()[:-1], N, dtype=odt)
+    else:
+        assert out.is_contiguous() and out.dtype == odt and out.numel() == M * N
+    pow2 = bool(a_scale_pow2) if a_scale_pow2 is not None else a_s.dtype == E8M0
+    if _scale_flag(a_s, "fp4_gemm a_s"):
+        a_s = e8m0_to_f32(a_s)  # the kernel streams fp32 activation scales
+    bs = fp4_weight_scale(b_s)
+    _lib.call(
+        "sgl_fp4_gemm",
+        a.data_ptr(), a_s.data_ptr(), int(pow2), bq.data_ptr(), bs.data_ptr(),
+        out.data_ptr(), _lib.SGL_BF16 if odt == torch.bfloat16 else _lib.SGL_F32,
+        M, N, K, _lib.stream_of(a),
+    )
+    return out
+
+
+def cast_e2m1fn_to_e4m3fn(x: torch.Tensor, scale: torch.Tensor):
+    """Lossless FP4 -> FP8 weight repack (deepseek_infer/convert.py:17-52):
+    packed e2m1 [out, in/2] (int8 / uint8 / float4_e2m1fn_x2) with e8m0 scales
+    [out, in/32] -> (e4m3 [out, in], e8m0 [out/128, in/128])."""
+    xb = fp4_bytes(x)
+    assert xb.ndim == 2
+    out_dim, in_dim = xb.size()
+    in_dim *= 2
+    assert in_dim % 128 == 0 and out_dim % 128 == 0
+    assert scale.size(0) == out_dim and scale.size(1) == in_dim // 32
+    _lib.require_device(xb, scale, what="cast_e2m1fn_to_e4m3fn")
+    sb = fp4_weight_scale(scale)
+    q = torch.empty(out_dim, in_dim, dtype=FP8, device=xb.device)
+    s = torch.empty(out_dim // 128, in_dim // 128, dtype=E8M0, device=xb.device)
+    _lib.call("sgl_fp4_to_fp8_weight", xb.contiguous().data_ptr(), sb.data_ptr(), out_dim, in_dim,
+              q.data_ptr(), s.data_ptr(), _lib.stream_of(xb))
+    return q, s
+
+
 __all__ = [
     "act_quant",
     "act_quant_formula",
+    "cast_e2m1fn_to_e4m3fn",
     "e8m0_to_f32",
+    "fp4_gemm",
     "fp8_gemm",
     "per_block_cast_to_fp8",
     "per_token_cast_to_fp8",

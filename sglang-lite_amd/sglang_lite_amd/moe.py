@@ -23,7 +23,7 @@ from typing import List, Optional, Sequence, Tuple
 import torch
 
 from . import _lib
-from .kernel import FP8, E8M0, e8m0_to_f32
+from .kernel import FP4, FP8, E8M0, e8m0_to_f32, fp4_bytes, fp4_weight_scale
 
 SCORE_FUNCS = {"softmax": _lib.SCORE_SOFTMAX, "sigmoid": _lib.SCORE_SIGMOID,
                "sqrtsoftplus": _lib.SCORE_SQRTSOFTPLUS}
@@ -52,33 +52,52 @@ class ExpertTable:
     I: int
     has_shared: bool
     keep: List[torch.Tensor] = field(default_factory=list)
+    fmt: int = _lib.EXPERT_FP8_BLOCK128  # sgl_expert_format of the routed experts
 
     @staticmethod
     def build(experts: Sequence[Tuple[torch.Tensor, ...]],
               shared: Optional[Tuple[torch.Tensor, ...]] = None) -> "ExpertTable":
-        """``experts``: per expert ``(w1, w3, w2, s1, s3, s2)`` with w1/w3 e4m3
-        [I, H], w2 e4m3 [H, I] and their 128x128 scales (fp32 or e8m0)."""
+        """``experts``: per expert ``(w1, w3, w2, s1, s3, s2)``, either FP8 (w1/w3
+        e4m3 [I, H], w2 e4m3 [H, I], 128x128 scales fp32 or e8m0) or FP4 (w1/w3
+        packed e2m1 [I, H/2], w2 [H, I/2] as float4_e2m1fn_x2 / int8 / uint8,
+        e8m0 scales per 32 inputs: [I, H/32], [H, I/32]); every routed expert in
+        one format.  The shared expert is FP8 (deepseek_infer/model.py:626)."""
         rows = list(experts) + ([shared] if shared is not None else [])
         if not rows:
             raise ValueError("ExpertTable needs at least one expert")
+        fp4 = bool(experts) and experts[0][0].dtype in (FP4, torch.int8, torch.uint8)
         w1 = rows[0][0]
-        I, H = int(w1.shape[0]), int(w1.shape[1])
+        I = int(w1.shape[0])
+        H = int(w1.shape[1]) * (2 if fp4 else 1)  # packed e2m1 rows hold two inputs per byte
         dev = w1.device
         keep: List[torch.Tensor] = []
         vals = []
-        for r in rows:
+        for i, r in enumerate(rows):
             w1, w3, w2, s1, s3, s2 = r
-            for w, shape in ((w1, (I, H)), (w3, (I, H)), (w2, (H, I))):
-                if w.dtype != FP8 or tuple(w.shape) != shape or not w.is_contiguous():
-                    raise ValueError(f"expert weight must be contiguous e4m3 {shape}, got "
-                                     f"{w.dtype} {tuple(w.shape)}")
-                _lib.require_device(w, what="ExpertTable")
-            fs = [_f32_scale(s) for s in (s1, s3, s2)]
-            keep += [w1, w3, w2, *fs]
-            vals.append([w1.data_ptr(), w3.data_ptr(), w2.data_ptr(),
+            if fp4 and i < len(experts):
+                ws = [fp4_bytes(w) for w in (w1, w3, w2)]
+                for w, shape in zip(ws, ((I, H // 2), (I, H // 2), (H, I // 2))):
+                    if tuple(w.shape) != shape or not w.is_contiguous():
+                        raise ValueError(f"FP4 expert weight must be contiguous {shape}, got "
+                                         f"{tuple(w.shape)}")
+                fs = [fp4_weight_scale(s) for s in (s1, s3, s2)]
+                for sc, shape in zip(fs, ((I, H // 32), (I, H // 32), (H, I // 32))):
+                    if tuple(sc.shape) != shape:
+                        raise ValueError(f"FP4 expert scale must be {shape}, got {tuple(sc.shape)}")
+            else:
+                ws = [w1, w3, w2]
+                for w, shape in zip(ws, ((I, H), (I, H), (H, I))):
+                    if w.dtype != FP8 or tuple(w.shape) != shape or not w.is_contiguous():
+                        raise ValueError(f"expert weight must be contiguous e4m3 {shape}, got "
+                                         f"{w.dtype} {tuple(w.shape)}")
+                fs = [_f32_scale(s) for s in (s1, s3, s2)]
+            _lib.require_device(*ws, *fs, what="ExpertTable")
+            keep += [*ws, *fs]
+            vals.append([ws[0].data_ptr(), ws[1].data_ptr(), ws[2].data_ptr(),
                          fs[0].data_ptr(), fs[1].data_ptr(), fs[2].data_ptr()])
         ptrs = torch.tensor(vals, dtype=torch.int64).to(dev)
-        return ExpertTable(ptrs, len(experts), H, I, shared is not None, keep)
+        fmt = _lib.EXPERT_FP4_E2M1 if fp4 else _lib.EXPERT_FP8_BLOCK128
+        return ExpertTable(ptrs, len(experts), H, I, shared is not None, keep, fmt)
 
 
 def route_topk(logits: torch.Tensor, k: int, score_func: str = "softmax",
@@ -135,18 +154,21 @@ def gate_up(xq, xs, offsets, sorted_slot, route_w, table: ExpertTable, k: int,
     hs = torch.empty(rows, table.I // 128, dtype=torch.float32, device=xq.device)
     _lib.call("sgl_moe_gate_up", xq.data_ptr(), xs.data_ptr(), T, H, table.I, table.E, k,
               offsets.data_ptr(), sorted_slot.data_ptr(), _lib.ptr(route_w), table.ptrs.data_ptr(),
-              int(table.has_shared), float(swiglu_limit), int(scale_mode), hq.data_ptr(),
+              int(table.has_shared), table.fmt, float(swiglu_limit), int(scale_mode), hq.data_ptr(),
               hs.data_ptr(), _lib.stream_of(xq))
     return hq, hs
 
 
-def down(hq, hs, offsets, sorted_slot, table: ExpertTable, T: int, k: int):
-    """Grouped down GEMM.  Returns bf16 [T, k (+1), H] (token-major expert rows)."""
+def down(hq, hs, offsets, sorted_slot, table: ExpertTable, T: int, k: int,
+         scale_mode: int = _lib.SCALE_TORCH_FP32):
+    """Grouped down GEMM (``scale_mode``: the mode ``hs`` was made with).
+    Returns bf16 [T, k (+1), H] (token-major expert rows)."""
     kk = k + (1 if table.has_shared else 0)
     out = torch.empty(T, kk, table.H, dtype=torch.bfloat16, device=hq.device)
     _lib.call("sgl_moe_down", hq.data_ptr(), hs.data_ptr(), T, table.H, table.I, table.E, k,
               offsets.data_ptr(), sorted_slot.data_ptr(), table.ptrs.data_ptr(),
-              int(table.has_shared), out.data_ptr(), _lib.stream_of(hq))
+              int(table.has_shared), table.fmt, int(scale_mode), out.data_ptr(),
+              _lib.stream_of(hq))
     return out
 
 
@@ -193,8 +215,9 @@ def moe_forward(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, table
     ws = (workspace or MoEWorkspace()).get(nbytes, x.device)
     y = out if out is not None else torch.empty(T, H, dtype=torch.bfloat16, device=x.device)
     _lib.call("sgl_moe_forward", x.data_ptr(), T, H, table.I, table.E, k, ids.data_ptr(),
-              w.data_ptr(), table.ptrs.data_ptr(), int(table.has_shared), float(swiglu_limit),
-              int(scale_mode), ws.data_ptr(), ws.numel(), y.data_ptr(), _lib.stream_of(x))
+              w.data_ptr(), table.ptrs.data_ptr(), int(table.has_shared), table.fmt,
+              float(swiglu_limit), int(scale_mode), ws.data_ptr(), ws.numel(), y.data_ptr(),
+              _lib.stream_of(x))
     return y
 
 

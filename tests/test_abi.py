@@ -40,7 +40,9 @@ def test_library_exports_every_declared_symbol():
     lib = _lib()
     for name in declared_symbols():
         assert hasattr(lib, name), name
-    assert lib.sgl_abi_version() == 1
+    from sglang_lite_amd import _lib as L
+
+    assert lib.sgl_abi_version() == L.ABI_VERSION == 2
 
 
 def test_probe_without_gpu_reports_why():
