@@ -82,6 +82,23 @@ def make_weights(torch, M, dev, seed=4):
     return table, (w13, s13, w2, s2)
 
 
+def make_fp4_weights(torch, M, dev, shared, seed=6):
+    """256 routed MXFP4 experts (the reference's live routed format: packed
+    e2m1 codes drawn uniformly, e8m0 1x32 scales in [2^-9, 2^-5]) plus the
+    given FP8 shared expert."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    u8 = torch.uint8
+    w13 = torch.randint(0, 256, (E, 2, I, H // 2), dtype=u8, device=dev, generator=g)
+    s13 = torch.randint(118, 123, (E, 2, I, H // 32), dtype=u8, device=dev, generator=g)
+    w2 = torch.randint(0, 256, (E, H, I // 2), dtype=u8, device=dev, generator=g)
+    s2 = torch.randint(118, 123, (E, H, I // 32), dtype=u8, device=dev, generator=g)
+    e8 = torch.float8_e8m0fnu
+    experts = [(w13[e, 0], w13[e, 1], w2[e], s13[e, 0].view(e8), s13[e, 1].view(e8), s2[e].view(e8))
+               for e in range(E)]
+    return M.ExpertTable.build(experts, shared)
+
+
 def zipf_logits(torch, T, seed, s=1.1):
     g = torch.Generator().manual_seed(seed)
     p = torch.arange(1, E + 1, dtype=torch.float64) ** -s
@@ -127,8 +144,9 @@ def event_avg_ms(torch, fn, iters, flush=None):
 class Prefill:
     """The staged prefill pipeline with events around each stage."""
 
-    def __init__(self, torch, M, K, table, T, dev, seed):
+    def __init__(self, torch, M, K, table, T, dev, seed, mode=0):
         self.torch, self.M, self.K, self.table, self.T = torch, M, K, table, T
+        self.mode = mode  # sgl_scale_mode of the activation quant
         g = torch.Generator().manual_seed(seed)
         self.x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
         self.logits = torch.randn(T, E, generator=g).to(dev)
@@ -137,7 +155,8 @@ class Prefill:
 
     def step(self):
         w, ids = self.M.route_topk(self.logits, K_TOP)
-        self.M.moe_forward(self.x, ids, w, self.table, workspace=self.ws, out=self.y)
+        self.M.moe_forward(self.x, ids, w, self.table, workspace=self.ws, out=self.y,
+                           scale_mode=self.mode)
         return ids
 
     def staged(self, iters):
@@ -149,13 +168,15 @@ class Prefill:
             ev[0].record()
             w, ids = M.route_topk(self.logits, K_TOP)
             ev[1].record()
-            xq, xs = K.act_quant(self.x)
+            xq, xs = K.act_quant(self.x, scale_mode=self.mode)
             ev[2].record()
             _, offsets, sorted_slot, _ = M.permute(ids, E)
             ev[3].record()
-            hq, hs = M.gate_up(xq, xs, offsets, sorted_slot, w.reshape(-1), self.table, K_TOP)
+            hq, hs = M.gate_up(xq, xs, offsets, sorted_slot, w.reshape(-1), self.table, K_TOP,
+                               scale_mode=self.mode)
             ev[4].record()
-            out = M.down(hq, hs, offsets, sorted_slot, self.table, self.T, K_TOP)
+            out = M.down(hq, hs, offsets, sorted_slot, self.table, self.T, K_TOP,
+                         scale_mode=self.mode)
             ev[5].record()
             M.combine(out, ids, True)
             ev[6].record()
@@ -163,6 +184,85 @@ class Prefill:
             for i, n in enumerate(names):
                 tot[n] += ev[i].elapsed_time(ev[i + 1])
         return {n: v / iters for n, v in tot.items()}
+
+
+def fp4_extra(torch, M, K, weights, dev, args, flush):
+    """FP8 x MXFP4 (the reference's live routed-expert format): the MoE layer
+    at the prefill and decode shapes with FP4 routed experts and the FP8
+    shared expert, in fp32-scale mode 0 and the live ue8m0 mode 3 (scales
+    applied inside the MFMA), and the dense FP8 x FP4 GEMM (N=4096, K=7168)."""
+    w13, s13, w2, s2 = weights
+    shared = (w13[E, 0], w13[E, 1], w2[E], s13[E, 0], s13[E, 1], s2[E])
+    log("generating FP4 expert weights on the device")
+    table4 = make_fp4_weights(torch, M, dev, shared)
+    out = {"flops_note": "mixed fp8 x fp4 MFMA runs at the fp8 rate: peak 5.0 PF dense"}
+    T = 8192
+    rows = T * K_TOP + T
+    for mode in (0, 3):
+        pre = Prefill(torch, M, K, table4, T, dev, seed=4, mode=mode)
+        ms = time_steps(torch, pre.step, args.steps, args.warmup)
+        st = pre.staged(max(3, min(args.steps, 10)))
+        gu = rows * 4.0 * H * I / (st["gate_up"] / 1e3) / 1e12
+        dn = rows * 2.0 * H * I / (st["down"] / 1e3) / 1e12
+        out[f"prefill_mode{mode}"] = {
+            "tokens": T, "ms": round(ms, 4), "tokens_per_s": round(T / ms * 1e3, 1),
+            "layer_tflops": round(moe_flops(rows) / (ms / 1e3) / 1e12, 2),
+            "mfma_frac": round(moe_flops(rows) / (ms / 1e3) / 1e12 / PEAK_FP8_TFLOPS, 4),
+            "gate_up_tflops": round(gu, 1), "down_tflops": round(dn, 1),
+            "stages_ms": {k_: round(v, 4) for k_, v in st.items()}}
+        log(f"fp4 prefill mode {mode}: {ms:.3f} ms, gate_up {gu:.0f} TF, down {dn:.0f} TF")
+    dec = []
+    wb = 3 * I * H // 2 + 3 * I * H // 32  # packed e2m1 + e8m0 bytes per routed expert
+    sb_ = 3 * I * H + 3 * 4 * (I // 128) * (H // 128)  # the FP8 shared expert
+    for Td, seed in ((64, 31), (256, 32), (512, 33)):
+        logits = zipf_logits(torch, Td, seed).to(dev)
+        xd = torch.randn(Td, H, generator=torch.Generator().manual_seed(seed)).to(
+            torch.bfloat16).to(dev)
+        ws = M.MoEWorkspace()
+        yd = torch.empty(Td, H, dtype=torch.bfloat16, device=dev)
+
+        def dstep():
+            w, ids = M.route_topk(logits, K_TOP)
+            M.moe_forward(xd, ids, w, table4, workspace=ws, out=yd, scale_mode=3)
+
+        msd = time_steps(torch, dstep, max(args.steps, 10), args.warmup)
+        _, ids = M.route_topk(logits, K_TOP)
+        touched = int(torch.unique(ids).numel())
+        by = touched * wb + sb_ + 4 * Td * H + 4 * Td * E
+        dec.append({"tokens": Td, "ms": round(msd, 4), "tokens_per_s": round(Td / msd * 1e3, 1),
+                    "experts_touched": touched, "bytes": by, "gbs": round(by / msd / 1e6, 1),
+                    "hbm_frac": round(by / msd / 1e6 / PEAK_HBM_GBS, 4)})
+        log(f"fp4 decode T={Td}: {msd:.3f} ms, {by / msd / 1e6:.0f} GB/s")
+    out["decode_mode3"] = dec
+    gw = torch.Generator(device=dev).manual_seed(7)
+    bq = torch.randint(0, 256, (4096, 3584), dtype=torch.uint8, device=dev, generator=gw)
+    bs = torch.randint(118, 123, (4096, 224), dtype=torch.uint8, device=dev,
+                       generator=gw).view(torch.float8_e8m0fnu)
+    dense = []
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        for Md in (16, 128, 1024, 4096):
+            a = torch.randn(Md, 7168, generator=gw, device=dev).to(torch.bfloat16)
+            for pow2 in (False, True):
+                aq, as_ = K.act_quant(a, scale_mode=3 if pow2 else 0)
+                c = torch.empty(Md, 4096, dtype=torch.bfloat16, device=dev)
+                fn = lambda: K.fp4_gemm(aq, as_, bq, bs, out=c, a_scale_pow2=pow2)  # noqa: E731
+                for _ in range(2):
+                    fn()
+                msg = event_avg_ms(torch, fn, 10, flush)
+                fl = 2.0 * Md * 4096 * 7168
+                byt = Md * 7168 + 4 * Md * 56 + 4096 * 3584 + 4096 * 224 + 2 * Md * 4096
+                dense.append({"M": Md, "N": 4096, "K": 7168, "a_scale_pow2": pow2,
+                              "ms": round(msg, 5), "tflops": round(fl / msg / 1e9, 2),
+                              "mfma_frac": round(fl / msg / 1e9 / PEAK_FP8_TFLOPS, 4),
+                              "gbs": round(byt / msg / 1e6, 1),
+                              "hbm_frac": round(byt / msg / 1e6 / PEAK_HBM_GBS, 4)})
+                log(f"fp4 dense M={Md} pow2={pow2}: {msg * 1e3:.1f} us")
+    finally:
+        torch.set_default_dtype(prev)
+    out["dense_gemm"] = dense
+    return out
 
 
 def moe_flops(rows):
@@ -408,6 +508,7 @@ def main():
                                           "hbm_frac": round(ab / msa / 1e6 / PEAK_HBM_GBS, 4)},
         }
         log(f"kv pack {msp * 1e3:.1f} us, gather {msg_ * 1e3:.1f} us, pack A paged {msa * 1e3:.1f} us")
+        extra["fp4"] = fp4_extra(torch, M, K, weights, dev, args, flush)
         result["extra"] = extra
 
     if not args.no_cpu_baseline:

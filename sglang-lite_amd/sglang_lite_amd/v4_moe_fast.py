@@ -7,7 +7,9 @@ experts on the host (``torch.unique(...).tolist()`` and one ``torch.where``
 per expert, both device->host syncs), the replacement runs the whole layer as
 five HIP launches with no host sync: 1x128 act quant, stable permutation,
 grouped gate/up (+SwiGLU, routing weight, requant), grouped down, ordered
-combine with the shared expert.  Results follow the reference's arithmetic:
+combine with the shared expert.  Routed experts may be FP8 (128x128 scales)
+or MXFP4 (``expert_dtype="fp4"``, model.py:623-624: packed e2m1 with e8m0
+1x32 scales, the reference's live format); the shared expert is FP8.  Results follow the reference's arithmetic:
 weight applied before ``w2``, fp32 sum over experts in ascending id, shared
 expert added last, bf16 out.
 
@@ -32,6 +34,7 @@ import torch.nn.functional as F
 
 from . import kernel as HK
 from . import moe as HM
+from .v4_deep_gemm import is_fp4_weight
 
 logger = logging.getLogger("sglang_lite_amd.v4_moe_fast")
 MARK = "_sglang_lite_moe_fast"
@@ -52,6 +55,17 @@ def _official_model():
 def _is_fp8(linear) -> bool:
     w = getattr(linear, "weight", None)
     return w is not None and w.dtype == torch.float8_e4m3fn and getattr(w, "scale", None) is not None
+
+
+def _is_fp4(linear) -> bool:
+    w = getattr(linear, "weight", None)
+    return w is not None and getattr(w, "scale", None) is not None and is_fp4_weight(w)
+
+
+def _quantized(expert) -> bool:
+    """Every projection FP8, or every projection FP4."""
+    lins = (expert.w1, expert.w3, expert.w2)
+    return all(_is_fp8(l) for l in lins) or all(_is_fp4(l) for l in lins)
 
 
 def _expert_entry(expert):
@@ -75,9 +89,9 @@ def expert_table(moe) -> HM.ExpertTable:
 
 
 def _expert_forward_fused(self, x: torch.Tensor, weights: Optional[torch.Tensor] = None):
-    """Expert SwiGLU (model.py:596-606 / v4_moe_fast.py:43-76) for FP8 experts
-    as a one-expert grouped launch; other weight formats use the official forward."""
-    if not (_is_fp8(self.w1) and _is_fp8(self.w2) and _is_fp8(self.w3)):
+    """Expert SwiGLU (model.py:596-606 / v4_moe_fast.py:43-76) for FP8 or FP4
+    experts as a one-expert grouped launch; bf16 experts use the official forward."""
+    if not _quantized(self):
         return self._sgl_orig_forward(x, weights)  # bf16 experts: not this path
     shape = x.shape
     x2 = x.reshape(-1, shape[-1])
@@ -111,8 +125,9 @@ def _moe_forward_fused(self, x: torch.Tensor, input_ids: torch.Tensor):
     M = sys.modules.get("model")
     if (M is not None and getattr(M, "world_size", 1) > 1) or \
             any(e is None for e in self.experts) or \
-            not all(_is_fp8(e.w1) for e in (self.experts[0], self.shared_experts)):
-        # expert-sharded ranks / non-FP8 experts are not this path
+            not all(_quantized(e) for e in (self.experts[0], self.shared_experts)) or \
+            not _is_fp8(self.shared_experts.w1):
+        # expert-sharded ranks / bf16 experts are not this path
         return self._sgl_orig_forward(x, input_ids)
     shape = x.size()
     x2 = x.view(-1, self.dim)

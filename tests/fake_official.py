@@ -30,6 +30,20 @@ def install():
     M.scale_dtype = torch.float32
     M.act_quant = K.act_quant
     M.fp8_gemm = K.fp8_gemm
+    M.fp4_gemm = K.fp4_gemm
+
+    def linear(x, weight, bias=None):
+        """The dispatch of model.py:108-120 on the module's (patchable) names."""
+        assert bias is None
+        if weight.dtype == torch.float4_e2m1fn_x2:
+            xq, s = M.act_quant(x, M.block_size, M.scale_fmt, M.scale_dtype)
+            return M.fp4_gemm(xq, s, weight, weight.scale, M.scale_dtype)
+        if weight.dtype == torch.float8_e4m3fn:
+            xq, s = M.act_quant(x, M.block_size, M.scale_fmt, M.scale_dtype)
+            return M.fp8_gemm(xq, s, weight, weight.scale, M.scale_dtype)
+        return torch.nn.functional.linear(x, weight)
+
+    M.linear = linear
 
     class Linear(nn.Module):
         def __init__(self, w_q: torch.Tensor, s: torch.Tensor):

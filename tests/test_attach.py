@@ -49,11 +49,27 @@ def test_failed_probe_leaves_official_functions(official):
     assert D.is_armed() is False
 
 
-def test_fp4_path_is_reported_not_built():
+def test_fp4_path_refuses_cpu_tensors():
     from sglang_lite_amd import v4_deep_gemm as D
 
-    with pytest.raises(NotImplementedError):
-        D.fp4_gemm_nt(None, None, None, None)
+    a = torch.zeros(2, 256, dtype=torch.float8_e4m3fn)
+    s = torch.ones(2, 2)
+    b = torch.zeros(16, 128, dtype=torch.uint8)
+    bs = torch.ones(16, 8)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        D.fp4_gemm_nt(a, s, b, bs)
+
+
+def test_fp4_weight_detection():
+    from sglang_lite_amd import v4_deep_gemm as D
+
+    w = torch.nn.Parameter(torch.zeros(64, 128, dtype=torch.int8), requires_grad=False)
+    w.scale = torch.nn.Parameter(torch.ones(64, 8), requires_grad=False)  # in = 256, 256/32 = 8
+    assert D.is_fp4_weight(w)
+    w.scale = torch.nn.Parameter(torch.ones(1, 2), requires_grad=False)  # 128x128 block scale
+    assert not D.is_fp4_weight(w)
+    w4 = torch.zeros(64, 128, dtype=torch.uint8).view(torch.float4_e2m1fn_x2)
+    assert D.is_fp4_weight(w4)
 
 
 def test_scale_formula_switch(monkeypatch):

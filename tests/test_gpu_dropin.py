@@ -12,6 +12,7 @@ import torch.nn.functional as F
 
 import fake_official
 from helpers import assert_gemm_close, bf16_values, f32, to_dev_bf16, to_dev_f32, to_dev_fp8, u8
+from oracle import fp4 as F4
 from oracle import moe as OM
 from oracle import quant as Q
 
@@ -104,3 +105,59 @@ def test_expert_forward_and_linear_dropins(official, gpu):
     ref = OM.fp8_gemm(q_ref, s_ref, e8["w1"], e8["s1"], out_bf16=False)
     assert_gemm_close(f32(c), ref, "patched kernel.fp8_gemm")
     assert getattr(ex.w1.weight, "_dg_s_f32", None) is not None  # scale cache on the Parameter
+
+
+def _dev_fp4_expert(e, dev):
+    def w4(a):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(dev).view(torch.float4_e2m1fn_x2)
+
+    def s8(a):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(dev).view(torch.float8_e8m0fnu)
+
+    return (w4(e["w1"]), w4(e["w3"]), w4(e["w2"]), s8(e["s1"]), s8(e["s3"]), s8(e["s2"]))
+
+
+def test_fp4_linear_expert_and_moe_dropins(official, gpu):
+    """The reference's live configuration: FP4 routed experts, FP8 shared
+    expert, scale_fmt "ue8m0" with e8m0 activation scales (model.py:40-42,
+    113-115, 623-626): the official linear() through the patched
+    kernel.fp4_gemm, Expert.forward and MoE.forward, against the oracle."""
+    from sglang_lite_amd import v4_deep_gemm as D
+    from sglang_lite_amd import v4_moe_fast as MF
+
+    M, K = official
+    M.scale_fmt = "ue8m0"
+    M.scale_dtype = torch.float8_e8m0fnu
+    rng = np.random.default_rng(43)
+    T, H, I, E, k = 40, 512, 256, 8, 2
+    x = bf16_values(rng, (T, H))
+    experts = [OM.make_fp4_expert(rng, H, I) for _ in range(E)]
+    sh = OM.make_expert(rng, H, I)
+    W = (rng.standard_normal((E, H)) * H ** -0.5).astype(np.float32)
+    gate = M.Gate(to_dev_f32(W, gpu), k)
+    moe = M.MoE(H, gate, [M.Expert(_dev_fp4_expert(e, gpu)) for e in experts],
+                M.Expert(_dev_expert(sh, gpu)))
+    st = D.attach_v4_deep_gemm(moe)
+    assert st["enabled"] and st["scale_cache"] == 3 * (E + 1)
+    assert K.fp4_gemm is M.fp4_gemm and getattr(K.fp4_gemm, D.MARK, False)
+    assert MF.attach_v4_moe_fast(moe)["enabled"]
+    xd = to_dev_bf16(x, gpu)
+    mode = 1  # scale_fmt "ue8m0" with the torch formula: power-of-two activation scales
+    q_ref, s_ref = Q.per_token_cast_to_fp8(x, True, 128)
+    # official linear() -> patched act_quant + fp4_gemm (e8m0 activation scales)
+    ex0 = moe.experts[0]
+    y_lin = M.linear(xd, ex0.w1.weight)
+    assert y_lin.dtype == torch.get_default_dtype()
+    assert_gemm_close(f32(y_lin), F4.fp4_gemm(q_ref, s_ref, experts[0]["w1"], experts[0]["s1"],
+                                              out_bf16=False), "linear fp4")
+    # Expert.forward of one FP4 expert
+    w = rng.uniform(0.1, 1.0, (T, 1)).astype(np.float32)
+    y_ex = ex0(xd, to_dev_f32(w, gpu))
+    assert_gemm_close(f32(y_ex), OM.expert_forward(x, experts[0], w, mode=mode), "Expert.forward fp4")
+    # MoE.forward: FP4 routed + FP8 shared
+    y = moe(xd.view(1, T, H), torch.zeros(1, T, dtype=torch.long, device=gpu))
+    logits = F.linear(xd.float(), gate.weight.float()).cpu().numpy()
+    w_ref, ids_ref = OM.route_topk(logits, k)
+    assert OM.topk_margin(logits, k) > 1e-6
+    y_ref = OM.moe_forward(x, ids_ref, w_ref, experts, sh, mode=mode)
+    assert_gemm_close(f32(y[0]), y_ref, "patched MoE.forward fp4")
