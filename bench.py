@@ -47,9 +47,10 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extra", action="store_true", help="headline prefill line only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--profile-kernels", action="store_true",
-                    help="run only the prefill stages (plus a 256 MiB copy for counter "
-                         "calibration) for rocprofv3 --pmc runs; prints no JSON")
+    ap.add_argument("--profile-kernels", nargs="?", const="fp8", choices=("fp8", "fp4"),
+                    help="run only 3 prefill steps (FP8 experts, or FP4 routed experts in the "
+                         "ue8m0 scale mode) plus a counter-calibration kernel, for rocprofv3 "
+                         "runs; prints no JSON")
     return ap.parse_args()
 
 
@@ -360,6 +361,11 @@ def main():
     pre = Prefill(torch, M, K, table, T, dev, seed=4)
 
     if args.profile_kernels:
+        if args.profile_kernels == "fp4":
+            w13, s13, w2, s2 = weights
+            shared = (w13[E, 0], w13[E, 1], w2[E], s13[E, 0], s13[E, 1], s2[E])
+            pre = Prefill(torch, M, K, make_fp4_weights(torch, M, dev, shared), T, dev, seed=4,
+                          mode=3)
         for _ in range(3):
             pre.step()
         # counter calibration: e8m0_to_f32 over 64 MiB reads 64 MiB, writes 256 MiB
