@@ -211,6 +211,8 @@ def fp4_extra(torch, M, K, weights, dev, args, flush):
             "mfma_frac": round(moe_flops(rows) / (ms / 1e3) / 1e12 / PEAK_FP8_TFLOPS, 4),
             "gate_up_tflops": round(gu, 1), "down_tflops": round(dn, 1),
             "stages_ms": {k_: round(v, 4) for k_, v in st.items()}}
+        if mode == 3:
+            out["prefill_mode3"]["gate_up_traffic_bytes"] = read_traffic("moe_fp4_gate_up_prefill")
         log(f"fp4 prefill mode {mode}: {ms:.3f} ms, gate_up {gu:.0f} TF, down {dn:.0f} TF")
     dec = []
     wb = 3 * I * H // 2 + 3 * I * H // 32  # packed e2m1 + e8m0 bytes per routed expert
