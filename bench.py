@@ -448,6 +448,23 @@ def main():
                         "hbm_frac": round(by / msd / 1e6 / PEAK_HBM_GBS, 4)})
             log(f"decode T={Td}: {msd:.3f} ms, touched {touched}, {by / msd / 1e6:.0f} GB/s")
         extra["decode"] = dec
+        # ---- fused gate (router projection on bf16 MFMA + score + top-k), model.py:564-584
+        gate = []
+        gg = torch.Generator(device=dev).manual_seed(8)
+        Wr = (torch.randn(E, H, generator=gg, device=dev) * H ** -0.5).to(torch.bfloat16)
+        br = torch.randn(E, generator=gg, device=dev) * 0.05
+        for Tg in (64, 512, 8192):
+            xg = torch.randn(Tg, H, generator=gg, device=dev).to(torch.bfloat16)
+            lg = torch.empty(Tg, E, dtype=torch.float32, device=dev)
+            fn = lambda: M.gate(xg, Wr, K_TOP, "sqrtsoftplus", br, 1.5, logits=lg)  # noqa: E731
+            for _ in range(3):
+                fn()
+            msg = event_avg_ms(torch, fn, 20)
+            byt = E * H * 2 + Tg * H * 2 + Tg * E * 4 + Tg * K_TOP * 8
+            gate.append({"tokens": Tg, "ms": round(msg, 5), "gbs": round(byt / msg / 1e6, 1),
+                         "tflops": round(2.0 * Tg * H * E / msg / 1e9, 1)})
+            log(f"gate T={Tg}: {msg * 1e3:.1f} us")
+        extra["gate_sqrtsoftplus_bias"] = gate
         # ---- dense GEMM
         # cold-cache timing: read 512 MiB between runs so neither L2 nor the
         # memory-side cache holds the inputs.  A read, not a fill: a fill

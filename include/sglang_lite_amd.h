@@ -195,6 +195,22 @@ int sgl_moe_route_topk(const float* logits, int64_t T, int E, int k, int score_f
                        const float* bias, float route_scale, int32_t* ids, float* weights,
                        sgl_stream_t stream);
 
+/* The whole gate of a MoE layer from the hidden states: router projection
+ * logits[t, e] = sum_h x[t, h] * W[e, h] (bf16 x [T, H] and bf16 W [E, H], every
+ * product exact, fp32 accumulation; logits fp32 [T, E] is written, the caller's
+ * buffer), then the selection of sgl_moe_route_topk, or with tid2eid non-NULL
+ * the hash routing ids[t] = tid2eid[input_ids[t]] (tid2eid int32 [vocab, k],
+ * input_ids int32 or int64 [T]; ids outside [0, vocab) and table entries outside
+ * [0, E) are clamped, where torch would raise) with weights = the scores at
+ * those experts, renormalised unless softmax, times route_scale; bias is
+ * ignored for hash routing.  H % 32 == 0, E <= 512.
+ * Replaces deepseek_infer/model.py:564-584 Gate.forward (projection, score
+ * function, bias, top-k or tid2eid lookup, renormalisation, route_scale). */
+int sgl_moe_gate(const void* x, const void* w, int64_t T, int64_t H, int E, int k, int score_func,
+                 const float* bias, float route_scale, const int32_t* tid2eid, int64_t vocab,
+                 const void* input_ids, int input_ids_int64, float* logits, int32_t* ids,
+                 float* weights, sgl_stream_t stream);
+
 /* Stable counting sort of the T*k routing slots (slot = t*k + j) by expert id:
  *   counts [E], offsets [E+1] (exclusive prefix sum, offsets[E] = T*k),
  *   sorted_slot [T*k] (slot at each sorted position, token-ascending inside an
@@ -272,6 +288,20 @@ int sgl_moe_forward(const void* x, int64_t T, int64_t H, int64_t I, int E, int k
  * Replaces engine/dsv4_kv_pack.py:40-75 pack_dsv4_kv_bf16 (+ :104-146). */
 int sgl_kv_pack(const void* kv, int dtype, int64_t T, int64_t ldkv, int layout, int scale_mode,
                 int paged, int page_size, void* out, sgl_stream_t stream);
+
+/* Packed-page writer: layout A rows of kv [T, 512] (bf16 / f16, row stride
+ * ldkv; scale_mode as for sgl_kv_pack) written straight into a RadixCache
+ * packed pool uint8 [num_layers, num_blocks, 1, page_size, 584]: token
+ * position p = start_pos + t goes to block block_table[p / page_size] (device
+ * int32 [n_pages]), slot p % page_size, of layer layer_idx.  A block table
+ * shorter than the span is an error (as in the reference); table entries
+ * outside [0, num_blocks) are skipped (the reference raises on them; the
+ * kernel cannot).  Replaces engine/kv_cache.py:340-390 write_packed_kv fed by
+ * engine/dsv4_kv_pack.py:40-75 (the write of engine/v4_dual_pool.py:73-128). */
+int sgl_kv_pack_to_pages(const void* kv, int dtype, int64_t T, int64_t ldkv, int scale_mode,
+                         const int32_t* block_table, int64_t n_pages, int64_t start_pos,
+                         int page_size, int64_t num_blocks, int layer_idx, int num_layers,
+                         void* pool, sgl_stream_t stream);
 
 /* Logical [T, 584] rows -> footer pages [ceil(T/page), page*584] (padding rows
  * zero).  Replaces engine/dsv4_kv_pack.py:104-146 to_paged_hnd. */

@@ -129,3 +129,16 @@ def split_swa_compress_indices(topk: np.ndarray, window: int
         comp = np.zeros((b * s, 0), np.int32)
         comp_lens = np.zeros(b * s, np.int32)
     return swa, swa_lens, comp, comp_lens
+
+
+def write_packed_pages(pool: np.ndarray, block_table, start_pos: int, rows: np.ndarray,
+                       layer_idx: int) -> np.ndarray:
+    """engine/kv_cache.py:340-390 write_packed_kv: token start_pos + t goes to
+    pool[layer, block_table[(start_pos + t) // page], 0, (start_pos + t) % page].
+    ``pool`` uint8 [layers, blocks, 1, page, D]; returns the updated copy."""
+    out = np.array(pool, copy=True)
+    page = out.shape[3]
+    for t in range(rows.shape[0]):
+        pos = start_pos + t
+        out[layer_idx, block_table[pos // page], 0, pos % page] = rows[t]
+    return out

@@ -51,6 +51,28 @@ def route_topk(logits: np.ndarray, k: int, score_func: str = "softmax",
     return w, ids
 
 
+def route_hash(logits: np.ndarray, tid2eid: np.ndarray, input_ids: np.ndarray, k: int,
+               score_func: str = "sqrtsoftplus", route_scale: float = 1.0
+               ) -> Tuple[np.ndarray, np.ndarray]:
+    """deepseek_infer/model.py:565-584 with ``self.hash`` (:576-577): ids =
+    tid2eid[input_ids]; weights = the scores at those experts (table order),
+    renormalised unless softmax, times route_scale (the bias is None there)."""
+    scores = route_scores(logits, score_func)
+    ids = np.asarray(tid2eid)[np.asarray(input_ids).reshape(-1)].astype(np.int64)
+    assert ids.shape[1] == k
+    w = np.take_along_axis(scores, ids, axis=1).astype(np.float32)
+    if score_func != "softmax":
+        w = (w / w.sum(axis=-1, keepdims=True, dtype=np.float32)).astype(np.float32)
+    return (w * np.float32(route_scale)).astype(np.float32), ids
+
+
+def router_logits(x_bf16: np.ndarray, w_bf16: np.ndarray) -> np.ndarray:
+    """model.py:565 linear(x.float(), W.float()) for bf16 x and W: the exact
+    dot products (float64 holds every bf16 x bf16 product and their sum over
+    H <= 2^20 terms to far below fp32 resolution), rounded to fp32."""
+    return (np.asarray(x_bf16, np.float64) @ np.asarray(w_bf16, np.float64).T).astype(np.float32)
+
+
 def topk_margin(logits: np.ndarray, k: int, score_func: str = "softmax",
                 bias: Optional[np.ndarray] = None) -> float:
     """Smallest gap between the k-th and (k+1)-th selection value over tokens

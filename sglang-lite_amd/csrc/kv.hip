@@ -52,11 +52,21 @@ __device__ __forceinline__ void load8(const uint8_t* row, int elem, float* f, ui
 // page, scales at page*576 + l*8) and zero-fills padding rows.  A wavefront
 // takes R consecutive rows per step and issues all their loads first, so R
 // rows of reads are in flight per wavefront.
+// Row t of a RadixCache packed pool write (engine/kv_cache.py:340-390): token
+// position start + t lands in block block_table[(start + t) / page], slot
+// (start + t) % page of one layer's [num_blocks, page, 584] slab.
+struct PageTable {
+  const int32_t* block_table;  // null: plain / footer-paged output
+  int64_t start;
+  int64_t num_blocks;
+};
+
 template <int DT, int R>
 __global__ __launch_bounds__(256) void kv_pack_a_kernel(const uint8_t* __restrict__ kv, int64_t T,
                                                         int64_t ld_bytes, int mode, int paged,
                                                         int page, int64_t rows_total,
-                                                        uint8_t* __restrict__ out) {
+                                                        uint8_t* __restrict__ out,
+                                                        const PageTable pt) {
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * 4;
   const int64_t w0 = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -72,7 +82,13 @@ __global__ __launch_bounds__(256) void kv_pack_a_kernel(const uint8_t* __restric
       if (t >= rows_total) break;
       uint8_t* data;
       uint8_t* foot;
-      if (paged) {
+      if (pt.block_table) {
+        const int64_t pos = pt.start + t;
+        const int64_t bid = pt.block_table[pos / page];
+        if (bid < 0 || bid >= pt.num_blocks) continue;  // not a block of this pool
+        data = out + (bid * page + pos % page) * A_ROW;
+        foot = data + A_DATA;
+      } else if (paged) {
         const int64_t pg = t / page, l = t - pg * page;
         uint8_t* pbase = out + pg * (int64_t)page * A_ROW;
         data = pbase + l * A_DATA;
@@ -349,11 +365,11 @@ int sgl_kv_pack(const void* kv, int dtype, int64_t T, int64_t ldkv, int layout, 
     if (dtype == SGL_BF16)
       sgl::kv_pack_a_kernel<SGL_BF16, sgl::kKvRows><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
                                                          scale_mode, paged, page_size, rows,
-                                                         (uint8_t*)out);
+                                                         (uint8_t*)out, sgl::PageTable{});
     else
       sgl::kv_pack_a_kernel<SGL_F16, sgl::kKvRows><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
                                                         scale_mode, paged, page_size, rows,
-                                                        (uint8_t*)out);
+                                                        (uint8_t*)out, sgl::PageTable{});
     return sgl::check_launch("kv_pack_a");
   }
   SGL_REQUIRE(!paged, "kv_pack: layout B has no paged form");
@@ -373,6 +389,43 @@ int sgl_kv_pack(const void* kv, int dtype, int64_t T, int64_t ldkv, int layout, 
     sgl::kv_pack_b_kernel<SGL_F32, sgl::kKvRows><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
                                                       (uint8_t*)out);
   return sgl::check_launch("kv_pack_b");
+}
+
+int sgl_kv_pack_to_pages(const void* kv, int dtype, int64_t T, int64_t ldkv, int scale_mode,
+                         const int32_t* block_table, int64_t n_pages, int64_t start_pos,
+                         int page_size, int64_t num_blocks, int layer_idx, int num_layers,
+                         void* pool, sgl_stream_t stream) {
+  SGL_REQUIRE(T >= 0 && start_pos >= 0 && page_size > 0 && num_blocks >= 0,
+              "kv_pack_to_pages: bad T / start_pos / page_size / num_blocks");
+  SGL_REQUIRE(dtype == SGL_BF16 || dtype == SGL_F16,
+              "kv_pack_to_pages: kv must be bf16 or f16 (the 584-byte row stores 16-bit rope)");
+  SGL_REQUIRE(scale_mode == SGL_SCALE_KV_UE8M0 || scale_mode == SGL_SCALE_TILELANG_UE8M0,
+              "kv_pack_to_pages: layout A needs a ue8m0 scale mode (got %d)", scale_mode);
+  SGL_REQUIRE(layer_idx >= 0 && layer_idx < num_layers, "kv_pack_to_pages: layer_idx %d out of range (%d)",
+              layer_idx, num_layers);
+  SGL_REQUIRE(ldkv >= 512, "kv_pack_to_pages: row stride %lld < 512", (long long)ldkv);
+  if (T == 0) return SGL_OK;
+  const int64_t pages_needed = sgl::ceil_div(start_pos + T, (int64_t)page_size);
+  if (pages_needed > n_pages) {
+    sgl::set_error("kv_pack_to_pages: block_table too short for packed pos=%lld: pages=%lld",
+                   (long long)(start_pos + T - 1), (long long)n_pages);
+    return SGL_ERR_INVALID_ARG;
+  }
+  SGL_REQUIRE(kv && block_table && pool, "kv_pack_to_pages: null pointer");
+  const int es = 2;
+  SGL_REQUIRE(sgl::aligned(pool, 8) && sgl::aligned(kv, 16) && (ldkv * es) % 16 == 0,
+              "kv_pack_to_pages: kv rows must be 16-byte aligned, pool 8-byte aligned");
+  uint8_t* slab = (uint8_t*)pool + (int64_t)layer_idx * num_blocks * page_size * sgl::A_ROW;
+  const sgl::PageTable pt{block_table, start_pos, num_blocks};
+  const unsigned g = sgl::grid_for_rows(T, sgl::kKvRows);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == SGL_BF16)
+    sgl::kv_pack_a_kernel<SGL_BF16, sgl::kKvRows><<<g, 256, 0, st>>>(
+        (const uint8_t*)kv, T, ldkv * es, scale_mode, 0, page_size, T, slab, pt);
+  else
+    sgl::kv_pack_a_kernel<SGL_F16, sgl::kKvRows><<<g, 256, 0, st>>>(
+        (const uint8_t*)kv, T, ldkv * es, scale_mode, 0, page_size, T, slab, pt);
+  return sgl::check_launch("kv_pack_to_pages");
 }
 
 int sgl_kv_to_paged(const void* packed, int64_t T, int page_size, void* pages,

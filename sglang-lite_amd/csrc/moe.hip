@@ -21,12 +21,23 @@ constexpr int kPermWaves = kPermThreads / 64;
 
 // ------------------------------------------------------------ route top-k
 
+// Hash routing (deepseek_infer/model.py:576-577): the token's experts come
+// from the table row tid2eid[input_ids[t]]; token ids outside [0, vocab) and
+// table entries outside [0, E) are clamped into range (torch would raise).
+struct HashRoute {
+  const int32_t* tid2eid;  // [vocab, k], or null: score top-k
+  const void* input_ids;   // [T] int32 or int64
+  int ids64;
+  int64_t vocab;
+};
+
 template <int EPL>
 __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits, int64_t T,
                                                          int E, int k, int score_func,
                                                          const float* __restrict__ bias,
                                                          float route_scale, int32_t* __restrict__ ids,
-                                                         float* __restrict__ weights) {
+                                                         float* __restrict__ weights,
+                                                         const HashRoute hash) {
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
@@ -77,6 +88,32 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
   float wsum = 0.0f;
   int my_e = 0;      // lane j keeps the j-th pick
   float my_s = 0.0f;
+  if (hash.tid2eid) {
+    // weights = the original scores gathered at the table's experts, in table order
+    int64_t tok = hash.ids64 ? reinterpret_cast<const int64_t*>(hash.input_ids)[t]
+                             : (int64_t) reinterpret_cast<const int32_t*>(hash.input_ids)[t];
+    tok = tok < 0 ? 0 : (tok >= hash.vocab ? hash.vocab - 1 : tok);
+    for (int j = 0; j < k; ++j) {
+      int e = hash.tid2eid[tok * k + j];
+      e = (e < 0 || e >= E) ? 0 : e;
+      float v = 0.0f;
+#pragma unroll
+      for (int q = 0; q < EPL; ++q) v = (e >> 6) == q ? sc[q] : v;
+      const float bs = __shfl(v, e & 63, 64);
+      if (lane == j) {
+        my_e = e;
+        my_s = bs;
+      }
+      wsum += bs;
+    }
+    if (lane < k) {
+      float w = my_s;
+      if (score_func != SGL_SCORE_SOFTMAX) w = w / wsum;
+      ids[t * k + lane] = my_e;
+      weights[t * k + lane] = w * route_scale;
+    }
+    return;
+  }
   for (int j = 0; j < k; ++j) {
     float bv = NEG_INF;
     int be = 0x7FFFFFFF;
@@ -114,6 +151,94 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
     if (score_func != SGL_SCORE_SOFTMAX) w = w / wsum;
     ids[t * k + lane] = my_e;
     weights[t * k + lane] = w * route_scale;
+  }
+}
+
+// ------------------------------------------------------ router projection
+
+// logits[t, e] = sum_h x[t, h] * W[e, h] for bf16 x [T, H] and bf16 W [E, H]:
+// the reference computes linear(x.float(), W.float()) (deepseek_infer/model.py:
+// 565); every bf16 x bf16 product is exact in fp32, so the bf16 MFMA with
+// fp32 accumulation (v_mfma_f32_16x16x32_bf16) forms the same products and
+// sums them in fp32 (in its own order).  A workgroup owns 16 TM tokens x 16 TE
+// experts; its NWV wavefronts split K (32-deep steps w, w + NWV, ...) loading
+// their operands straight from global memory, NB steps' loads in flight
+// together, and the partial tiles are summed through LDS.  Rows past T / E
+// re-read the last row; their outputs are dropped.
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v4f_r __attribute__((ext_vector_type(4)));
+
+template <int TM, int TE, int NWV, int NB>
+__global__ __launch_bounds__(64 * NWV) void router_logits_kernel(const uint16_t* __restrict__ x,
+                                                                 const uint16_t* __restrict__ w,
+                                                                 int64_t T, int H, int E,
+                                                                 float* __restrict__ logits) {
+  constexpr int RT = 16 * TM, RE = 16 * TE;
+  __shared__ float sRed[NWV][RT * RE];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g4 = lane >> 4, r16 = lane & 15;
+  const int64_t t0 = (int64_t)blockIdx.y * RT;
+  const int e0 = blockIdx.x * RE;
+  const uint16_t* arow[TM];
+  const uint16_t* brow[TE];
+#pragma unroll
+  for (int mi = 0; mi < TM; ++mi) {
+    int64_t r = t0 + 16 * mi + r16;
+    if (r > T - 1) r = T - 1;
+    arow[mi] = x + r * H + 8 * g4;
+  }
+#pragma unroll
+  for (int nj = 0; nj < TE; ++nj) {
+    int r = e0 + 16 * nj + r16;
+    if (r > E - 1) r = E - 1;
+    brow[nj] = w + (int64_t)r * H + 8 * g4;
+  }
+  v4f_r acc[TM][TE];
+#pragma unroll
+  for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < TE; ++nj) acc[mi][nj] = v4f_r{0.0f, 0.0f, 0.0f, 0.0f};
+  const int steps = H / 32;
+  for (int s0 = wave; s0 < steps; s0 += NWV * NB) {
+    v8bf a[NB][TM], b[NB][TE];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int s = s0 + j * NWV;
+      if (s < steps) {
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi) a[j][mi] = *reinterpret_cast<const v8bf*>(arow[mi] + s * 32);
+#pragma unroll
+        for (int nj = 0; nj < TE; ++nj) b[j][nj] = *reinterpret_cast<const v8bf*>(brow[nj] + s * 32);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      if (s0 + j * NWV < steps) {
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+          for (int nj = 0; nj < TE; ++nj)
+            acc[mi][nj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j][mi], b[j][nj], acc[mi][nj], 0, 0, 0);
+      }
+    }
+  }
+  // lane (g4, r16) holds rows 4 g4 + r (tokens), column r16 (expert) of each 16x16 tile
+#pragma unroll
+  for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < TE; ++nj)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        sRed[wave][(16 * mi + 4 * g4 + r) * RE + 16 * nj + r16] = acc[mi][nj][r];
+  __syncthreads();
+  for (int i = tid; i < RT * RE; i += 64 * NWV) {
+    float v = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NWV; ++q) v += sRed[q][i];
+    const int64_t t = t0 + i / RE;
+    const int e = e0 + i % RE;
+    if (t < T && e < E) logits[t * E + e] = v;
   }
 }
 
@@ -546,6 +671,32 @@ int run_down(const void* hq, const float* hs, int64_t T, int64_t H, int64_t I, i
   return launch_gemm(KIND_DOWN, sh, T, stream);
 }
 
+int launch_route(const char* what, const float* logits, int64_t T, int E, int k, int score_func,
+                 const float* bias, float route_scale, int32_t* ids, float* weights,
+                 const HashRoute& hash, hipStream_t st) {
+  SGL_REQUIRE(T >= 0, "%s: negative T", what);
+  SGL_REQUIRE(E >= 1 && E <= kMaxRouteE, "%s: E=%d not in [1, %d]", what, E, kMaxRouteE);
+  SGL_REQUIRE(k >= 1 && k <= 16 && k <= E, "%s: k=%d not in [1, min(16, E)]", what, k);
+  SGL_REQUIRE(score_func >= 0 && score_func <= 2, "%s: bad score_func %d", what, score_func);
+  if (T == 0) return SGL_OK;
+  SGL_REQUIRE(logits && ids && weights, "%s: null pointer", what);
+  const unsigned blocks = (unsigned)ceil_div(T, 4);
+  const int epl = (E + 63) / 64;
+#define SGL_ROUTE(n)                                                                               \
+  case n:                                                                                          \
+    route_topk_kernel<n><<<blocks, 256, 0, st>>>(logits, T, E, k, score_func, bias, route_scale,  \
+                                                 ids, weights, hash);                              \
+    break;
+  switch (epl) {
+    SGL_ROUTE(1) SGL_ROUTE(2) SGL_ROUTE(3) SGL_ROUTE(4) SGL_ROUTE(5) SGL_ROUTE(6) SGL_ROUTE(7)
+    default:
+      route_topk_kernel<8><<<blocks, 256, 0, st>>>(logits, T, E, k, score_func, bias, route_scale,
+                                                   ids, weights, hash);
+  }
+#undef SGL_ROUTE
+  return check_launch(what);
+}
+
 }  // namespace
 }  // namespace sgl
 
@@ -554,29 +705,39 @@ extern "C" {
 int sgl_moe_route_topk(const float* logits, int64_t T, int E, int k, int score_func,
                        const float* bias, float route_scale, int32_t* ids, float* weights,
                        sgl_stream_t stream) {
-  SGL_REQUIRE(T >= 0, "route_topk: negative T");
-  SGL_REQUIRE(E >= 1 && E <= sgl::kMaxRouteE, "route_topk: E=%d not in [1, %d]", E,
-              sgl::kMaxRouteE);
-  SGL_REQUIRE(k >= 1 && k <= 16 && k <= E, "route_topk: k=%d not in [1, min(16, E)]", k);
-  SGL_REQUIRE(score_func >= 0 && score_func <= 2, "route_topk: bad score_func %d", score_func);
+  return sgl::launch_route("route_topk", logits, T, E, k, score_func, bias, route_scale, ids,
+                           weights, sgl::HashRoute{nullptr, nullptr, 0, 0}, (hipStream_t)stream);
+}
+
+int sgl_moe_gate(const void* x, const void* w, int64_t T, int64_t H, int E, int k, int score_func,
+                 const float* bias, float route_scale, const int32_t* tid2eid, int64_t vocab,
+                 const void* input_ids, int input_ids_int64, float* logits, int32_t* ids,
+                 float* weights, sgl_stream_t stream) {
+  SGL_REQUIRE(T >= 0 && H > 0 && H % 32 == 0, "moe_gate: H=%lld must be a positive multiple of 32",
+              (long long)H);
+  SGL_REQUIRE(E >= 1 && E <= sgl::kMaxRouteE, "moe_gate: E=%d not in [1, %d]", E, sgl::kMaxRouteE);
   if (T == 0) return SGL_OK;
-  SGL_REQUIRE(logits && ids && weights, "route_topk: null pointer");
-  const unsigned blocks = (unsigned)sgl::ceil_div(T, 4);
+  SGL_REQUIRE(x && w && logits, "moe_gate: null pointer");
+  SGL_REQUIRE(sgl::aligned(x, 16) && sgl::aligned(w, 16), "moe_gate: x and W must be 16-byte aligned");
+  SGL_REQUIRE(!tid2eid || (input_ids && vocab >= 1), "moe_gate: hash routing needs input_ids and vocab");
+  SGL_REQUIRE(T < ((int64_t)1 << 31) / 16, "moe_gate: T too large");
   hipStream_t st = (hipStream_t)stream;
-  const int epl = (E + 63) / 64;
-#define SGL_ROUTE(n)                                                                               \
-  case n:                                                                                          \
-    sgl::route_topk_kernel<n><<<blocks, 256, 0, st>>>(logits, T, E, k, score_func, bias,           \
-                                                      route_scale, ids, weights);                  \
-    break;
-  switch (epl) {
-    SGL_ROUTE(1) SGL_ROUTE(2) SGL_ROUTE(3) SGL_ROUTE(4) SGL_ROUTE(5) SGL_ROUTE(6) SGL_ROUTE(7)
-    default:
-      sgl::route_topk_kernel<8><<<blocks, 256, 0, st>>>(logits, T, E, k, score_func, bias,
-                                                        route_scale, ids, weights);
+  const uint16_t* xb = (const uint16_t*)x;
+  const uint16_t* wb = (const uint16_t*)w;
+  // decode-sized batches: 16 tokens x 16 experts per workgroup, 16
+  // wavefronts with all their K steps in flight (many small workgroups
+  // spread the weight read); prefill: 64 x 64, 8 wavefronts, 4 steps in flight
+  if (T <= 256) {
+    dim3 grid((unsigned)E / 16 + (E % 16 != 0), (unsigned)sgl::ceil_div(T, 16));
+    sgl::router_logits_kernel<1, 1, 16, 8><<<grid, 1024, 0, st>>>(xb, wb, T, (int)H, E, logits);
+  } else {
+    dim3 grid((unsigned)sgl::ceil_div((int64_t)E, 64), (unsigned)sgl::ceil_div(T, 64));
+    sgl::router_logits_kernel<4, 4, 8, 4><<<grid, 512, 0, st>>>(xb, wb, T, (int)H, E, logits);
   }
-#undef SGL_ROUTE
-  return sgl::check_launch("route_topk");
+  int rc = sgl::check_launch("moe_gate");
+  if (rc) return rc;
+  return sgl::launch_route("moe_gate", logits, T, E, k, score_func, bias, route_scale, ids, weights,
+                           sgl::HashRoute{tid2eid, input_ids, input_ids_int64 ? 1 : 0, vocab}, st);
 }
 
 int sgl_moe_permute(const int32_t* ids, int64_t T, int k, int E, int32_t* counts, int32_t* offsets,

@@ -55,6 +55,10 @@ SIGNATURES = {
     "sgl_fp4_gemm": (c_int, [P, P, c_int, P, P, P, c_int, I64, I64, I64, P]),
     "sgl_fp4_to_fp8_weight": (c_int, [P, P, I64, I64, P, P, P]),
     "sgl_moe_route_topk": (c_int, [P, I64, c_int, c_int, c_int, P, c_float, P, P, P]),
+    "sgl_moe_gate": (
+        c_int,
+        [P, P, I64, I64, c_int, c_int, c_int, P, c_float, P, I64, P, c_int, P, P, P, P],
+    ),
     "sgl_moe_permute": (c_int, [P, I64, c_int, c_int, P, P, P, P, P]),
     "sgl_moe_gate_up": (
         c_int,
@@ -70,6 +74,9 @@ SIGNATURES = {
         [P, I64, I64, I64, c_int, c_int, P, P, P, c_int, c_int, c_float, c_int, P, c_size_t, P, P],
     ),
     "sgl_kv_pack": (c_int, [P, c_int, I64, I64, c_int, c_int, c_int, c_int, P, P]),
+    "sgl_kv_pack_to_pages": (
+        c_int, [P, c_int, I64, I64, c_int, P, I64, I64, c_int, I64, c_int, c_int, P, P]
+    ),
     "sgl_kv_to_paged": (c_int, [P, I64, c_int, P, P]),
     "sgl_kv_gather_dequant": (c_int, [P, c_int, c_int, c_int, I64, P, I64, I64, P, P]),
     "sgl_split_swa_compress_indices": (c_int, [P, c_int, I64, I64, I64, P, P, P, P, P]),

@@ -99,6 +99,50 @@ def pack_dsv4_kv_paged(kv: torch.Tensor, page_size: int = DSV4_PAGE_SIZE, *,
     return out
 
 
+def write_packed_kv_bf16(pool: torch.Tensor, block_table, start_pos: int, kv: torch.Tensor, *,
+                         layer_idx: int = 0, act_quant_fn=None) -> None:
+    """Packed-page writer: ``pack_dsv4_kv_bf16(kv)`` written straight into a
+    RadixCache packed pool ``[layers, blocks, 1, page, 584]`` (the write of
+    engine/kv_cache.py:340-390 ``write_packed_kv`` as
+    engine/v4_dual_pool.py:73-128 feeds it) in one kernel.  ``block_table`` is
+    a list of block ids (checked on the host against the pool, as the
+    reference does) or a device int32 tensor (graph-capturable; entries
+    outside the pool are skipped)."""
+    if pool.dim() != 5 or pool.dtype != torch.uint8 or pool.shape[2] != 1 or \
+            pool.shape[-1] != DSV4_PACKED_BYTES or not pool.is_contiguous():
+        raise ValueError(f"expected a contiguous uint8 [layers, blocks, 1, page, 584] pool, "
+                         f"got {pool.dtype} {tuple(pool.shape)}")
+    num_layers, num_blocks, _, page, _ = pool.shape
+    if layer_idx < 0 or layer_idx >= num_layers:
+        raise ValueError(f"layer_idx {layer_idx} out of range ({num_layers})")
+    if kv.shape[-1] != DSV4_HEAD_DIM:
+        raise ValueError(f"expected head_dim={DSV4_HEAD_DIM}, got {kv.shape[-1]}")
+    if kv.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"unsupported kv dtype {kv.dtype}")
+    _lib.require_device(pool, kv, what="write_packed_kv_bf16")
+    if not isinstance(block_table, torch.Tensor):
+        if not block_table:
+            raise ValueError("write_packed_kv requires block_table")
+        bad = [b for b in block_table if not 0 <= int(b) < num_blocks]
+        if bad:
+            raise RuntimeError(f"block id {bad[0]} out of range ({num_blocks})")
+        block_table = torch.tensor([int(b) for b in block_table], dtype=torch.int32).to(pool.device)
+    bt = block_table.to(torch.int32).contiguous()
+    _lib.require_device(bt, what="write_packed_kv_bf16")
+    z, T = _rows(kv, DSV4_HEAD_DIM)
+    if T == 0:
+        return
+    mode = _lib.SCALE_KV_UE8M0 if act_quant_fn is None else _lib.SCALE_TILELANG_UE8M0
+    try:
+        _lib.call("sgl_kv_pack_to_pages", z.data_ptr(), _DT[kv.dtype], T, z.stride(0), mode,
+                  bt.data_ptr(), bt.numel(), int(start_pos), int(page), int(num_blocks),
+                  int(layer_idx), int(num_layers), pool.data_ptr(), _lib.stream_of(kv))
+    except ValueError as e:  # the reference raises RuntimeError for a short table
+        if "block_table too short" in str(e):
+            raise RuntimeError(str(e)) from None
+        raise
+
+
 def fp8_ue8m0_quant(x: torch.Tensor, block_size: int = DSV4_FP8_BLOCK):
     """The reference's ``_torch_fp8_ue8m0_quant`` (dsv4_kv_pack.py:78-101) on the
     device: returns ``(y float8_e4m3fn, s float8_e8m0fnu [..., n // block])``."""
@@ -216,5 +260,5 @@ __all__ = [
     "DSV4_PACKED_BYTES", "DSV4_PAGE_SIZE", "DSV4_ROPE_DIM", "DSV4_SCALE_BYTES",
     "DSV4_SCALE_STRIDE", "LATENT_PACKED_BYTES", "fp8_ue8m0_quant", "gather_dequant",
     "pack_dsv4_kv_bf16", "pack_dsv4_kv_paged", "pack_kv_latent_rope", "split_swa_compress_indices",
-    "to_paged_hnd",
+    "to_paged_hnd", "write_packed_kv_bf16",
 ]

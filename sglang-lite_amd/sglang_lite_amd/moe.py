@@ -120,6 +120,51 @@ def route_topk(logits: torch.Tensor, k: int, score_func: str = "softmax",
     return w, ids
 
 
+def gate(x: torch.Tensor, weight: torch.Tensor, k: int, score_func: str = "softmax",
+         bias: Optional[torch.Tensor] = None, route_scale: float = 1.0,
+         tid2eid: Optional[torch.Tensor] = None, input_ids: Optional[torch.Tensor] = None,
+         logits: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Gate.forward (deepseek_infer/model.py:564-584) in two launches: the router
+    projection ``linear(x.float(), W.float())`` on bf16 MFMA (bf16 products are
+    exact, fp32 accumulation), then score function, bias, top-k (or the hash
+    table row ``tid2eid[input_ids]`` when ``tid2eid`` is given, model.py:576-577),
+    renormalisation and ``route_scale``.  ``x`` bf16 [T, H], ``weight`` bf16 [E, H].
+    Returns ``(weights f32 [T, k], ids int32 [T, k])``; ``logits`` (fp32 [T, E],
+    optional) receives the projection."""
+    _lib.require_device(x, weight, bias, tid2eid, input_ids, what="moe_gate")
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError(f"moe_gate: x and weight must be bfloat16, got {x.dtype}, {weight.dtype}")
+    x2 = x.reshape(-1, x.shape[-1]).contiguous()
+    W = weight.contiguous()
+    T, H = x2.shape
+    E = W.shape[0]
+    if W.shape[1] != H:
+        raise ValueError(f"moe_gate: weight is {tuple(W.shape)}, x has H={H}")
+    dev = x2.device
+    lg = logits if logits is not None else torch.empty(T, E, dtype=torch.float32, device=dev)
+    assert lg.dtype == torch.float32 and lg.is_contiguous() and lg.numel() == T * E
+    b = bias.to(torch.float32).contiguous() if bias is not None else None
+    tab = ids_in = None
+    vocab = 0
+    if tid2eid is not None:
+        if input_ids is None:
+            raise ValueError("moe_gate: hash routing needs input_ids")
+        tab = tid2eid.to(torch.int32).contiguous()
+        if tab.dim() != 2 or tab.shape[1] != k:
+            raise ValueError(f"moe_gate: tid2eid must be [vocab, {k}], got {tuple(tab.shape)}")
+        vocab = tab.shape[0]
+        ids_in = input_ids.reshape(-1).contiguous()
+        if ids_in.dtype not in (torch.int32, torch.int64) or ids_in.numel() != T:
+            raise ValueError("moe_gate: input_ids must be int32/int64 with one id per token")
+    ids = torch.empty(T, k, dtype=torch.int32, device=dev)
+    w = torch.empty(T, k, dtype=torch.float32, device=dev)
+    _lib.call("sgl_moe_gate", x2.data_ptr(), W.data_ptr(), T, H, E, k, SCORE_FUNCS[score_func],
+              _lib.ptr(b), float(route_scale), _lib.ptr(tab), vocab, _lib.ptr(ids_in),
+              int(ids_in is not None and ids_in.dtype == torch.int64), lg.data_ptr(),
+              ids.data_ptr(), w.data_ptr(), _lib.stream_of(x2))
+    return w, ids
+
+
 def _ids32(ids: torch.Tensor) -> torch.Tensor:
     if ids.dtype == torch.int32:
         return ids.contiguous()
@@ -225,5 +270,5 @@ def workspace_size(T: int, H: int, I: int, E: int, k: int, has_shared: bool) -> 
     return int(_lib.load().sgl_moe_workspace_size(T, H, I, E, k, int(has_shared)))
 
 
-__all__ = ["ExpertTable", "MoEWorkspace", "combine", "down", "gate_up", "moe_forward", "permute",
-           "route_topk", "workspace_size"]
+__all__ = ["ExpertTable", "MoEWorkspace", "combine", "down", "gate", "gate_up", "moe_forward",
+           "permute", "route_topk", "workspace_size"]

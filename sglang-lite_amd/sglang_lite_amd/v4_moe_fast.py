@@ -112,7 +112,16 @@ def _expert_forward_fused(self, x: torch.Tensor, weights: Optional[torch.Tensor]
 
 
 def _gate_topk(gate, x: torch.Tensor, input_ids: torch.Tensor):
-    if getattr(gate, "hash", False):
+    """Gate.forward (model.py:564-584).  bf16 router weights (the checkpoint's
+    dtype) take the fused gate kernel, hash-routed layers included; other
+    dtypes keep torch's fp32 projection followed by the top-k kernel."""
+    hashed = bool(getattr(gate, "hash", False))
+    if gate.weight.dtype == torch.bfloat16 and x.dtype == torch.bfloat16:
+        return HM.gate(x, gate.weight, int(gate.topk), str(gate.score_func),
+                       None if hashed else getattr(gate, "bias", None), float(gate.route_scale),
+                       tid2eid=gate.tid2eid if hashed else None,
+                       input_ids=input_ids if hashed else None)
+    if hashed:
         return gate(x, input_ids.flatten())
     logits = F.linear(x.float(), gate.weight.float())
     weights, ids = HM.route_topk(logits, int(gate.topk), str(gate.score_func),

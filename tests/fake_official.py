@@ -55,10 +55,13 @@ def install():
             return _unpatched()
 
     class Gate(nn.Module):
-        def __init__(self, W, topk, score_func="softmax", route_scale=1.0, bias=None):
+        def __init__(self, W, topk, score_func="softmax", route_scale=1.0, bias=None, tid2eid=None):
             super().__init__()
             self.weight = nn.Parameter(W, requires_grad=False)
-            self.topk, self.score_func, self.route_scale, self.hash = topk, score_func, route_scale, False
+            self.topk, self.score_func, self.route_scale = topk, score_func, route_scale
+            self.hash = tid2eid is not None
+            if self.hash:
+                self.tid2eid = nn.Parameter(tid2eid, requires_grad=False)
             self.bias = None if bias is None else nn.Parameter(bias, requires_grad=False)
 
         def forward(self, x, input_ids=None):

@@ -161,3 +161,83 @@ def test_fp4_linear_expert_and_moe_dropins(official, gpu):
     assert OM.topk_margin(logits, k) > 1e-6
     y_ref = OM.moe_forward(x, ids_ref, w_ref, experts, sh, mode=mode)
     assert_gemm_close(f32(y[0]), y_ref, "patched MoE.forward fp4")
+
+
+def test_moe_forward_with_bf16_and_hash_gates(official, gpu):
+    """MoE.forward with the checkpoint's bf16 router weight: the fused gate
+    kernel for a score-routed layer (sqrtsoftplus + bias, route_scale 1.5) and
+    a hash-routed one (tid2eid[input_ids]), each against the oracle."""
+    from sglang_lite_amd import v4_moe_fast as MF
+
+    M, K = official
+    rng = np.random.default_rng(44)
+    T, H, I, E, k, V = 40, 512, 256, 16, 4, 500
+    x = bf16_values(rng, (T, H))
+    Wb = bf16_values(rng, (E, H), scale=H ** -0.5)
+    bias = (rng.standard_normal(E) * 0.05).astype(np.float32)
+    experts = [OM.make_expert(rng, H, I) for _ in range(E)]
+    sh = OM.make_expert(rng, H, I)
+    tid2eid = np.stack([rng.permutation(E)[:k] for _ in range(V)]).astype(np.int32)
+    input_ids = rng.integers(0, V, (1, T))
+    xd = to_dev_bf16(x, gpu)
+    iid = torch.from_numpy(input_ids).to(gpu)
+    for hashed in (False, True):
+        gate = M.Gate(to_dev_bf16(Wb, gpu), k, "sqrtsoftplus", 1.5,
+                      None if hashed else to_dev_f32(bias, gpu),
+                      torch.from_numpy(tid2eid).to(gpu) if hashed else None)
+        moe = M.MoE(H, gate, [M.Expert(_dev_expert(e, gpu)) for e in experts],
+                    M.Expert(_dev_expert(sh, gpu)))
+        assert MF.attach_v4_moe_fast(moe)["enabled"]
+        y = moe(xd.view(1, T, H), iid)
+        logits = OM.router_logits(x, Wb)
+        if hashed:
+            w_ref, ids_ref = OM.route_hash(logits, tid2eid, input_ids, k, "sqrtsoftplus", 1.5)
+        else:
+            assert OM.topk_margin(logits, k, "sqrtsoftplus", bias) > 1e-5
+            w_ref, ids_ref = OM.route_topk(logits, k, "sqrtsoftplus", bias, 1.5)
+        y_ref = OM.moe_forward(x, ids_ref, w_ref, experts, sh)
+        assert_gemm_close(f32(y[0]), y_ref, f"MoE.forward bf16 gate hash={hashed}")
+
+
+def test_moe_layer_captures_into_a_hip_graph(official, gpu):
+    """The patched MoE.forward captured the way the reference's decode runner
+    captures the model (v4_runner/cuda_graph.py:98-137: warmup, synchronize,
+    capture, replay into static buffers).  The official forward cannot be
+    captured (bincount().tolist() syncs, model.py:634); this one launches
+    only HIP kernels on torch's stream.  Every replay, with eager work and
+    syncs between replays, equals the eager forward on the same input bit
+    for bit."""
+    from sglang_lite_amd import v4_moe_fast as MF
+
+    M, K = official
+    rng = np.random.default_rng(45)
+    T, H, I, E, k = 64, 512, 256, 16, 4
+    Wb = bf16_values(rng, (E, H), scale=H ** -0.5)
+    experts = [OM.make_expert(rng, H, I) for _ in range(E)]
+    sh = OM.make_expert(rng, H, I)
+    gate = M.Gate(to_dev_bf16(Wb, gpu), k, "sqrtsoftplus", 1.5,
+                  to_dev_f32((rng.standard_normal(E) * 0.05).astype(np.float32), gpu))
+    moe = M.MoE(H, gate, [M.Expert(_dev_expert(e, gpu)) for e in experts],
+                M.Expert(_dev_expert(sh, gpu)))
+    assert MF.attach_v4_moe_fast(moe)["enabled"]
+    ids0 = torch.zeros(1, T, dtype=torch.long, device=gpu)
+    x_static = to_dev_bf16(bf16_values(rng, (T, H)), gpu).view(1, T, H)
+    for _ in range(3):
+        moe(x_static, ids0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y_static = moe(x_static, ids0)
+    for i in range(4):
+        xi = to_dev_bf16(bf16_values(rng, (T, H)), gpu).view(1, T, H)
+        x_static.copy_(xi)
+        g.replay()
+        torch.cuda.synchronize()
+        eager = moe(xi.clone(), ids0)  # eager launches between replays
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(u8(y_static), u8(eager), err_msg=f"replay {i}")
+    # and the eager result is the oracle's layer
+    x_last = f32(xi[0])
+    logits = OM.router_logits(x_last, Wb)
+    w_ref, ids_ref = OM.route_topk(logits, k, "sqrtsoftplus", f32(gate.bias), 1.5)
+    assert_gemm_close(f32(eager[0]), OM.moe_forward(x_last, ids_ref, w_ref, experts, sh), "graph MoE")

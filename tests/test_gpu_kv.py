@@ -159,3 +159,39 @@ def test_layout_a_dequant_equals_qat_inplace(gpu):
     qat, _ = Q.act_quant_inplace_tilelang(xv[:, :448], 64, round_scale=True)
     np.testing.assert_array_equal(deq[:, :448], qat)
     np.testing.assert_array_equal(deq[:, 448:], xv[:, 448:])
+
+
+@pytest.mark.parametrize("table_on_device", [False, True])
+def test_packed_page_writer_bit_exact(gpu, table_on_device):
+    """write_packed_kv_bf16 = pack_dsv4_kv_bf16 + RadixCache.write_packed_kv
+    (kv_cache.py:340-390) in one kernel: the whole pool, untouched blocks and
+    layers included, equals the oracle's page write of the packed rows."""
+    from sglang_lite_amd import dsv4_kv_pack as KVP
+
+    rng = np.random.default_rng(12 + table_on_device)
+    L, NB, page, T, start = 3, 10, 64, 150, 37
+    xv, xt = _kv(rng, T, 512, torch.bfloat16)
+    rope = xt[:, 448:].contiguous().view(torch.uint8).numpy()
+    rows = OK.pack_layout_a(xv, rope, 4)
+    table = [7, 2, 9, 0]
+    init = rng.integers(0, 256, (L, NB, 1, page, 584), dtype=np.uint8)
+    pool = torch.from_numpy(init).to(gpu)
+    bt = torch.tensor(table, dtype=torch.int32, device=gpu) if table_on_device else table
+    KVP.write_packed_kv_bf16(pool, bt, start, xt.to(gpu), layer_idx=1)
+    want = OK.write_packed_pages(init, table, start, rows, 1)
+    np.testing.assert_array_equal(pool.cpu().numpy(), want)
+
+
+def test_packed_page_writer_errors(gpu):
+    from sglang_lite_amd import dsv4_kv_pack as KVP
+
+    pool = torch.zeros(2, 4, 1, 64, 584, dtype=torch.uint8, device=gpu)
+    kv = torch.zeros(100, 512, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(RuntimeError, match="block_table too short"):
+        KVP.write_packed_kv_bf16(pool, [0], 10, kv)
+    with pytest.raises(RuntimeError, match="out of range"):
+        KVP.write_packed_kv_bf16(pool, [0, 4], 0, kv)
+    with pytest.raises(ValueError, match="layer_idx"):
+        KVP.write_packed_kv_bf16(pool, [0, 1], 0, kv, layer_idx=2)
+    with pytest.raises(ValueError, match="requires block_table"):
+        KVP.write_packed_kv_bf16(pool, [], 0, kv)

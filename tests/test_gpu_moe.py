@@ -244,3 +244,66 @@ def test_tiny_moe_golden_fixture(gpu):
                       "golden h")
     y_ref = (gold["y_bf16_bits"].astype(np.uint32) << 16).view(np.float32)
     assert_gemm_close(f32(y), y_ref, "golden y")
+
+
+def _gate_case(rng, T, H, E, scale=None):
+    x = bf16_values(rng, (T, H))
+    W = bf16_values(rng, (E, H), scale=(scale or H ** -0.5))
+    return x, W
+
+
+@pytest.mark.parametrize("T,H,E,k,score_func,use_bias", [
+    (64, 4096, 256, 8, "sqrtsoftplus", True),
+    (300, 1024, 64, 6, "softmax", False),
+    (32, 256, 8, 2, "sigmoid", True),
+    (1000, 512, 256, 8, "sqrtsoftplus", False),
+    (7, 4096, 256, 8, "softmax", True),
+])
+def test_gate_kernel_matches_oracle(gpu, T, H, E, k, score_func, use_bias):
+    """model.py:564-584 from the hidden states: the bf16-MFMA projection within
+    the fp32 summation bound of the exact logits, the routing of those logits
+    exact, and equal to the oracle's routing of the exact logits where no
+    near-tie lies within the projection's error."""
+    from sglang_lite_amd import moe as M
+
+    print(f"gate T={T} H={H} E={E} k={k} {score_func} bias={use_bias}", flush=True)
+    rng = np.random.default_rng(T + H + E)
+    x, W = _gate_case(rng, T, H, E)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32) if use_bias else None
+    lg = torch.empty(T, E, dtype=torch.float32, device=gpu)
+    w, ids = M.gate(to_dev_bf16(x, gpu), to_dev_bf16(W, gpu), k, score_func,
+                    to_dev_f32(bias, gpu) if use_bias else None, 1.5, logits=lg)
+    torch.cuda.synchronize()
+    exact = OM.router_logits(x, W)
+    mag = (np.abs(x).astype(np.float64) @ np.abs(W).astype(np.float64).T)
+    got = f32(lg)
+    assert np.all(np.abs(got.astype(np.float64) - exact) <= 2.0 ** -21 * mag + 1e-30)
+    w_dev, ids_dev = OM.route_topk(got, k, score_func, bias, 1.5)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_dev)
+    np.testing.assert_allclose(f32(w), w_dev, rtol=2e-6, atol=1e-7)
+    w_ex, ids_ex = OM.route_topk(exact, k, score_func, bias, 1.5)
+    err = float(np.max(np.abs(got.astype(np.float64) - exact)))
+    ok = np.array([OM.topk_margin(exact[t:t + 1], k, score_func, bias) > 8 * err for t in range(T)])
+    assert ok.mean() > 0.9
+    np.testing.assert_array_equal(ids.cpu().numpy()[ok], ids_ex[ok])
+
+
+@pytest.mark.parametrize("ids64", [False, True])
+def test_gate_hash_routing(gpu, ids64):
+    """Hash-routed layers (model.py:576-577): ids = tid2eid[input_ids] exactly,
+    weights = the sqrtsoftplus scores there, renormalised, times route_scale."""
+    from sglang_lite_amd import moe as M
+
+    rng = np.random.default_rng(55 + ids64)
+    T, H, E, k, V = 100, 512, 64, 6, 1000
+    x, W = _gate_case(rng, T, H, E)
+    tid2eid = np.stack([rng.permutation(E)[:k] for _ in range(V)]).astype(np.int32)
+    input_ids = rng.integers(0, V, T).astype(np.int64 if ids64 else np.int32)
+    lg = torch.empty(T, E, dtype=torch.float32, device=gpu)
+    w, ids = M.gate(to_dev_bf16(x, gpu), to_dev_bf16(W, gpu), k, "sqrtsoftplus", None, 1.5,
+                    tid2eid=torch.from_numpy(tid2eid).to(gpu),
+                    input_ids=torch.from_numpy(input_ids).to(gpu), logits=lg)
+    np.testing.assert_array_equal(ids.cpu().numpy(), tid2eid[input_ids])
+    w_ref, ids_ref = OM.route_hash(f32(lg), tid2eid, input_ids, k, "sqrtsoftplus", 1.5)
+    np.testing.assert_array_equal(ids_ref, tid2eid[input_ids])
+    np.testing.assert_allclose(f32(w), w_ref, rtol=2e-6, atol=1e-7)
