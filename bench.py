@@ -142,6 +142,34 @@ def event_avg_ms(torch, fn, iters, flush=None):
     return tot / iters
 
 
+def graph_ms(torch, fn, iters=20, warmup=3):
+    """Device time per call of ``fn`` captured into a HIP graph and replayed
+    back to back between two events: the launch-bound decode path as a
+    serving loop runs it (the reference's decode runner captures the model the
+    same way, engine/v4_runner/cuda_graph.py:98-137), without the Python and
+    ctypes launch overhead that paces an eager loop."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(warmup):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    g.replay()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(iters):
+        g.replay()
+    b.record()
+    b.synchronize()
+    return a.elapsed_time(b) / iters
+
+
 class Prefill:
     """The staged prefill pipeline with events around each stage."""
 
@@ -229,12 +257,15 @@ def fp4_extra(torch, M, K, weights, dev, args, flush):
             M.moe_forward(xd, ids, w, table4, workspace=ws, out=yd, scale_mode=3)
 
         msd = time_steps(torch, dstep, max(args.steps, 10), args.warmup)
+        msg_d = graph_ms(torch, dstep, max(args.steps, 10))
         _, ids = M.route_topk(logits, K_TOP)
         touched = int(torch.unique(ids).numel())
         by = touched * wb + sb_ + 4 * Td * H + 4 * Td * E
         dec.append({"tokens": Td, "ms": round(msd, 4), "tokens_per_s": round(Td / msd * 1e3, 1),
                     "experts_touched": touched, "bytes": by, "gbs": round(by / msd / 1e6, 1),
-                    "hbm_frac": round(by / msd / 1e6 / PEAK_HBM_GBS, 4)})
+                    "hbm_frac": round(by / msd / 1e6 / PEAK_HBM_GBS, 4),
+                    "graph_ms": round(msg_d, 4),
+                    "graph_hbm_frac": round(by / msg_d / 1e6 / PEAK_HBM_GBS, 4)})
         log(f"fp4 decode T={Td}: {msd:.3f} ms, {by / msd / 1e6:.0f} GB/s")
     out["decode_mode3"] = dec
     gw = torch.Generator(device=dev).manual_seed(7)
@@ -438,6 +469,7 @@ def main():
                 M.moe_forward(xd, ids, w, table, workspace=ws, out=yd)
 
             msd = time_steps(torch, dstep, max(args.steps, 10), args.warmup)
+            msg_d = graph_ms(torch, dstep, max(args.steps, 10))
             _, ids = M.route_topk(logits, K_TOP)
             touched = int(torch.unique(ids).numel())
             by = (touched + 1) * (W_BYTES_PER_EXPERT + SCALE_BYTES_PER_EXPERT) + 4 * Td * H + \
@@ -445,8 +477,11 @@ def main():
             dec.append({"tokens": Td, "ms": round(msd, 4), "tokens_per_s": round(Td / msd * 1e3, 1),
                         "experts_touched": touched, "bytes": by,
                         "gbs": round(by / msd / 1e6, 1),
-                        "hbm_frac": round(by / msd / 1e6 / PEAK_HBM_GBS, 4)})
-            log(f"decode T={Td}: {msd:.3f} ms, touched {touched}, {by / msd / 1e6:.0f} GB/s")
+                        "hbm_frac": round(by / msd / 1e6 / PEAK_HBM_GBS, 4),
+                        "graph_ms": round(msg_d, 4),
+                        "graph_hbm_frac": round(by / msg_d / 1e6 / PEAK_HBM_GBS, 4)})
+            log(f"decode T={Td}: {msd:.3f} ms eager, {msg_d:.3f} ms graph, touched {touched}, "
+                f"{by / msg_d / 1e6:.0f} GB/s (graph)")
         extra["decode"] = dec
         # ---- fused gate (router projection on bf16 MFMA + score + top-k), model.py:564-584
         gate = []
@@ -457,11 +492,9 @@ def main():
             xg = torch.randn(Tg, H, generator=gg, device=dev).to(torch.bfloat16)
             lg = torch.empty(Tg, E, dtype=torch.float32, device=dev)
             fn = lambda: M.gate(xg, Wr, K_TOP, "sqrtsoftplus", br, 1.5, logits=lg)  # noqa: E731
-            for _ in range(3):
-                fn()
-            msg = event_avg_ms(torch, fn, 20)
+            msg = graph_ms(torch, fn, 20)
             byt = E * H * 2 + Tg * H * 2 + Tg * E * 4 + Tg * K_TOP * 8
-            gate.append({"tokens": Tg, "ms": round(msg, 5), "gbs": round(byt / msg / 1e6, 1),
+            gate.append({"tokens": Tg, "graph_ms": round(msg, 5), "gbs": round(byt / msg / 1e6, 1),
                          "tflops": round(2.0 * Tg * H * E / msg / 1e9, 1)})
             log(f"gate T={Tg}: {msg * 1e3:.1f} us")
         extra["gate_sqrtsoftplus_bias"] = gate
