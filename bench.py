@@ -566,6 +566,26 @@ def main():
                                           "hbm_frac": round(ab / msa / 1e6 / PEAK_HBM_GBS, 4)},
         }
         log(f"kv pack {msp * 1e3:.1f} us, gather {msg_ * 1e3:.1f} us, pack A paged {msa * 1e3:.1f} us")
+        # ---- sparse MLA attention straight off the packed FP8 pages (64 heads,
+        # 128 query tokens x 2048 gathered rows of the 65536-row cache)
+        from sglang_lite_amd import v4_sparse_mla as SA
+        ga = torch.Generator().manual_seed(6)
+        qa = torch.randn(1, 128, 64, 512, generator=ga).to(torch.bfloat16).to(dev)
+        pages_a = KVP.pack_dsv4_kv_paged(kva, 64).unsqueeze(0)
+        ia = torch.stack([torch.randperm(65536, generator=ga)[:2048] for _ in range(128)]).to(
+            torch.int32).view(1, 128, 2048).to(dev)
+        sink_a = torch.randn(64, generator=ga).to(dev)
+        fa = lambda: SA.sparse_attn_packed(qa, pages_a, sink_a, ia, 512 ** -0.5)  # noqa: E731
+        fa()
+        msa_ = event_avg_ms(torch, fa, 10, flush)
+        ab_ = 128 * 2048 * 584 + 2 * 128 * 64 * 512 * 2 + 128 * 2048 * 4
+        afl = 4.0 * 128 * 64 * 2048 * 512
+        extra["sparse_attn_packed_128x2048_h64"] = {
+            "ms": round(msa_, 5), "gbs": round(ab_ / msa_ / 1e6, 1),
+            "hbm_frac": round(ab_ / msa_ / 1e6 / PEAK_HBM_GBS, 4),
+            "tflops": round(afl / msa_ / 1e9, 1),
+            "mfma_frac_bf16": round(afl / msa_ / 1e9 / 2500.0, 4)}
+        log(f"sparse attn packed: {msa_ * 1e3:.1f} us")
         extra["fp4"] = fp4_extra(torch, M, K, weights, dev, args, flush)
         result["extra"] = extra
 

@@ -303,6 +303,36 @@ int sgl_kv_pack_to_pages(const void* kv, int dtype, int64_t T, int64_t ldkv, int
                          int page_size, int64_t num_blocks, int layer_idx, int num_layers,
                          void* pool, sgl_stream_t stream);
 
+/* KV row formats the sparse attention reads. */
+enum sgl_attn_kv_format {
+  SGL_ATTN_KV_BF16 = 0,    /* bf16 rows [n, ld] (ld >= 512, ld % 8 == 0) */
+  SGL_ATTN_KV_A = 1,       /* layout A 584-byte rows [n, 584] (dsv4_kv_pack.py:40-75) */
+  SGL_ATTN_KV_A_PAGED = 2  /* layout A footer pages of page_size rows (dsv4_kv_pack.py:104-146) */
+};
+
+/* Sparse multi-head attention with an attention sink over gathered KV rows:
+ * for query (b, m) and head h, s_j = (q[b,m,h] . kv[b, idx[b,m,j]]) * scale
+ * (idx -1, or outside [0, n), masked), online softmax over blocks of 64 rows
+ * with bf16 probabilities in the P.V product and fp32 ones in the normaliser,
+ * o = acc / (sum + exp(attn_sink[h] - max)) as bf16.  q bf16 [B, M, Hh, 512],
+ * o bf16 [B, M, Hh, 512], attn_sink fp32 [Hh], topk_idxs int32 [B, M, K]; the
+ * kv rows of batch element b start kv_batch_stride bytes apart; the FP8
+ * layouts are dequantized on the way in (exactly: e4m3 * 2^(e8m0-127) fits
+ * bf16), so the packed cache is read directly.  A small batch (decode) splits
+ * the K rows over workgroups and needs a device workspace of
+ * sgl_sparse_attn_workspace_size(B, M, Hh, K) bytes (0: none), 16-byte aligned.
+ * Replaces deepseek_infer/kernel.py:350-368 sparse_attn (kernel :276-347) and
+ * engine/v4_sparse_torch.py:20-106 sparse_attn_torch; with the FP8 formats,
+ * the gather-dequant + attention of engine/v4_sparse_mla.py:104-118. */
+int sgl_sparse_attn(const void* q, int64_t B, int64_t M, int Hh, const void* kv, int kv_format,
+                    int page_size, int64_t n, int64_t kv_batch_stride, int64_t ld,
+                    const float* attn_sink, const int32_t* topk_idxs, int64_t K,
+                    float softmax_scale, void* o, void* workspace, size_t workspace_bytes,
+                    sgl_stream_t stream);
+
+/* Workspace bytes sgl_sparse_attn needs for this shape on the current device. */
+size_t sgl_sparse_attn_workspace_size(int64_t B, int64_t M, int Hh, int64_t K);
+
 /* Logical [T, 584] rows -> footer pages [ceil(T/page), page*584] (padding rows
  * zero).  Replaces engine/dsv4_kv_pack.py:104-146 to_paged_hnd. */
 int sgl_kv_to_paged(const void* packed, int64_t T, int page_size, void* pages,

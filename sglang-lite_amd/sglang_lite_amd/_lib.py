@@ -38,6 +38,8 @@ SCORE_SOFTMAX, SCORE_SIGMOID, SCORE_SQRTSOFTPLUS = 0, 1, 2
 KV_LAYOUT_A, KV_LAYOUT_B = 0, 1
 # sgl_expert_format
 EXPERT_FP8_BLOCK128, EXPERT_FP4_E2M1 = 0, 1
+# sgl_attn_kv_format
+ATTN_KV_BF16, ATTN_KV_A, ATTN_KV_A_PAGED = 0, 1, 2
 
 P = c_void_p
 I64 = c_int64
@@ -77,6 +79,11 @@ SIGNATURES = {
     "sgl_kv_pack_to_pages": (
         c_int, [P, c_int, I64, I64, c_int, P, I64, I64, c_int, I64, c_int, c_int, P, P]
     ),
+    "sgl_sparse_attn": (
+        c_int,
+        [P, I64, I64, c_int, P, c_int, c_int, I64, I64, I64, P, P, I64, c_float, P, P, c_size_t, P],
+    ),
+    "sgl_sparse_attn_workspace_size": (c_size_t, [I64, I64, c_int, I64]),
     "sgl_kv_to_paged": (c_int, [P, I64, c_int, P, P]),
     "sgl_kv_gather_dequant": (c_int, [P, c_int, c_int, c_int, I64, P, I64, I64, P, P]),
     "sgl_split_swa_compress_indices": (c_int, [P, c_int, I64, I64, I64, P, P, P, P, P]),

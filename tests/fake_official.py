@@ -22,6 +22,7 @@ def install():
     K.act_quant = _unpatched
     K.fp8_gemm = _unpatched
     K.fp4_gemm = _unpatched
+    K.sparse_attn = _unpatched
     M = types.ModuleType("model")
     M.world_size = 1
     M.rank = 0
@@ -31,6 +32,7 @@ def install():
     M.act_quant = K.act_quant
     M.fp8_gemm = K.fp8_gemm
     M.fp4_gemm = K.fp4_gemm
+    M.sparse_attn = K.sparse_attn
 
     def linear(x, weight, bias=None):
         """The dispatch of model.py:108-120 on the module's (patchable) names."""
