@@ -9,22 +9,32 @@
 //         l = l a + sum_j exp(s_j - m');  o = o a + sum_j bf16(exp(s_j - m')) kv_j
 //     o / (l + exp(sink[h] - m))  -> bf16
 // The probabilities are cast to bf16 for the P.V product and summed in fp32
-// for l, as the reference kernel does.  The KV rows are bf16, or the 584-byte
-// layout A rows / footer pages of engine/dsv4_kv_pack.py dequantized on the
-// way in (e4m3 * 2^(e8m0-127) is exact in bf16), so the packed cache feeds
-// the attention with no bf16 copy of it in HBM.
+// for l, as the reference kernel does (the exponentials are taken base 2 on
+// log2(e)-scaled scores, the same values up to fp32 rounding).  The KV rows
+// are bf16, or the 584-byte layout A rows / footer pages of
+// engine/dsv4_kv_pack.py dequantized on the way in (e4m3 * 2^(e8m0-127) is
+// exact in bf16; v_cvt_scalef32_pk_bf16_fp8 rounds it exactly), so the packed
+// cache feeds the attention with no bf16 copy of it in HBM.
 //
 // One workgroup per (query token, group of 64 heads, split of the rows); a
 // small batch (decode) splits its rows over several workgroups so every CU
 // has one, and a second kernel merges the splits' partial maxima, sums and
-// outputs.  Per block of 64 rows: the eight wavefronts gather and
-// dequantize the rows into LDS twice — row-major [token][d] (the A operand of
-// S^T = KV . Q^T, v_mfma_f32_16x16x32_bf16) and transposed [d][token] (the B
-// operand of O += P . V, v_mfma_f32_16x16x16_bf16) — both swizzled so the
-// 16-lane fragment reads are conflict-free.  S^T comes out of the MFMA with
-// lane (g, r) holding tokens 4g..4g+3 of head r, which is exactly the A
-// fragment layout of P for the P.V MFMA: the probabilities never leave the
-// registers.  Q stays in registers for the whole kernel.
+// outputs.  Eight wavefronts, two per SIMD: wavefront (hg, dq) owns heads
+// [32 hg, +32) of the group.  Per block of 64 rows:
+//   gather:  each wavefront dequantizes 8 rows (loaded during the previous
+//            block) into one row-major bf16 tile in LDS (swizzled);
+//   S^T = KV . Q^T (v_mfma_f32_32x32x16_bf16, Q^T fragments parked in LDS):
+//            wavefront dq = 2 dh + th the partial of the 32 tokens of half th
+//            over dims [256 dh, +256); the partials meet in LDS and each of
+//            the group's four wavefronts sums and finishes the softmax
+//            (identically);
+//   O^T += V^T . P^T: P^T is the S^T accumulator itself, cast to bf16 (the
+//            32x32 output layout of S^T is the B operand layout of the next
+//            MFMA), and V^T fragments come straight from the row-major tile
+//            with ds_read_b64_tr_b16, so no transposed copy is stored; each
+//            wavefront its 128 dims [128 dq, +128) over all 64 tokens.
+// In both products lane (head c, half g) owns head c: the running max, sum
+// and rescale factor of a head live in the lanes that hold its outputs.
 #include "sgl_common.h"
 #include "sgl_numeric.h"
 
@@ -33,12 +43,15 @@ namespace {
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef short v4s __attribute__((ext_vector_type(4)));
-typedef float v4f __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef v4s __attribute__((address_space(3))) lds_v4s;
 
 constexpr int kD = 512;     // head dim: 448 latent + 64 rope
 constexpr int kBlk = 64;    // gathered rows per block
 constexpr int kHG = 64;     // heads per workgroup
 constexpr int kARow = 584, kAData = 576, kANope = 448;
+constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnArgs {
   const uint16_t* q;   // [B, M, Hh, 512] bf16
@@ -47,6 +60,7 @@ struct AttnArgs {
   int64_t kv_bstride;  // bytes between batch elements
   int64_t ld;          // bf16 rows: elements per row
   int page;            // footer pages: rows per page
+  int page_shift;      // log2(page) when page is a power of two, else -1
   const float* sink;   // [Hh]
   const int32_t* idx;  // [B, M, K]
   int64_t M, K;
@@ -56,317 +70,308 @@ struct AttnArgs {
   int nsplit;          // > 1: the K rows are split over workgroups, partials to ws
   int bps;             // 64-row blocks per split
   float* ws_acc;       // [B, M, nsplit, Hh, 512] unnormalised outputs
-  float* ws_ml;        // [B, M, nsplit, Hh, 2] running max and sum
+  float* ws_ml;        // [B, M, nsplit, Hh, 2] running max (log2 units) and sum
 };
 
-// row-major copy: token t, 16-byte chunk c (8 dims) at t*1024 + ((c ^ (t & 15)) << 4)
-__device__ __forceinline__ uint32_t kv_off(int t, int c) { return (uint32_t)(t * 1024 + ((c ^ (t & 15)) << 4)); }
-// transposed copy: dim d, token quad q (4 tokens, 8 bytes) at d*136 + 8q: the
-// 136-byte row pitch puts the 16 dims a fragment read touches on 16 distinct
-// bank pairs, and keeps every offset affine in the tile indices
-constexpr int kTPitch = 136;
-__device__ __forceinline__ uint32_t kvt_off(int d, int q) { return (uint32_t)(d * kTPitch + 8 * q); }
+// Row-major tile: token t, 16-byte chunk c (8 dims) at t*1024 + ((c ^ sw(t)) << 4).
+// sw rotates the token's low four bits, which keeps conflict-free both the
+// S^T fragment reads (16 B of one chunk from 16 consecutive tokens) and the
+// transpose reads (8 B of 4 consecutive chunks from 4 consecutive tokens).
+__device__ __forceinline__ uint32_t sw(int t) { return (uint32_t)(((t & 3) << 2) | ((t >> 2) & 3)); }
 
-__device__ __forceinline__ uint32_t word_of(const uint4& v, int c) {
-  return c < 2 ? (c == 0 ? v.x : v.y) : (c == 2 ? v.z : v.w);
+__device__ __forceinline__ v4s lds_tr16(const uint8_t* base, uint32_t off) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(base + off));
 }
 
-// Raw bytes of row `id` for this lane, issued early and converted later:
-// bf16 rows -> 8 bf16 values; layout A -> lanes < 56: 8 e4m3 bytes in x,y and
-// the group's e8m0 byte in z; lanes 56..63: 8 rope bf16 values.
-template <int FMT>
-__device__ __forceinline__ uint4 load_raw(const AttnArgs& a, const uint8_t* kvb, int64_t id, int lane) {
-  if constexpr (FMT == SGL_ATTN_KV_BF16) {
-    return *reinterpret_cast<const uint4*>(kvb + (id * a.ld + lane * 8) * 2);
-  } else {
-    const uint8_t* data;
-    const uint8_t* foot;
-    if constexpr (FMT == SGL_ATTN_KV_A_PAGED) {
-      const int64_t pg = id / a.page, l = id - pg * a.page;
-      const uint8_t* pbase = kvb + pg * (int64_t)a.page * kARow;
-      data = pbase + l * kAData;
-      foot = pbase + (int64_t)a.page * kAData + l * 8;
-    } else {
-      data = kvb + id * kARow;
-      foot = data + kAData;
-    }
-    if (lane < 56) {
-      const uint2 qv = *reinterpret_cast<const uint2*>(data + lane * 8);
-      return make_uint4(qv.x, qv.y, foot[lane >> 3], 0u);
-    }
-    const uint8_t* src = data + kANope + (lane - 56) * 16;
-    const uint2 x = *reinterpret_cast<const uint2*>(src);
-    const uint2 y = *reinterpret_cast<const uint2*>(src + 8);
-    return make_uint4(x.x, x.y, y.x, y.y);
-  }
+template <bool HI>
+__device__ __forceinline__ uint32_t cvt2_e4m3_bf16(uint32_t w, float sc) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, sc, HI));
 }
 
 template <int FMT>
-__device__ __forceinline__ uint4 convert_raw(const uint4 r, int lane) {
-  if constexpr (FMT == SGL_ATTN_KV_BF16) {
-    return r;
-  } else {
-    if (lane >= 56) return r;
-    const uint32_t sb = r.z;
-    const float sc = sb == 0xFFu ? bits_f32(0x7FC00000u) : (sb == 0 ? bits_f32(0x00400000u) : bits_f32(sb << 23));
-    float d[8];
-    unpack4_e4m3(r.x, d);
-    unpack4_e4m3(r.y, d + 4);
-    return make_uint4(pk2_bf16_exact(d[0] * sc, d[1] * sc), pk2_bf16_exact(d[2] * sc, d[3] * sc),
-                      pk2_bf16_exact(d[4] * sc, d[5] * sc), pk2_bf16_exact(d[6] * sc, d[7] * sc));
-  }
-}
-
-// Eight wavefronts: wavefront w owns heads [16 (w%4), +16) of the workgroup's
-// group and dims [256 (w/4), +256) of the output.  Per block of 64 rows:
-//   gather: each wavefront dequantizes 8 rows (its registers were loaded
-//           during the previous block) into the row-major and transposed copies;
-//   S^T:    each wavefront the partial over its 256 dims; the upper-half
-//           wavefronts hand theirs over in LDS;
-//   softmax: the lower-half wavefront of each head group, which passes the
-//           bf16 probabilities and the rescale factors on in LDS;
-//   P.V:    each wavefront its 256 output dims (16 tiles of 16).
-template <int FMT>
-__global__ __launch_bounds__(512) void sparse_attn_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void sparse_attn_kernel(const AttnArgs a) {
   __shared__ __align__(16) uint8_t sKV[kBlk * 1024];
-  __shared__ __align__(16) uint8_t sKVT[kD * kTPitch];
-  __shared__ __align__(16) v4f sS[4][kBlk / 16][64];
-  __shared__ __align__(16) v4s sP[4][kBlk / 16][64];
-  __shared__ float sAlpha[4][16];
-  __shared__ float sDen[4][16];
+  __shared__ __align__(16) uint4 sQ[2][2][16][64];   // Q^T fragments, [hg][dh][ks][lane]
+  __shared__ __align__(16) float4 sS[8][4][64];      // S^T partials, [wave][quad][lane]
 
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int hg = wave & 3, dh = wave >> 2;
-  const int g4 = lane >> 4, r16 = lane & 15;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // wavefront (hg, dq): heads [32 hg, +32) of the group; S^T over dims
+  // [256 dh, +256) for tokens [32 th, +32) of a block (dq = 2 dh + th), and
+  // O^T over dims [128 dq, +128) for all 64 tokens
+  const int hg = wave & 1, dq = wave >> 1, dh = dq >> 1, th = dq & 1;
+  const int g2 = lane >> 5, c32 = lane & 31;
   const int64_t m = blockIdx.x, b = blockIdx.y;
   const int split = (int)(blockIdx.z % a.nsplit);
-  const int h0 = (int)(blockIdx.z / a.nsplit) * kHG + hg * 16;  // this wavefront's first head
+  const int h0 = (int)(blockIdx.z / a.nsplit) * kHG + 32 * hg;  // this wavefront's first head
   const bool active = h0 < a.Hh;
   const uint8_t* kvb = a.kv + b * a.kv_bstride;
   const int32_t* idxp = a.idx + (b * a.M + m) * a.K;
-  const int d0 = 256 * dh;
-  // row-major fragment bases: token r16, chunk 32 dh + 4 c + g4 (c = ks % 4)
-  uint32_t qb[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) qb[c] = kv_off(r16, 32 * dh + 4 * c + g4);
-  const uint32_t vbase = kvt_off(d0 + r16, g4);  // transposed fragment base
 
-  // Q^T fragments over this wavefront's 256 dims: lane (g, r) holds
-  // q[h0 + r][d0 + 32 ks + 8 g, +8)
-  v8bf qf[8];
+  // S^T A operand: token 32 th + c32, chunk 32 dh + 2 ks + g2; the swizzle
+  // only touches the chunk's low four bits, so ks % 8 picks one of eight
+  // bases and the rest is an immediate offset
+  uint32_t qa[8];
+#pragma unroll
+  for (int k8 = 0; k8 < 8; ++k8)
+    qa[k8] = (32 * th + c32) * 1024 + 512 * dh + ((((2 * k8 + g2) ^ sw(c32)) & 15) << 4);
+  // V^T A operand by transpose read: in each 16-lane group G, source lane s
+  // reads 4 dims of token 16 s4 + 8 e + 4 (G >> 1) + (s >> 2), and the read
+  // hands each lane 4 consecutive tokens of one dim, i.e. 4 consecutive K
+  // elements of one row of V^T.  Bases for each (e, dt).
+  uint32_t va[2][4];
   {
-    const int h = min(h0 + r16, a.Hh - 1);
-    const uint16_t* qrow = a.q + ((b * a.M + m) * a.Hh + h) * (int64_t)kD + d0;
+    const int G = lane >> 4, s16 = lane & 15;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qf[ks] = *reinterpret_cast<const v8bf*>(qrow + 32 * ks + 8 * g4);
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const int tok = 8 * e + 4 * (G >> 1) + (s16 >> 2);
+        const int cl = 4 * dt + 2 * (G & 1) + ((s16 & 3) >> 1);
+        va[e][dt] = tok * 1024 + 256 * dq + ((cl ^ sw(tok)) << 4) + 8 * (s16 & 1);
+      }
   }
-  v4f acc[16];
-#pragma unroll
-  for (int dt = 0; dt < 16; ++dt) acc[dt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  const float NEG_INF = -__builtin_huge_valf();
-  float m_run = NEG_INF, l_run = 0.0f;  // lower-half wavefronts: per head r16
 
-  // block j's indices (one per lane) and this wavefront's 8 raw rows: token
-  // quads wave and wave + 8
+  // Q^T B operand: lane (head c32, half g2) of step ks holds
+  // q[h0 + c32][256 dh + 16 ks + 8 g2, +8); the two token halves share it
+  {
+    const int h = min(h0 + c32, a.Hh - 1);
+    const uint16_t* qrow = a.q + ((b * a.M + m) * a.Hh + h) * (int64_t)kD + 256 * dh + 8 * g2;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int ks = 8 * th + k;
+      sQ[hg][dh][ks][lane] = *reinterpret_cast<const uint4*>(qrow + 16 * ks);
+    }
+  }
+  v16f acc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[dt][r] = 0.0f;
+  const float NEG_INF = -__builtin_huge_valf();
+  const float c1 = a.scale * kLog2e;
+  float m_run = NEG_INF, l_run = 0.0f;  // head c32: reference point (log2 units) and sum
+
+  // layout A per-lane byte offsets: lanes < 56 take 8 e4m3 bytes and the
+  // row's 8-byte scale footer, lanes 56..63 the 16 rope bytes in two halves
+  const bool nope_lane = lane < 56;
+  const uint32_t o0 = nope_lane ? 8 * lane : kANope + 16 * (lane - 56);
+  const uint32_t o1r = kANope + 8 + 16 * (lane - 56);  // rope second half (rope lanes)
+  const int sb_shift = 8 * ((lane >> 3) & 3);
+  const bool sb_hi = (lane >> 3) >= 4;
+
   auto load_ids = [&](int j) -> int32_t {
     const int64_t p = (int64_t)j * kBlk + lane;
     const int32_t id = p < a.K ? idxp[p] : -1;
     return (id >= 0 && id < a.n) ? id : -1;
   };
+  // this wavefront's 8 rows of the block: tokens 8 wave + rr
   uint4 raw[8];
   auto load_rows = [&](int32_t ids) {
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const int t = 4 * (wave + 8 * (r >> 2)) + (r & 3);
-      const int id = __builtin_amdgcn_readfirstlane(__shfl(ids, t, 64));
-      raw[r] = id >= 0 ? load_raw<FMT>(a, kvb, id, lane) : make_uint4(0, 0, 0, 0);
+    for (int rr = 0; rr < 8; ++rr) {
+      const int id = __builtin_amdgcn_readlane(ids, 8 * wave + rr);
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (id >= 0) {
+        if constexpr (FMT == SGL_ATTN_KV_BF16) {
+          v = *reinterpret_cast<const uint4*>(kvb + (int64_t)id * a.ld * 2 + lane * 16);
+        } else {
+          const uint8_t* data;
+          const uint8_t* foot;
+          if constexpr (FMT == SGL_ATTN_KV_A_PAGED) {
+            const int pg = a.page_shift >= 0 ? id >> a.page_shift : (int)((uint32_t)id / (uint32_t)a.page);
+            const int l = id - pg * a.page;
+            const uint8_t* pbase = kvb + (int64_t)pg * a.page * kARow;
+            data = pbase + l * kAData;
+            foot = pbase + a.page * kAData + l * 8;
+          } else {
+            data = kvb + (int64_t)id * kARow;
+            foot = data + kAData;
+          }
+          const uint2 x = *reinterpret_cast<const uint2*>(data + o0);
+          const uint2 y = *reinterpret_cast<const uint2*>(nope_lane ? foot : data + o1r);
+          v = make_uint4(x.x, x.y, y.x, y.y);
+        }
+      }
+      raw[rr] = v;
+    }
+  };
+  auto store_rows = [&]() {
+#pragma unroll
+    for (int rr = 0; rr < 8; ++rr) {
+      uint4 v = raw[rr];
+      if constexpr (FMT != SGL_ATTN_KV_BF16) {
+        const uint32_t word = sb_hi ? v.w : v.z;
+        const float sc = bits_f32(((word >> sb_shift) & 0xFFu) << 23);  // 2^(e8m0 - 127)
+        // word by word: a select of whole uint4 values goes through scratch
+        const uint32_t c0 = cvt2_e4m3_bf16<false>(v.x, sc), c1 = cvt2_e4m3_bf16<true>(v.x, sc);
+        const uint32_t c2 = cvt2_e4m3_bf16<false>(v.y, sc), c3 = cvt2_e4m3_bf16<true>(v.y, sc);
+        v.x = nope_lane ? c0 : v.x;
+        v.y = nope_lane ? c1 : v.y;
+        v.z = nope_lane ? c2 : v.z;
+        v.w = nope_lane ? c3 : v.w;
+      }
+      const int t = 8 * wave + rr;
+      *reinterpret_cast<uint4*>(sKV + t * 1024 + ((lane ^ sw(t)) << 4)) = v;
     }
   };
 
   const int nblk_all = (int)((a.K + kBlk - 1) / kBlk);
-  const int jb = split * a.bps;                    // this split's first block
+  const int jb = split * a.bps;  // this split's first block
   const int nblk = jb + a.bps < nblk_all ? jb + a.bps : nblk_all;
-  // indices run two blocks ahead of the rows, the rows one block ahead of the
-  // MFMAs, so neither load latency sits in front of a block's compute
+  // indices run two blocks ahead of the MFMAs, the rows one block ahead
   int32_t ids = jb < nblk ? load_ids(jb) : -1;
   int32_t ids_next = jb + 1 < nblk ? load_ids(jb + 1) : -1;
   load_rows(ids);
   for (int j = jb; j < nblk; ++j) {
     const uint64_t valid = __ballot(ids >= 0);
-    __syncthreads();  // the previous block's LDS is consumed
-#pragma unroll
-    for (int qh = 0; qh < 2; ++qh) {
-      const int qd = wave + 8 * qh;
-      uint4 v[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        v[u] = convert_raw<FMT>(raw[4 * qh + u], lane);
-        *reinterpret_cast<uint4*>(sKV + kv_off(4 * qd + u, lane)) = v[u];
-      }
-      // dim 8 lane + c of the four tokens as one 8-byte word per c
-      uint2 cw[8];
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const int sh = (c & 1) * 16;
-        const uint32_t t0 = (word_of(v[0], c >> 1) >> sh) & 0xFFFFu, t1 = (word_of(v[1], c >> 1) >> sh) & 0xFFFFu;
-        const uint32_t t2 = (word_of(v[2], c >> 1) >> sh) & 0xFFFFu, t3 = (word_of(v[3], c >> 1) >> sh) & 0xFFFFu;
-        cw[c] = make_uint2(t0 | (t1 << 16), t2 | (t3 << 16));
-      }
-      // lanes start at different c (a select chain, no dynamic register
-      // index) so the lanes sharing a bank pair write at different steps
-#pragma unroll
-      for (int w = 0; w < 8; ++w) {
-        const int c = (w + lane) & 7;
-        uint2 x = cw[0];
-#pragma unroll
-        for (int e = 1; e < 8; ++e) x = c == e ? cw[e] : x;
-        *reinterpret_cast<uint2*>(sKVT + kvt_off(8 * lane + c, qd)) = x;
-      }
-    }
-    __syncthreads();  // block j is in LDS
-    if (j + 1 < nblk) {  // the next block's rows load while this one is computed
+    __syncthreads();  // the previous block's tile is consumed
+    store_rows();
+    __syncthreads();  // block j (and, the first time, Q) is in LDS
+    if (j + 1 < nblk) {
       ids = ids_next;
       load_rows(ids);
       if (j + 2 < nblk) ids_next = load_ids(j + 2);
     }
-
-    // partial S^T over this wavefront's dims
-    v4f s[kBlk / 16];
+    if (!active) {
+      __syncthreads();  // (partials exchanged)
+      continue;
+    }
+    // partial S^T of tile th over dims [256 dh, +256): lane (head c32, g2)
+    // gets token 32 th + 8 (r / 4) + 4 g2 + r % 4 in sp[r]
+    v16f sp;
 #pragma unroll
-    for (int tt = 0; tt < kBlk / 16; ++tt) s[tt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    if (active) {
+    for (int r = 0; r < 16; ++r) sp[r] = 0.0f;
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        // chunk 32 dh + 4 ks + g of token 16 tt + r: the swizzle only flips the
-        // low 4 chunk bits, so the address is qb[ks % 4] plus a constant
-        const uint32_t off = (uint32_t)(256 * (ks >> 2));
-        v8bf kvf[kBlk / 16];
+    for (int ks = 0; ks < 16; ++ks) {
+      const v8bf qf = __builtin_bit_cast(v8bf, sQ[hg][dh][ks][lane]);
+      const v8bf kvf = *reinterpret_cast<const v8bf*>(sKV + qa[ks & 7] + 256 * (ks >> 3));
+      sp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kvf, qf, sp, 0, 0, 0);
+    }
 #pragma unroll
-        for (int tt = 0; tt < kBlk / 16; ++tt)
-          kvf[tt] = *reinterpret_cast<const v8bf*>(sKV + qb[ks & 3] + off + 16384 * tt);
+    for (int q4 = 0; q4 < 4; ++q4)
+      sS[wave][q4][lane] = make_float4(sp[4 * q4], sp[4 * q4 + 1], sp[4 * q4 + 2], sp[4 * q4 + 3]);
+    __syncthreads();  // partials exchanged
+    // full S^T of both tiles: tile tt = partial (dh 0) + partial (dh 1), the
+    // same sum in each of the head group's four wavefronts
+    v16f s[2];
 #pragma unroll
-        for (int tt = 0; tt < kBlk / 16; ++tt)
-          s[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kvf[tt], qf[ks], s[tt], 0, 0, 0);
-        // (keeps the compiler from hoisting every read of the block ahead of
-        // the MFMAs, which would need 128 more registers)
-        if (ks & 1) __builtin_amdgcn_sched_barrier(0);
-      }
-      if (dh == 1) {
+    for (int tt = 0; tt < 2; ++tt) {
+      const int w0 = hg + 2 * tt, w1 = hg + 4 + 2 * tt;  // (hg, dh = 0 / 1, th = tt)
 #pragma unroll
-        for (int tt = 0; tt < kBlk / 16; ++tt) sS[hg][tt][lane] = s[tt];
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const float4 x = sS[w0][q4][lane], y = sS[w1][q4][lane];
+        s[tt][4 * q4] = x.x + y.x;
+        s[tt][4 * q4 + 1] = x.y + y.y;
+        s[tt][4 * q4 + 2] = x.z + y.z;
+        s[tt][4 * q4 + 3] = x.w + y.w;
       }
     }
-    __syncthreads();
-    v4s pk[kBlk / 16];
-    if (active && dh == 0) {
-      // full S^T (lane (g, r): tokens 16 tt + 4 g + i of head r), online softmax
-      float mb = NEG_INF;
+    if (valid != ~0ull) {
+      const uint64_t vl = g2 ? (valid >> 4) : valid;
 #pragma unroll
-      for (int tt = 0; tt < kBlk / 16; ++tt) {
-        const v4f o = sS[hg][tt][lane];
+      for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int t = 16 * tt + 4 * g4 + i;
-          const float x = ((valid >> t) & 1ull) ? (s[tt][i] + o[i]) * a.scale : NEG_INF;
-          s[tt][i] = x;
-          mb = fmaxf_(mb, x);
-        }
-      }
-      mb = fmaxf_(mb, __shfl_xor(mb, 16, 64));
-      mb = fmaxf_(mb, __shfl_xor(mb, 32, 64));
-      const float m_new = fmaxf_(m_run, mb);
-      const float ref = m_new == NEG_INF ? 0.0f : m_new;  // a fully masked prefix keeps o = 0
-      const float alpha = expf(m_run - ref);
-      float ls = 0.0f;
-#pragma unroll
-      for (int tt = 0; tt < kBlk / 16; ++tt) {
-        float p[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p[i] = expf(s[tt][i] - ref);
-          ls += p[i];
-        }
-        const uint32_t w0 = pk2_bf16_exact(p[0], p[1]), w1 = pk2_bf16_exact(p[2], p[3]);
-        pk[tt] = v4s{(short)(w0 & 0xFFFFu), (short)(w0 >> 16), (short)(w1 & 0xFFFFu), (short)(w1 >> 16)};
-        sP[hg][tt][lane] = pk[tt];
-      }
-      ls += __shfl_xor(ls, 16, 64);
-      ls += __shfl_xor(ls, 32, 64);
-      l_run = l_run * alpha + ls;
-      m_run = m_new;
-      if (g4 == 0) sAlpha[hg][r16] = alpha;
+        for (int r = 0; r < 16; ++r)
+          if (!((vl >> (32 * tt + 8 * (r >> 2) + (r & 3))) & 1ull)) s[tt][r] = NEG_INF;
     }
-    __syncthreads();
-    if (active) {
-      if (dh == 1) {
+    // online softmax of head c32 (scale > 0: max(s) * c1 = max(s * c1))
+    float mx = NEG_INF;
 #pragma unroll
-        for (int tt = 0; tt < kBlk / 16; ++tt) pk[tt] = sP[hg][tt][lane];
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, s[tt][r]);
+    mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+    // The reference point moves only when the block maximum exceeds it by
+    // more than 8 (log2 units): the probabilities stay <= 256 (exact range
+    // in bf16, same relative rounding) and the accumulator is rarely
+    // rescaled.  Any reference >= the running max gives the same softmax.
+    const float m_blk = mx * c1;
+    const bool move = !(m_blk <= m_run + 8.0f);  // also true while m_run = -inf
+    const float m_new = move ? __builtin_fmaxf(m_run, m_blk) : m_run;
+    const float ref = m_new == NEG_INF ? 0.0f : m_new;  // a fully masked prefix keeps o = 0
+    const float alpha = move ? __builtin_amdgcn_exp2f(m_run - ref) : 1.0f;
+    float ls = 0.0f;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[tt][r], c1, -ref));
+        ls += p;
+        s[tt][r] = p;
       }
-      // O rows are heads 4 g + i
-      float al[4];
+    ls += __shfl_xor(ls, 32, 64);
+    l_run = l_run * alpha + ls;
+    m_run = m_new;
+    // P^T B operands: K step s4 (16 tokens) = tile s4 / 2, registers 8 (s4 % 2) + e
+    v8bf pb[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) al[i] = sAlpha[hg][4 * g4 + i];
+    for (int s4 = 0; s4 < 4; ++s4) {
+      v8s w;
 #pragma unroll
-      for (int dt = 0; dt < 16; ++dt)
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t pk = pk2_bf16(s[s4 >> 1][8 * (s4 & 1) + 2 * e], s[s4 >> 1][8 * (s4 & 1) + 2 * e + 1]);
+        w[2 * e] = (short)(pk & 0xFFFFu);
+        w[2 * e + 1] = (short)(pk >> 16);
+      }
+      pb[s4] = __builtin_bit_cast(v8bf, w);
+    }
+    if (j > jb && __ballot(alpha != 1.0f)) {  // (the accumulator is zero before the first block)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[dt][i] *= al[i];
-      // O += P . V over this wavefront's 16 dim tiles
+      for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int dt = 0; dt < 16; ++dt) {
-        v4s vb[kBlk / 16];
+        for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+    }
+    // O^T += V^T . P^T over this wavefront's 4 tiles of 32 dims (K step
+    // outer: four independent accumulators between dependent MFMAs)
 #pragma unroll
-        for (int tt = 0; tt < kBlk / 16; ++tt) {
-          const uint2 vv = *reinterpret_cast<const uint2*>(sKVT + vbase + 16 * kTPitch * dt + 32 * tt);
-          vb[tt] = v4s{(short)(vv.x & 0xFFFFu), (short)(vv.x >> 16), (short)(vv.y & 0xFFFFu), (short)(vv.y >> 16)};
-        }
+    for (int s4 = 0; s4 < 4; ++s4) {
 #pragma unroll
-        for (int tt = 0; tt < kBlk / 16; ++tt)
-          acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pk[tt], vb[tt], acc[dt], 0, 0, 0);
-        if (dt & 1) __builtin_amdgcn_sched_barrier(0);
+      for (int dt = 0; dt < 4; ++dt) {
+        const v4s lo = lds_tr16(sKV, va[0][dt] + 16384 * s4);
+        const v4s hi = lds_tr16(sKV, va[1][dt] + 16384 * s4);
+        const v8bf vf = __builtin_bit_cast(v8bf, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[s4], acc[dt], 0, 0, 0);
       }
     }
   }
+  if (!active) return;
+  const int h = h0 + c32;
+  if (h >= a.Hh) return;
+  // lane (head h, g2) holds dims 128 dq + 32 dt + 8 (r / 4) + 4 g2 + r % 4 in acc[dt][r]
   if (a.nsplit > 1) {
-    // partials: the running max and sum per head, the unnormalised rows
     const int64_t qs = (b * a.M + m) * a.nsplit + split;
-    if (active && dh == 0 && g4 == 0 && h0 + r16 < a.Hh) {
-      float* ml = a.ws_ml + (qs * a.Hh + h0 + r16) * 2;
+    if (dq == 0 && g2 == 0) {
+      float* ml = a.ws_ml + (qs * a.Hh + h) * 2;
       ml[0] = m_run;
       ml[1] = l_run;
     }
-    if (!active) return;
+    float* row = a.ws_acc + (qs * a.Hh + h) * (int64_t)kD + 128 * dq + 4 * g2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = h0 + 4 * g4 + i;
-      if (h >= a.Hh) continue;
-      float* row = a.ws_acc + (qs * a.Hh + h) * (int64_t)kD + d0;
+    for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int dt = 0; dt < 16; ++dt) row[16 * dt + r16] = acc[dt][i];
-    }
+      for (int q4 = 0; q4 < 4; ++q4)
+        *reinterpret_cast<float4*>(row + 32 * dt + 8 * q4) =
+            make_float4(acc[dt][4 * q4], acc[dt][4 * q4 + 1], acc[dt][4 * q4 + 2], acc[dt][4 * q4 + 3]);
     return;
   }
-  // o = acc / (l + exp(sink - m)) for heads 4 g + i, dims d0 + 16 dt + r
-  if (active && dh == 0 && g4 == 0) {
-    const int hs = min(h0 + r16, a.Hh - 1);
-    const float ref = m_run == NEG_INF ? 0.0f : m_run;
-    sDen[hg][r16] = l_run + expf(a.sink[hs] - ref);
-  }
-  __syncthreads();
-  if (!active) return;
+  // o = acc / (l + exp(sink - m))
+  const float ref = m_run == NEG_INF ? 0.0f : m_run;
+  const float inv = 1.0f / (l_run + __builtin_amdgcn_exp2f(a.sink[h] * kLog2e - ref));
+  uint16_t* orow = a.o + ((b * a.M + m) * a.Hh + h) * (int64_t)kD + 128 * dq + 4 * g2;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int h = h0 + 4 * g4 + i;
-    if (h >= a.Hh) continue;
-    const float dn = sDen[hg][4 * g4 + i];
-    uint16_t* orow = a.o + ((b * a.M + m) * a.Hh + h) * (int64_t)kD + d0;
+  for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-    for (int dt = 0; dt < 16; ++dt) orow[16 * dt + r16] = bf16_bits_exact(acc[dt][i] / dn);
-  }
+    for (int q4 = 0; q4 < 4; ++q4)
+      *reinterpret_cast<uint2*>(orow + 32 * dt + 8 * q4) =
+          make_uint2(pk2_bf16(acc[dt][4 * q4] * inv, acc[dt][4 * q4 + 1] * inv),
+                     pk2_bf16(acc[dt][4 * q4 + 2] * inv, acc[dt][4 * q4 + 3] * inv));
 }
 
-// Merge of the per-split partials, one wavefront per (query, head):
-//   M = max_s m_s;  o = sum_s acc_s e^(m_s - M) / (sum_s l_s e^(m_s - M) + e^(sink - M))
+// Merge of the per-split partials, one wavefront per (query, head), maxima in
+// log2 units:
+//   M = max_s m_s;  o = sum_s acc_s 2^(m_s - M) / (sum_s l_s 2^(m_s - M) + e^(sink) 2^(-M))
 // (splits whose rows were all masked carry m = -inf and add nothing).
 __global__ __launch_bounds__(256) void sparse_attn_combine_kernel(const AttnArgs a, int64_t rows) {
   const int lane = threadIdx.x & 63;
@@ -383,14 +388,14 @@ __global__ __launch_bounds__(256) void sparse_attn_combine_kernel(const AttnArgs
   for (int sp = 0; sp < a.nsplit; ++sp) {
     const int64_t r = (q * a.nsplit + sp) * a.Hh + h;
     const float ms = a.ws_ml[r * 2];
-    const float f = expf(ms - ref);  // 0 for an all-masked split
+    const float f = __builtin_amdgcn_exp2f(ms - ref);  // 0 for an all-masked split
     l += a.ws_ml[r * 2 + 1] * f;
     const float4* src = reinterpret_cast<const float4*>(a.ws_acc + r * kD + lane * 8);
     const float4 u = src[0], v = src[1];
     o[0] += u.x * f; o[1] += u.y * f; o[2] += u.z * f; o[3] += u.w * f;
     o[4] += v.x * f; o[5] += v.y * f; o[6] += v.z * f; o[7] += v.w * f;
   }
-  const float den = l + expf(a.sink[h] - ref);
+  const float den = l + __builtin_amdgcn_exp2f(a.sink[h] * kLog2e - ref);
   uint32_t wv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) wv[i] = pk2_bf16_exact(o[2 * i] / den, o[2 * i + 1] / den);
@@ -426,6 +431,7 @@ extern "C" int sgl_sparse_attn(const void* q, int64_t B, int64_t M, int Hh, cons
                                int64_t K, float softmax_scale, void* o, void* workspace,
                                size_t workspace_bytes, sgl_stream_t stream) {
   SGL_REQUIRE(B >= 0 && M >= 0 && K >= 0 && n >= 0 && Hh >= 1, "sparse_attn: bad sizes");
+  SGL_REQUIRE(softmax_scale > 0.0f, "sparse_attn: softmax_scale must be positive");
   SGL_REQUIRE(kv_format == SGL_ATTN_KV_BF16 || kv_format == SGL_ATTN_KV_A ||
                   kv_format == SGL_ATTN_KV_A_PAGED,
               "sparse_attn: bad kv_format %d", kv_format);
@@ -447,6 +453,7 @@ extern "C" int sgl_sparse_attn(const void* q, int64_t B, int64_t M, int Hh, cons
   a.kv_bstride = kv_batch_stride;
   a.ld = ld;
   a.page = page_size;
+  a.page_shift = (page_size > 0 && (page_size & (page_size - 1)) == 0) ? __builtin_ctz((unsigned)page_size) : -1;
   a.sink = attn_sink;
   a.idx = topk_idxs;
   a.M = M;
