@@ -8,8 +8,11 @@ route -> 1x128 act quant -> permute -> grouped gate/up (+SiLU*mul*w, requant)
 -> grouped down -> ordered combine.  Inputs and weights are resident in HBM
 before the timed region.  Also measured (reported under "extra"): the decode
 configs (T = 64/256/512, Zipf(1.1) expert load), the dense FP8 GEMM
-(M = 16..4096, N = 4096, K = 7168), and the FP8 KV pack (65536 rows, 656-byte
-layout) + sparse-MLA gather-dequant (128 queries x 2048 rows).
+(M = 16..4096, N = 4096, K = 7168), the FP8 x MXFP4 variants, the router gate,
+the FP8 KV pack (65536 rows, 656-byte layout) + sparse-MLA gather-dequant
+(128 queries x 2048 rows), and the sparse attention straight off the packed
+FP8 pages (64 heads; 128 queries x 2048 rows, and a 32-sequence decode batch
+with 640 rows each).
 
 Prints ONE JSON line.  ``--gpus N`` with N > 1 exits: this build runs on one GPU.
 """
@@ -578,14 +581,35 @@ def main():
         fa = lambda: SA.sparse_attn_packed(qa, pages_a, sink_a, ia, 512 ** -0.5)  # noqa: E731
         fa()
         msa_ = event_avg_ms(torch, fa, 10, flush)
+        gsa_ = graph_ms(torch, fa)
         ab_ = 128 * 2048 * 584 + 2 * 128 * 64 * 512 * 2 + 128 * 2048 * 4
         afl = 4.0 * 128 * 64 * 2048 * 512
         extra["sparse_attn_packed_128x2048_h64"] = {
-            "ms": round(msa_, 5), "gbs": round(ab_ / msa_ / 1e6, 1),
-            "hbm_frac": round(ab_ / msa_ / 1e6 / PEAK_HBM_GBS, 4),
-            "tflops": round(afl / msa_ / 1e9, 1),
-            "mfma_frac_bf16": round(afl / msa_ / 1e9 / 2500.0, 4)}
-        log(f"sparse attn packed: {msa_ * 1e3:.1f} us")
+            "ms": round(msa_, 5), "graph_ms": round(gsa_, 5), "gbs": round(ab_ / gsa_ / 1e6, 1),
+            "hbm_frac": round(ab_ / gsa_ / 1e6 / PEAK_HBM_GBS, 4),
+            "tflops": round(afl / gsa_ / 1e9, 1),
+            "mfma_frac_bf16": round(afl / gsa_ / 1e9 / 2500.0, 4)}
+        log(f"sparse attn packed 128x2048: {msa_ * 1e3:.1f} us eager, {gsa_ * 1e3:.1f} us graph")
+        del pages_a, qa, ia
+        # decode: 32 sequences, one query token each, 640 gathered rows (top-k
+        # 512 + window 128) from each sequence's own 32768-row packed cache
+        # (612 MB in all, larger than the on-die cache: the rows come from HBM)
+        Bd, NRd, Kd = 32, 32768, 640
+        kvd = torch.randn(Bd * NRd, 512, generator=ga).to(torch.bfloat16).to(dev)
+        pages_d = KVP.pack_dsv4_kv_paged(kvd, 64).view(Bd, NRd // 64, 1, 64, 584)
+        del kvd
+        qd = torch.randn(Bd, 1, 64, 512, generator=ga).to(torch.bfloat16).to(dev)
+        idd = torch.randint(0, NRd, (Bd, 1, Kd), generator=ga).to(torch.int32).to(dev)
+        fd = lambda: SA.sparse_attn_packed(qd, pages_d, sink_a, idd, 512 ** -0.5)  # noqa: E731
+        fd()
+        msd = event_avg_ms(torch, fd, 10, flush)
+        gsd = graph_ms(torch, fd)
+        bd = Bd * Kd * 584 + 2 * Bd * 64 * 512 * 2 + Bd * Kd * 4
+        extra["sparse_attn_packed_decode_b32_k640_h64"] = {
+            "ms": round(msd, 5), "graph_ms": round(gsd, 5), "gbs": round(bd / gsd / 1e6, 1),
+            "hbm_frac": round(bd / gsd / 1e6 / PEAK_HBM_GBS, 4)}
+        log(f"sparse attn packed decode b32: {msd * 1e3:.1f} us eager, {gsd * 1e3:.1f} us graph")
+        del pages_d, qd, idd
         extra["fp4"] = fp4_extra(torch, M, K, weights, dev, args, flush)
         result["extra"] = extra
 
