@@ -35,6 +35,8 @@
 // MoE tiles: an M tile never straddles two experts.  The workgroup first
 // prefix-sums ceil(count_e / BM) over the expert offsets into LDS, so the
 // grid is sized without reading routing data on the host.
+#include <type_traits>
+
 #include "sgl_gemm.h"
 #include "sgl_numeric.h"
 
@@ -614,53 +616,74 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
       // reciprocal (about 1 ulp each, far below the bf16 rounding of h).
       uint16_t* hbuf = reinterpret_cast<uint16_t*>(smem);
       const float lim = args.swiglu_limit;
+      auto swiglu = [&](auto clamp_c) {
+        constexpr bool CLAMP = decltype(clamp_c)::value;
 #pragma unroll
-      for (int mi = 0; mi < TM; ++mi)
+        for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = (wm * TM + mi) * 16 + 4 * g4 + r;
-          const float w = sW[row];
+          for (int r = 0; r < 4; ++r) {
+            const int row = (wm * TM + mi) * 16 + 4 * g4 + r;
+            const float w = sW[row];
 #pragma unroll
-          for (int j = 0; j < TN / 2; ++j) {
-            float gt = bf16_round(acc[mi][j][r]);
-            float up = bf16_round(acc[mi][j + TN / 2][r]);
-            if (lim > 0.0f) {
-              up = clampf_(up, -lim, lim);
-              gt = gt > lim ? lim : gt;
+            for (int j = 0; j < TN / 2; ++j) {
+              float gt = bf16_round(acc[mi][j][r]);
+              float up = bf16_round(acc[mi][j + TN / 2][r]);
+              if constexpr (CLAMP) {
+                up = clampf_(up, -lim, lim);
+                gt = gt > lim ? lim : gt;
+              }
+              const float ex = __builtin_amdgcn_exp2f(gt * -1.4426950408889634f);
+              const float silu = gt * __builtin_amdgcn_rcpf(1.0f + ex);
+              hbuf[row * HALF + wn * HW + j * 16 + r16] = bf16_bits_exact(w * (silu * up));
             }
-            const float ex = __builtin_amdgcn_exp2f(gt * -1.4426950408889634f);
-            const float silu = gt * __builtin_amdgcn_rcpf(1.0f + ex);
-            hbuf[row * HALF + wn * HW + j * 16 + r16] = bf16_bits_exact(w * (silu * up));
           }
-        }
+      };
+      if (lim > 0.0f)
+        swiglu(std::true_type{});
+      else
+        swiglu(std::false_type{});
       __syncthreads();
       constexpr int LPR = HALF / 8;  // 16 lanes per 128-column row
       static_assert((BM * LPR) % NT == 0, "requant loop must be uniform");
       const int64_t NB = N / 128;
+      // the scale mode is a compile-time constant inside (one copy per mode),
+      // so the scale formula and the quantization fold to straight-line code
+      auto requant = [&](auto mode_c) {
+        constexpr int MODE = decltype(mode_c)::value;
 #pragma unroll
-      for (int it = 0; it < BM * LPR / NT; ++it) {
-        const int task = tid + it * NT;
-        const int row = task / LPR, sub = task % LPR;
-        const uint4 v = *reinterpret_cast<const uint4*>(hbuf + row * HALF + sub * 8);
-        const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
-        float f[8];
+        for (int it = 0; it < BM * LPR / NT; ++it) {
+          const int task = tid + it * NT;
+          const int row = task / LPR, sub = task % LPR;
+          const uint4 v = *reinterpret_cast<const uint4*>(hbuf + row * HALF + sub * 8);
+          const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+          float f[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          f[2 * i] = bits_f32(wv[i] << 16);
-          f[2 * i + 1] = bits_f32(wv[i] & 0xFFFF0000u);
+          for (int i = 0; i < 4; ++i) {
+            f[2 * i] = bits_f32(wv[i] << 16);
+            f[2 * i + 1] = bits_f32(wv[i] & 0xFFFF0000u);
+          }
+          // IEEE maximum (v_maximum3_f32): a NaN element makes the group's
+          // amax NaN, as the reference's amax does
+          float amax = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) amax = __builtin_elementwise_maximum(amax, fabsf(f[i]));
+#pragma unroll
+          for (int o = LPR / 2; o > 0; o >>= 1)
+            amax = __builtin_elementwise_maximum(amax, __shfl_xor(amax, o, 64));
+          if (row < rows) {
+            const float sf = group_scale(MODE, amax);
+            const uint2 qv = quant8_e4m3(MODE, f, sf);
+            const int64_t p = row0 + row;
+            *reinterpret_cast<uint2*>(args.hq + p * N + n0 + sub * 8) = qv;
+            if (sub == 0) args.hs[p * NB + n0 / 128] = sf;
+          }
         }
-        float amax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) amax = fmaxf_(amax, fabsf(f[i]));
-#pragma unroll
-        for (int o = LPR / 2; o > 0; o >>= 1) amax = fmaxf_(amax, __shfl_xor(amax, o, 64));
-        if (row < rows) {
-          const float sf = group_scale(args.scale_mode, amax);
-          const uint2 qv = quant8_e4m3(args.scale_mode, f, sf);
-          const int64_t p = row0 + row;
-          *reinterpret_cast<uint2*>(args.hq + p * N + n0 + sub * 8) = qv;
-          if (sub == 0) args.hs[p * NB + n0 / 128] = sf;
-        }
+      };
+      switch (args.scale_mode) {
+        case SCALE_TORCH_FP32: requant(std::integral_constant<int, SCALE_TORCH_FP32>{}); break;
+        case SCALE_TORCH_UE8M0: requant(std::integral_constant<int, SCALE_TORCH_UE8M0>{}); break;
+        case SCALE_TILELANG_FP32: requant(std::integral_constant<int, SCALE_TILELANG_FP32>{}); break;
+        default: requant(std::integral_constant<int, SCALE_TILELANG_UE8M0>{}); break;
       }
     }
     __syncthreads();  // the next tile's DMA overwrites the stage ring
