@@ -61,9 +61,9 @@ struct PageTable {
   int64_t num_blocks;
 };
 
-template <int DT, int R>
+template <int DT, int R, int MODE>
 __global__ __launch_bounds__(256) void kv_pack_a_kernel(const uint8_t* __restrict__ kv, int64_t T,
-                                                        int64_t ld_bytes, int mode, int paged,
+                                                        int64_t ld_bytes, int paged,
                                                         int page, int64_t rows_total,
                                                         uint8_t* __restrict__ out,
                                                         const PageTable pt) {
@@ -103,26 +103,28 @@ __global__ __launch_bounds__(256) void kv_pack_a_kernel(const uint8_t* __restric
         if (lane == 0) *reinterpret_cast<uint2*>(foot) = make_uint2(0, 0);
         continue;
       }
+      // IEEE maximum (v_maximum3_f32): NaN propagates into the group's scale
       float amax = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) amax = fmaxf_(amax, fabsf(f[r][i]));
+      for (int i = 0; i < 8; ++i) amax = __builtin_elementwise_maximum(amax, fabsf(f[r][i]));
 #pragma unroll
-      for (int o = 4; o > 0; o >>= 1) amax = fmaxf_(amax, __shfl_xor(amax, o, 64));
-      const float sf = group_scale(mode, amax);
+      for (int o = 4; o > 0; o >>= 1) amax = __builtin_elementwise_maximum(amax, __shfl_xor(amax, o, 64));
+      const float sf = group_scale(MODE, amax);
       const uint32_t sbyte = pow2_to_e8m0(sf);
       if (lane < 56) {
-        *reinterpret_cast<uint2*>(data + lane * 8) = quant8_e4m3(mode, f[r], sf);
+        *reinterpret_cast<uint2*>(data + lane * 8) = quant8_e4m3(MODE, f[r], sf);
       } else {
         // rope bytes as given (bf16 / f16), 16 per lane at 448 + 16*(lane-56)
         uint8_t* dst = data + A_NOPE + (lane - 56) * 16;
         *reinterpret_cast<uint2*>(dst) = make_uint2(raw[r].x, raw[r].y);
         *reinterpret_cast<uint2*>(dst + 8) = make_uint2(raw[r].z, raw[r].w);
       }
-      // 7 scale bytes + zero pad -> one 8-byte store by lane 0
+      // 7 scale bytes + zero pad -> one 8-byte store by lane 0 (the bytes
+      // are read lane by lane into scalar registers)
       uint32_t lo = 0, hi = 0;
 #pragma unroll
       for (int g = 0; g < 7; ++g) {
-        const uint32_t b = (uint32_t)__shfl((int)sbyte, g * 8, 64) & 0xFFu;
+        const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)sbyte, g * 8) & 0xFFu;
         if (g < 4)
           lo |= b << (8 * g);
         else
@@ -337,6 +339,17 @@ unsigned grid_for_rows(int64_t rows, int rows_per_wave = 1) {
   return (unsigned)(blocks < 1 ? 1 : blocks);
 }
 
+// layout A launch for the two ue8m0 scale modes (compile-time in the kernel)
+template <int DT>
+void launch_pack_a(unsigned g, hipStream_t st, int mode, const uint8_t* kv, int64_t T, int64_t ld_bytes,
+                   int paged, int page, int64_t rows, uint8_t* out, const PageTable& pt) {
+  if (mode == SGL_SCALE_KV_UE8M0)
+    kv_pack_a_kernel<DT, kKvRows, SGL_SCALE_KV_UE8M0><<<g, 256, 0, st>>>(kv, T, ld_bytes, paged, page, rows, out, pt);
+  else
+    kv_pack_a_kernel<DT, kKvRows, SGL_SCALE_TILELANG_UE8M0><<<g, 256, 0, st>>>(kv, T, ld_bytes, paged, page, rows,
+                                                                             out, pt);
+}
+
 }  // namespace
 }  // namespace sgl
 
@@ -363,13 +376,11 @@ int sgl_kv_pack(const void* kv, int dtype, int64_t T, int64_t ldkv, int layout, 
                 "kv_pack: kv rows must be 16-byte aligned, out 8-byte aligned");
     const unsigned g = sgl::grid_for_rows(rows, sgl::kKvRows);
     if (dtype == SGL_BF16)
-      sgl::kv_pack_a_kernel<SGL_BF16, sgl::kKvRows><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
-                                                         scale_mode, paged, page_size, rows,
-                                                         (uint8_t*)out, sgl::PageTable{});
+      sgl::launch_pack_a<SGL_BF16>(g, st, scale_mode, (const uint8_t*)kv, T, ldkv * es, paged, page_size,
+                                   rows, (uint8_t*)out, sgl::PageTable{});
     else
-      sgl::kv_pack_a_kernel<SGL_F16, sgl::kKvRows><<<g, 256, 0, st>>>((const uint8_t*)kv, T, ldkv * es,
-                                                        scale_mode, paged, page_size, rows,
-                                                        (uint8_t*)out, sgl::PageTable{});
+      sgl::launch_pack_a<SGL_F16>(g, st, scale_mode, (const uint8_t*)kv, T, ldkv * es, paged, page_size,
+                                  rows, (uint8_t*)out, sgl::PageTable{});
     return sgl::check_launch("kv_pack_a");
   }
   SGL_REQUIRE(!paged, "kv_pack: layout B has no paged form");
@@ -420,11 +431,9 @@ int sgl_kv_pack_to_pages(const void* kv, int dtype, int64_t T, int64_t ldkv, int
   const unsigned g = sgl::grid_for_rows(T, sgl::kKvRows);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == SGL_BF16)
-    sgl::kv_pack_a_kernel<SGL_BF16, sgl::kKvRows><<<g, 256, 0, st>>>(
-        (const uint8_t*)kv, T, ldkv * es, scale_mode, 0, page_size, T, slab, pt);
+    sgl::launch_pack_a<SGL_BF16>(g, st, scale_mode, (const uint8_t*)kv, T, ldkv * es, 0, page_size, T, slab, pt);
   else
-    sgl::kv_pack_a_kernel<SGL_F16, sgl::kKvRows><<<g, 256, 0, st>>>(
-        (const uint8_t*)kv, T, ldkv * es, scale_mode, 0, page_size, T, slab, pt);
+    sgl::launch_pack_a<SGL_F16>(g, st, scale_mode, (const uint8_t*)kv, T, ldkv * es, 0, page_size, T, slab, pt);
   return sgl::check_launch("kv_pack_to_pages");
 }
 
