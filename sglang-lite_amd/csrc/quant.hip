@@ -5,6 +5,8 @@
 // lanes, each holding 8 values (one 16-byte load), so a 64-lane wavefront
 // covers 8 (G = 64) or 4 (G = 128) groups per iteration and the group's |x|
 // maximum needs log2(G/8) cross-lane steps.
+#include <type_traits>
+
 #include "sgl_common.h"
 #include "sgl_numeric.h"
 
@@ -27,23 +29,31 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
   }
 }
 
+// IEEE maximum (v_maximum3_f32) over the group's lanes: a NaN element makes
+// the group's amax NaN, as the reference's amax does
 template <int LPG>
 __device__ __forceinline__ float group_max(float v) {
 #pragma unroll
-  for (int o = LPG / 2; o > 0; o >>= 1) v = fmaxf_(v, __shfl_xor(v, o, 64));
+  for (int o = LPG / 2; o > 0; o >>= 1) v = __builtin_elementwise_maximum(v, __shfl_xor(v, o, 64));
   return v;
 }
 
 // R groups per thread and step (group g, g + sweep, ...), loads first, so R
 // 16-byte reads per lane are in flight.
-template <int GROUP, bool INPLACE, int R>
+// The scale mode is a template parameter (one straight-line kernel per mode);
+// IDX32: group indices fit 32 bits, so row = g / gpr is a 32-bit division.
+template <int GROUP, bool INPLACE, int R, int MODE, bool IDX32>
 __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restrict__ x, int64_t M,
                                                         int64_t K, int64_t ldx, void* __restrict__ y,
                                                         int64_t ldy, void* __restrict__ s,
-                                                        int64_t lds, int mode, int scale_e8m0) {
+                                                        int64_t lds, int scale_e8m0) {
   constexpr int LPG = GROUP / 8;
   const int64_t gpr = K / GROUP;
   const int64_t total = M * gpr;
+  auto row_of = [&](int64_t g) -> int64_t {
+    if constexpr (IDX32) return (int64_t)((uint32_t)g / (uint32_t)gpr);
+    return g / gpr;
+  };
   const int sub = threadIdx.x % LPG;
   const int64_t sweep = (int64_t)gridDim.x * blockDim.x / LPG;
   for (int64_t gb = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / LPG; gb < total;
@@ -53,7 +63,7 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
     for (int r = 0; r < R; ++r) {
       const int64_t g = gb + r * sweep;
       if (g < total) {
-        const int64_t row = g / gpr;
+        const int64_t row = row_of(g);
         const int64_t col = (g - row * gpr) * GROUP + sub * 8;
         v[r] = *reinterpret_cast<const uint4*>(x + row * ldx + col);
       }
@@ -62,16 +72,16 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
     for (int r = 0; r < R; ++r) {
       const int64_t g = gb + r * sweep;
       if (g >= total) break;
-      const int64_t row = g / gpr;
+      const int64_t row = row_of(g);
       const int64_t col = (g - row * gpr) * GROUP + sub * 8;
       float f[8];
       unpack_bf16x8(v[r], f);
       float amax = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) amax = fmaxf_(amax, fabsf(f[i]));
+      for (int i = 0; i < 8; ++i) amax = __builtin_elementwise_maximum(amax, fabsf(f[i]));
       amax = group_max<LPG>(amax);
-      const float sf = group_scale(mode, amax);
-      const uint2 qv = quant8_e4m3(mode, f, sf);
+      const float sf = group_scale(MODE, amax);
+      const uint2 qv = quant8_e4m3(MODE, f, sf);
       if (INPLACE) {
         // quant-dequant back to bf16: bf16(fp32(e4m3) * s)
         float d[8];
@@ -290,12 +300,29 @@ int launch_act_quant(const void* x, int64_t M, int64_t K, int64_t ldx, void* y, 
   int64_t blocks = ceil_div(total_threads, 256 * R);
   if (blocks > max_blocks) blocks = max_blocks;
   if (blocks < 1) blocks = 1;
-  if (inplace)
-    act_quant_kernel<GROUP, true, R><<<(unsigned)blocks, 256, 0, stream>>>(
-        (const uint16_t*)x, M, K, ldx, y, ldy, s, lds, mode, scale_e8m0);
-  else
-    act_quant_kernel<GROUP, false, R><<<(unsigned)blocks, 256, 0, stream>>>(
-        (const uint16_t*)x, M, K, ldx, y, ldy, s, lds, mode, scale_e8m0);
+  const bool idx32 = M * (K / GROUP) + (int64_t)blocks * 256 * R < ((int64_t)1 << 31);
+  auto go = [&](auto inplace_c, auto mode_c, auto idx_c) {
+    act_quant_kernel<GROUP, decltype(inplace_c)::value, R, decltype(mode_c)::value, decltype(idx_c)::value>
+        <<<(unsigned)blocks, 256, 0, stream>>>((const uint16_t*)x, M, K, ldx, y, ldy, s, lds, scale_e8m0);
+  };
+  auto with_mode = [&](auto inplace_c, auto idx_c) {
+    switch (mode) {
+      case SCALE_TORCH_FP32: go(inplace_c, std::integral_constant<int, SCALE_TORCH_FP32>{}, idx_c); break;
+      case SCALE_TORCH_UE8M0: go(inplace_c, std::integral_constant<int, SCALE_TORCH_UE8M0>{}, idx_c); break;
+      case SCALE_TILELANG_FP32: go(inplace_c, std::integral_constant<int, SCALE_TILELANG_FP32>{}, idx_c); break;
+      case SCALE_TILELANG_UE8M0:
+        go(inplace_c, std::integral_constant<int, SCALE_TILELANG_UE8M0>{}, idx_c);
+        break;
+      default: go(inplace_c, std::integral_constant<int, SCALE_KV_UE8M0>{}, idx_c); break;
+    }
+  };
+  if (inplace) {
+    if (idx32) with_mode(std::true_type{}, std::true_type{});
+    else with_mode(std::true_type{}, std::false_type{});
+  } else {
+    if (idx32) with_mode(std::false_type{}, std::true_type{});
+    else with_mode(std::false_type{}, std::false_type{});
+  }
   return check_launch("act_quant");
 }
 
