@@ -126,20 +126,29 @@ struct Cfg {
   static constexpr int A_BYTES = BM * 128 * KS;  // KS sub-blocks of BM x 128 bytes
   static constexpr int B_BYTES = BN * 128;
   static constexpr int SB_BYTES = WF == WF_FP4 ? BN * 8 : 0;  // e8m0 weight scales: 8 per column
-  static constexpr int SBI = SB_BYTES / (NW * 256);           // their dword DMAs per wavefront
+  // DMA issuers: with 8 wavefronts (two per SIMD) only the second half, one
+  // wavefront per SIMD, issues a stage's loads; the first half starts its
+  // MFMAs right after the stage barrier instead of queueing behind the CU's
+  // address unit with every other wavefront
+  static constexpr int IW = NW == 8 ? NW / 2 : NW;
+  static constexpr int SBI = SB_BYTES / (IW * 256);  // weight-scale dword DMAs per issuer
   static constexpr int SA_ROWS = BM / NW;  // row scales each wavefront loads per stage
   static constexpr int STAGE = A_BYTES + B_BYTES + SB_BYTES;
   static constexpr int SA_SLOT = NW * 256;           // one stage of row scales
   static constexpr int ACH = BM * KS / 8;            // 1 KB DMA chunks of A per stage
   static constexpr int CHUNKS = ACH + BN / 8;        // ... of A and B
-  static constexpr int CPW = CHUNKS / NW;       // per wavefront
-  static constexpr int LPS = CPW + 1 + SBI;     // DMA instructions per wavefront per stage
+  static constexpr int CPW = CHUNKS / IW;       // per issuer
+  static constexpr int SAI = NW / IW;           // row-scale DMAs per issuer (one per wavefront)
+  static constexpr int QA = BM / 8 / IW;        // distinct A row groups per issuer
+  static constexpr int LPS = CPW + SAI + SBI;   // DMA instructions per issuer per stage
   static constexpr int NSA = NSTAGE;  // row-scale slots (a ring of their own)
   static constexpr int RING = NSTAGE * STAGE;
   static constexpr int SMEM = RING + NSA * SA_SLOT;
-  static_assert(CHUNKS % NW == 0, "chunks must split evenly over wavefronts");
+  static_assert(CHUNKS % IW == 0, "chunks must split evenly over the issuers");
+  static_assert(IW % 2 == 0 && (BM / 8) % IW == 0 && (HALF / 8) % IW == 0,
+                "every chunk index of an issuer maps to one operand, half and swizzle parity");
   static_assert(SA_ROWS >= 1 && SA_ROWS * KS <= 64, "row scales per wavefront");
-  static_assert(SB_BYTES % (NW * 256) == 0, "weight-scale DMAs must split evenly");
+  static_assert(SB_BYTES % (IW * 256) == 0, "weight-scale DMAs must split evenly");
   static_assert(TM >= 1 && TN >= 1, "tile too small");
   static_assert(KIND != KIND_GATE_UP || (TN % 2 == 0 && HALF == 128), "gate_up needs 128 h columns");
   static_assert(KIND == KIND_GATE_UP ? BM * HALF * 2 <= RING : BM * BN * 4 <= RING,
@@ -347,41 +356,47 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
 
     const int src0 = __builtin_amdgcn_readfirstlane(sSrc[0]);
 
-    // chunk c = wave + j * NW: for c < ACH, rows [8c', 8c'+8) of A's K
-    // sub-block c / (BM/8) (c' = c % (BM/8)); else B rows
-    uint32_t voff[C::CPW];
+    // Issuer iw (wavefront NW - IW + iw) moves chunks c = iw + j * IW of
+    // every stage, A's first: A chunk c holds rows [8c', 8c'+8) of K
+    // sub-block c / (BM/8) (c' = c % (BM/8)), its lane offsets one register
+    // per distinct c' (the sub-block adds 128 bytes); B chunk b = c - ACH
+    // holds weight rows [8b, 8b+8).  Since IW is even, every B chunk of an
+    // issuer has the same swizzle parity (b & 1 = iw & 1), so the B lane
+    // offset is one register plus a wave-uniform row base.  The other
+    // wavefronts issue nothing (their offsets are issuer 0's, never used).
+    const bool issuer = wave >= NW - C::IW;
+    const int iw = issuer ? wave - (NW - C::IW) : 0;
+    const int rr = lane >> 3, pc = lane & 7;
+    uint32_t voffA[C::QA];
 #pragma unroll
-    for (int j = 0; j < C::CPW; ++j) {
-      const int c = wave + j * NW;
-      const int rr = lane >> 3, pc = lane & 7;
-      if (c < C::ACH) {
-        const int sub = c / (BM / 8);
-        const int r = (c - sub * (BM / 8)) * 8 + rr;
-        const int s = sSrc[r] >= 0 ? sSrc[r] : src0;
-        voff[j] = (uint32_t)((int64_t)s * K + sub * 128 + ((pc ^ swz(r)) << 4));
-      } else {
-        const int r = (c - C::ACH) * 8 + rr;
-        const bool up_half = KIND == KIND_GATE_UP && r >= HALF;
-        int64_t n = n0 + (up_half ? r - HALF : r);
-        if (n >= N) n = n0;
-        voff[j] = (uint32_t)(n * KROW + ((pc ^ swz(r)) << 4));
-      }
+    for (int q = 0; q < C::QA; ++q) {
+      const int r = (iw + q * C::IW) * 8 + rr;
+      const int s = sSrc[r] >= 0 ? sSrc[r] : src0;
+      voffA[q] = (uint32_t)((int64_t)s * K + ((pc ^ swz(r)) << 4));
     }
-    // row scales: lane l < KS * SA_ROWS loads row wave * SA_ROWS + l % SA_ROWS,
-    // K step l / SA_ROWS of the stage (the other lanes repeat lane 0's load)
+    const uint32_t chunkB = (uint32_t)((pc ^ ((rr & 6) | (iw & 1))) << 4);
+    const uint32_t laneB = (uint32_t)(rr * KROW) + chunkB;
+    const uint32_t clampB = (uint32_t)(n0 * KROW) + chunkB;  // rows past N re-read row n0
+    // row scales of wavefront w = iw + q IW (its 256-byte slot): lane l <
+    // KS * SA_ROWS loads row w * SA_ROWS + l % SA_ROWS, K step l / SA_ROWS of
+    // the stage (the other lanes repeat lane 0's load)
     const int sa_l = lane < KS * C::SA_ROWS ? lane : 0;
-    const int sa_row = wave * C::SA_ROWS + sa_l % C::SA_ROWS;
-    const int sa_src = sSrc[sa_row] >= 0 ? sSrc[sa_row] : src0;
-    const uint32_t sa_off = (uint32_t)(((int64_t)sa_src * KB + sa_l / C::SA_ROWS) * 4);
+    uint32_t sa_off[C::SAI];
+#pragma unroll
+    for (int q = 0; q < C::SAI; ++q) {
+      const int sa_row = (iw + q * C::IW) * C::SA_ROWS + sa_l % C::SA_ROWS;
+      const int sa_src = sSrc[sa_row] >= 0 ? sSrc[sa_row] : src0;
+      sa_off[q] = (uint32_t)(((int64_t)sa_src * KB + sa_l / C::SA_ROWS) * 4);
+    }
     const uint8_t* sa_base = uniform_ptr(args.sa);
     const uint32_t smem_lds = __builtin_amdgcn_readfirstlane(lds_u32(smem));
-    // fp4 weight scales: dword d = (q NW + wave) 64 + lane of the stage's
+    // fp4 weight scales: dword d = (q IW + iw) 64 + lane of the stage's
     // [BN][8] bytes is column d / 2, half d % 2 (32 columns per instruction,
     // so a gate_up instruction is wholly gate or wholly up)
     uint32_t sb_off[C::SBI > 0 ? C::SBI : 1];
 #pragma unroll
     for (int q = 0; q < C::SBI; ++q) {
-      const int d = (q * NW + wave) * 64 + lane;
+      const int d = (q * C::IW + iw) * 64 + lane;
       const int col = d >> 1;
       const bool up_half = KIND == KIND_GATE_UP && col >= HALF;
       int64_t n = n0 + (up_half ? col - HALF : col);
@@ -394,33 +409,36 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
     // DMA stage st (K steps st*KS ...) into operand slot `slot` and
     // row-scale slot `sa_slot` (defaults: st % NSTAGE, st % NSA)
     auto issue = [&](int st, int slot = -1, int sa_slot = -1) {
+      if (!issuer) return;
       if (slot < 0) slot = st % NSTAGE;
       if (sa_slot < 0) sa_slot = st % C::NSA;
       const uint32_t sl = smem_lds + (uint32_t)(slot * C::STAGE);
+      // chunk j of every issuer is of the same kind: decided at compile time
 #pragma unroll
       for (int j = 0; j < C::CPW; ++j) {
-        const int c = wave + j * NW;
-        bool isA, up_half;
-        if constexpr (C::ACH % NW == 0 && (HALF / 8) % NW == 0) {
-          // chunk j of every wavefront is of the same kind: decided at compile time
-          isA = j < C::ACH / NW;
-          up_half = KIND == KIND_GATE_UP && j >= (C::ACH + HALF / 8) / NW;
+        const int c = iw + j * C::IW;
+        if (j < C::ACH / C::IW) {
+          const int q = j % C::QA, sub = j / C::QA;
+          dma16(baseA, voffA[q] + (uint32_t)(sub * 128) + (uint32_t)st * (128u * KS),
+                sl + (uint32_t)c * 1024u);
         } else {
-          isA = c < C::ACH;
-          up_half = KIND == KIND_GATE_UP && !isA && (c - C::ACH) * 8 >= HALF;
+          const int b = c - C::ACH;
+          const bool up_half = KIND == KIND_GATE_UP && j >= (C::ACH + HALF / 8) / C::IW;
+          const int64_t nrow = n0 + (up_half ? b * 8 - HALF : b * 8);
+          const uint32_t vo = nrow + rr < N ? (uint32_t)(nrow * KROW) + laneB : clampB;
+          dma16(up_half ? b1 : b0, vo + (uint32_t)st * 128u, sl + (uint32_t)c * 1024u);
         }
-        const uint8_t* base = isA ? baseA : (up_half ? b1 : b0);
-        const uint32_t koff = isA ? (uint32_t)st * (128u * KS) : (uint32_t)st * 128u;
-        dma16(base, voff[j] + koff, sl + (uint32_t)c * 1024u);
       }
 #pragma unroll
       for (int q = 0; q < C::SBI; ++q) {
-        const bool up_half = KIND == KIND_GATE_UP && (q * NW + wave) * 32 >= HALF;
+        const bool up_half = KIND == KIND_GATE_UP && (q * C::IW + iw) * 32 >= HALF;
         dma4(up_half ? sbp1 : sbp0, sb_off[q] + (uint32_t)st * 8u,
-             sl + (uint32_t)(C::A_BYTES + C::B_BYTES + (q * NW + wave) * 256));
+             sl + (uint32_t)(C::A_BYTES + C::B_BYTES + (q * C::IW + iw) * 256));
       }
-      dma4(sa_base, sa_off + (uint32_t)st * (4u * KS),
-           smem_lds + (uint32_t)(C::RING + sa_slot * C::SA_SLOT + wave * 256));
+#pragma unroll
+      for (int q = 0; q < C::SAI; ++q)
+        dma4(sa_base, sa_off[q] + (uint32_t)st * (4u * KS),
+             smem_lds + (uint32_t)(C::RING + sa_slot * C::SA_SLOT + (iw + q * C::IW) * 256));
     };
 
     v4f acc[TM][TN];
