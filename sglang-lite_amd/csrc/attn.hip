@@ -161,19 +161,31 @@ void sparse_attn_kernel(const AttnArgs a) {
   const int sb_shift = 8 * ((lane >> 3) & 3);
   const bool sb_hi = (lane >> 3) >= 4;
 
+  // A block's indices are loaded unconditionally (clamped to the last one)
+  // and checked where they are used: the check waits for the load, and since
+  // loads complete in order, a check right after the load would also wait
+  // for every row gather issued before it.
   auto load_ids = [&](int j) -> int32_t {
     const int64_t p = (int64_t)j * kBlk + lane;
-    const int32_t id = p < a.K ? idxp[p] : -1;
-    return (id >= 0 && id < a.n) ? id : -1;
+    return idxp[p < a.K ? p : a.K - 1];
   };
-  // this wavefront's 8 rows of the block: tokens 8 wave + rr
+  auto check_id = [&](int j, int32_t id) -> int32_t {
+    const int64_t p = (int64_t)j * kBlk + lane;
+    return (p < a.K && id >= 0 && id < a.n) ? id : -1;
+  };
+  // this wavefront's 8 rows of the block: tokens 8 wave + rr.  The gathers
+  // are unconditional (a missing row reads row 0, which store_rows zeroes),
+  // so no branch splits the loads and the compiler's wait before the stores
+  // counts the loads in flight instead of draining them.
   uint4 raw[8];
   auto load_rows = [&](int32_t ids) {
+    if (a.n == 0) return;  // no rows at all: store_rows zeroes every row
 #pragma unroll
     for (int rr = 0; rr < 8; ++rr) {
-      const int id = __builtin_amdgcn_readlane(ids, 8 * wave + rr);
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (id >= 0) {
+      const int idr = __builtin_amdgcn_readlane(ids, 8 * wave + rr);
+      const int id = idr >= 0 ? idr : 0;
+      uint4 v;
+      {
         if constexpr (FMT == SGL_ATTN_KV_BF16) {
           v = *reinterpret_cast<const uint4*>(kvb + (int64_t)id * a.ld * 2 + lane * 16);
         } else {
@@ -197,10 +209,11 @@ void sparse_attn_kernel(const AttnArgs a) {
       raw[rr] = v;
     }
   };
-  auto store_rows = [&]() {
+  auto store_rows = [&](int32_t ids) {
 #pragma unroll
     for (int rr = 0; rr < 8; ++rr) {
       uint4 v = raw[rr];
+      if (__builtin_amdgcn_readlane(ids, 8 * wave + rr) < 0) v = make_uint4(0, 0, 0, 0);
       if constexpr (FMT != SGL_ATTN_KV_BF16) {
         const uint32_t word = sb_hi ? v.w : v.z;
         const float sc = bits_f32(((word >> sb_shift) & 0xFFu) << 23);  // 2^(e8m0 - 127)
@@ -220,19 +233,21 @@ void sparse_attn_kernel(const AttnArgs a) {
   const int nblk_all = (int)((a.K + kBlk - 1) / kBlk);
   const int jb = split * a.bps;  // this split's first block
   const int nblk = jb + a.bps < nblk_all ? jb + a.bps : nblk_all;
-  // indices run two blocks ahead of the MFMAs, the rows one block ahead
-  int32_t ids = jb < nblk ? load_ids(jb) : -1;
-  int32_t ids_next = jb + 1 < nblk ? load_ids(jb + 1) : -1;
+  // indices run two blocks ahead of the MFMAs, the rows one block ahead;
+  // past the last block the loads repeat it (their results are unused)
+  int32_t ids = jb < nblk ? check_id(jb, load_ids(jb)) : -1;
+  int32_t ids_next = load_ids(jb + 1 < nblk ? jb + 1 : jb);  // raw
   load_rows(ids);
   for (int j = jb; j < nblk; ++j) {
     const uint64_t valid = __ballot(ids >= 0);
     __syncthreads();  // the previous block's tile is consumed
-    store_rows();
+    store_rows(ids);
     __syncthreads();  // block j (and, the first time, Q) is in LDS
-    if (j + 1 < nblk) {
-      ids = ids_next;
+    {
+      const int jn = j + 1 < nblk ? j + 1 : j;
+      ids = j + 1 < nblk ? check_id(jn, ids_next) : -1;
+      ids_next = load_ids(j + 2 < nblk ? j + 2 : jn);  // before the rows it would wait behind
       load_rows(ids);
-      if (j + 2 < nblk) ids_next = load_ids(j + 2);
     }
     if (!active) {
       __syncthreads();  // (partials exchanged)
