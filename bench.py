@@ -560,6 +560,12 @@ def main():
         kva = torch.randn(65536, 512, generator=gk).to(torch.bfloat16).to(dev)
         msa = event_avg_ms(torch, lambda: KVP.pack_dsv4_kv_paged(kva, 64), 10, flush)
         ab = 65536 * (1024 + 584)
+        # gather-dequant of the same 128 x 2048 indices from layout A footer pages
+        pages_ga = KVP.pack_dsv4_kv_paged(kva, 64)
+        out_a = torch.empty(128, 2048, 512, dtype=torch.bfloat16, device=dev)
+        msga = event_avg_ms(torch, lambda: KVP.gather_dequant(pages_ga, idx, layout="A", page_size=64,
+                                                              out=out_a), 10, flush)
+        gab = 128 * 2048 * (584 + 1024)
         extra["kv"] = {
             "pack_layout_b_65536": {"ms": round(msp, 5), "gbs": round(pb / msp / 1e6, 1),
                                     "hbm_frac": round(pb / msp / 1e6 / PEAK_HBM_GBS, 4)},
@@ -567,6 +573,8 @@ def main():
                                         "hbm_frac": round(gb / msg_ / 1e6 / PEAK_HBM_GBS, 4)},
             "pack_layout_a_paged_65536": {"ms": round(msa, 5), "gbs": round(ab / msa / 1e6, 1),
                                           "hbm_frac": round(ab / msa / 1e6 / PEAK_HBM_GBS, 4)},
+            "gather_dequant_a_paged_128x2048": {"ms": round(msga, 5), "gbs": round(gab / msga / 1e6, 1),
+                                                "hbm_frac": round(gab / msga / 1e6 / PEAK_HBM_GBS, 4)},
         }
         log(f"kv pack {msp * 1e3:.1f} us, gather {msg_ * 1e3:.1f} us, pack A paged {msa * 1e3:.1f} us")
         # ---- sparse MLA attention straight off the packed FP8 pages (64 heads,

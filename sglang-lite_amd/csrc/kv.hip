@@ -19,7 +19,17 @@ constexpr int B_LAT = 512, B_DIM = 576, B_ROW = 656;
 #ifndef SGL_KV_BLOCKS_PER_CU
 #define SGL_KV_BLOCKS_PER_CU 32
 #endif
-constexpr int kKvRows = SGL_KV_ROWS;  // rows per wavefront step in the pack / gather kernels
+constexpr int kKvRows = SGL_KV_ROWS;  // rows per wavefront step in the pack kernels
+// rows per wavefront step in the gather (measured at 128 x 2048 rows of a
+// 65536-row cache: layout A 87 -> 74 us with 4, layout B best with 1)
+#ifndef SGL_KV_GATHER_ROWS_A
+#define SGL_KV_GATHER_ROWS_A 4
+#endif
+#ifndef SGL_KV_GATHER_ROWS_B
+#define SGL_KV_GATHER_ROWS_B 1
+#endif
+constexpr int kKvGatherRowsA = SGL_KV_GATHER_ROWS_A;
+constexpr int kKvGatherRowsB = SGL_KV_GATHER_ROWS_B;
 
 template <int DT>
 __device__ __forceinline__ void load8(const uint8_t* row, int elem, float* f, uint4* raw) {
@@ -213,11 +223,14 @@ __global__ __launch_bounds__(256) void kv_to_paged_kernel(const uint8_t* __restr
   }
 }
 
-// One wavefront per gathered row, R rows per step: the R indices come in
-// with one load, then every row's loads are issued before any is used.
-// Layout A: out 512 bf16 = 448 dequantized (e4m3 * 2^(e8m0-127), exact in
-// bf16) + 64 rope; layout B: out 576 bf16 = 512 bf16(e4m3 * fp32 scale) + 64
-// rope.  Indices outside [0, n_rows) give zero rows.
+// One wavefront per gathered row, R rows per step.  The R indices of a step
+// come in with one load, issued in the step before (ahead of that step's row
+// loads, so waiting for them never waits for rows), and the row loads are
+// unconditional (an index outside [0, n_rows) reads row 0, and its output
+// row is written as zeros), so no branch splits them and all R rows stay in
+// flight together.  Layout A: out 512 bf16 = 448 dequantized (e4m3 *
+// 2^(e8m0-127), exact in bf16) + 64 rope; layout B: out 576 bf16 = 512
+// bf16(e4m3 * fp32 scale) + 64 rope.
 template <int LAYOUT, int R>
 __global__ __launch_bounds__(256) void kv_gather_kernel(const uint8_t* __restrict__ cache,
                                                         int paged, int page, int64_t n_rows,
@@ -227,49 +240,63 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const uint8_t* __restric
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * 4;
   const int64_t w0 = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  for (int64_t rb = w0 * R; rb < total; rb += nwaves * R) {
-    const int32_t my_id = (lane < R && rb + lane < total) ? idx[rb + lane] : -1;
+  // lane r < R: index r of the step starting at rb (clamped into the array)
+  auto load_idx = [&](int64_t rb) -> int32_t {
+    const int64_t i = rb + (lane < R ? lane : 0);
+    return idx[i < total ? i : total - 1];
+  };
+  int64_t rb = w0 * R;
+  int32_t my_id = rb < total ? load_idx(rb) : -1;
+  for (; rb < total; rb += nwaves * R) {
     int32_t id[R];
+    bool ok[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int32_t v = __builtin_amdgcn_readfirstlane(__shfl(my_id, r, 64));
+      ok[r] = rb + r < total && v >= 0 && v < n_rows;
+      id[r] = ok[r] ? v : 0;
+    }
+    if (rb + nwaves * R < total) my_id = load_idx(rb + nwaves * R);
     uint2 qv[R];
     uint32_t sraw[R];  // layout A: the e8m0 byte; layout B: the fp32 scale bits
     uint4 rope[R];
+    if (n_rows > 0) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      id[r] = __builtin_amdgcn_readfirstlane(__shfl(my_id, r, 64));
-      if (id[r] < 0 || id[r] >= n_rows) continue;
-      if constexpr (LAYOUT == SGL_KV_LAYOUT_A) {
-        const uint8_t* data;
-        const uint8_t* foot;
-        if (paged) {
-          const int64_t pg = id[r] / page, l = id[r] - pg * page;
-          const uint8_t* pbase = cache + pg * (int64_t)page * A_ROW;
-          data = pbase + l * A_DATA;
-          foot = pbase + (int64_t)page * A_DATA + l * 8;
+      for (int r = 0; r < R; ++r) {
+        if constexpr (LAYOUT == SGL_KV_LAYOUT_A) {
+          const uint8_t* data;
+          const uint8_t* foot;
+          if (paged) {
+            const int64_t pg = id[r] / page, l = id[r] - pg * page;
+            const uint8_t* pbase = cache + pg * (int64_t)page * A_ROW;
+            data = pbase + l * A_DATA;
+            foot = pbase + (int64_t)page * A_DATA + l * 8;
+          } else {
+            data = cache + (int64_t)id[r] * A_ROW;
+            foot = data + A_DATA;
+          }
+          // lanes < 56: 8 e4m3 bytes + the group's scale byte; lanes 56..63:
+          // 16 rope bytes (two 8-byte halves)
+          const uint8_t* src = lane < 56 ? data + lane * 8 : data + A_NOPE + (lane - 56) * 16;
+          const uint2 x = *reinterpret_cast<const uint2*>(src);
+          const uint2 y = *reinterpret_cast<const uint2*>(lane < 56 ? foot : src + 8);
+          qv[r] = x;
+          sraw[r] = (y.x >> (8 * ((lane >> 3) & 3))) & 0xFFu;
+          if ((lane >> 3) >= 4) sraw[r] = (y.y >> (8 * ((lane >> 3) & 3))) & 0xFFu;
+          rope[r] = make_uint4(x.x, x.y, y.x, y.y);
         } else {
-          data = cache + (int64_t)id[r] * A_ROW;
-          foot = data + A_DATA;
+          const uint8_t* row = cache + (int64_t)id[r] * B_ROW;
+          qv[r] = *reinterpret_cast<const uint2*>(row + lane * 8);
+          sraw[r] = *reinterpret_cast<const uint32_t*>(row + 640 + (lane >> 4) * 4);
+          rope[r] = *reinterpret_cast<const uint4*>(row + B_LAT + (lane & 7) * 16);
         }
-        if (lane < 56) {
-          qv[r] = *reinterpret_cast<const uint2*>(data + lane * 8);
-          sraw[r] = foot[lane >> 3];
-        } else {
-          const uint8_t* src = data + A_NOPE + (lane - 56) * 16;
-          const uint2 a = *reinterpret_cast<const uint2*>(src);
-          const uint2 b = *reinterpret_cast<const uint2*>(src + 8);
-          rope[r] = make_uint4(a.x, a.y, b.x, b.y);
-        }
-      } else {
-        const uint8_t* row = cache + (int64_t)id[r] * B_ROW;
-        qv[r] = *reinterpret_cast<const uint2*>(row + lane * 8);
-        sraw[r] = *reinterpret_cast<const uint32_t*>(row + 640 + (lane >> 4) * 4);
-        if (lane < 8) rope[r] = *reinterpret_cast<const uint4*>(row + B_LAT + lane * 16);
       }
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (rb + r >= total) break;
       uint16_t* o = out + (rb + r) * ODIM;
-      if (id[r] < 0 || id[r] >= n_rows) {
+      if (!ok[r]) {
         const uint4 z = make_uint4(0, 0, 0, 0);
         *reinterpret_cast<uint4*>(o + lane * 8) = z;
         if (LAYOUT == SGL_KV_LAYOUT_B && lane < 8) *reinterpret_cast<uint4*>(o + 512 + lane * 8) = z;
@@ -461,13 +488,14 @@ int sgl_kv_gather_dequant(const void* cache, int layout, int paged, int page_siz
   SGL_REQUIRE(idx && out && (n_rows == 0 || cache), "kv_gather: null pointer");
   SGL_REQUIRE(sgl::aligned(out, 16) && sgl::aligned(cache, layout == SGL_KV_LAYOUT_B ? 16 : 8),
               "kv_gather: misaligned cache/out");
-  const unsigned g = sgl::grid_for_rows(total, sgl::kKvRows);
   hipStream_t st = (hipStream_t)stream;
   if (layout == SGL_KV_LAYOUT_A)
-    sgl::kv_gather_kernel<SGL_KV_LAYOUT_A, sgl::kKvRows><<<g, 256, 0, st>>>(
+    sgl::kv_gather_kernel<SGL_KV_LAYOUT_A, sgl::kKvGatherRowsA>
+        <<<sgl::grid_for_rows(total, sgl::kKvGatherRowsA), 256, 0, st>>>(
         (const uint8_t*)cache, paged, page_size, n_rows, idx, total, (uint16_t*)out);
   else
-    sgl::kv_gather_kernel<SGL_KV_LAYOUT_B, sgl::kKvRows><<<g, 256, 0, st>>>(
+    sgl::kv_gather_kernel<SGL_KV_LAYOUT_B, sgl::kKvGatherRowsB>
+        <<<sgl::grid_for_rows(total, sgl::kKvGatherRowsB), 256, 0, st>>>(
         (const uint8_t*)cache, 0, 1, n_rows, idx, total, (uint16_t*)out);
   return sgl::check_launch("kv_gather_dequant");
 }
