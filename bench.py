@@ -130,7 +130,11 @@ def time_steps(torch, fn, steps, warmup):
 
 def event_avg_ms(torch, fn, iters, flush=None):
     """Average duration of fn on torch's current stream (the stream the
-    library launches on), timed with HIP events, optional cache flush between."""
+    library launches on), timed with HIP events, optional cache flush between.
+    One untimed call first, so an output the allocator has to map for the
+    first call is not inside the average."""
+    fn()
+    torch.cuda.synchronize()
     tot = 0.0
     for _ in range(iters):
         if flush is not None:
