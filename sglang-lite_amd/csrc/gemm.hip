@@ -153,7 +153,7 @@ struct Cfg {
   static_assert(KIND != KIND_GATE_UP || (TN % 2 == 0 && HALF == 128), "gate_up needs 128 h columns");
   static_assert(KIND == KIND_GATE_UP ? BM * HALF * 2 <= RING : BM * BN * 4 <= RING,
                 "epilogue staging must fit in the stage ring");
-  static_assert(NSTAGE >= 2 && NSTAGE <= 4, "stages");
+  static_assert(NSTAGE >= 2 && NSTAGE <= 6, "stages");
   static_assert(WF == WF_FP4 || !SAHW, "in-MFMA activation scales are an FP4-weight path");
 };
 
@@ -462,7 +462,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
     for (int st = 0; st < NST; ++st) {
       // loads of stage st are the oldest in flight: allow the younger ones
       const int younger = min(NSTAGE - 2, NST - 1 - st);
-      if (younger >= 2) wait_vmcnt<2 * C::LPS>();
+      if (NSTAGE >= 6 && younger >= 4) wait_vmcnt<(NSTAGE >= 6 ? 4 : 0) * C::LPS>();
+      else if (NSTAGE >= 5 && younger == 3) wait_vmcnt<(NSTAGE >= 5 ? 3 : 0) * C::LPS>();
+      else if (younger >= 2) wait_vmcnt<2 * C::LPS>();
       else if (younger == 1) wait_vmcnt<C::LPS>();
       else wait_vmcnt<0>();
       __builtin_amdgcn_s_barrier();
@@ -825,7 +827,9 @@ __global__ __launch_bounds__(64 * Skinny<TM>::WAVES) void gemm_skinny_kernel(con
     if (tid < KB) skv = load_scale(args.sb, (n0 / 128) * KB + tid, args.sb_e8m0);
   }
 
-  constexpr int NB = 4;  // K blocks per wavefront whose loads are in flight together
+  // K blocks per wavefront whose loads are in flight together (the 128-row
+  // tile holds 8 A fragments per block, so two blocks fit the VGPR budget)
+  constexpr int NB = TM >= 8 ? 2 : 4;
   v8i af[NB][TM], bf[NB];
   auto load_chunk = [&](int base) {
 #pragma unroll
@@ -951,6 +955,7 @@ int launch_fp4(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
         if (a.M <= 32) return launch_skinny<2, WF_FP4, SAHW>(a, stream);
         return launch_skinny<4, WF_FP4, SAHW>(a, stream);
       }
+      if (a.M <= 256) return launch_cfg<KIND_DENSE, 32, 128, 1, 4, 3, WF_FP4, SAHW>(a, stream);
       if (a.M <= 2048) return launch_cfg<KIND_DENSE, 64, 128, 2, 2, 2, WF_FP4, SAHW>(a, stream);
       return launch_cfg<KIND_DENSE, 128, 256, 2, 4, 2, WF_FP4, SAHW>(a, stream);
     case KIND_GATE_UP:
@@ -984,7 +989,13 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
         return launch_skinny<4>(a, stream);
       }
       // 128 x 256 tiles from M = 2048 up; below, 64 x 128 tiles (two
-      // workgroups per CU) so the grid still covers every CU
+      // workgroups per CU) so the grid still covers every CU.  A workgroup
+      // streams its operands at a capped rate (about 35 GB/s measured,
+      // whatever the stage depth or wavefront count), so for M <= 256 the
+      // tiles shrink until there is about one per CU: N = 4096, K = 7168 at
+      // M = 128 takes 23 us with 32 x 64 tiles, 39 us with 64 x 128
+      if (a.M <= 128) return launch_cfg<KIND_DENSE, 32, 64, 1, 4, 4>(a, stream);
+      if (a.M <= 256) return launch_cfg<KIND_DENSE, 32, 128, 1, 4, 4>(a, stream);
       if (a.M <= 2048) return launch_cfg<KIND_DENSE, 64, 128, 2, 2, 3>(a, stream);
       return launch_cfg<KIND_DENSE, 128, 256, 2, 4, 3>(a, stream);
     case KIND_GATE_UP:
