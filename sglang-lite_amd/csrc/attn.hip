@@ -236,7 +236,7 @@ void sparse_attn_kernel(const AttnArgs a) {
   // indices run two blocks ahead of the MFMAs, the rows one block ahead;
   // past the last block the loads repeat it (their results are unused)
   int32_t ids = jb < nblk ? check_id(jb, load_ids(jb)) : -1;
-  int32_t ids_next = load_ids(jb + 1 < nblk ? jb + 1 : jb);  // raw
+  int32_t ids_next = jb < nblk ? load_ids(jb + 1 < nblk ? jb + 1 : jb) : -1;  // raw (none when K == 0)
   load_rows(ids);
   for (int j = jb; j < nblk; ++j) {
     const uint64_t valid = __ballot(ids >= 0);

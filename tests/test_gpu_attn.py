@@ -130,3 +130,25 @@ def test_sparse_attn_workspace_contract(gpu):
                              kvd.stride(0) * 2, 512, sd.data_ptr(), idd.data_ptr(), 256, 0.04,
                              o.data_ptr(), ws.data_ptr(), need - 16, _lib.stream_of(qd))
     assert rc == _lib.SGL_ERR_WORKSPACE and "workspace" in _lib.last_error()
+
+
+def test_sparse_attn_without_indices_gives_zero_output(gpu):
+    """K = 0 (no selected rows, null index pointer): the kernel reads no index
+    and the output is the sink-only softmax's zero (the oracle's closed form
+    with no gathered rows)."""
+    from sglang_lite_amd import _lib
+
+    lib = _lib.load()
+    print("sparse_attn K=0 B=1 S=2 H=64 n=300", flush=True)
+    rng = np.random.default_rng(6)
+    q, kv, sink, _ = _case(rng, 1, 2, 64, 300, 64)
+    qd, kvd = to_dev_bf16(q, gpu), to_dev_bf16(kv, gpu)
+    sd = to_dev_f32(sink, gpu)
+    o = torch.full_like(qd, 7.0)
+    assert lib.sgl_sparse_attn_workspace_size(1, 2, 64, 0) == 0
+    rc = lib.sgl_sparse_attn(qd.data_ptr(), 1, 2, 64, kvd.data_ptr(), _lib.ATTN_KV_BF16, 0, 300,
+                             kvd.stride(0) * 2, 512, sd.data_ptr(), None, 0, 0.04,
+                             o.data_ptr(), None, 0, _lib.stream_of(qd))
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(o).item() == 0
