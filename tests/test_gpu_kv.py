@@ -195,3 +195,36 @@ def test_packed_page_writer_errors(gpu):
         KVP.write_packed_kv_bf16(pool, [0, 1], 0, kv, layer_idx=2)
     with pytest.raises(ValueError, match="requires block_table"):
         KVP.write_packed_kv_bf16(pool, [], 0, kv)
+
+
+def test_gather_dequant_ragged_steps_out_of_range_and_empty_cache(gpu):
+    """Indices past the cache give zero rows; a gather whose row count is not
+    a multiple of the rows per step (3 x 301) ends cleanly; an empty cache
+    gives all-zero rows without reading it (layouts A, A pages, B)."""
+    from sglang_lite_amd import dsv4_kv_pack as KVP
+
+    print("gather ragged / out of range / empty cache", flush=True)
+    rng = np.random.default_rng(23)
+    T = 128
+    xv, xt = _kv(rng, T, 512, torch.bfloat16)
+    rows_a = OK.pack_layout_a(xv, xt[:, 448:].contiguous().view(torch.uint8).numpy(), 4)
+    idx = rng.integers(0, T, (3, 301)).astype(np.int32)
+    idx[0, :4] = [T, T + 7, 2 ** 30, -5]
+    idx[2, -1] = T - 1
+    d_idx = torch.from_numpy(idx).to(gpu)
+    ref = OK.gather_dequant(rows_a, idx, "A")
+    d_rows = torch.from_numpy(rows_a).to(gpu)
+    got = KVP.gather_dequant(d_rows, d_idx, layout="A").float().cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+    pages = KVP.to_paged_hnd(d_rows, 64)
+    got_p = KVP.gather_dequant(pages, d_idx, layout="A", page_size=64).float().cpu().numpy()
+    np.testing.assert_array_equal(got_p.view(np.uint32), ref.view(np.uint32))
+    xb, xbt = _kv(rng, T, 576, torch.bfloat16)
+    rows_b = OK.pack_layout_b(xb[:, :512], xbt[:, 512:].contiguous().view(torch.uint8).numpy())
+    ref_b = OK.gather_dequant(rows_b, idx, "B")
+    got_b = KVP.gather_dequant(torch.from_numpy(rows_b).to(gpu), d_idx, layout="B")
+    np.testing.assert_array_equal(got_b.float().cpu().numpy().view(np.uint32), ref_b.view(np.uint32))
+    for layout, width in (("A", 584), ("B", 656)):
+        empty = torch.zeros(0, width, dtype=torch.uint8, device=gpu)
+        z = KVP.gather_dequant(empty, d_idx, layout=layout)
+        assert torch.count_nonzero(z).item() == 0
