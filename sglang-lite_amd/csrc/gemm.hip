@@ -996,7 +996,10 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       // M = 128 takes 23 us with 32 x 64 tiles, 39 us with 64 x 128
       if (a.M <= 128) return launch_cfg<KIND_DENSE, 32, 64, 1, 4, 4>(a, stream);
       if (a.M <= 256) return launch_cfg<KIND_DENSE, 32, 128, 1, 4, 4>(a, stream);
-      if (a.M <= 2048) return launch_cfg<KIND_DENSE, 64, 128, 2, 2, 3>(a, stream);
+      if (a.M <= 512) return launch_cfg<KIND_DENSE, 64, 128, 2, 2, 3>(a, stream);
+      // 128 x 128 with 8 wavefronts (the issuer split) from M = 512: M = 1024
+      // in 52 us where 64 x 128 tiles take 64 us
+      if (a.M <= 2048) return launch_cfg<KIND_DENSE, 128, 128, 2, 4, 3>(a, stream);
       return launch_cfg<KIND_DENSE, 128, 256, 2, 4, 3>(a, stream);
     case KIND_GATE_UP:
       return big ? launch_cfg<KIND_GATE_UP, 128, 256, 2, 4, 3>(a, stream)

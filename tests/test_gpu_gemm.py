@@ -26,8 +26,9 @@ def _operands(rng, M, N, K):
                                     (128, 4096, 7168),
                                     (129, 512, 2048), (300, 1040, 512),
                                     # ragged last N tile on the 32 x 64 (M <= 128), 32 x 128
-                                    # (M <= 256) and 128 x 256 (M > 2048) tiles
-                                    (100, 1040, 512), (200, 1040, 512), (2304, 1040, 512)])
+                                    # (M <= 256), 128 x 128 (M <= 2048) and 128 x 256 tiles
+                                    (100, 1040, 512), (200, 1040, 512), (1000, 1040, 512),
+                                    (2304, 1040, 512)])
 def test_fp8_gemm_matches_oracle(gpu, M, N, K):
     from sglang_lite_amd import kernel as K_
 
