@@ -956,7 +956,8 @@ int launch_fp4(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
         return launch_skinny<4, WF_FP4, SAHW>(a, stream);
       }
       if (a.M <= 256) return launch_cfg<KIND_DENSE, 32, 128, 1, 4, 3, WF_FP4, SAHW>(a, stream);
-      if (a.M <= 2048) return launch_cfg<KIND_DENSE, 64, 128, 2, 2, 2, WF_FP4, SAHW>(a, stream);
+      if (a.M <= 512) return launch_cfg<KIND_DENSE, 64, 128, 2, 2, 2, WF_FP4, SAHW>(a, stream);
+      if (a.M <= 2048) return launch_cfg<KIND_DENSE, 128, 128, 2, 4, 2, WF_FP4, SAHW>(a, stream);
       return launch_cfg<KIND_DENSE, 128, 256, 2, 4, 2, WF_FP4, SAHW>(a, stream);
     case KIND_GATE_UP:
       return big ? launch_cfg<KIND_GATE_UP, 128, 256, 2, 4, 2, WF_FP4, SAHW>(a, stream)

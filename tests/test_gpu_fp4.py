@@ -47,7 +47,8 @@ def _gemm(gpu, aq, sa, bp, sb, out_dtype=torch.bfloat16, **kw):
 # skinny (M <= 64), 64 x 128 tiles (M <= 2048) and 128 x 256 tiles
 @pytest.mark.parametrize("M,N,K", [(1, 256, 256), (16, 512, 1024), (33, 272, 1536), (64, 768, 1024),
                                     (65, 640, 512), (300, 1040, 768), (128, 4096, 7168),
-                                    (200, 1040, 512), (2100, 512, 512), (2100, 1040, 512)])
+                                    (200, 1040, 512), (1000, 1040, 512), (2100, 512, 512),
+                                    (2100, 1040, 512)])
 @pytest.mark.parametrize("pow2", [False, True])
 def test_fp4_gemm_matches_oracle(gpu, M, N, K, pow2):
     print(f"fp4_gemm M={M} N={N} K={K} pow2={pow2}", flush=True)
