@@ -21,8 +21,17 @@ Pinning (what checks each function against something other than itself):
 * ``moe.route_topk``: torch.topk / softmax as library routines.
 * ``moe.permute``: brute-force torch.where loop of the reference
   (model.py:634-640) and invariants (bijection, offsets = cumsum(bincount)).
-* ``moe.moe_forward``: the reference's own toy test (tests/test_v4_moe_fast.py:
-  10-43, activated-only loop == full loop) plus closed forms of the expert.
+* ``moe.expert_forward`` / ``moe.moe_forward``: vectors written by the
+  reference's own layer code (tests/golden/make_ref_moe.py runs the official
+  Gate / Expert / MoE of deepseek_infer/model.py and engine/v4_moe_fast.py's
+  activated-only dispatch with a dequantize-to-fp32 stand-in GEMM): routing
+  ids and the x quant exact, h (the input of w2's act_quant) within one bf16
+  ulp and its quant bytes exact where h agrees, expert and layer outputs
+  within the GEMM tolerance (tests/test_golden_ref_moe.py); the full loop of
+  model.py:629-644 (``moe_forward_full_loop``) equal to the activated-only
+  loop bit for bit.
+* ``fp4``: the e2m1 table (code 8 = +0.0) and the repack bytes against the
+  reference converter's output (tests/golden/make_ref_fp4_repack.py).
 * ``kv``: the reference's tests (tests/test_dsv4_kv_pack.py:16-65,
   tests/test_v4_dual_pool.py:57-75) and closed forms of the footer layout.
   Layout B has no reference producer: parity unpinned beyond its closed form.

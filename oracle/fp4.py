@@ -17,9 +17,12 @@ import numpy as np
 from . import quant as Q
 
 # deepseek_infer/convert.py:11-14 (the OCP MX e2m1 value set: sign, 2-bit
-# exponent with bias 1, 1-bit mantissa; code 8 is -0)
+# exponent with bias 1, 1-bit mantissa).  Code 8 is the format's -0; the
+# converter's table (and deep_gemm_sm120/utils/math.py `_dequantize_from_fp4_e2m1`,
+# which negates only nonzero magnitudes) give +0.0 there, so the repack of a
+# code-8 nibble is the e4m3 byte 0x00.
 E2M1 = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
-                 -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0], dtype=np.float32)
+                 0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0], dtype=np.float32)
 
 
 def e2m1_to_f32(code: np.ndarray) -> np.ndarray:
@@ -49,11 +52,18 @@ def e8m0_to_f32(b: np.ndarray) -> np.ndarray:
     return out
 
 
+# value pair (low nibble, high nibble) of every packed byte
+_PAIR = np.stack([E2M1[np.arange(256) & 0xF], E2M1[np.arange(256) >> 4]], axis=-1).astype(np.float32)
+
+
 def dequant_fp4(packed: np.ndarray, sb: np.ndarray) -> np.ndarray:
-    """fp32 value of an FP4 weight: e2m1 * 2^(e8m0 - 127) per 1 x 32 block."""
-    v = e2m1_to_f32(unpack_fp4(packed))
-    s = np.repeat(e8m0_to_f32(sb), 32, axis=-1)
-    return (v * s).astype(np.float32)
+    """fp32 value of an FP4 weight: e2m1 * 2^(e8m0 - 127) per 1 x 32 block
+    (exact: a power-of-two scale times a 2-bit significand)."""
+    p = np.asarray(packed, dtype=np.uint8)
+    v = _PAIR[p].reshape(*p.shape[:-1], p.shape[-1] * 2)
+    s = e8m0_to_f32(sb)
+    g = v.reshape(*v.shape[:-1], v.shape[-1] // 32, 32) * s[..., None]
+    return g.reshape(v.shape).astype(np.float32)
 
 
 def fp4_gemm(aq: np.ndarray, sa: np.ndarray, bp: np.ndarray, sb: np.ndarray,

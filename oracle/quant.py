@@ -14,8 +14,10 @@ INV448 = np.float32(1.0) / np.float32(448.0)  # fp32(1/448): torch scalar ops us
 # ------------------------------------------------------------------ formats
 
 
-def e4m3_to_f32(code: np.ndarray) -> np.ndarray:
-    """Decode OCP e4m3fn bytes (exact)."""
+def _e4m3_decode(code: np.ndarray) -> np.ndarray:
+    """OCP e4m3fn bytes -> float32 from the bit fields (exact): sign bit 7,
+    exponent bits 6..3 with bias 7 (0 = subnormal, m * 2^-9), mantissa bits
+    2..0; S.1111.111 is NaN."""
     c = np.asarray(code, dtype=np.uint8).astype(np.int64)
     sign = np.where(c & 0x80, -1.0, 1.0)
     e = (c >> 3) & 0xF
@@ -24,6 +26,15 @@ def e4m3_to_f32(code: np.ndarray) -> np.ndarray:
     out = (sign * mag).astype(np.float32)
     out[(e == 0xF) & (m == 0x7)] = np.nan
     return out
+
+
+_E4M3_LUT = _e4m3_decode(np.arange(256, dtype=np.uint8))
+
+
+def e4m3_to_f32(code: np.ndarray) -> np.ndarray:
+    """Decode OCP e4m3fn bytes (exact): the bit-field decode tabulated over
+    all 256 codes."""
+    return _E4M3_LUT[np.asarray(code, dtype=np.uint8)]
 
 
 # the 127 non-negative finite e4m3 values, increasing with the code
@@ -230,5 +241,9 @@ def dequant_blocks(q: np.ndarray, s: np.ndarray, gran: int = 128) -> np.ndarray:
     _dequant_fp8 semantics: w * s[n // 128, k // 128])."""
     v = e4m3_to_f32(q).astype(np.float32)
     n, k = v.shape
-    rs = np.repeat(np.repeat(np.asarray(s, dtype=np.float32), gran, 0), gran, 1)[:n, :k]
+    s = np.asarray(s, dtype=np.float32)
+    if n % gran == 0 and k % gran == 0:
+        blk = v.reshape(n // gran, gran, k // gran, gran) * s[:n // gran, None, :k // gran, None]
+        return blk.reshape(n, k)
+    rs = np.repeat(np.repeat(s, gran, 0), gran, 1)[:n, :k]
     return v * rs

@@ -545,6 +545,11 @@ int check_moe_shapes(const char* what, int64_t T, int64_t H, int64_t I, int E, i
   SGL_REQUIRE(k >= 1 && k <= 16 && k <= E, "%s: k=%d not in [1, min(16, E)]", what, k);
   SGL_REQUIRE(T * k < 0x7FFFFFFF && T * (k + 1) * H < ((int64_t)1 << 46), "%s: too many tokens",
               what);
+  // the grouped GEMMs address operand rows with 32-bit lane offsets: the
+  // gate/up A operand is xq [T, H], the down A operand hq [T (k + 1), I]
+  SGL_REQUIRE(T * H < ((int64_t)1 << 31) && T * (k + 1) * I < ((int64_t)1 << 31),
+              "%s: T=%lld tokens exceed the 2 GiB operand limit (T*H=%lld, T*(k+1)*I=%lld)", what,
+              (long long)T, (long long)(T * H), (long long)(T * (k + 1) * I));
   return SGL_OK;
 }
 

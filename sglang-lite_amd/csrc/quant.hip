@@ -178,11 +178,14 @@ __global__ void e8m0_to_f32_kernel(const uint8_t* __restrict__ src, float* __res
 }
 
 // e2m1 code -> fp32: sign bit 3, exponent bits 2..1 (bias 1), mantissa bit 0
-// (0, 0.5, 1, 1.5, 2, 3, 4, 6 and their negatives)
+// (0, 0.5, 1, 1.5, 2, 3, 4, 6 and their negatives).  Code 8 (the format's -0)
+// decodes to +0.0 as the checkpoint converter's table has it
+// (deepseek_infer/convert.py:11-14, FP4_TABLE[8] = 0.0), so the repack writes
+// e4m3 0x00 there, not 0x80.
 __device__ __forceinline__ float e2m1_value(uint32_t c) {
   const uint32_t e = (c >> 1) & 3u, m = c & 1u;
   const float mag = e == 0 ? 0.5f * (float)m : ldexpf(1.0f + 0.5f * (float)m, (int)e - 1);
-  return (c & 8u) ? -mag : mag;
+  return ((c & 8u) && (c & 7u)) ? -mag : mag;
 }
 
 // Lossless FP4 -> FP8 weight repack (deepseek_infer/convert.py:17-52), one

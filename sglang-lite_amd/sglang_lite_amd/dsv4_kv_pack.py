@@ -19,11 +19,12 @@ Layout B (576-dim latent+rope rows, no reference producer; 656 B)::
     [512:640) RoPE as 64 x bf16
     [640:656) 4 x fp32 scales (little endian)
 
-``pack_dsv4_kv_bf16`` quantizes with the reference's torch fallback formula
-(``_torch_fp8_ue8m0_quant``, :78-101) when ``act_quant_fn`` is None, and with
-the official ``act_quant(..., "ue8m0", float8_e8m0fnu)`` formula
-(``kernel.py:22-37,79-96``) when one is given; the packing itself always runs
-the fused HIP kernel.
+``act_quant_fn`` (dsv4_kv_pack.py:58-61): None quantizes with the reference's
+torch fallback formula (``_torch_fp8_ue8m0_quant``, :78-101); the official
+``kernel.act_quant`` (TileLang, ``kernel.py:22-37,79-96``) or this package's
+``kernel.act_quant`` are computed by the fused HIP kernel with that
+function's ue8m0 formula; any other function is called on the NoPE part as
+the reference calls it, and its bytes are packed.
 """
 
 from __future__ import annotations
@@ -61,6 +62,38 @@ def _rows(x: torch.Tensor, dim: int) -> Tuple[torch.Tensor, int]:
     return z, z.shape[0]
 
 
+def _fused_quant_mode(act_quant_fn) -> Optional[int]:
+    """The sgl_scale_mode the fused pack kernel computes in place of
+    ``act_quant_fn(nope, 64, "ue8m0", float8_e8m0fnu, False)``, or None when
+    the function is not one whose formula the kernel holds (then it is called)."""
+    if act_quant_fn is None:
+        return _lib.SCALE_KV_UE8M0
+    from . import kernel as HK
+
+    if act_quant_fn is HK.act_quant:
+        return HK.scale_mode_for("ue8m0")
+    if getattr(act_quant_fn, "__module__", None) == "kernel" and \
+            getattr(act_quant_fn, "__name__", None) == "act_quant":
+        return _lib.SCALE_TILELANG_UE8M0  # the official TileLang act_quant's ue8m0 rule
+    return None
+
+
+def _pack_rows_with(kv: torch.Tensor, act_quant_fn) -> torch.Tensor:
+    """dsv4_kv_pack.py:55-75 with a caller's quantizer: call it on the NoPE
+    part and place its e4m3 bytes, the RoPE bytes and its 7 e8m0 scale bytes."""
+    nope = kv[..., :DSV4_NOPE_DIM].contiguous()
+    rope = kv[..., DSV4_NOPE_DIM:].contiguous()
+    y, s = act_quant_fn(nope, DSV4_FP8_BLOCK, "ue8m0", torch.float8_e8m0fnu, False)
+    out = torch.empty(*kv.shape[:-1], DSV4_PACKED_BYTES, dtype=torch.uint8, device=kv.device)
+    out[..., :DSV4_NOPE_DIM] = y.view(torch.uint8).view(*y.shape[:-1], DSV4_NOPE_DIM)
+    out[..., DSV4_NOPE_DIM:DSV4_DATA_BYTES] = rope.view(torch.uint8).view(
+        *rope.shape[:-1], DSV4_ROPE_DIM * 2)
+    out[..., DSV4_DATA_BYTES:DSV4_DATA_BYTES + DSV4_SCALE_BYTES] = s.view(torch.uint8).view(
+        *s.shape[:-1], DSV4_SCALE_BYTES)
+    out[..., DSV4_PACKED_BYTES - 1] = 0
+    return out
+
+
 def pack_dsv4_kv_bf16(kv: torch.Tensor, *, act_quant_fn=None) -> torch.Tensor:
     """Pack KV ``[..., 512]`` -> logical uint8 ``[..., 584]`` (dsv4_kv_pack.py:40-75)."""
     if kv.shape[-1] != DSV4_HEAD_DIM:
@@ -71,7 +104,9 @@ def pack_dsv4_kv_bf16(kv: torch.Tensor, *, act_quant_fn=None) -> torch.Tensor:
     if kv.dtype == torch.float32:
         # the reference views fp32 rope bytes into a 128-byte slot, which fails
         raise RuntimeError("pack_dsv4_kv_bf16: fp32 rope does not fit the 128-byte rope slot")
-    mode = _lib.SCALE_KV_UE8M0 if act_quant_fn is None else _lib.SCALE_TILELANG_UE8M0
+    mode = _fused_quant_mode(act_quant_fn)
+    if mode is None:
+        return _pack_rows_with(kv, act_quant_fn)
     z, T = _rows(kv, DSV4_HEAD_DIM)
     out = torch.empty(*kv.shape[:-1], DSV4_PACKED_BYTES, dtype=torch.uint8, device=kv.device)
     _lib.call("sgl_kv_pack", _lib.ptr(z) if T else None, _DT[kv.dtype], T,
@@ -89,7 +124,9 @@ def pack_dsv4_kv_paged(kv: torch.Tensor, page_size: int = DSV4_PAGE_SIZE, *,
     if kv.dtype not in (torch.bfloat16, torch.float16):
         raise TypeError(f"unsupported kv dtype {kv.dtype}")
     _lib.require_device(kv, what="pack_dsv4_kv_paged")
-    mode = _lib.SCALE_KV_UE8M0 if act_quant_fn is None else _lib.SCALE_TILELANG_UE8M0
+    mode = _fused_quant_mode(act_quant_fn)
+    if mode is None:
+        return to_paged_hnd(_pack_rows_with(kv, act_quant_fn), page_size)
     z, T = _rows(kv, DSV4_HEAD_DIM)
     n_pages = (T + page_size - 1) // page_size
     out = torch.empty(n_pages, 1, page_size, DSV4_PACKED_BYTES, dtype=torch.uint8, device=kv.device)
@@ -107,7 +144,14 @@ def write_packed_kv_bf16(pool: torch.Tensor, block_table, start_pos: int, kv: to
     engine/v4_dual_pool.py:73-128 feeds it) in one kernel.  ``block_table`` is
     a list of block ids (checked on the host against the pool, as the
     reference does) or a device int32 tensor (graph-capturable; entries
-    outside the pool are skipped)."""
+    outside the pool are skipped).  ``act_quant_fn`` must be None or an
+    ``act_quant`` whose formula the fused kernel holds (the official or this
+    package's); rows quantized by another function are packed with
+    ``pack_dsv4_kv_bf16`` and written by the caller."""
+    mode = _fused_quant_mode(act_quant_fn)
+    if mode is None:
+        raise TypeError("write_packed_kv_bf16: act_quant_fn must be None or kernel.act_quant; "
+                        "pack rows from another quantizer with pack_dsv4_kv_bf16")
     if pool.dim() != 5 or pool.dtype != torch.uint8 or pool.shape[2] != 1 or \
             pool.shape[-1] != DSV4_PACKED_BYTES or not pool.is_contiguous():
         raise ValueError(f"expected a contiguous uint8 [layers, blocks, 1, page, 584] pool, "
@@ -132,7 +176,6 @@ def write_packed_kv_bf16(pool: torch.Tensor, block_table, start_pos: int, kv: to
     z, T = _rows(kv, DSV4_HEAD_DIM)
     if T == 0:
         return
-    mode = _lib.SCALE_KV_UE8M0 if act_quant_fn is None else _lib.SCALE_TILELANG_UE8M0
     try:
         _lib.call("sgl_kv_pack_to_pages", z.data_ptr(), _DT[kv.dtype], T, z.stride(0), mode,
                   bt.data_ptr(), bt.numel(), int(start_pos), int(page), int(num_blocks),

@@ -229,15 +229,37 @@ def combine(out: torch.Tensor, ids: torch.Tensor, has_shared: bool) -> torch.Ten
 
 
 class MoEWorkspace:
-    """Reusable device workspace for :func:`moe_forward` (grown on demand)."""
+    """Reusable device workspace for :func:`moe_forward`, grown on demand.
+
+    A buffer once handed out is never freed while the workspace lives: a HIP
+    graph captured with it keeps its address and writes there on every
+    replay, so when a larger call needs more bytes the old buffer moves to
+    ``retired`` instead of going back to torch's pool (where another tensor
+    could take it).  Growth is geometric (at least 1.5x), which bounds the
+    retired bytes by twice the largest buffer; :meth:`reserve` sizes the
+    workspace once up front (e.g. for the largest batch a runner captures).
+    """
 
     def __init__(self):
         self.buf: Optional[torch.Tensor] = None
+        self.retired: List[torch.Tensor] = []
 
     def get(self, nbytes: int, device) -> torch.Tensor:
-        if self.buf is None or self.buf.numel() < nbytes or self.buf.device != torch.device(device):
-            self.buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        dev = torch.device(device)
+        if self.buf is not None and self.buf.device != dev:
+            self.retired.append(self.buf)
+            self.buf = None
+        if self.buf is None or self.buf.numel() < nbytes:
+            size = max(nbytes, 256)
+            if self.buf is not None:
+                size = max(size, self.buf.numel() * 3 // 2)
+                self.retired.append(self.buf)
+            self.buf = torch.empty(size, dtype=torch.uint8, device=dev)
         return self.buf
+
+    def reserve(self, T: int, table: "ExpertTable", k: int, device) -> torch.Tensor:
+        """Size the workspace for layers of up to ``T`` tokens over ``table``."""
+        return self.get(workspace_size(T, table.H, table.I, table.E, k, table.has_shared), device)
 
 
 def moe_forward(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, table: ExpertTable,

@@ -59,3 +59,129 @@ def bf16_values(rng: np.random.Generator, shape, scale=1.0) -> np.ndarray:
     from oracle.quant import bf16_round
 
     return bf16_round((rng.standard_normal(shape, dtype=np.float32) * np.float32(scale)).astype(np.float32))
+
+
+def ref_moe_case(name: str):
+    """Inputs of a reference-generated MoE golden case (tests/golden/
+    ref_moe_<name>.npz) rebuilt with the oracle: FP8 weights quantized by the
+    oracle's per_block_cast_to_fp8 (the fixture's digest of the reference's
+    bytes checks them), FP4 weights as drawn.  Returns (case dict, fixture
+    dict, experts, shared, digest) with oracle-format expert dicts; e8m0
+    scales are kept as bytes under ``s*`` and decoded under ``s*_f32``."""
+    import os
+    import sys
+
+    here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    if here not in sys.path:
+        sys.path.insert(0, here)
+    import ref_moe_cases as C
+    from oracle import fp4 as F4
+    from oracle import quant as Q
+
+    c = C.CASES[name]
+    gold = dict(np.load(C.path(name)))
+    inp = C.draw(name)
+
+    def fp8(e):
+        out = {}
+        for nm in ("1", "3", "2"):
+            q, s = Q.per_block_cast_to_fp8(e["w" + nm], use_ue8m0=c["ue8m0"])
+            out["w" + nm] = q
+            out["s" + nm] = Q.e8m0_byte(s) if c["ue8m0"] else s
+        return out
+
+    def fp4(e):
+        out = {"fmt": "fp4"}
+        out.update(e)
+        return out
+
+    stored = [fp4(e) if c["fp4"] else fp8(e) for e in inp["experts"]]
+    shared = fp8(inp["shared"])
+    digest = C.digest(stored, shared)
+
+    def oracle_view(e):
+        if e.get("fmt") == "fp4":
+            return e
+        o = dict(e)
+        for nm in ("1", "3", "2"):
+            o["s" + nm] = F4.e8m0_to_f32(e["s" + nm]) if c["ue8m0"] else e["s" + nm]
+        return o
+
+    return (c, gold, inp, [oracle_view(e) for e in stored], oracle_view(shared), stored, shared,
+            digest)
+
+
+def gemm_err_stats(out: np.ndarray, ref: np.ndarray) -> dict:
+    """Error of ``out`` against ``ref`` in units of the GEMM elementwise bound."""
+    out = np.asarray(out, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    r = np.abs(out - ref) / (ATOL + RTOL_BF16 * np.abs(ref))
+    return {"rel_l2": float(np.linalg.norm(out - ref) / max(np.linalg.norm(ref), 1e-30)),
+            "max_ratio": float(r.max()), "n_over": int(np.sum(r > 1)), "n": int(r.size),
+            "p999_ratio": float(np.quantile(r, 0.999))}
+
+
+def assert_layer_close(out: np.ndarray, ref: np.ndarray, what: str = "layer",
+                       tail: float = 5e-4) -> dict:
+    """A whole MoE layer against the oracle's layer.  The layer requantizes
+    twice inside (x, and h between gate/up and down): where the device's bf16
+    h and the oracle's differ by one ulp across an e4m3 rounding boundary, or
+    move a 128-group's amax, the requantized codes move by one e4m3 step
+    (2^-3 relative) and that step reaches the output through w2 -- a tail the
+    single-GEMM bound does not model (each GEMM is held to that bound on its
+    own inputs by the stage tests).  Bound: rel-L2 <= 1e-2; the GEMM
+    elementwise bound for all but a fraction ``tail`` of the elements, and
+    twice the bound for every element."""
+    st = gemm_err_stats(out, ref)
+    print(f"{what}: {st}", flush=True)
+    assert np.all(np.isfinite(np.asarray(out, dtype=np.float64))), f"{what}: non-finite output"
+    assert st["rel_l2"] <= REL_L2, f"{what}: rel-L2 {st['rel_l2']:.3e} > {REL_L2}"
+    assert st["n_over"] <= tail * st["n"], f"{what}: {st['n_over']} of {st['n']} beyond the bound"
+    assert st["max_ratio"] <= 2.0, f"{what}: an element at {st['max_ratio']:.2f}x the bound"
+    return st
+
+
+def assert_requant_close(q_dev: np.ndarray, s_dev: np.ndarray, q_ref: np.ndarray,
+                         s_ref: np.ndarray, what: str = "requant", max_diff: float = 0.01) -> dict:
+    """1x128 FP8-requantized rows of a GEMM epilogue (the gate/up kernel's h)
+    against the oracle's requantization of its own h.  The two h agree to
+    rounding (bf16 ulps), so their quantizations agree except where a value
+    straddles an e4m3 rounding boundary or a group's amax moves by an ulp:
+    bytes equal for all but ``max_diff`` of the elements, scales within
+    2^-6 relative, rel-L2 of the dequantized rows <= 1e-2, and every
+    dequantized pair within the sum of the two quantization errors and the
+    h difference: h = bf16(w silu(g) u) of bf16 g, u differs by at most two
+    bf16 ulps (2^-6 |h|) between the two, and each quantization errs by at
+    most half an e4m3 step (2^-4 |h|, or 2^-10 of the scale below the
+    normal range), so |d| <= (2^-3 + 2^-6)(1 + 2^-4) max(|dev|, |ref|) +
+    2^-9 max(scale), plus 2^-14 of the group's amax (448 scale): the MFMA
+    forms each 128-deep fp8 partial to about 1e-5 of the sum of its
+    |products| (not an IEEE fp32 sum), so a gate or up output near zero --
+    and the h value made from it, far below its group's amax -- carries an
+    absolute error that no relative bound covers."""
+    from oracle.quant import dequant_rows
+
+    q_dev, q_ref = np.asarray(q_dev, np.uint8), np.asarray(q_ref, np.uint8)
+    s_dev, s_ref = np.asarray(s_dev, np.float32), np.asarray(s_ref, np.float32)
+    dd = dequant_rows(q_dev, s_dev).astype(np.float64)
+    dr = dequant_rows(q_ref, s_ref).astype(np.float64)
+    frac = float(np.mean(q_dev != q_ref))
+    srel = float(np.max(np.abs(s_dev.astype(np.float64) / s_ref - 1.0))) if s_ref.size else 0.0
+    smax = np.repeat(np.maximum(s_dev, s_ref).astype(np.float64), 128, axis=-1)
+    mag = np.maximum(np.abs(dd), np.abs(dr))
+    step = (2.0 ** -3 + 2.0 ** -6) * (1 + 2.0 ** -4) * mag + (2.0 ** -9 + 448.0 * 2.0 ** -14) * smax
+    over = int(np.sum(np.abs(dd - dr) > step))
+    rel = float(np.linalg.norm(dd - dr) / max(np.linalg.norm(dr), 1e-30))
+    st = {"byte_diff": frac, "scale_rel": srel, "over_step": over, "rel_l2": rel}
+    if over:
+        bad = np.argwhere(np.abs(dd - dr) > step)[:4]
+        sd = np.repeat(s_dev, 128, axis=-1)
+        sr = np.repeat(s_ref, 128, axis=-1)
+        st["worst"] = [(tuple(int(v) for v in i), float(dd[tuple(i)]), float(dr[tuple(i)]),
+                        int(q_dev[tuple(i)]), int(q_ref[tuple(i)]), float(sd[tuple(i)]),
+                        float(sr[tuple(i)])) for i in bad]
+    assert frac <= max_diff, f"{what}: {frac:.4f} of the bytes differ ({st})"
+    assert srel <= 2.0 ** -6, f"{what}: scales differ by {srel:.3e} ({st})"
+    assert over == 0, f"{what}: {over} values beyond the requantization bound ({st})"
+    assert rel <= REL_L2, f"{what}: rel-L2 {rel:.3e} ({st})"
+    return st

@@ -178,3 +178,27 @@ def test_product_refuses_cpu_tensors():
         KVP.pack_dsv4_kv_bf16(torch.zeros(2, 512, dtype=torch.int32))
     with pytest.raises(AssertionError):
         K.act_quant(torch.zeros(2, 100, dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("name", ["sgl_moe_forward", "sgl_moe_gate_up", "sgl_moe_down"])
+@pytest.mark.parametrize("T", [300_000, 600_000])
+def test_moe_rejects_tokens_beyond_32_bit_operand_offsets(name, T):
+    """The grouped GEMMs address A rows with 32-bit lane offsets (xq [T, H],
+    hq [T (k + 1), I]): a T whose operands pass 2 GiB is refused with
+    ValueError before any launch (null pointers: nothing is touched)."""
+    from sglang_lite_amd import _lib as L
+
+    H, I, E, k = 4096, 2048, 256, 8
+    args = {
+        "sgl_moe_forward": (None, T, H, I, E, k, None, None, None, 1, 0, 0.0, 0, None, 0, None, None),
+        "sgl_moe_gate_up": (None, None, T, H, I, E, k, None, None, None, None, 1, 0, 0.0, 0, None,
+                            None, None),
+        "sgl_moe_down": (None, None, T, H, I, E, k, None, None, None, 1, 0, 0, None, None),
+    }[name]
+    with pytest.raises(ValueError, match="2 GiB operand limit"):
+        L.call(name, *args)
+    # a prefill-sized T passes the shape checks (then fails on the null pointers)
+    small = list(args)
+    small[args.index(T)] = 8192
+    with pytest.raises(ValueError, match="null pointer"):
+        L.call(name, *small)

@@ -241,3 +241,55 @@ def test_moe_layer_captures_into_a_hip_graph(official, gpu):
     logits = OM.router_logits(x_last, Wb)
     w_ref, ids_ref = OM.route_topk(logits, k, "sqrtsoftplus", f32(gate.bias), 1.5)
     assert_gemm_close(f32(eager[0]), OM.moe_forward(x_last, ids_ref, w_ref, experts, sh), "graph MoE")
+
+
+def test_graph_replay_after_the_workspace_grows(official, gpu):
+    """A decode graph captured at T = 64 keeps its workspace address.  An eager
+    call with more tokens grows the module's workspace; the captured buffer
+    must stay allocated (not return to torch's pool, where the tensor
+    allocated next could take it), so replaying the T = 64 graph afterwards
+    still equals the eager forward bit for bit and leaves other tensors alone."""
+    from sglang_lite_amd import moe as HM
+    from sglang_lite_amd import v4_moe_fast as MF
+
+    M, K = official
+    rng = np.random.default_rng(46)
+    T, H, I, E, k = 64, 512, 256, 16, 4
+    Wb = bf16_values(rng, (E, H), scale=H ** -0.5)
+    experts = [OM.make_expert(rng, H, I) for _ in range(E)]
+    sh = OM.make_expert(rng, H, I)
+    gate = M.Gate(to_dev_bf16(Wb, gpu), k, "softmax", 1.0, None)
+    moe = M.MoE(H, gate, [M.Expert(_dev_expert(e, gpu)) for e in experts],
+                M.Expert(_dev_expert(sh, gpu)))
+    assert MF.attach_v4_moe_fast(moe)["enabled"]
+    ids0 = torch.zeros(1, T, dtype=torch.long, device=gpu)
+    x_static = to_dev_bf16(bf16_values(rng, (T, H)), gpu).view(1, T, H)
+    for _ in range(3):
+        moe(x_static, ids0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y_static = moe(x_static, ids0)
+    ws = moe._sgl_ws
+    captured = ws.buf.data_ptr()
+    # an eager prefill-sized call grows the workspace
+    T_big = 1024
+    xb = to_dev_bf16(bf16_values(rng, (T_big, H)), gpu).view(1, T_big, H)
+    moe(xb, torch.zeros(1, T_big, dtype=torch.long, device=gpu))
+    torch.cuda.synchronize()
+    assert ws.buf.data_ptr() != captured
+    assert any(b.data_ptr() == captured for b in ws.retired)
+    # tensors allocated now must not receive the graph's writes
+    fence = [torch.full((n,), 0xA5, dtype=torch.uint8, device=gpu)
+             for n in (r.numel() for r in ws.retired)]
+    for i in range(3):
+        xi = to_dev_bf16(bf16_values(rng, (T, H)), gpu).view(1, T, H)
+        x_static.copy_(xi)
+        g.replay()
+        torch.cuda.synchronize()
+        eager = moe(xi.clone(), ids0)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(u8(y_static), u8(eager), err_msg=f"replay {i}")
+    for f in fence:
+        assert bool((f == 0xA5).all()), "a graph replay wrote into a tensor allocated after capture"
+    assert isinstance(ws, HM.MoEWorkspace)

@@ -123,6 +123,22 @@ def test_fp4_to_fp8_repack_bit_exact(gpu, N, K, spread):
     np.testing.assert_array_equal(u8(q), q_ref)
 
 
+def test_fp4_to_fp8_repack_reference_bytes(gpu):
+    """The repack on the device against the reference converter's bytes
+    (tests/golden/ref_fp4_repack.npz from convert.py cast_e2m1fn_to_e4m3fn):
+    an all-0x88 block (nibble code 8 -> e4m3 0x00), a code 8 / code 0 mix and
+    uniform codes with scales spread over 2^10."""
+    import os
+
+    from sglang_lite_amd import kernel as K_
+
+    d = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                             "ref_fp4_repack.npz"))
+    q, s = K_.cast_e2m1fn_to_e4m3fn(dev_fp4(d["bp"], gpu).view(torch.int8), dev_e8m0(d["sb"], gpu))
+    np.testing.assert_array_equal(u8(q), d["q"])
+    np.testing.assert_array_equal(u8(s), d["s"])
+
+
 def test_repacked_fp8_gemm_equals_fp4_gemm(gpu):
     """The lossless repack feeds the FP8 path: fp8_gemm on the repacked weight
     and fp4_gemm on the original agree to fp32 summation order."""

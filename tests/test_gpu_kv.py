@@ -15,6 +15,16 @@ from oracle import quant as Q
 pytestmark = pytest.mark.gpu
 
 
+def _official_act_quant():
+    """Stand-in for the official TileLang ``kernel.act_quant`` (identified by
+    module and name): the pack kernels compute its ue8m0 formula themselves,
+    so it is never called."""
+    def act_quant(*a, **k):
+        raise AssertionError("the official act_quant's formula runs in the fused kernel")
+    act_quant.__module__ = "kernel"
+    return act_quant
+
+
 def _kv(rng, T, dim, dtype):
     x = bf16_values(rng, (T, dim))
     t = torch.from_numpy(x).to(dtype)
@@ -35,12 +45,52 @@ def test_pack_layout_a_bit_exact(gpu, dtype, mode, T):
     rope = xt[:, 448:].contiguous().view(torch.uint8).numpy()
     ref = OK.pack_layout_a(xv, rope, mode)
     d = xt.to(gpu)
-    out = KVP.pack_dsv4_kv_bf16(d, act_quant_fn=None if mode == 4 else (lambda *a: None))
+    out = KVP.pack_dsv4_kv_bf16(d, act_quant_fn=None if mode == 4 else _official_act_quant())
     np.testing.assert_array_equal(out.cpu().numpy(), ref)
-    pages = KVP.pack_dsv4_kv_paged(d, 64, act_quant_fn=None if mode == 4 else (lambda *a: None))
+    pages = KVP.pack_dsv4_kv_paged(d, 64, act_quant_fn=None if mode == 4 else _official_act_quant())
     np.testing.assert_array_equal(pages.cpu().numpy(), OK.to_paged_hnd(ref, 64))
     pages2 = KVP.to_paged_hnd(out, 64)
     np.testing.assert_array_equal(pages2.cpu().numpy(), OK.to_paged_hnd(ref, 64))
+
+
+def test_pack_calls_an_injected_quantizer(gpu):
+    """dsv4_kv_pack.py:58-61: a quantizer other than the official act_quant is
+    called on the NoPE part as (nope, 64, "ue8m0", float8_e8m0fnu, False) and
+    its bytes are packed: with the KV formula it reproduces the default pack,
+    with a constant quantizer its bytes land in place (rows and pages)."""
+    import functools
+
+    from sglang_lite_amd import dsv4_kv_pack as KVP
+    from sglang_lite_amd import kernel as K_
+
+    rng = np.random.default_rng(31)
+    xv, xt = _kv(rng, 130, 512, torch.bfloat16)
+    d = xt.to(gpu)
+    calls = []
+
+    def kv_formula(x, block, fmt, sdtype, inplace):
+        calls.append((tuple(x.shape), block, fmt, sdtype, inplace))
+        return K_.act_quant(x, block, fmt, sdtype, inplace, scale_mode=4)
+
+    got = KVP.pack_dsv4_kv_bf16(d, act_quant_fn=kv_formula)
+    assert calls == [((130, 448), 64, "ue8m0", torch.float8_e8m0fnu, False)]
+    np.testing.assert_array_equal(got.cpu().numpy(), KVP.pack_dsv4_kv_bf16(d).cpu().numpy())
+
+    def const(x, block, fmt, sdtype, inplace):
+        y = torch.full(x.shape, 0x3C, dtype=torch.uint8, device=x.device).view(torch.float8_e4m3fn)
+        s = torch.full((*x.shape[:-1], x.shape[-1] // block), 0x7A, dtype=torch.uint8,
+                       device=x.device).view(torch.float8_e8m0fnu)
+        return y, s
+
+    rows = KVP.pack_dsv4_kv_bf16(d, act_quant_fn=const).cpu().numpy()
+    assert np.all(rows[:, :448] == 0x3C) and np.all(rows[:, 576:583] == 0x7A)
+    assert np.all(rows[:, 583] == 0)
+    np.testing.assert_array_equal(rows[:, 448:576], xt[:, 448:].contiguous().view(torch.uint8).numpy())
+    pages = KVP.pack_dsv4_kv_paged(d, 64, act_quant_fn=functools.partial(const)).cpu().numpy()
+    np.testing.assert_array_equal(pages, OK.to_paged_hnd(rows, 64))
+    pool = torch.zeros(1, 4, 1, 64, 584, dtype=torch.uint8, device=gpu)
+    with pytest.raises(TypeError, match="act_quant_fn"):
+        KVP.write_packed_kv_bf16(pool, [0, 1, 2], 0, d, act_quant_fn=const)
 
 
 def test_reference_pack_shape_and_rope_bytes(gpu):
@@ -153,7 +203,7 @@ def test_layout_a_dequant_equals_qat_inplace(gpu):
     rng = np.random.default_rng(23)
     xv, xt = _kv(rng, 200, 512, torch.bfloat16)
     d = xt.to(gpu)
-    rows = KVP.pack_dsv4_kv_bf16(d, act_quant_fn=lambda *a: None)
+    rows = KVP.pack_dsv4_kv_bf16(d, act_quant_fn=_official_act_quant())
     idx = torch.arange(200, dtype=torch.int32, device=gpu)[None]
     deq = KVP.gather_dequant(rows, idx, layout="A")[0].float().cpu().numpy()
     qat, _ = Q.act_quant_inplace_tilelang(xv[:, :448], 64, round_scale=True)

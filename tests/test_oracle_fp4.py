@@ -14,13 +14,17 @@ from oracle import quant as Q
 
 def test_e2m1_table_is_the_ocp_definition():
     # sign bit 3, exponent bits 2..1 with bias 1, mantissa bit 0; exponent 0 is
-    # subnormal (m * 2^-1); convert.py:11-14 lists the same 16 values
+    # subnormal (m * 2^-1).  Code 8 (the format's -0) is +0.0, as in the
+    # converter's table (convert.py:11-14, FP4_TABLE[8] = 0.0) and
+    # deep_gemm_sm120/utils/math.py `_dequantize_from_fp4_e2m1` (sign only on
+    # nonzero magnitudes): the repack of code 8 must be the e4m3 byte 0x00.
     for c in range(16):
         s, e, m = c >> 3, (c >> 1) & 3, c & 1
         mag = m * 0.5 if e == 0 else (1.0 + m / 2.0) * 2.0 ** (e - 1)
         want = -mag if s else mag
         got = float(F4.E2M1[c])
-        assert got == want and np.signbit(got) == bool(s), (c, got, want)
+        assert got == want and np.signbit(got) == bool(s and mag != 0.0), (c, got, want)
+    assert not np.signbit(F4.E2M1[8])
     assert sorted(set(np.abs(F4.E2M1).tolist())) == [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
 
 
@@ -35,11 +39,12 @@ def test_e8m0_decode_matches_torch():
 
 def test_nibble_order_known_answer():
     # byte 0x21: low nibble 1 (0.5) is element 0, high nibble 2 (1.0) element 1
-    # (convert.py:31-33 stacks low then high); 0xF8: -0 then -6
+    # (convert.py:31-33 stacks low then high); 0xF8: code 8 (+0) then -6
     p = np.array([[0x21, 0xF8]], dtype=np.uint8)
     np.testing.assert_array_equal(F4.unpack_fp4(p), [[1, 2, 8, 15]])
     v = F4.e2m1_to_f32(F4.unpack_fp4(p))
-    np.testing.assert_array_equal(v, np.array([[0.5, 1.0, -0.0, -6.0]], np.float32))
+    np.testing.assert_array_equal(v, np.array([[0.5, 1.0, 0.0, -6.0]], np.float32))
+    assert not np.signbit(v[0, 2])
     rng = np.random.default_rng(0)
     c = rng.integers(0, 16, (5, 64), dtype=np.uint8)
     np.testing.assert_array_equal(F4.unpack_fp4(F4.pack_fp4(c)), c)
@@ -158,3 +163,31 @@ def test_quant_fp4_weight_reconstructs_within_half_a_step():
     amax = np.abs(w.reshape(64, 8, 32)).max(-1)
     s = F4.e8m0_to_f32(sb)
     assert np.all(amax / s <= 6.0) and np.all(amax / (s / 2) > 6.0)
+
+
+def test_repack_of_code_8_is_byte_zero():
+    """Closed form: every element of an all-0x88 block (nibble code 8 = +0.0 in
+    the converter's table) repacks to the e4m3 byte 0x00, whatever its scales."""
+    N, K = 128, 256
+    bp = np.full((N, K // 2), 0x88, np.uint8)
+    sb = np.random.default_rng(7).integers(100, 130, (N, K // 32)).astype(np.uint8)
+    q, s = F4.fp4_to_fp8_repack(bp, sb)
+    assert np.all(q == 0x00)
+    # each nibble code's byte under a unit offset: the e4m3 code of the table value
+    codes = np.arange(16, dtype=np.uint8)
+    want = Q.f32_to_e4m3(F4.E2M1[codes])
+    assert want[8] == 0x00 and want[0] == 0x00
+
+
+def test_repack_matches_reference_converter_bytes():
+    """tests/golden/ref_fp4_repack.npz: convert.py cast_e2m1fn_to_e4m3fn's
+    bytes (written by tests/golden/make_ref_fp4_repack.py) for uniform codes,
+    an all-0x88 block and a code 8 / code 0 mix, scales spread over 2^10."""
+    import os
+
+    d = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                             "ref_fp4_repack.npz"))
+    q, s = F4.fp4_to_fp8_repack(d["bp"], d["sb"])
+    np.testing.assert_array_equal(q, d["q"])
+    np.testing.assert_array_equal(s, d["s"])
+    assert np.all(d["q"][:128, :128] == 0)
