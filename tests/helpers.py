@@ -111,11 +111,12 @@ def ref_moe_case(name: str):
             digest)
 
 
-def gemm_err_stats(out: np.ndarray, ref: np.ndarray) -> dict:
-    """Error of ``out`` against ``ref`` in units of the GEMM elementwise bound."""
+def gemm_err_stats(out: np.ndarray, ref: np.ndarray, atol_scale: float = 1.0) -> dict:
+    """Error of ``out`` against ``ref`` in units of the GEMM elementwise bound
+    (its absolute term times ``atol_scale``)."""
     out = np.asarray(out, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
-    r = np.abs(out - ref) / (ATOL + RTOL_BF16 * np.abs(ref))
+    r = np.abs(out - ref) / (ATOL * atol_scale + RTOL_BF16 * np.abs(ref))
     return {"rel_l2": float(np.linalg.norm(out - ref) / max(np.linalg.norm(ref), 1e-30)),
             "max_ratio": float(r.max()), "n_over": int(np.sum(r > 1)), "n": int(r.size),
             "p999_ratio": float(np.quantile(r, 0.999))}
@@ -131,8 +132,13 @@ def assert_layer_close(out: np.ndarray, ref: np.ndarray, what: str = "layer",
     single-GEMM bound does not model (each GEMM is held to that bound on its
     own inputs by the stage tests).  Bound: rel-L2 <= 1e-2; the GEMM
     elementwise bound for all but a fraction ``tail`` of the elements, and
-    twice the bound for every element."""
-    st = gemm_err_stats(out, ref)
+    twice the bound for every element.  The bound's 2e-2 absolute term is
+    sized for unit-scale outputs (N(0, 1) activations through N(0, 0.02)
+    weights, the configurations' data); for a layer whose outputs are larger
+    it is scaled by the reference output's RMS."""
+    rms = float(np.sqrt(np.mean(np.square(np.asarray(ref, dtype=np.float64))))) if np.size(ref) else 0.0
+    st = gemm_err_stats(out, ref, max(1.0, rms))
+    st["ref_rms"] = rms
     print(f"{what}: {st}", flush=True)
     assert np.all(np.isfinite(np.asarray(out, dtype=np.float64))), f"{what}: non-finite output"
     assert st["rel_l2"] <= REL_L2, f"{what}: rel-L2 {st['rel_l2']:.3e} > {REL_L2}"
