@@ -276,6 +276,25 @@ int sgl_moe_forward(const void* x, int64_t T, int64_t H, int64_t I, int E, int k
                     int has_shared, int expert_format, float swiglu_limit, int scale_mode,
                     void* workspace, size_t workspace_bytes, void* y, sgl_stream_t stream);
 
+/* Size of the static device workspace of sgl_moe_forward_noalloc: 64 MiB
+ * per GPU, held from library load to process end (T <= 690 tokens at hidden
+ * 4096, intermediate 2048, top-8 + shared). */
+#define SGL_MOE_SCRATCH_BYTES (64u << 20)
+
+/* sgl_moe_forward without a workspace argument and without any allocation:
+ * the layer's workspace is a static device array of SGL_MOE_SCRATCH_BYTES
+ * per GPU (its address resolved once per device, by sgl_probe or on the
+ * first call).  No counterpart in the reference: for callers that cannot
+ * allocate device memory (HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Returns SGL_ERR_WORKSPACE when
+ * sgl_moe_workspace_size(T, ...) exceeds SGL_MOE_SCRATCH_BYTES.  Every call
+ * on one GPU shares that GPU's array, which keeps the last call's contents:
+ * calls that overlap on one GPU (concurrent streams, threads) race. */
+int sgl_moe_forward_noalloc(const void* x, int64_t T, int64_t H, int64_t I, int E, int k,
+                            const int32_t* ids, const float* weights,
+                            const sgl_expert_ptrs* experts, int has_shared, int expert_format,
+                            float swiglu_limit, int scale_mode, void* y, sgl_stream_t stream);
+
 /* ------------------------------------------------------------- KV cache */
 
 /* Pack KV rows.  Layout A: kv [T, 512] (bf16 / f16 / f32, row stride ldkv)

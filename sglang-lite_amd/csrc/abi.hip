@@ -62,6 +62,10 @@ int sgl_probe(void) {
     sgl::set_error("device %d is %s; this library is built for gfx950 only", dev, prop.gcnArchName);
     return 0;
   }
+  // set-up: resolve this device's static MoE workspace address now, outside
+  // any stream capture
+  void* scratch = nullptr;
+  if (sgl::moe_scratch_ptr(&scratch) != SGL_OK) return 0;
   return 1;
 }
 

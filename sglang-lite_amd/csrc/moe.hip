@@ -8,6 +8,8 @@
 // permutation is a stable counting sort of slot = t*k + j by expert id; the
 // combine adds the bf16 expert outputs of a token into an fp32 zero in
 // ascending expert order, then adds the shared expert, then rounds to bf16.
+#include <mutex>
+
 #include "sgl_gemm.h"
 #include "sgl_numeric.h"
 
@@ -490,6 +492,44 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
 
 int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
+}  // namespace
+
+// ------------------------------------------------- static layer workspace
+// The workspace of sgl_moe_forward_noalloc: a file-scope device array (each
+// GPU holds its own copy for the life of the process).  In host code its
+// name is a stand-in, not a device address: the address comes from
+// hipGetSymbolAddress, resolved once per device with that device current
+// and kept in scratch_dev[]; only that pointer is ever passed to kernels.
+constexpr size_t kScratchBytes = SGL_MOE_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex scratch_mu;
+static void* scratch_dev[kMaxDevices] = {};
+
+// Device address of the current device's scratch array (resolved on the
+// first call for that device).
+int moe_scratch_ptr(void** out) {
+  int dev = 0;
+  SGL_CHECK_HIP(hipGetDevice(&dev));
+  SGL_REQUIRE(dev >= 0 && dev < kMaxDevices, "moe scratch: device %d above %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_dev[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("moe scratch: hipGetSymbolAddress failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return SGL_ERR_HIP;
+    }
+    scratch_dev[dev] = p;
+  }
+  *out = scratch_dev[dev];
+  return SGL_OK;
+}
+
+namespace {
+
 struct MoeWorkspace {
   uint8_t* xq;
   float* xs;
@@ -782,6 +822,28 @@ int sgl_moe_combine(const void* out, const int32_t* ids, int64_t T, int k, int64
 size_t sgl_moe_workspace_size(int64_t T, int64_t H, int64_t I, int E, int k, int has_shared) {
   if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0) return 0;
   return sgl::carve(nullptr, T, H, I, E, k, has_shared ? 1 : 0).bytes;
+}
+
+int sgl_moe_forward_noalloc(const void* x, int64_t T, int64_t H, int64_t I, int E, int k,
+                            const int32_t* ids, const float* weights,
+                            const sgl_expert_ptrs* experts, int has_shared, int expert_format,
+                            float swiglu_limit, int scale_mode, void* y, sgl_stream_t stream) {
+  int rc = sgl::check_moe_shapes("moe_forward_noalloc", T, H, I, E, k, expert_format);
+  if (rc) return rc;
+  const size_t need = sgl::carve(nullptr, T, H, I, E, k, has_shared ? 1 : 0).bytes;
+  if (need > sgl::kScratchBytes) {
+    sgl::set_error("moe_forward_noalloc: T=%lld needs %zu bytes of workspace, above the static "
+                   "%zu (SGL_MOE_SCRATCH_BYTES); use sgl_moe_forward with a caller workspace",
+                   (long long)T, need, sgl::kScratchBytes);
+    return SGL_ERR_WORKSPACE;
+  }
+  if (T == 0) return SGL_OK;
+  void* ws = nullptr;
+  if ((rc = sgl::moe_scratch_ptr(&ws))) return rc;
+  // every buffer the layer reads is written first inside the call (the
+  // permute kernel zeroes the GEMM tile counters), so the array needs no clear
+  return sgl_moe_forward(x, T, H, I, E, k, ids, weights, experts, has_shared, expert_format,
+                         swiglu_limit, scale_mode, ws, sgl::kScratchBytes, y, stream);
 }
 
 int sgl_moe_forward(const void* x, int64_t T, int64_t H, int64_t I, int E, int k,

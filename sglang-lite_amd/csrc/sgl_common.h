@@ -26,6 +26,10 @@ inline int check_launch(const char* what) {
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 
+// Device address of the current device's static MoE workspace (moe.hip),
+// resolved with hipGetSymbolAddress on the first call for that device.
+int moe_scratch_ptr(void** out);
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }

@@ -75,6 +75,9 @@ SIGNATURES = {
         c_int,
         [P, I64, I64, I64, c_int, c_int, P, P, P, c_int, c_int, c_float, c_int, P, c_size_t, P, P],
     ),
+    "sgl_moe_forward_noalloc": (
+        c_int, [P, I64, I64, I64, c_int, c_int, P, P, P, c_int, c_int, c_float, c_int, P, P],
+    ),
     "sgl_kv_pack": (c_int, [P, c_int, I64, I64, c_int, c_int, c_int, c_int, P, P]),
     "sgl_kv_pack_to_pages": (
         c_int, [P, c_int, I64, I64, c_int, P, I64, I64, c_int, I64, c_int, c_int, P, P]
