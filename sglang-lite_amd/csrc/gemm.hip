@@ -112,10 +112,15 @@ __device__ __forceinline__ v8i read_frag(const uint8_t* block, FragLane fl) {
   return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 }
 
-template <int KIND, int BM, int BN, int WM, int WN, int NSTAGE, int WF, bool SAHW>
+template <int KIND, int BM, int BN, int WM, int WN, int NSTAGE, int WF, bool SAHW, int LW>
 struct Cfg {
-  static constexpr int NT = 64 * WM * WN;
-  static constexpr int NW = WM * WN;
+  // LW > 0: LW loader wavefronts (after the WM x WN compute wavefronts) issue
+  // every stage DMA and compute nothing, so no compute wavefront ever stalls
+  // behind the CU's address unit; LW == 0: the DMAs are issued by compute
+  // wavefronts (with 8, by the second half, one per SIMD)
+  static constexpr int NWC = WM * WN;        // compute wavefronts
+  static constexpr int NW = NWC + LW;        // all wavefronts
+  static constexpr int NT = 64 * NW;
   static constexpr int TM = BM / (WM * 16);
   static constexpr int TN = BN / (WN * 16);
   static constexpr int HALF = BN / 2;   // gate_up: gate columns, then the same up columns
@@ -130,21 +135,22 @@ struct Cfg {
   // wavefront per SIMD, issues a stage's loads; the first half starts its
   // MFMAs right after the stage barrier instead of queueing behind the CU's
   // address unit with every other wavefront
-  static constexpr int IW = NW == 8 ? NW / 2 : NW;
+  static constexpr int IW = LW > 0 ? LW : (NWC == 8 ? NWC / 2 : NWC);
   static constexpr int SBI = SB_BYTES / (IW * 256);  // weight-scale dword DMAs per issuer
-  static constexpr int SA_ROWS = BM / NW;  // row scales each wavefront loads per stage
+  static constexpr int SA_ROWS = BM / NWC;  // row scales per compute wavefront slot per stage
   static constexpr int STAGE = A_BYTES + B_BYTES + SB_BYTES;
-  static constexpr int SA_SLOT = NW * 256;           // one stage of row scales
+  static constexpr int SA_SLOT = NWC * 256;          // one stage of row scales
   static constexpr int ACH = BM * KS / 8;            // 1 KB DMA chunks of A per stage
   static constexpr int CHUNKS = ACH + BN / 8;        // ... of A and B
   static constexpr int CPW = CHUNKS / IW;       // per issuer
-  static constexpr int SAI = NW / IW;           // row-scale DMAs per issuer (one per wavefront)
+  static constexpr int SAI = NWC / IW;          // row-scale DMAs per issuer (one per slot)
   static constexpr int QA = BM / 8 / IW;        // distinct A row groups per issuer
   static constexpr int LPS = CPW + SAI + SBI;   // DMA instructions per issuer per stage
   static constexpr int NSA = NSTAGE;  // row-scale slots (a ring of their own)
   static constexpr int RING = NSTAGE * STAGE;
   static constexpr int SMEM = RING + NSA * SA_SLOT;
   static_assert(CHUNKS % IW == 0, "chunks must split evenly over the issuers");
+  static_assert(NWC % IW == 0, "row-scale slots must split evenly over the issuers");
   static_assert(IW % 2 == 0 && (BM / 8) % IW == 0 && (HALF / 8) % IW == 0,
                 "every chunk index of an issuer maps to one operand, half and swizzle parity");
   static_assert(SA_ROWS >= 1 && SA_ROWS * KS <= 64, "row scales per wavefront");
@@ -157,10 +163,11 @@ struct Cfg {
   static_assert(WF == WF_FP4 || !SAHW, "in-MFMA activation scales are an FP4-weight path");
 };
 
-template <int KIND, int BM, int BN, int WM, int WN, int NSTAGE, int WF, bool SAHW>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs args) {
-  using C = Cfg<KIND, BM, BN, WM, WN, NSTAGE, WF, SAHW>;
-  constexpr int NT = C::NT, NW = C::NW, TM = C::TM, TN = C::TN, HALF = C::HALF, HW = C::HW;
+template <int KIND, int BM, int BN, int WM, int WN, int NSTAGE, int WF, bool SAHW, int LW>
+__global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const GemmArgs args) {
+  using C = Cfg<KIND, BM, BN, WM, WN, NSTAGE, WF, SAHW, LW>;
+  constexpr int NT = C::NT, NW = C::NW, NWC = C::NWC, TM = C::TM, TN = C::TN, HALF = C::HALF,
+                HW = C::HW;
   constexpr int KS = C::KS;
   constexpr bool FP4 = WF == WF_FP4;
 
@@ -174,7 +181,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / WN, wn = wave % WN;
+  const bool computes = LW == 0 || wave < NWC;  // loader wavefronts (LW > 0) compute nothing
+  const int wm = computes ? wave / WN : 0, wn = computes ? wave % WN : 0;
   const int g4 = lane >> 4, r16 = lane & 15;
   const FragLane fl = frag_lane(r16, g4);
   const FragLane fla = FP4 ? frag_lane_fp4a(r16, g4) : fl;
@@ -364,7 +372,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
     // issuer has the same swizzle parity (b & 1 = iw & 1), so the B lane
     // offset is one register plus a wave-uniform row base.  The other
     // wavefronts issue nothing (their offsets are issuer 0's, never used).
-    const bool issuer = wave >= NW - C::IW;
+    const bool issuer = wave >= NW - C::IW;  // the loaders, or the last IW compute wavefronts
     const int iw = issuer ? wave - (NW - C::IW) : 0;
     const int rr = lane >> 3, pc = lane & 7;
     uint32_t voffA[C::QA];
@@ -455,21 +463,17 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
         return (wn * TN + nj) * 16;
     };
 
-#pragma unroll
-    for (int s = 0; s < NSTAGE - 1; ++s)
-      if (s < NST) issue(s);
-
-    for (int st = 0; st < NST; ++st) {
-      // loads of stage st are the oldest in flight: allow the younger ones
+    // DMA waits: the loads of stage st are the oldest in flight; allow the younger ones
+    auto wait_stage = [&](int st) {
       const int younger = min(NSTAGE - 2, NST - 1 - st);
       if (NSTAGE >= 6 && younger >= 4) wait_vmcnt<(NSTAGE >= 6 ? 4 : 0) * C::LPS>();
       else if (NSTAGE >= 5 && younger == 3) wait_vmcnt<(NSTAGE >= 5 ? 3 : 0) * C::LPS>();
       else if (younger >= 2) wait_vmcnt<2 * C::LPS>();
       else if (younger == 1) wait_vmcnt<C::LPS>();
       else wait_vmcnt<0>();
-      __builtin_amdgcn_s_barrier();
-      if (st + NSTAGE - 1 < NST) issue(st + NSTAGE - 1);
-
+    };
+    // the MFMAs (and promotion) of stage st, from the stage's LDS slot
+    auto compute_stage = [&](int st) {
       const uint8_t* stg = smem + (st % NSTAGE) * C::STAGE;
       const uint8_t* tB = stg + C::A_BYTES;
       const float* tS = reinterpret_cast<const float*>(smem + C::RING + (st % C::NSA) * C::SA_SLOT);
@@ -479,14 +483,58 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
       };
 
       // a wavefront whose rows all lie past the tile's last row has no work
-      if ((wm * TM) * 16 < rows) {
+      if (computes && (wm * TM) * 16 < rows) {
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           const uint8_t* tA = stg + ks * (BM * 128);
           v8i af[TM];
 #pragma unroll
           for (int mi = 0; mi < TM; ++mi) af[mi] = read_frag(tA + (wm * TM + mi) * 16 * 128, fla);
-          if constexpr (!FP4) {
+          if constexpr (!FP4 && LW > 0) {
+            // two compute wavefronts share each SIMD (the loaders issue the
+            // DMAs), so the MFMAs of one overlap the other's promotion and
+            // LDS reads: no software pipelining, which keeps the live set in
+            // the 168-VGPR budget of three wavefronts per SIMD.  Per half
+            // (gate, then up; one half for dense / down) the scale products
+            // sa * sb of the wavefront's rows, then per column block: B
+            // fragment, TM MFMAs, TM x 4 promotion FMAs.
+            const int kb = st;
+            constexpr int HALVES = KIND == KIND_GATE_UP ? 2 : 1;
+            // row scales of the lane's rows (wm TM + mi) 16 + 4 g4 + r: with
+            // 16 rows per slot they are the 4 consecutive floats at slot
+            // wm TM + mi, offset 4 g4 -- one 16-byte read per mi
+            static_assert(C::SA_ROWS == 16, "row-scale slot layout");
+            const float* rsl = tS + (wm * TM) * 64 + 4 * g4;
+            float4 sa4[TM];
+#pragma unroll
+            for (int mi = 0; mi < TM; ++mi) sa4[mi] = *reinterpret_cast<const float4*>(rsl + mi * 64);
+#pragma unroll
+            for (int hv = 0; hv < HALVES; ++hv) {
+              const float sbv = sSb[KIND == KIND_GATE_UP ? hv : wave_blk][kb];
+              float ss[TM][4];
+#pragma unroll
+              for (int mi = 0; mi < TM; ++mi) {
+                ss[mi][0] = sa4[mi].x * sbv;
+                ss[mi][1] = sa4[mi].y * sbv;
+                ss[mi][2] = sa4[mi].z * sbv;
+                ss[mi][3] = sa4[mi].w * sbv;
+              }
+#pragma unroll
+              for (int nh = 0; nh < TN / HALVES; ++nh) {
+                const int nj = hv * (TN / HALVES) + nh;
+                const v8i bf = read_frag(tB + tile_col(nj) * 128, fl);
+                v4f pr[TM];
+#pragma unroll
+                for (int mi = 0; mi < TM; ++mi)
+                  pr[mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[mi], bf, vzero, 0, 0, 0, 0,
+                                                                            0, 0);
+#pragma unroll
+                for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+                  for (int r = 0; r < 4; ++r) acc[mi][nj][r] = fmaf(pr[mi][r], ss[mi][r], acc[mi][nj][r]);
+              }
+            }
+          } else if constexpr (!FP4) {
             const int kb = st;
             const float sbv0 = sSb[wave_blk][kb];
             const float sbv1 = KIND == KIND_GATE_UP ? sSb[1][kb] : 0.0f;
@@ -597,6 +645,40 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
           }
         }
       }
+    };
+
+    if constexpr (LW > 0) {
+      // loaders and compute wavefronts run separate loops with the same
+      // barriers, so neither keeps the other's registers live: the loaders
+      // wait for stage st's DMAs, meet the barrier, then refill the slot
+      // stage st - 1 used; the compute wavefronts meet the barrier with
+      // their reads of stage st - 1 complete, then compute stage st
+      if (!computes) {
+#pragma unroll
+        for (int s = 0; s < NSTAGE - 1; ++s)
+          if (s < NST) issue(s);
+        for (int st = 0; st < NST; ++st) {
+          wait_stage(st);
+          __builtin_amdgcn_s_barrier();
+          if (st + NSTAGE - 1 < NST) issue(st + NSTAGE - 1);
+        }
+      } else {
+        for (int st = 0; st < NST; ++st) {
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          __builtin_amdgcn_s_barrier();
+          compute_stage(st);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < NSTAGE - 1; ++s)
+        if (s < NST) issue(s);
+      for (int st = 0; st < NST; ++st) {
+        wait_stage(st);
+        __builtin_amdgcn_s_barrier();
+        if (st + NSTAGE - 1 < NST) issue(st + NSTAGE - 1);
+        compute_stage(st);
+      }
     }
     __syncthreads();  // every wavefront is done with the stage ring
 
@@ -604,20 +686,22 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
       // ---- stage the tile in LDS, then coalesced 16-byte row stores
       const bool f32out = KIND == KIND_DENSE && args.out_f32;
       const int esz = f32out ? 4 : 2;
+      if (computes) {
 #pragma unroll
-      for (int mi = 0; mi < TM; ++mi)
+        for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
-        for (int nj = 0; nj < TN; ++nj)
+          for (int nj = 0; nj < TN; ++nj)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int row = (wm * TM + mi) * 16 + 4 * g4 + r;
-            const int col = tile_col(nj) + r16;
-            const float v = acc[mi][nj][r];
-            if (f32out)
-              reinterpret_cast<float*>(smem)[row * BN + col] = v;
-            else
-              reinterpret_cast<uint16_t*>(smem)[row * BN + col] = bf16_bits_exact(v);
-          }
+            for (int r = 0; r < 4; ++r) {
+              const int row = (wm * TM + mi) * 16 + 4 * g4 + r;
+              const int col = tile_col(nj) + r16;
+              const float v = acc[mi][nj][r];
+              if (f32out)
+                reinterpret_cast<float*>(smem)[row * BN + col] = v;
+              else
+                reinterpret_cast<uint16_t*>(smem)[row * BN + col] = bf16_bits_exact(v);
+            }
+      }
       __syncthreads();
       const int chunks_per_row = BN * esz / 16;
       for (int task = tid; task < BM * chunks_per_row; task += NT) {
@@ -658,21 +742,26 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
             }
           }
       };
-      if (lim > 0.0f)
+      if (!computes) {
+      } else if (lim > 0.0f) {
         swiglu(std::true_type{});
-      else
+      } else {
         swiglu(std::false_type{});
+      }
       __syncthreads();
       constexpr int LPR = HALF / 8;  // 16 lanes per 128-column row
-      static_assert((BM * LPR) % NT == 0, "requant loop must be uniform");
+      // a wavefront's 64 tasks are 4 whole rows, in range or not together
+      static_assert((BM * LPR) % 64 == 0, "requant rows must fill wavefronts");
+      constexpr int RQ_IT = (BM * LPR + NT - 1) / NT;
       const int64_t NB = N / 128;
       // the scale mode is a compile-time constant inside (one copy per mode),
       // so the scale formula and the quantization fold to straight-line code
       auto requant = [&](auto mode_c) {
         constexpr int MODE = decltype(mode_c)::value;
 #pragma unroll
-        for (int it = 0; it < BM * LPR / NT; ++it) {
+        for (int it = 0; it < RQ_IT; ++it) {
           const int task = tid + it * NT;
+          if ((BM * LPR) % NT != 0 && task >= BM * LPR) break;  // wave-uniform
           const int row = task / LPR, sub = task % LPR;
           const uint4 v = *reinterpret_cast<const uint4*>(hbuf + row * HALF + sub * 8);
           const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
@@ -710,7 +799,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_fp8_kernel(const GemmArgs a
   }
 }
 
-template <int KIND, int BM, int BN, int WM, int WN, int NSTAGE, int WF = WF_FP8, bool SAHW = false>
+template <int KIND, int BM, int BN, int WM, int WN, int NSTAGE, int WF = WF_FP8, bool SAHW = false,
+          int LW = 0>
 int launch_cfg(GemmArgs& a, hipStream_t stream) {
   const int64_t half = KIND == KIND_GATE_UP ? BN / 2 : BN;
   a.n_tiles = (int)ceil_div(a.N, half);
@@ -725,7 +815,7 @@ int launch_cfg(GemmArgs& a, hipStream_t stream) {
   if (tiles == 0) return SGL_OK;
   // persistent: as many workgroups per CU as their LDS allows (the 160 KB
   // of a CU), a multiple of 8 so every XCD gets the same number
-  using C = Cfg<KIND, BM, BN, WM, WN, NSTAGE, WF, SAHW>;
+  using C = Cfg<KIND, BM, BN, WM, WN, NSTAGE, WF, SAHW, LW>;
   constexpr int kLdsPerCU = 160 * 1024;
   constexpr int kExtra = (KIND == KIND_DENSE ? 4 : 4 * (kMaxGroups + 1)) + BM * 12 +
                          2 * (WF == WF_FP4 ? 1 : kMaxKB) * 4;
@@ -736,7 +826,7 @@ int launch_cfg(GemmArgs& a, hipStream_t stream) {
   const int64_t need = (tiles + 7) / 8 * 8;
   if (need < wgs) wgs = need;
   a.m_tiles = (int)mt_bound;
-  gemm_fp8_kernel<KIND, BM, BN, WM, WN, NSTAGE, WF, SAHW><<<(unsigned)wgs, 64 * WM * WN, 0, stream>>>(a);
+  gemm_fp8_kernel<KIND, BM, BN, WM, WN, NSTAGE, WF, SAHW, LW><<<(unsigned)wgs, C::NT, 0, stream>>>(a);
   return check_launch("gemm_fp8");
 }
 
@@ -750,6 +840,12 @@ int launch_cfg(GemmArgs& a, hipStream_t stream) {
 // partial tiles are summed through LDS at the end.  B, the weight stream, is
 // read once (per row tile); the grid holds N/16 x ceil(M / 16 TM) workgroups,
 // enough to keep every CU streaming where the 128 x 256 tiles leave most idle.
+#ifndef SGL_LW
+#define SGL_LW 4
+#endif
+#ifndef SGL_LWN
+#define SGL_LWN 4
+#endif
 #ifndef SGL_SKINNY_MAX_M
 #define SGL_SKINNY_MAX_M 64
 #endif
@@ -1003,10 +1099,10 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       if (a.M <= 2048) return launch_cfg<KIND_DENSE, 128, 128, 2, 4, 3>(a, stream);
       return launch_cfg<KIND_DENSE, 128, 256, 2, 4, 3>(a, stream);
     case KIND_GATE_UP:
-      return big ? launch_cfg<KIND_GATE_UP, 128, 256, 2, 4, 3>(a, stream)
+      return big ? launch_cfg<KIND_GATE_UP, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)
                  : launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 4>(a, stream);
     default:
-      return big ? launch_cfg<KIND_DOWN, 128, 256, 2, 4, 3>(a, stream)
+      return big ? launch_cfg<KIND_DOWN, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)
                  : launch_cfg<KIND_DOWN, 32, 256, 1, 4, 4>(a, stream);
   }
 }
