@@ -177,6 +177,8 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
   __shared__ int sDst[BM];
   __shared__ float sW[BM];
   __shared__ float sSb[2][FP4 ? 1 : kMaxKB];  // fp8: the tile's weight scales per K block
+  // register epilogue of gate/up (LW > 0): each compute wavefront's row |h| maximum
+  __shared__ float sAmax[KIND == KIND_GATE_UP && LW > 0 ? WN : 1][KIND == KIND_GATE_UP && LW > 0 ? BM : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -494,31 +496,29 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
             // two compute wavefronts share each SIMD (the loaders issue the
             // DMAs), so the MFMAs of one overlap the other's promotion and
             // LDS reads: no software pipelining, which keeps the live set in
-            // the 168-VGPR budget of three wavefronts per SIMD.  Per half
-            // (gate, then up; one half for dense / down) the scale products
-            // sa * sb of the wavefront's rows, then per column block: B
-            // fragment, TM MFMAs, TM x 4 promotion FMAs.
+            // the 168-VGPR budget of three wavefronts per SIMD.
+            // Transposed product: the weight fragment is the MFMA's A operand
+            // (16 columns n), the activation fragment its B operand (16 rows
+            // m), so lane (g4, r16) accumulates row r16 of each 16-row block
+            // and columns 4 g4 .. 4 g4 + 3 of each 16-column block: one row
+            // scale per lane and block, and four consecutive output columns
+            // for the epilogue's vector stores.  Per half (gate, then up; one
+            // half for dense / down): the products sa * sb, then per column
+            // block the weight fragment, TM MFMAs and TM x 4 promotion FMAs.
             const int kb = st;
             constexpr int HALVES = KIND == KIND_GATE_UP ? 2 : 1;
-            // row scales of the lane's rows (wm TM + mi) 16 + 4 g4 + r: with
-            // 16 rows per slot they are the 4 consecutive floats at slot
-            // wm TM + mi, offset 4 g4 -- one 16-byte read per mi
+            // the row scale of row (wm TM + mi) 16 + r16 sits in slot
+            // wm TM + mi at position r16 (16 rows per slot)
             static_assert(C::SA_ROWS == 16, "row-scale slot layout");
-            const float* rsl = tS + (wm * TM) * 64 + 4 * g4;
-            float4 sa4[TM];
+            float sa1[TM];
 #pragma unroll
-            for (int mi = 0; mi < TM; ++mi) sa4[mi] = *reinterpret_cast<const float4*>(rsl + mi * 64);
+            for (int mi = 0; mi < TM; ++mi) sa1[mi] = tS[(wm * TM + mi) * 64 + r16];
 #pragma unroll
             for (int hv = 0; hv < HALVES; ++hv) {
               const float sbv = sSb[KIND == KIND_GATE_UP ? hv : wave_blk][kb];
-              float ss[TM][4];
+              float ss[TM];
 #pragma unroll
-              for (int mi = 0; mi < TM; ++mi) {
-                ss[mi][0] = sa4[mi].x * sbv;
-                ss[mi][1] = sa4[mi].y * sbv;
-                ss[mi][2] = sa4[mi].z * sbv;
-                ss[mi][3] = sa4[mi].w * sbv;
-              }
+              for (int mi = 0; mi < TM; ++mi) ss[mi] = sa1[mi] * sbv;
 #pragma unroll
               for (int nh = 0; nh < TN / HALVES; ++nh) {
                 const int nj = hv * (TN / HALVES) + nh;
@@ -526,12 +526,12 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
                 v4f pr[TM];
 #pragma unroll
                 for (int mi = 0; mi < TM; ++mi)
-                  pr[mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[mi], bf, vzero, 0, 0, 0, 0,
+                  pr[mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf, af[mi], vzero, 0, 0, 0, 0,
                                                                             0, 0);
 #pragma unroll
                 for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
-                  for (int r = 0; r < 4; ++r) acc[mi][nj][r] = fmaf(pr[mi][r], ss[mi][r], acc[mi][nj][r]);
+                  for (int r = 0; r < 4; ++r) acc[mi][nj][r] = fmaf(pr[mi][r], ss[mi], acc[mi][nj][r]);
               }
             }
           } else if constexpr (!FP4) {
@@ -682,7 +682,114 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
     }
     __syncthreads();  // every wavefront is done with the stage ring
 
-    if constexpr (KIND != KIND_GATE_UP) {
+    if constexpr (LW > 0 && KIND != KIND_GATE_UP) {
+      // ---- transposed layout: lane (g4, r16) holds row (wm TM + mi) 16 + r16,
+      // columns tile_col(nj) + 4 g4 .. + 3: four consecutive outputs per
+      // store (8 bytes bf16 / 16 bytes fp32), a wavefront's 64 columns of a
+      // row in four stores
+      const bool f32out = KIND == KIND_DENSE && args.out_f32;
+      if (computes) {
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi) {
+          const int row = (wm * TM + mi) * 16 + r16;
+          if (row < rows) {
+            const int64_t drow = sDst[row];
+#pragma unroll
+            for (int nj = 0; nj < TN; ++nj) {
+              const int64_t col = n0 + tile_col(nj) + 4 * g4;
+              if (col < N) {
+                const v4f v = acc[mi][nj];
+                if (f32out) {
+                  *reinterpret_cast<float4*>(reinterpret_cast<float*>(args.c) + drow * N + col) =
+                      make_float4(v[0], v[1], v[2], v[3]);
+                } else {
+                  *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(args.c) + drow * N + col) =
+                      make_uint2(pk2_bf16_exact(v[0], v[1]), pk2_bf16_exact(v[2], v[3]));
+                }
+              }
+            }
+          }
+        }
+      }
+    } else if constexpr (LW > 0) {
+      // ---- SwiGLU + 1x128 requant in registers (transposed layout): lane
+      // (g4, r16) holds h of row (wm TM + mi) 16 + r16 at columns
+      // wn HW + 16 j + 4 g4 .. + 3 (j < TN/2), gate and up of the same
+      // columns in the same lane.  h = bf16(w * silu(bf16(gate)) * bf16(up)),
+      // silu(g) = g / (1 + 2^(-g log2 e)) with the hardware exp2 and
+      // reciprocal.  The row's |h| maximum over its 128 columns: the lane's
+      // 8 values, the 4 lanes of the row (xor 16, 32), then the WN
+      // wavefronts through sAmax.  Each lane quantizes its 8 values and
+      // stores them as two 4-byte runs.
+      const float lim = args.swiglu_limit;
+      float h[TM][8];
+      auto swiglu = [&](auto clamp_c) {
+        constexpr bool CLAMP = decltype(clamp_c)::value;
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi) {
+          const int row = (wm * TM + mi) * 16 + r16;
+          const float w = sW[row];
+          float am = 0.0f;
+#pragma unroll
+          for (int j = 0; j < TN / 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float gt = bf16_round(acc[mi][j][r]);
+              float up = bf16_round(acc[mi][j + TN / 2][r]);
+              if constexpr (CLAMP) {
+                up = clampf_(up, -lim, lim);
+                gt = gt > lim ? lim : gt;
+              }
+              const float ex = __builtin_amdgcn_exp2f(gt * -1.4426950408889634f);
+              const float silu = gt * __builtin_amdgcn_rcpf(1.0f + ex);
+              const float hv = bits_f32((uint32_t)bf16_bits_exact(w * (silu * up)) << 16);
+              h[mi][4 * j + r] = hv;
+              // IEEE maximum (v_maximum_f32): a NaN element makes the row's
+              // amax NaN, as the reference's amax does
+              am = __builtin_elementwise_maximum(am, fabsf(hv));
+            }
+          am = __builtin_elementwise_maximum(am, __shfl_xor(am, 16, 64));
+          am = __builtin_elementwise_maximum(am, __shfl_xor(am, 32, 64));
+          if (g4 == 0) sAmax[wn][row] = am;
+        }
+      };
+      static_assert(TN == 4, "the register epilogue packs 2 x 4 h values per row and lane");
+      if (!computes) {
+      } else if (lim > 0.0f) {
+        swiglu(std::true_type{});
+      } else {
+        swiglu(std::false_type{});
+      }
+      __syncthreads();
+      const int64_t NB = N / 128;
+      auto requant = [&](auto mode_c) {
+        constexpr int MODE = decltype(mode_c)::value;
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi) {
+          const int row = (wm * TM + mi) * 16 + r16;
+          if (row < rows) {
+            float am = sAmax[0][row];
+#pragma unroll
+            for (int q = 1; q < WN; ++q) am = __builtin_elementwise_maximum(am, sAmax[q][row]);
+            const float sf = group_scale(MODE, am);
+            const uint2 qv = quant8_e4m3(MODE, h[mi], sf);
+            const int64_t p = row0 + row;
+            uint8_t* dst = args.hq + p * N + n0 + wn * HW + 4 * g4;
+            *reinterpret_cast<uint32_t*>(dst) = qv.x;
+            *reinterpret_cast<uint32_t*>(dst + 16) = qv.y;
+            if (wn == 0 && g4 == 0) args.hs[p * NB + n0 / 128] = sf;
+          }
+        }
+      };
+      if (computes) {
+        switch (args.scale_mode) {
+          case SCALE_TORCH_FP32: requant(std::integral_constant<int, SCALE_TORCH_FP32>{}); break;
+          case SCALE_TORCH_UE8M0: requant(std::integral_constant<int, SCALE_TORCH_UE8M0>{}); break;
+          case SCALE_TILELANG_FP32: requant(std::integral_constant<int, SCALE_TILELANG_FP32>{}); break;
+          default: requant(std::integral_constant<int, SCALE_TILELANG_UE8M0>{}); break;
+        }
+      }
+    } else if constexpr (KIND != KIND_GATE_UP) {
       // ---- stage the tile in LDS, then coalesced 16-byte row stores
       const bool f32out = KIND == KIND_DENSE && args.out_f32;
       const int esz = f32out ? 4 : 2;
@@ -818,7 +925,8 @@ int launch_cfg(GemmArgs& a, hipStream_t stream) {
   using C = Cfg<KIND, BM, BN, WM, WN, NSTAGE, WF, SAHW, LW>;
   constexpr int kLdsPerCU = 160 * 1024;
   constexpr int kExtra = (KIND == KIND_DENSE ? 4 : 4 * (kMaxGroups + 1)) + BM * 12 +
-                         2 * (WF == WF_FP4 ? 1 : kMaxKB) * 4;
+                         2 * (WF == WF_FP4 ? 1 : kMaxKB) * 4 +
+                         (KIND == KIND_GATE_UP && LW > 0 ? WN * BM * 4 : 4);
   static_assert(C::SMEM + kExtra <= kLdsPerCU, "tile configuration exceeds the LDS of a CU");
   constexpr int per_cu = kLdsPerCU / (C::SMEM + kExtra) >= 2 ? 2 : 1;
   int64_t wgs = (int64_t)device_cu_count() * per_cu;
