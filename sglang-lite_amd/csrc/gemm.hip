@@ -71,6 +71,17 @@ __device__ __forceinline__ void dma4(const uint8_t* base, uint32_t voff, uint32_
                :: "v"(voff), "s"(base), "s"(lds) : "memory");
 }
 
+// The same with a per-lane 64-bit address (no scalar base): lane i copies 16
+// (dma16v) or 4 (dma4v) bytes from addr to LDS m0 + 16 i (4 i).
+__device__ __forceinline__ void dma16v(uint64_t addr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(addr), "s"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4v(uint64_t addr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(addr), "s"(lds) : "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" :: "n"(N) : "memory");
@@ -157,7 +168,7 @@ struct Cfg {
   static_assert(SB_BYTES % (IW * 256) == 0, "weight-scale DMAs must split evenly");
   static_assert(TM >= 1 && TN >= 1, "tile too small");
   static_assert(KIND != KIND_GATE_UP || (TN % 2 == 0 && HALF == 128), "gate_up needs 128 h columns");
-  static_assert(KIND == KIND_GATE_UP ? BM * HALF * 2 <= RING : BM * BN * 4 <= RING,
+  static_assert(LW > 0 || (KIND == KIND_GATE_UP ? BM * HALF * 2 <= RING : BM * BN * 4 <= RING),
                 "epilogue staging must fit in the stage ring");
   static_assert(NSTAGE >= 2 && NSTAGE <= 6, "stages");
   static_assert(WF == WF_FP4 || !SAHW, "in-MFMA activation scales are an FP4-weight path");
@@ -508,26 +519,33 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
             const int kb = st;
             constexpr int HALVES = KIND == KIND_GATE_UP ? 2 : 1;
             // the row scale of row (wm TM + mi) 16 + r16 sits in slot
-            // wm TM + mi at position r16 (16 rows per slot)
+            // wm TM + mi at position r16 (16 rows per slot); all scales of
+            // the stage are read up front with the A fragments, and the
+            // weight fragment of block nj + 1 is read while the MFMAs of
+            // block nj run (two fragment buffers), so no MFMA waits on LDS
             static_assert(C::SA_ROWS == 16, "row-scale slot layout");
             float sa1[TM];
 #pragma unroll
             for (int mi = 0; mi < TM; ++mi) sa1[mi] = tS[(wm * TM + mi) * 64 + r16];
+            float sbh[HALVES];
+#pragma unroll
+            for (int hv = 0; hv < HALVES; ++hv) sbh[hv] = sSb[KIND == KIND_GATE_UP ? hv : wave_blk][kb];
+            v8i bf[2];
+            bf[0] = read_frag(tB + tile_col(0) * 128, fl);
 #pragma unroll
             for (int hv = 0; hv < HALVES; ++hv) {
-              const float sbv = sSb[KIND == KIND_GATE_UP ? hv : wave_blk][kb];
               float ss[TM];
 #pragma unroll
-              for (int mi = 0; mi < TM; ++mi) ss[mi] = sa1[mi] * sbv;
+              for (int mi = 0; mi < TM; ++mi) ss[mi] = sa1[mi] * sbh[hv];
 #pragma unroll
               for (int nh = 0; nh < TN / HALVES; ++nh) {
                 const int nj = hv * (TN / HALVES) + nh;
-                const v8i bf = read_frag(tB + tile_col(nj) * 128, fl);
+                if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + tile_col(nj + 1) * 128, fl);
                 v4f pr[TM];
 #pragma unroll
                 for (int mi = 0; mi < TM; ++mi)
-                  pr[mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf, af[mi], vzero, 0, 0, 0, 0,
-                                                                            0, 0);
+                  pr[mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[nj & 1], af[mi], vzero, 0, 0,
+                                                                            0, 0, 0, 0);
 #pragma unroll
                 for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
@@ -906,6 +924,599 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
   }
 }
 
+// ------------------------------------------------------------ pipelined tiles
+// The grouped FP8 GEMMs at prefill sizes: 128 x 256 tiles (gate/up: 128 rows
+// x (128 gate + 128 up) columns; down: 128 x 256), eight compute wavefronts
+// (2 x 4, 64 x 64 each) and four loader wavefronts, a 3-stage ring of 48 KB.
+//
+// The loaders run one tile ahead.  During tile i's K loop they DMA tile
+// i+1's row slots and weight scales into the second table buffer; after
+// tile i's last stage they issue tile i+1's first two stages while the
+// compute wavefronts run tile i's epilogue (which keeps everything in
+// registers and leaves the ring alone) and fetch the index of tile i+2.  So
+// neither the table loads nor the first stages' latency separate two tiles.
+// Every loader global access is an LDS DMA counted by the explicit vmcnt
+// waits, except the tile-counter atomic, issued where nothing else is in
+// flight that its wait could hold up.
+//
+// Compute (as in the loader form of gemm_fp8_kernel): the transposed product
+// (weight fragment = MFMA A operand), lane (g4, r16) accumulating row
+// (wm 4 + mi) 16 + r16 and columns 16 nj + 4 g4 .. + 3; per 128-deep K
+// block C += P (sa sb); SwiGLU + 1x128 requant (gate/up) or bf16 stores
+// (down) from registers.
+namespace pipe {
+constexpr int BM = 128, BN = 256, WM = 2, WN = 4, TM = 4, TN = 4, NWC = 8, LW = 4, NW = 12;
+constexpr int NT = 64 * NW, NSTAGE = 3, HALF = 128, HW = HALF / WN;
+constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128, STAGE = A_BYTES + B_BYTES;
+constexpr int SA_ROWS = BM / NWC;     // rows per 256-byte row-scale slot
+constexpr int SA_SLOT = NWC * 256;    // one stage of row scales
+constexpr int RING = NSTAGE * STAGE;
+constexpr int SMEM = RING + NSTAGE * SA_SLOT;
+constexpr int CPW = (BM / 8 + BN / 8) / LW;  // 1 KB operand DMAs per loader per stage
+constexpr int QA = BM / 8 / LW;              // A row groups per loader
+constexpr int SAI = NWC / LW;                // row-scale DMAs per loader per stage
+constexpr int LPS = CPW + SAI;               // DMA instructions per loader per stage
+constexpr int kMaxKBp = 64;                  // K <= 8192: the tile's weight scales in LDS
+static_assert(SA_ROWS == 16 && CPW == 12 && QA == 4, "layout");
+}  // namespace pipe
+
+template <int KIND>
+__global__ __launch_bounds__(pipe::NT) void gemm_pipe_kernel(const GemmArgs args) {
+  using namespace pipe;
+  static_assert(KIND == KIND_GATE_UP || KIND == KIND_DOWN, "grouped GEMMs only");
+  __shared__ __align__(16) uint8_t smem[SMEM];
+  __shared__ int sTstart[kMaxGroups + 1];
+  __shared__ int sSlot[BM];                // next tile's sorted slots (routed rows)
+  // per table buffer: the epilogue's routing weight (gate/up) or output row (down) per tile row
+  __shared__ float sRow[2][BM];
+  __shared__ float sSb[2][2][kMaxKBp];     // per table buffer: weight scales per K block
+  __shared__ float sAmax[KIND == KIND_GATE_UP ? WN : 1][BM];
+  __shared__ int sTile[2][5];              // per table buffer: valid, e, row0, rows, nt
+  __shared__ uint32_t sExp[2][12];         // per table buffer: the tile expert's sgl_expert_ptrs
+  __shared__ int sPend[5];                 // the tile after the next one, resolved
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool loader = wave >= NWC;
+  const int iw = loader ? wave - NWC : 0;
+  const int wm = loader ? 0 : wave / WN, wn = loader ? 0 : wave % WN;
+  const int g4 = lane >> 4, r16 = lane & 15;
+  const int64_t K = args.K, N = args.N;
+  const int KB = (int)(K / 128);
+  const int NST = KB;
+  const int n_tiles = args.n_tiles;
+  const int G = args.E + (args.has_shared ? 1 : 0);
+  const int64_t shared_base = args.offsets[args.E];
+
+  // ---- M-tile prefix over the expert groups (E routed, then the shared one)
+  if (wave == 0) {
+    int carry = 0;
+    if (lane == 0) sTstart[0] = 0;
+    for (int base = 0; base < G; base += 64) {
+      const int g = base + lane;
+      int cnt = 0;
+      if (g < args.E)
+        cnt = args.offsets[g + 1] - args.offsets[g];
+      else if (g < G)
+        cnt = (int)args.T;
+      int incl = (cnt + BM - 1) / BM;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += u;
+      }
+      if (g < G) sTstart[g + 1] = carry + incl;
+      carry += __shfl(incl, 63, 64);
+    }
+  }
+  __syncthreads();
+  const int total = sTstart[G] * n_tiles;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per_xcd = gridDim.x >> 3;
+  const int per = (total + 7) >> 3;
+  const int t_begin = xcd * per;
+  const int t_end = min(t_begin + per, total);
+
+  // the workgroup's next tile (wave-uniform local index): the XCD's tile
+  // counter, or the static order slot, slot + per_xcd, ...
+  int static_next = slot;
+  auto take_tile = [&]() -> int {
+    if (args.tile_ctr) return atomicAdd(&args.tile_ctr[xcd], 1);
+    const int l = static_next;
+    static_next += per_xcd;
+    return l;
+  };
+  struct Tile {
+    int valid, e, row0, rows, nt;
+  };
+  auto resolve = [&](int local) -> Tile {
+    Tile t = {0, 0, 0, 0, 0};
+    const int L = t_begin + local;
+    if (local < 0 || L >= t_end) return t;
+    int lo = 0, hi = G;  // g with sTstart[g] * n_tiles <= L < sTstart[g + 1] * n_tiles
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (sTstart[mid] * n_tiles <= L) lo = mid; else hi = mid;
+    }
+    const int m_in_g = sTstart[lo + 1] - sTstart[lo];
+    const int loc = L - sTstart[lo] * n_tiles;
+    const int nt = loc / m_in_g;
+    const int mt = loc - nt * m_in_g;
+    const int cnt = lo < args.E ? args.offsets[lo + 1] - args.offsets[lo] : (int)args.T;
+    const int base = lo < args.E ? args.offsets[lo] : (int)shared_base;
+    // the search reads LDS per lane: make the fields wave-uniform again
+    t.valid = 1;
+    t.e = __builtin_amdgcn_readfirstlane(lo);
+    t.row0 = __builtin_amdgcn_readfirstlane(base + mt * BM);
+    t.rows = __builtin_amdgcn_readfirstlane(min(BM, cnt - mt * BM));
+    t.nt = __builtin_amdgcn_readfirstlane(nt);
+    return t;
+  };
+  auto read_tile = [&](int buf) -> Tile {
+    Tile t;
+    t.valid = __builtin_amdgcn_readfirstlane(sTile[buf][0]);
+    t.e = __builtin_amdgcn_readfirstlane(sTile[buf][1]);
+    t.row0 = __builtin_amdgcn_readfirstlane(sTile[buf][2]);
+    t.rows = __builtin_amdgcn_readfirstlane(sTile[buf][3]);
+    t.nt = __builtin_amdgcn_readfirstlane(sTile[buf][4]);
+    return t;
+  };
+  auto write_tile = [&](int buf, const Tile& t) {
+    sTile[buf][0] = t.valid;
+    sTile[buf][1] = t.e;
+    sTile[buf][2] = t.row0;
+    sTile[buf][3] = t.rows;
+    sTile[buf][4] = t.nt;
+  };
+  auto write_pend = [&](const Tile& t) {
+    sPend[0] = t.valid;
+    sPend[1] = t.e;
+    sPend[2] = t.row0;
+    sPend[3] = t.rows;
+    sPend[4] = t.nt;
+  };
+  auto read_pend = [&]() -> Tile {
+    Tile t;
+    t.valid = __builtin_amdgcn_readfirstlane(sPend[0]);
+    t.e = __builtin_amdgcn_readfirstlane(sPend[1]);
+    t.row0 = __builtin_amdgcn_readfirstlane(sPend[2]);
+    t.rows = __builtin_amdgcn_readfirstlane(sPend[3]);
+    t.nt = __builtin_amdgcn_readfirstlane(sPend[4]);
+    return t;
+  };
+  // pointer field f of table buffer buf's expert record (w_gate 0, w_up 1,
+  // w_down 2, s_gate 3, s_up 4, s_down 5)
+  static_assert(sizeof(sgl_expert_ptrs) == 48, "expert record layout");
+  auto exp_ptr = [&](int buf, int f) -> uint64_t {
+    return ((uint64_t)sExp[buf][2 * f + 1] << 32) | sExp[buf][2 * f];
+  };
+  // address of weight scale kb of half j of tile t (record in buffer buf):
+  // gate/up tiles read row n0/128 of the gate and up scales; down tiles the
+  // (clamped) blocks n0/128 and n0/128 + 1
+  auto scale_addr = [&](int buf, const Tile& t, int j, int kb) -> uint64_t {
+    if constexpr (KIND == KIND_GATE_UP) {
+      return exp_ptr(buf, j ? 4 : 3) + (uint64_t)(((int64_t)t.nt * HALF / 128) * KB + kb) * 4;
+    } else {
+      const int64_t nb = (N + 127) / 128;
+      int64_t blk = (int64_t)t.nt * BN / 128 + j;
+      if (blk > nb - 1) blk = nb - 1;
+      return exp_ptr(buf, 5) + (uint64_t)(blk * KB + kb) * 4;
+    }
+  };
+
+  // the epilogue value of tile row i (routed rows: from its sorted slot sl):
+  // gate/up the routing weight, down the output row t (k + shared) + j
+  auto row_value = [&](const Tile& t, int i, int sl) -> float {
+    if constexpr (KIND == KIND_GATE_UP) {
+      return (t.e < args.E && args.route_w) ? args.route_w[sl] : 1.0f;
+    } else {
+      const int p = t.row0 + (i < t.rows ? i : 0);
+      const int tok = t.e < args.E ? sl / args.k : p - (int)shared_base;
+      const int j = t.e < args.E ? sl - tok * args.k : args.k;
+      return __int_as_float(tok * args.out_k + j);
+    }
+  };
+
+  // ---- the first tile's tables, with plain loads (nothing else in flight);
+  // loader 0 alone, the barrier below publishes them
+  if (loader && iw == 0) {
+    int first = 0, second = 0;
+    if (lane == 0) {
+      first = take_tile();
+      second = take_tile();
+    }
+    const Tile t0 = resolve(__builtin_amdgcn_readfirstlane(__shfl(first, 0, 64)));
+    const Tile t1 = resolve(__builtin_amdgcn_readfirstlane(__shfl(second, 0, 64)));
+    if (lane == 0) {
+      write_tile(0, t0);
+      write_pend(t1);
+    }
+    if (t0.valid) {
+      if (lane < 12) sExp[0][lane] = reinterpret_cast<const uint32_t*>(args.experts + t0.e)[lane];
+      for (int i = lane; i < BM; i += 64) {
+        const int sl = (t0.e < args.E && i < t0.rows) ? args.sorted_slot[t0.row0 + i] : 0;
+        sSlot[i] = sl;
+        sRow[0][i] = row_value(t0, i, sl);
+      }
+    }
+  }
+  __syncthreads();
+  if (loader && iw == 0) {
+    const Tile t0 = read_tile(0);
+    if (t0.valid)
+      for (int j = 0; j < 2; ++j)
+        for (int kb = lane; kb < KB; kb += 64)
+          sSb[0][j][kb] = *reinterpret_cast<const float*>(scale_addr(0, t0, j, kb));
+  }
+  __syncthreads();
+
+  const v4f vzero = {0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t smem_lds = __builtin_amdgcn_readfirstlane(lds_u32(smem));
+  const int rr = lane >> 3, pc = lane & 7;
+
+  // ---- loader state of the tile whose stages it issues
+  // per-lane 64-bit DMA addresses (stage 0) -- no scalar base pointers, so
+  // nothing of the loader's state competes for SGPRs with the tile loop's
+  struct LoadState {
+    uint64_t a[QA];     // A row group q
+    uint64_t sa[SAI];   // row-scale slot q
+    uint64_t b0, b1;    // weight bases (gate / up, or down twice)
+    uint32_t laneB, clampB;
+    int64_t n0;
+  };
+  auto setup = [&](int buf, const Tile& t) -> LoadState {
+    LoadState ls;
+    // A row of tile row r: the token (gate/up routed: slot / k; shared:
+    // p - shared_base) or the h row p (down); rows past the tile's last row
+    // re-read its first row
+    auto src_of = [&](int r) -> int {
+      const int rc = r < t.rows ? r : 0;
+      const int p = t.row0 + rc;
+      if constexpr (KIND == KIND_GATE_UP) return t.e < args.E ? sSlot[rc] / args.k : p - (int)shared_base;
+      else return p;
+    };
+#pragma unroll
+    for (int q = 0; q < QA; ++q) {
+      const int r = (iw + q * LW) * 8 + rr;
+      ls.a[q] = (uint64_t)(uintptr_t)args.a + (uint64_t)((int64_t)src_of(r) * K + ((pc ^ swz(r)) << 4));
+    }
+    const int sa_l = lane < SA_ROWS ? lane : 0;
+#pragma unroll
+    for (int q = 0; q < SAI; ++q) {
+      const int sa_row = (iw + q * LW) * SA_ROWS + sa_l;
+      ls.sa[q] = (uint64_t)(uintptr_t)args.sa + (uint64_t)((int64_t)src_of(sa_row) * KB * 4);
+    }
+    if constexpr (KIND == KIND_GATE_UP) {
+      ls.b0 = exp_ptr(buf, 0);
+      ls.b1 = exp_ptr(buf, 1);
+      ls.n0 = (int64_t)t.nt * HALF;
+    } else {
+      ls.b0 = exp_ptr(buf, 2);
+      ls.b1 = ls.b0;
+      ls.n0 = (int64_t)t.nt * BN;
+    }
+    const uint32_t chunkB = (uint32_t)((pc ^ ((rr & 6) | (iw & 1))) << 4);
+    ls.laneB = (uint32_t)(rr * K) + chunkB;
+    ls.clampB = (uint32_t)(ls.n0 * K) + chunkB;  // rows past N re-read row n0
+    return ls;
+  };
+  // DMA stage st of the tile: loader iw moves 1 KB chunks c = iw + 4 j (A's
+  // 16 chunks first, then B's 32) into slot st % 3 and its two row-scale
+  // slots; the swizzle as in gemm_fp8_kernel
+  auto issue = [&](const LoadState& ls, int st) {
+    const uint32_t sl = __builtin_amdgcn_readfirstlane(smem_lds + (uint32_t)((st % NSTAGE) * STAGE));
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      const int c = iw + j * LW;
+      if (j < QA) {
+        dma16v(ls.a[j] + (uint64_t)st * 128u, __builtin_amdgcn_readfirstlane(sl + (uint32_t)c * 1024u));
+      } else {
+        const int b = c - BM / 8;
+        const bool up_half = KIND == KIND_GATE_UP && b * 8 >= HALF;
+        const int64_t nrow = ls.n0 + (up_half ? b * 8 - HALF : b * 8);
+        const uint32_t vo = nrow + rr < N ? (uint32_t)(nrow * K) + ls.laneB : ls.clampB;
+        dma16v((up_half ? ls.b1 : ls.b0) + vo + (uint64_t)st * 128u,
+               __builtin_amdgcn_readfirstlane(sl + (uint32_t)c * 1024u));
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < SAI; ++q)
+      dma4v(ls.sa[q] + (uint64_t)st * 4u,
+            __builtin_amdgcn_readfirstlane(
+                smem_lds + (uint32_t)(RING + (st % NSTAGE) * SA_SLOT + (iw + q * LW) * 256)));
+  };
+  auto wait_stage = [&](int st) {
+    if (st + 1 < NST) wait_vmcnt<LPS>();
+    else wait_vmcnt<0>();
+  };
+  static_assert(NSTAGE == 3, "the waits allow exactly one younger stage in flight");
+  // The next tile's tables by DMA, after the barrier of stage 1 (step 1)
+  // and stage 2 (step 2) of the current tile; every loader DMA of a step is
+  // older than that iteration's stage DMAs, so the next stage wait covers it.
+  //   step 1: loaders 0 and 1 its 128 row slots (64 each; routed rows),
+  //           loader 2 its expert record (12 dwords)
+  //   step 2: loaders 0 and 1 the epilogue row values (routing weights by a
+  //           gather; output rows computed), loaders 2 and 3 its gate / up
+  //           (or two down) weight-scale rows
+  auto prep_step1 = [&](int buf, const Tile& t) {
+    if (!t.valid) return;
+    if (iw < 2) {
+      const bool routed = t.e < args.E;
+      const int i = iw * 64 + lane;
+      const int ic = routed ? (i < t.rows ? i : t.rows - 1) : 0;
+      dma4v((uint64_t)(uintptr_t)args.sorted_slot + (uint64_t)(routed ? t.row0 + ic : 0) * 4u,
+            __builtin_amdgcn_readfirstlane(lds_u32(&sSlot[iw * 64])));
+    } else if (iw == 2 && lane < 12) {
+      // the DMA writes one dword per ACTIVE lane (m0 + 4 lane): only the 12
+      // lanes that own a dword of the 48-byte record may be active
+      dma4v((uint64_t)(uintptr_t)(args.experts + t.e) + (uint64_t)lane * 4u,
+            __builtin_amdgcn_readfirstlane(lds_u32(&sExp[buf][0])));
+    }
+  };
+  auto prep_step2 = [&](int buf, const Tile& t) {
+    if (!t.valid) return;
+    if (iw < 2) {
+      const int i = iw * 64 + lane;
+      const int sl = sSlot[i < t.rows ? i : 0];
+      if constexpr (KIND == KIND_GATE_UP) {
+        if (t.e < args.E && args.route_w)
+          dma4v((uint64_t)(uintptr_t)args.route_w + (uint64_t)sl * 4u,
+                __builtin_amdgcn_readfirstlane(lds_u32(&sRow[buf][iw * 64])));
+        else
+          sRow[buf][i] = 1.0f;
+      } else {
+        sRow[buf][i] = row_value(t, i, sl);
+      }
+    } else {
+      const int j = iw - 2;
+      dma4v(scale_addr(buf, t, j, lane < KB ? lane : KB - 1),
+            __builtin_amdgcn_readfirstlane(lds_u32(&sSb[buf][j][0])));
+    }
+  };
+
+  // The two roles run separate tile loops (separate register live ranges:
+  // the loader state never coexists with the accumulators) that meet at the
+  // same barriers: per tile NST stage barriers, the ring-free barrier, the
+  // row-maxima barrier (gate/up only) and the epilogue-done barrier. Both
+  // read the same tile sequence from LDS, so they leave together.
+  if (loader) {
+    LoadState ls = {};
+    int cur = 0;
+    {
+      const Tile t0 = read_tile(0);
+      if (t0.valid) {
+        ls = setup(0, t0);
+        issue(ls, 0);
+        if (NST > 1) issue(ls, 1);
+      }
+    }
+    for (;;) {
+      if (!read_tile(cur).valid) break;
+      for (int st = 0; st < NST; ++st) {
+        wait_stage(st);
+        __builtin_amdgcn_s_barrier();
+        if (st == 1) {
+          // this tile's sSlot was last read by setup() before its first
+          // stage; the next tile was resolved before this tile
+          const Tile tn = read_pend();
+          prep_step1(cur ^ 1, tn);
+          if (iw == 0 && lane == 0) write_tile(cur ^ 1, tn);
+        } else if (st == 2) {
+          // step 1's DMAs have landed (the stage-2 wait and barrier)
+          prep_step2(cur ^ 1, read_tile(cur ^ 1));
+        }
+        if (st + 2 < NST) issue(ls, st + 2);
+      }
+      __syncthreads();  // the ring is free; the next tile's tables are in LDS
+      // the next tile's first two stages, then (loader 0) the tile after
+      // it, taken and resolved: its loads wait for those DMAs too, which the
+      // next tile's first stage waits for anyway; all of it overlaps the
+      // compute wavefronts' epilogue
+      const Tile tn = read_tile(cur ^ 1);
+      if (tn.valid) {
+        ls = setup(cur ^ 1, tn);
+        issue(ls, 0);
+        if (NST > 1) issue(ls, 1);
+      }
+      if (iw == 0) {
+        int idx = -1;
+        if (lane == 0 && tn.valid) idx = take_tile();
+        const Tile tp = resolve(__builtin_amdgcn_readfirstlane(__shfl(idx, 0, 64)));
+        if (lane == 0) write_pend(tp);
+      }
+      if constexpr (KIND == KIND_GATE_UP) __syncthreads();  // row maxima
+      __syncthreads();  // epilogue done
+      cur ^= 1;
+    }
+    return;
+  }
+
+  int cur = 0;
+  for (;;) {
+    const Tile tc = read_tile(cur);
+    if (!tc.valid) break;
+    const int row0 = tc.row0, rows = tc.rows;
+    const int64_t n0 = KIND == KIND_GATE_UP ? (int64_t)tc.nt * HALF : (int64_t)tc.nt * BN;
+
+    const FragLane fl = frag_lane(r16, g4);
+    auto tile_col = [&](int nj) -> int {
+      if constexpr (KIND == KIND_GATE_UP)
+        return nj < TN / 2 ? wn * HW + nj * 16 : HALF + wn * HW + (nj - TN / 2) * 16;
+      else
+        return (wn * TN + nj) * 16;
+    };
+    const int wave_blk = KIND == KIND_GATE_UP ? 0 : (wn * TN * 16) / 128;
+
+    v4f acc[TM][TN];
+#pragma unroll
+    for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+      for (int nj = 0; nj < TN; ++nj) acc[mi][nj] = vzero;
+
+    for (int st = 0; st < NST; ++st) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      const uint8_t* stg = smem + (st % NSTAGE) * STAGE;
+      const uint8_t* tB = stg + A_BYTES;
+      const float* tS = reinterpret_cast<const float*>(smem + RING + (st % NSTAGE) * SA_SLOT);
+      if ((wm * TM) * 16 < rows) {
+        v8i af[TM];
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi) af[mi] = read_frag(stg + (wm * TM + mi) * 16 * 128, fl);
+        constexpr int HALVES = KIND == KIND_GATE_UP ? 2 : 1;
+        float sa1[TM];
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi) sa1[mi] = tS[(wm * TM + mi) * 64 + r16];
+        float sbh[HALVES];
+#pragma unroll
+        for (int hv = 0; hv < HALVES; ++hv) sbh[hv] = sSb[cur][KIND == KIND_GATE_UP ? hv : wave_blk][st];
+        v8i bf[2];
+        bf[0] = read_frag(tB + tile_col(0) * 128, fl);
+#pragma unroll
+        for (int hv = 0; hv < HALVES; ++hv) {
+          float ss[TM];
+#pragma unroll
+          for (int mi = 0; mi < TM; ++mi) ss[mi] = sa1[mi] * sbh[hv];
+#pragma unroll
+          for (int nh = 0; nh < TN / HALVES; ++nh) {
+            const int nj = hv * (TN / HALVES) + nh;
+            if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + tile_col(nj + 1) * 128, fl);
+            v4f pr[TM];
+#pragma unroll
+            for (int mi = 0; mi < TM; ++mi)
+              pr[mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[nj & 1], af[mi], vzero, 0, 0,
+                                                                        0, 0, 0, 0);
+#pragma unroll
+            for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[mi][nj][r] = fmaf(pr[mi][r], ss[mi], acc[mi][nj][r]);
+          }
+        }
+      }
+    }
+    __syncthreads();  // the ring is free; the next tile's tables are in LDS
+
+    if constexpr (KIND == KIND_DOWN) {
+      {
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi) {
+          const int row = (wm * TM + mi) * 16 + r16;
+          if (row < rows) {
+            const int64_t drow = __float_as_int(sRow[cur][row]);
+#pragma unroll
+            for (int nj = 0; nj < TN; ++nj) {
+              const int64_t col = n0 + tile_col(nj) + 4 * g4;
+              if (col < N) {
+                const v4f v = acc[mi][nj];
+                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(args.c) + drow * N + col) =
+                    make_uint2(pk2_bf16_exact(v[0], v[1]), pk2_bf16_exact(v[2], v[3]));
+              }
+            }
+          }
+        }
+      }
+    } else {
+      // SwiGLU + 1x128 requant from registers (see gemm_fp8_kernel)
+      // h is bf16-exact: kept as packed pairs (16 registers, not 32) across
+      // the barrier that publishes the row maxima
+      const float lim = args.swiglu_limit;
+      uint32_t h2[TM][4];
+      auto swiglu = [&](auto clamp_c) {
+        constexpr bool CLAMP = decltype(clamp_c)::value;
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi) {
+          const int row = (wm * TM + mi) * 16 + r16;
+          const float w = sRow[cur][row];
+          float am = 0.0f;
+#pragma unroll
+          for (int j = 0; j < TN / 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float gt = bf16_round(acc[mi][j][r]);
+              float up = bf16_round(acc[mi][j + TN / 2][r]);
+              if constexpr (CLAMP) {
+                up = clampf_(up, -lim, lim);
+                gt = gt > lim ? lim : gt;
+              }
+              const float ex = __builtin_amdgcn_exp2f(gt * -1.4426950408889634f);
+              const float silu = gt * __builtin_amdgcn_rcpf(1.0f + ex);
+              const uint32_t hb = bf16_bits_exact(w * (silu * up));
+              const int q = 4 * j + r;
+              if (q & 1)
+                h2[mi][q >> 1] |= hb << 16;
+              else
+                h2[mi][q >> 1] = hb;
+              am = __builtin_elementwise_maximum(am, fabsf(bits_f32(hb << 16)));
+            }
+          am = __builtin_elementwise_maximum(am, __shfl_xor(am, 16, 64));
+          am = __builtin_elementwise_maximum(am, __shfl_xor(am, 32, 64));
+          if (g4 == 0) sAmax[wn][row] = am;
+        }
+      };
+      if (lim > 0.0f) {
+        swiglu(std::true_type{});
+      } else {
+        swiglu(std::false_type{});
+      }
+      __syncthreads();
+      const int64_t NB = N / 128;
+      auto requant = [&](auto mode_c) {
+        constexpr int MODE = decltype(mode_c)::value;
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi) {
+          const int row = (wm * TM + mi) * 16 + r16;
+          if (row < rows) {
+            float am = sAmax[0][row];
+#pragma unroll
+            for (int q = 1; q < WN; ++q) am = __builtin_elementwise_maximum(am, sAmax[q][row]);
+            const float sf = group_scale(MODE, am);
+            float hf[8];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              hf[2 * q] = bits_f32(h2[mi][q] << 16);
+              hf[2 * q + 1] = bits_f32(h2[mi][q] & 0xFFFF0000u);
+            }
+            const uint2 qv = quant8_e4m3(MODE, hf, sf);
+            const int64_t p = row0 + row;
+            uint8_t* dst = args.hq + p * N + n0 + wn * HW + 4 * g4;
+            *reinterpret_cast<uint32_t*>(dst) = qv.x;
+            *reinterpret_cast<uint32_t*>(dst + 16) = qv.y;
+            if (wn == 0 && g4 == 0) args.hs[p * NB + n0 / 128] = sf;
+          }
+        }
+      };
+      switch (args.scale_mode) {
+        case SCALE_TORCH_FP32: requant(std::integral_constant<int, SCALE_TORCH_FP32>{}); break;
+        case SCALE_TORCH_UE8M0: requant(std::integral_constant<int, SCALE_TORCH_UE8M0>{}); break;
+        case SCALE_TILELANG_FP32: requant(std::integral_constant<int, SCALE_TILELANG_FP32>{}); break;
+        default: requant(std::integral_constant<int, SCALE_TILELANG_UE8M0>{}); break;
+      }
+    }
+    __syncthreads();  // epilogue done (sAmax, the table buffer cur free)
+    cur ^= 1;
+  }
+}
+
+template <int KIND>
+int launch_pipe(GemmArgs& a, hipStream_t stream) {
+  using namespace pipe;
+  a.n_tiles = (int)ceil_div(a.N, KIND == KIND_GATE_UP ? HALF : BN);
+  const int64_t P = a.E > 0 ? a.T * a.k : 0;
+  const int64_t mt_bound = P / BM + (P < a.E ? P : a.E) + (a.has_shared ? ceil_div(a.T, BM) : 0);
+  const int64_t tiles = mt_bound * a.n_tiles;
+  if (tiles == 0) return SGL_OK;
+  constexpr int kLds = SMEM + 4 * (kMaxGroups + 1) + BM * 4 + 2 * BM * 4 + 2 * 2 * kMaxKBp * 4 +
+                       (KIND == KIND_GATE_UP ? WN * BM * 4 : 4) + 2 * 5 * 4 + 2 * 12 * 4 + 5 * 4;
+  static_assert(kLds <= 160 * 1024, "pipelined tile exceeds the LDS of a CU");
+  int64_t wgs = (int64_t)device_cu_count();
+  wgs = (wgs + 7) / 8 * 8;
+  const int64_t need = (tiles + 7) / 8 * 8;
+  if (need < wgs) wgs = need;
+  a.m_tiles = (int)mt_bound;
+  gemm_pipe_kernel<KIND><<<(unsigned)wgs, NT, 0, stream>>>(a);
+  return check_launch("gemm_pipe");
+}
+
 template <int KIND, int BM, int BN, int WM, int WN, int NSTAGE, int WF = WF_FP8, bool SAHW = false,
           int LW = 0>
 int launch_cfg(GemmArgs& a, hipStream_t stream) {
@@ -950,6 +1561,9 @@ int launch_cfg(GemmArgs& a, hipStream_t stream) {
 // enough to keep every CU streaming where the 128 x 256 tiles leave most idle.
 #ifndef SGL_LW
 #define SGL_LW 4
+#endif
+#ifndef SGL_PIPE
+#define SGL_PIPE 1
 #endif
 #ifndef SGL_LWN
 #define SGL_LWN 4
@@ -1186,6 +1800,9 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
                      : launch_fp4<false>(kind, a, rows_hint, stream);
   }
   const bool big = rows_hint >= 64;
+  // the pipelined prefill kernel: K in [512, 8192] (at least four stages; the
+  // tile's weight scales fit its LDS table) and fp32 weight scales
+  const bool pipe_ok = SGL_PIPE && a.K >= 512 && a.K <= 128 * pipe::kMaxKBp && !a.sb_e8m0;
   switch (kind) {
     case KIND_DENSE:
       if (a.M <= kSkinnyMaxM) {
@@ -1207,9 +1824,11 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       if (a.M <= 2048) return launch_cfg<KIND_DENSE, 128, 128, 2, 4, 3>(a, stream);
       return launch_cfg<KIND_DENSE, 128, 256, 2, 4, 3>(a, stream);
     case KIND_GATE_UP:
+      if (big && pipe_ok) return launch_pipe<KIND_GATE_UP>(a, stream);
       return big ? launch_cfg<KIND_GATE_UP, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)
                  : launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 4>(a, stream);
     default:
+      if (big && pipe_ok) return launch_pipe<KIND_DOWN>(a, stream);
       return big ? launch_cfg<KIND_DOWN, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)
                  : launch_cfg<KIND_DOWN, 32, 256, 1, 4, 4>(a, stream);
   }
