@@ -8,7 +8,8 @@ route -> 1x128 act quant -> permute -> grouped gate/up (+SiLU*mul*w, requant)
 -> grouped down -> ordered combine.  Inputs and weights are resident in HBM
 before the timed region.  Also measured (reported under "extra"): the decode
 configs (T = 64/256/512, Zipf(1.1) expert load), the dense FP8 GEMM
-(M = 16..4096, N = 4096, K = 7168), the FP8 x MXFP4 variants, the router gate,
+(M = 16..4096, N = 4096, K = 7168), the FP8 x MXFP4 variants, the power-of-two
+(e8m0) weight-scale format with both scales applied in the MFMA, the router gate,
 the FP8 KV pack (65536 rows, 656-byte layout) + sparse-MLA gather-dequant
 (128 queries x 2048 rows), and the sparse attention straight off the packed
 FP8 pages (64 heads; 128 queries x 2048 rows, and a 32-sequence decode batch
@@ -60,9 +61,10 @@ def parse():
 # ------------------------------------------------------------------ weights
 
 
-def make_weights(torch, M, dev, seed=4):
+def make_weights(torch, M, dev, seed=4, ue8m0=False):
     """256 routed + 1 shared FP8 experts: N(0, 0.02) fp32 drawn on the GPU from a
-    seeded generator, quantized 128x128 by the library's weight-quant kernel."""
+    seeded generator, quantized 128x128 by the library's weight-quant kernel
+    (``ue8m0``: power-of-two scales, the e8m0 form of deepseek_infer/model.py:138-142)."""
     from sglang_lite_amd import kernel as K
 
     g = torch.Generator(device=dev)
@@ -74,10 +76,10 @@ def make_weights(torch, M, dev, seed=4):
     s2 = torch.empty(n, H // 128, I // 128, dtype=torch.float32, device=dev)
     for e in range(n):
         for j in range(2):
-            q, s = K.per_block_cast_to_fp8(torch.randn(I, H, generator=g, device=dev) * 0.02, False)
+            q, s = K.per_block_cast_to_fp8(torch.randn(I, H, generator=g, device=dev) * 0.02, ue8m0)
             w13[e, j].copy_(q)
             s13[e, j].copy_(s)
-        q, s = K.per_block_cast_to_fp8(torch.randn(H, I, generator=g, device=dev) * 0.02, False)
+        q, s = K.per_block_cast_to_fp8(torch.randn(H, I, generator=g, device=dev) * 0.02, ue8m0)
         w2[e].copy_(q)
         s2[e].copy_(s)
     experts = [(w13[e, 0], w13[e, 1], w2[e], s13[e, 0], s13[e, 1], s2[e]) for e in range(E)]
@@ -220,6 +222,45 @@ class Prefill:
             for i, n in enumerate(names):
                 tot[n] += ev[i].elapsed_time(ev[i + 1])
         return {n: v / iters for n, v in tot.items()}
+
+
+def prefill_entry(torch, M, K, table, dev, args, mode):
+    """The prefill layer (T = 8192) with ``table``: whole-step time and the
+    staged gate/up and down rates."""
+    T = 8192
+    rows = T * K_TOP + T
+    pre = Prefill(torch, M, K, table, T, dev, seed=4, mode=mode)
+    ms = time_steps(torch, pre.step, args.steps, args.warmup)
+    st = pre.staged(max(3, min(args.steps, 10)))
+    gu = rows * 4.0 * H * I / (st["gate_up"] / 1e3) / 1e12
+    dn = rows * 2.0 * H * I / (st["down"] / 1e3) / 1e12
+    return {"tokens": T, "ms": round(ms, 4), "tokens_per_s": round(T / ms * 1e3, 1),
+            "layer_tflops": round(moe_flops(rows) / (ms / 1e3) / 1e12, 2),
+            "mfma_frac": round(moe_flops(rows) / (ms / 1e3) / 1e12 / PEAK_FP8_TFLOPS, 4),
+            "gate_up_tflops": round(gu, 1), "down_tflops": round(dn, 1),
+            "stages_ms": {k_: round(v, 4) for k_, v in st.items()}}
+
+
+def pow2_extra(torch, M, K, dev, args):
+    """The reference's live FP8 scale format: power-of-two (e8m0) 128x128
+    weight scales (deepseek_infer/model.py:138-142) with ue8m0 activation
+    scales (mode 3), both applied inside the MFMA with no fp32 promotion: the
+    prefill layer with FP8 routed experts, and with FP4 routed experts beside
+    the FP8 shared expert in that format (model.py:623-626)."""
+    from sglang_lite_amd import _lib
+
+    log("generating power-of-two-scaled FP8 expert weights on the device")
+    table2, (w13, s13, w2, s2) = make_weights(torch, M, dev, seed=4, ue8m0=True)
+    assert table2.fmt & _lib.EXPERT_POW2_SCALES
+    out = {"fp8_prefill_mode3": prefill_entry(torch, M, K, table2, dev, args, 3)}
+    log(f"pow2 fp8 prefill mode 3: {out['fp8_prefill_mode3']['ms']:.3f} ms")
+    shared = (w13[E, 0], w13[E, 1], w2[E], s13[E, 0], s13[E, 1], s2[E])
+    del table2
+    table4 = make_fp4_weights(torch, M, dev, shared)
+    assert table4.fmt & _lib.EXPERT_POW2_SCALES
+    out["fp4_prefill_mode3"] = prefill_entry(torch, M, K, table4, dev, args, 3)
+    log(f"pow2 fp4 prefill mode 3: {out['fp4_prefill_mode3']['ms']:.3f} ms")
+    return out
 
 
 def fp4_extra(torch, M, K, weights, dev, args, flush):
@@ -623,6 +664,7 @@ def main():
         log(f"sparse attn packed decode b32: {msd * 1e3:.1f} us eager, {gsd * 1e3:.1f} us graph")
         del pages_d, qd, idd
         extra["fp4"] = fp4_extra(torch, M, K, weights, dev, args, flush)
+        extra["pow2_scales"] = pow2_extra(torch, M, K, dev, args)
         result["extra"] = extra
 
     if not args.no_cpu_baseline:

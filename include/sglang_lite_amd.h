@@ -85,6 +85,15 @@ enum sgl_kv_layout { SGL_KV_LAYOUT_A = 0, SGL_KV_LAYOUT_B = 1 };
  *       expert_dtype "fp4", model.py:623-624)
  * The shared expert is always SGL_EXPERT_FP8_BLOCK128 (model.py:626). */
 enum sgl_expert_format { SGL_EXPERT_FP8_BLOCK128 = 0, SGL_EXPERT_FP4_E2M1 = 1 };
+/* Flag OR'ed into expert_format: every FP8 block scale of the layer (the FP8
+ * routed experts' and the shared expert's) is a power of two, as the
+ * float8_e8m0fnu scales of deepseek_infer/model.py:138-142 are once decoded by
+ * sgl_e8m0_to_f32 (the cast engine/v4_deep_gemm.py:136-141 makes before its
+ * GEMMs).  Their mantissa bits are then ignored.  With a power-of-two
+ * scale_mode (*_UE8M0) both scales of each FP8 product are applied as e8m0
+ * exponents inside the MFMA, which accumulates across K blocks in place (no
+ * fp32 promotion per 128-deep block). */
+#define SGL_EXPERT_POW2_SCALES 2
 
 /* Per-expert weight pointers of one MoE layer, stored in DEVICE memory as an
  * array of E routed experts followed by the shared expert; weights and

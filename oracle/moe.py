@@ -232,12 +232,14 @@ def moe_forward_full_loop(x_bf16, ids, weights, experts, shared, swiglu_limit=0.
     return Q.bf16_round(y)
 
 
-def make_expert(rng: np.random.Generator, H: int, I: int, std: float = 0.02) -> Dict[str, np.ndarray]:
-    """Synthetic FP8 expert: N(0, std) weights quantized 128x128 (utils/math.py:50-60)."""
+def make_expert(rng: np.random.Generator, H: int, I: int, std: float = 0.02,
+                ue8m0: bool = False) -> Dict[str, np.ndarray]:
+    """Synthetic FP8 expert: N(0, std) weights quantized 128x128 (utils/math.py:50-60;
+    ``ue8m0``: scales rounded up to powers of two, the e8m0 form model.py:138-142 stores)."""
     out = {}
     for name, shape in (("1", (I, H)), ("3", (I, H)), ("2", (H, I))):
         w = (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
-        q, s = Q.per_block_cast_to_fp8(w)
+        q, s = Q.per_block_cast_to_fp8(w, use_ue8m0=ue8m0)
         out["w" + name] = q
         out["s" + name] = s
     return out

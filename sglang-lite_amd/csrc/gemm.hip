@@ -958,9 +958,13 @@ constexpr int SAI = NWC / LW;                // row-scale DMAs per loader per st
 constexpr int LPS = CPW + SAI;               // DMA instructions per loader per stage
 constexpr int kMaxKBp = 64;                  // K <= 8192: the tile's weight scales in LDS
 static_assert(SA_ROWS == 16 && CPW == 12 && QA == 4, "layout");
+static_assert(WM * WN == NWC && WM * TM * 16 == BM && WN * TN * 16 == BN, "compute wavefront grid");
 }  // namespace pipe
 
-template <int KIND>
+// POW2: every row scale and weight scale is a power of two; both go into the
+// MFMA as e8m0 exponents (the fp32 exponent field) and the accumulators are
+// its C operand, so no fp32 promotion runs.
+template <int KIND, bool POW2>
 __global__ __launch_bounds__(pipe::NT) void gemm_pipe_kernel(const GemmArgs args) {
   using namespace pipe;
   static_assert(KIND == KIND_GATE_UP || KIND == KIND_DOWN, "grouped GEMMs only");
@@ -1360,18 +1364,48 @@ __global__ __launch_bounds__(pipe::NT) void gemm_pipe_kernel(const GemmArgs args
       const uint8_t* tB = stg + A_BYTES;
       const float* tS = reinterpret_cast<const float*>(smem + RING + (st % NSTAGE) * SA_SLOT);
       if ((wm * TM) * 16 < rows) {
+        // LDS reads in the order the MFMAs consume them (A0, B0 and the
+        // scales, then A1..A3): the reads complete in order, so the first
+        // MFMA waits for two fragments, not for the whole stage's burst of
+        // all eight wavefronts
         v8i af[TM];
-#pragma unroll
-        for (int mi = 0; mi < TM; ++mi) af[mi] = read_frag(stg + (wm * TM + mi) * 16 * 128, fl);
+        v8i bf[2];
         constexpr int HALVES = KIND == KIND_GATE_UP ? 2 : 1;
         float sa1[TM];
+        float sbh[HALVES];
+        af[0] = read_frag(stg + (wm * TM) * 16 * 128, fl);
+        bf[0] = read_frag(tB + tile_col(0) * 128, fl);
 #pragma unroll
         for (int mi = 0; mi < TM; ++mi) sa1[mi] = tS[(wm * TM + mi) * 64 + r16];
-        float sbh[HALVES];
 #pragma unroll
         for (int hv = 0; hv < HALVES; ++hv) sbh[hv] = sSb[cur][KIND == KIND_GATE_UP ? hv : wave_blk][st];
-        v8i bf[2];
-        bf[0] = read_frag(tB + tile_col(0) * 128, fl);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int mi = 1; mi < TM; ++mi) af[mi] = read_frag(stg + (wm * TM + mi) * 16 * 128, fl);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (POW2) {
+          // operand A = the weight fragment (one scale per 16-column
+          // fragment: the 128 x 128 block), operand B = the activation rows
+          // (lane r16's row scale); the scale of lane (g4, r16) covers its
+          // 32-deep K quarter, the same for all four quarters here
+          int sae[TM], sbe[HALVES];
+#pragma unroll
+          for (int mi = 0; mi < TM; ++mi) sae[mi] = (int)(__float_as_uint(sa1[mi]) >> 23);
+#pragma unroll
+          for (int hv = 0; hv < HALVES; ++hv) sbe[hv] = (int)(__float_as_uint(sbh[hv]) >> 23);
+#pragma unroll
+          for (int hv = 0; hv < HALVES; ++hv)
+#pragma unroll
+            for (int nh = 0; nh < TN / HALVES; ++nh) {
+              const int nj = hv * (TN / HALVES) + nh;
+              if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + tile_col(nj + 1) * 128, fl);
+#pragma unroll
+              for (int mi = 0; mi < TM; ++mi)
+                acc[mi][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                    bf[nj & 1], af[mi], acc[mi][nj], 0, 0, 0, sbe[hv], 0, sae[mi]);
+            }
+          continue;
+        }
 #pragma unroll
         for (int hv = 0; hv < HALVES; ++hv) {
           float ss[TM];
@@ -1497,7 +1531,7 @@ __global__ __launch_bounds__(pipe::NT) void gemm_pipe_kernel(const GemmArgs args
   }
 }
 
-template <int KIND>
+template <int KIND, bool POW2>
 int launch_pipe(GemmArgs& a, hipStream_t stream) {
   using namespace pipe;
   a.n_tiles = (int)ceil_div(a.N, KIND == KIND_GATE_UP ? HALF : BN);
@@ -1513,7 +1547,7 @@ int launch_pipe(GemmArgs& a, hipStream_t stream) {
   const int64_t need = (tiles + 7) / 8 * 8;
   if (need < wgs) wgs = need;
   a.m_tiles = (int)mt_bound;
-  gemm_pipe_kernel<KIND><<<(unsigned)wgs, NT, 0, stream>>>(a);
+  gemm_pipe_kernel<KIND, POW2><<<(unsigned)wgs, NT, 0, stream>>>(a);
   return check_launch("gemm_pipe");
 }
 
@@ -1803,6 +1837,9 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
   // the pipelined prefill kernel: K in [512, 8192] (at least four stages; the
   // tile's weight scales fit its LDS table) and fp32 weight scales
   const bool pipe_ok = SGL_PIPE && a.K >= 512 && a.K <= 128 * pipe::kMaxKBp && !a.sb_e8m0;
+  // both scales powers of two: the pipelined kernel applies them in the MFMA
+  // (other kernels promote in fp32, exact for such scales too)
+  const bool pow2 = a.sa_pow2 && a.sb_pow2;
   switch (kind) {
     case KIND_DENSE:
       if (a.M <= kSkinnyMaxM) {
@@ -1824,11 +1861,13 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       if (a.M <= 2048) return launch_cfg<KIND_DENSE, 128, 128, 2, 4, 3>(a, stream);
       return launch_cfg<KIND_DENSE, 128, 256, 2, 4, 3>(a, stream);
     case KIND_GATE_UP:
-      if (big && pipe_ok) return launch_pipe<KIND_GATE_UP>(a, stream);
+      if (big && pipe_ok)
+        return pow2 ? launch_pipe<KIND_GATE_UP, true>(a, stream) : launch_pipe<KIND_GATE_UP, false>(a, stream);
       return big ? launch_cfg<KIND_GATE_UP, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)
                  : launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 4>(a, stream);
     default:
-      if (big && pipe_ok) return launch_pipe<KIND_DOWN>(a, stream);
+      if (big && pipe_ok)
+        return pow2 ? launch_pipe<KIND_DOWN, true>(a, stream) : launch_pipe<KIND_DOWN, false>(a, stream);
       return big ? launch_cfg<KIND_DOWN, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)
                  : launch_cfg<KIND_DOWN, 32, 256, 1, 4, 4>(a, stream);
   }

@@ -572,14 +572,20 @@ MoeWorkspace carve(void* base, int64_t T, int64_t H, int64_t I, int E, int k, in
   return w;
 }
 
+// The routed experts' format without the power-of-two flag.
+bool fp4_experts(int expert_format) {
+  return (expert_format & ~SGL_EXPERT_POW2_SCALES) == SGL_EXPERT_FP4_E2M1;
+}
+
 int check_moe_shapes(const char* what, int64_t T, int64_t H, int64_t I, int E, int k,
                      int expert_format) {
   SGL_REQUIRE(T >= 0 && H > 0 && I > 0, "%s: bad shape T=%lld H=%lld I=%lld", what, (long long)T,
               (long long)H, (long long)I);
   SGL_REQUIRE(H % 128 == 0 && I % 128 == 0, "%s: H and I must be multiples of 128", what);
-  SGL_REQUIRE(expert_format == SGL_EXPERT_FP8_BLOCK128 || expert_format == SGL_EXPERT_FP4_E2M1,
+  SGL_REQUIRE((expert_format & ~SGL_EXPERT_POW2_SCALES) == SGL_EXPERT_FP8_BLOCK128 ||
+                  (expert_format & ~SGL_EXPERT_POW2_SCALES) == SGL_EXPERT_FP4_E2M1,
               "%s: bad expert_format %d", what, expert_format);
-  SGL_REQUIRE(expert_format != SGL_EXPERT_FP4_E2M1 || (H % 256 == 0 && I % 256 == 0),
+  SGL_REQUIRE(!fp4_experts(expert_format) || (H % 256 == 0 && I % 256 == 0),
               "%s: FP4 experts need H and I multiples of 256", what);
   SGL_REQUIRE(E >= 1 && E <= kMaxPermE, "%s: E=%d not in [1, %d]", what, E, kMaxPermE);
   SGL_REQUIRE(k >= 1 && k <= 16 && k <= E, "%s: k=%d not in [1, min(16, E)]", what, k);
@@ -643,7 +649,8 @@ int run_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I
   SGL_REQUIRE(xq && xs && offsets && sorted_slot && experts && hq && hs,
               "moe_gate_up: null pointer");
   SGL_REQUIRE(aligned(xq, 16) && aligned(hq, 8), "moe_gate_up: xq/hq misaligned");
-  const bool split = expert_format == SGL_EXPERT_FP4_E2M1;
+  const bool split = fp4_experts(expert_format);
+  const int pow2w = (expert_format & SGL_EXPERT_POW2_SCALES) ? 1 : 0;
   GemmArgs g = {};
   g.a = (const uint8_t*)xq;
   g.sa = xs;
@@ -664,6 +671,7 @@ int run_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I
   g.scale_mode = scale_mode;
   g.wfmt = split ? WF_FP4 : WF_FP8;
   g.sa_pow2 = pow2_scale_mode(scale_mode);
+  g.sb_pow2 = split ? 0 : pow2w;
   g.tile_ctr = tile_ctr;
   if ((rc = launch_gemm(KIND_GATE_UP, g, T * k / E, stream)) || !split || !has_shared) return rc;
   GemmArgs sh = g;  // the shared expert: one group whose rows start at offsets[E]
@@ -672,7 +680,7 @@ int run_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I
   sh.experts = experts + E;
   sh.has_shared = 1;
   sh.wfmt = WF_FP8;
-  sh.sa_pow2 = 0;
+  sh.sb_pow2 = pow2w;
   sh.tile_ctr = tile_ctr ? tile_ctr + 8 : nullptr;
   return launch_gemm(KIND_GATE_UP, sh, T, stream);
 }
@@ -686,7 +694,8 @@ int run_down(const void* hq, const float* hs, int64_t T, int64_t H, int64_t I, i
   if (T == 0) return SGL_OK;
   SGL_REQUIRE(hq && hs && offsets && sorted_slot && experts && out, "moe_down: null pointer");
   SGL_REQUIRE(aligned(hq, 16), "moe_down: hq misaligned");
-  const bool split = expert_format == SGL_EXPERT_FP4_E2M1;
+  const bool split = fp4_experts(expert_format);
+  const int pow2w = (expert_format & SGL_EXPERT_POW2_SCALES) ? 1 : 0;
   GemmArgs g = {};
   g.a = (const uint8_t*)hq;
   g.sa = hs;
@@ -703,6 +712,7 @@ int run_down(const void* hq, const float* hs, int64_t T, int64_t H, int64_t I, i
   g.c = out;
   g.wfmt = split ? WF_FP4 : WF_FP8;
   g.sa_pow2 = pow2_scale_mode(scale_mode);
+  g.sb_pow2 = split ? 0 : pow2w;
   g.tile_ctr = tile_ctr;
   if ((rc = launch_gemm(KIND_DOWN, g, T * k / E, stream)) || !split || !has_shared) return rc;
   GemmArgs sh = g;
@@ -711,7 +721,7 @@ int run_down(const void* hq, const float* hs, int64_t T, int64_t H, int64_t I, i
   sh.experts = experts + E;
   sh.has_shared = 1;
   sh.wfmt = WF_FP8;
-  sh.sa_pow2 = 0;
+  sh.sb_pow2 = pow2w;
   sh.tile_ctr = tile_ctr ? tile_ctr + 8 : nullptr;
   return launch_gemm(KIND_DOWN, sh, T, stream);
 }

@@ -28,6 +28,8 @@ struct GemmArgs {
   int sb_e8m0;
   int wfmt;           // WeightFmt of B (moe: of every expert in the launch)
   int sa_pow2;        // activation scales are powers of two: applied inside the MFMA
+  int sb_pow2;        // fp8 weight scales (fp32) are powers of two: with sa_pow2, both
+                      // scales go into the MFMA and no fp32 promotion runs
   const sgl_expert_ptrs* experts;  // moe: device array [E (+1)]
   const int32_t* offsets;          // moe: [E + 1]
   const int32_t* sorted_slot;      // moe: [T * k]

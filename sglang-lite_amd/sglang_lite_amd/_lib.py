@@ -38,6 +38,7 @@ SCORE_SOFTMAX, SCORE_SIGMOID, SCORE_SQRTSOFTPLUS = 0, 1, 2
 KV_LAYOUT_A, KV_LAYOUT_B = 0, 1
 # sgl_expert_format
 EXPERT_FP8_BLOCK128, EXPERT_FP4_E2M1 = 0, 1
+EXPERT_POW2_SCALES = 2  # flag: every FP8 block scale is a power of two
 # sgl_attn_kv_format
 ATTN_KV_BF16, ATTN_KV_A, ATTN_KV_A_PAGED = 0, 1, 2
 

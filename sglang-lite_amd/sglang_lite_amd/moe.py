@@ -38,6 +38,15 @@ def _f32_scale(s: torch.Tensor) -> torch.Tensor:
     raise TypeError(f"weight scale must be float32 or float8_e8m0fnu, got {s.dtype}")
 
 
+def _pow2_scale(s: torch.Tensor) -> bool:
+    """Whether a weight scale holds only powers of two: e8m0 by type, fp32
+    when every value is a positive normal float with no mantissa bits."""
+    if s.dtype == E8M0:
+        return True
+    bits = s.contiguous().view(torch.int32)
+    return bool(((bits & 0x807FFFFF) == 0).logical_and_(bits != 0).all().item())
+
+
 @dataclass
 class ExpertTable:
     """Device array of ``sgl_expert_ptrs`` (E routed experts, then the shared one).
@@ -52,7 +61,7 @@ class ExpertTable:
     I: int
     has_shared: bool
     keep: List[torch.Tensor] = field(default_factory=list)
-    fmt: int = _lib.EXPERT_FP8_BLOCK128  # sgl_expert_format of the routed experts
+    fmt: int = _lib.EXPERT_FP8_BLOCK128  # sgl_expert_format of the routed experts (+ flags)
 
     @staticmethod
     def build(experts: Sequence[Tuple[torch.Tensor, ...]],
@@ -61,7 +70,12 @@ class ExpertTable:
         e4m3 [I, H], w2 e4m3 [H, I], 128x128 scales fp32 or e8m0) or FP4 (w1/w3
         packed e2m1 [I, H/2], w2 [H, I/2] as float4_e2m1fn_x2 / int8 / uint8,
         e8m0 scales per 32 inputs: [I, H/32], [H, I/32]); every routed expert in
-        one format.  The shared expert is FP8 (deepseek_infer/model.py:626)."""
+        one format.  The shared expert is FP8 (deepseek_infer/model.py:626).
+
+        When every FP8 scale is a power of two (e8m0, as model.py:138-142
+        stores them, or fp32 without mantissa bits) the table carries
+        ``EXPERT_POW2_SCALES``: with a power-of-two activation ``scale_mode``
+        the FP8 GEMMs then apply both scales inside the MFMA."""
         rows = list(experts) + ([shared] if shared is not None else [])
         if not rows:
             raise ValueError("ExpertTable needs at least one expert")
@@ -72,6 +86,7 @@ class ExpertTable:
         dev = w1.device
         keep: List[torch.Tensor] = []
         vals = []
+        pow2 = True
         for i, r in enumerate(rows):
             w1, w3, w2, s1, s3, s2 = r
             if fp4 and i < len(experts):
@@ -90,6 +105,7 @@ class ExpertTable:
                     if w.dtype != FP8 or tuple(w.shape) != shape or not w.is_contiguous():
                         raise ValueError(f"expert weight must be contiguous e4m3 {shape}, got "
                                          f"{w.dtype} {tuple(w.shape)}")
+                pow2 = pow2 and all(_pow2_scale(s) for s in (s1, s3, s2))
                 fs = [_f32_scale(s) for s in (s1, s3, s2)]
             _lib.require_device(*ws, *fs, what="ExpertTable")
             keep += [*ws, *fs]
@@ -97,6 +113,8 @@ class ExpertTable:
                          fs[0].data_ptr(), fs[1].data_ptr(), fs[2].data_ptr()])
         ptrs = torch.tensor(vals, dtype=torch.int64).to(dev)
         fmt = _lib.EXPERT_FP4_E2M1 if fp4 else _lib.EXPERT_FP8_BLOCK128
+        if pow2:
+            fmt |= _lib.EXPERT_POW2_SCALES
         return ExpertTable(ptrs, len(experts), H, I, shared is not None, keep, fmt)
 
 

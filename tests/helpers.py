@@ -148,7 +148,8 @@ def assert_layer_close(out: np.ndarray, ref: np.ndarray, what: str = "layer",
 
 
 def assert_requant_close(q_dev: np.ndarray, s_dev: np.ndarray, q_ref: np.ndarray,
-                         s_ref: np.ndarray, what: str = "requant", max_diff: float = 0.01) -> dict:
+                         s_ref: np.ndarray, what: str = "requant", max_diff: float = 0.01,
+                         pow2: bool = False) -> dict:
     """1x128 FP8-requantized rows of a GEMM epilogue (the gate/up kernel's h)
     against the oracle's requantization of its own h.  The two h agree to
     rounding (bf16 ulps), so their quantizations agree except where a value
@@ -164,7 +165,12 @@ def assert_requant_close(q_dev: np.ndarray, s_dev: np.ndarray, q_ref: np.ndarray
     forms each 128-deep fp8 partial to about 1e-5 of the sum of its
     |products| (not an IEEE fp32 sum), so a gate or up output near zero --
     and the h value made from it, far below its group's amax -- carries an
-    absolute error that no relative bound covers."""
+    absolute error that no relative bound covers.
+
+    ``pow2``: power-of-two scales (the *_UE8M0 modes), where an amax ulp at a
+    binade edge moves a group's scale by a factor of two: every scale ratio
+    is then 1/2, 1 or 2, and at most ``max_diff`` of the groups move (the
+    per-value bound above holds either way)."""
     from oracle.quant import dequant_rows
 
     q_dev, q_ref = np.asarray(q_dev, np.uint8), np.asarray(q_ref, np.uint8)
@@ -172,7 +178,13 @@ def assert_requant_close(q_dev: np.ndarray, s_dev: np.ndarray, q_ref: np.ndarray
     dd = dequant_rows(q_dev, s_dev).astype(np.float64)
     dr = dequant_rows(q_ref, s_ref).astype(np.float64)
     frac = float(np.mean(q_dev != q_ref))
-    srel = float(np.max(np.abs(s_dev.astype(np.float64) / s_ref - 1.0))) if s_ref.size else 0.0
+    ratio = s_dev.astype(np.float64) / s_ref if s_ref.size else np.ones(1)
+    if pow2:
+        assert np.all(np.isin(ratio, (0.5, 1.0, 2.0))), f"{what}: scale ratios {np.unique(ratio)[:8]}"
+        moved = float(np.mean(ratio != 1.0))
+        assert moved <= max_diff, f"{what}: {moved:.4f} of the groups changed binade"
+        ratio = np.ones(1)
+    srel = float(np.max(np.abs(ratio - 1.0)))
     smax = np.repeat(np.maximum(s_dev, s_ref).astype(np.float64), 128, axis=-1)
     mag = np.maximum(np.abs(dd), np.abs(dr))
     step = (2.0 ** -3 + 2.0 ** -6) * (1 + 2.0 ** -4) * mag + (2.0 ** -9 + 448.0 * 2.0 ** -14) * smax

@@ -202,3 +202,25 @@ def test_moe_rejects_tokens_beyond_32_bit_operand_offsets(name, T):
     small[args.index(T)] = 8192
     with pytest.raises(ValueError, match="null pointer"):
         L.call(name, *small)
+
+
+def test_expert_format_pow2_flag():
+    """Power-of-two weight scales are recognised (e8m0 by type, fp32 with no
+    mantissa bits, positive); the C boundary accepts SGL_EXPERT_POW2_SCALES
+    OR'ed into either weight format and refuses any other bit before a launch."""
+    from sglang_lite_amd import _lib as L
+    from sglang_lite_amd import moe as M
+
+    e8 = torch.tensor([1, 120, 127, 254], dtype=torch.uint8).view(torch.float8_e8m0fnu)
+    assert M._pow2_scale(e8)
+    assert M._pow2_scale(torch.tensor([0.25, 1.0, 2.0 ** -20, 2.0 ** 60]))
+    assert not M._pow2_scale(torch.tensor([0.25, 0.3]))           # a mantissa bit
+    assert not M._pow2_scale(torch.tensor([1.0, 0.0]))            # zero
+    assert not M._pow2_scale(torch.tensor([-1.0, 1.0]))           # sign
+    assert not M._pow2_scale(torch.tensor([2.0 ** -130]))         # subnormal
+    assert L.EXPERT_POW2_SCALES == 2
+    H, I, E, k = 4096, 2048, 256, 8
+    for fmt, ok in ((0, True), (1, True), (2, True), (3, True), (4, False), (6, False)):
+        args = (None, None, 64, H, I, E, k, None, None, None, None, 1, fmt, 0.0, 0, None, None, None)
+        with pytest.raises(ValueError, match="null pointer" if ok else "bad expert_format"):
+            L.call("sgl_moe_gate_up", *args)

@@ -169,6 +169,11 @@ def test_moe_stages_tiny(gpu):
     (100, 512, 256, 16, 4, True, 10.0, False),
     (64, 1024, 512, 32, 8, True, 0.0, True),
     (7, 512, 384, 5, 3, False, 0.5, False),
+    # >= 64 rows per expert on average: the pipelined 128 x 256 kernels, with
+    # five (gate/up, K = 640) and four (down, K = 512) K stages, a partial
+    # last column tile in down (N = 640) whose second scale block is clamped,
+    # and skewed routing (empty and one-row experts beside full tiles)
+    (300, 640, 512, 12, 3, True, 7.0, True),
 ])
 def test_moe_forward_matches_oracle(gpu, T, H, I, E, k, shared, lim, zipf):
     from sglang_lite_amd import moe as M
