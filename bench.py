@@ -365,19 +365,37 @@ def read_traffic(kernel_tag):
 # ------------------------------------------------------------- cpu baseline
 
 
-def cpu_baseline(torch, table, weights, pre, budget_s=20.0):
-    """The oracle (numpy restatement of the reference MoE path) timed on the
-    host on a bounded sample of the same prefill workload and extrapolated to
-    the whole layer by row count."""
+def cpu_model() -> str:
+    """The host CPU's model string (/proc/cpuinfo), else what platform reports."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline(torch, weights, pre, workers=None):
+    """The oracle (numpy restatement of the reference MoE layer) timed on the
+    host over the WHOLE prefill layer of the GPU workload: softmax top-8 routing
+    of the same logits (oracle.moe.route_topk), then oracle.moe.moe_forward --
+    per activated expert the row gather, 1x128 act quant, dequantize-to-fp32
+    gate/up GEMMs (float64 BLAS), SwiGLU x routing weight, 1x128 requant and
+    down GEMM, for all 256 routed experts and the shared one, and the
+    ascending-expert fp32 combine.  Experts run on ``workers`` threads with one
+    BLAS thread each; the weights are on the host before the clock starts
+    (as they are in HBM for the GPU)."""
     import numpy as np
+    from threadpoolctl import threadpool_info, threadpool_limits
 
     from oracle import moe as OM
 
     w13, s13, w2, s2 = weights
     torch.cuda.synchronize()
-    w, ids = pre.M.route_topk(pre.logits, K_TOP)
-    ids_np = ids.cpu().numpy()
-    w_np = w.cpu().numpy()
+    workers = workers or max(1, min(os.cpu_count() or 1, 16))
+    logits = pre.logits.cpu().numpy()
     x_np = pre.x.float().cpu().numpy()
 
     def expert_np(e):
@@ -387,32 +405,34 @@ def cpu_baseline(torch, table, weights, pre, budget_s=20.0):
                 "s1": s13[e, 0].cpu().numpy(), "s3": s13[e, 1].cpu().numpy(),
                 "s2": s2[e].cpu().numpy()}
 
-    rows_done, t_spent, experts_done = 0, 0.0, 0
-    for e in range(E):
-        tok, top = np.nonzero(ids_np == e)
-        if tok.size == 0:
-            continue
-        ex = expert_np(e)
+    experts = [expert_np(e) for e in range(E)]
+    shared = expert_np(E)
+    blas = [f"{i['internal_api']}" for i in threadpool_info() if i.get("user_api") == "blas"]
+    with threadpool_limits(limits=1, user_api="blas"):
         t0 = time.perf_counter()
-        OM.expert_forward(x_np[tok], ex, w_np[tok, top][:, None])
-        t_spent += time.perf_counter() - t0
-        rows_done += tok.size
-        experts_done += 1
-        if t_spent > budget_s:
-            break
-    # time per routed row -> whole layer (routed rows T*k plus T shared rows)
-    total_rows = pre.T * K_TOP + pre.T
-    t_layer = t_spent / rows_done * total_rows
+        w, ids = OM.route_topk(logits, K_TOP)
+        y = OM.moe_forward(x_np, ids, w, experts, shared, workers=workers)
+        dt = time.perf_counter() - t0
+    # cross-check: the host layer against the device layer of the same inputs
+    y_dev = pre.y.float().cpu().numpy()
+    rel = float(np.linalg.norm(y_dev - y) / max(np.linalg.norm(y), 1e-30))
+    del experts, shared
     return {
-        "value": round(pre.T / t_layer, 3),
+        "value": round(pre.T / dt, 3),
         "unit": "tokens/s",
-        "cores": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)),
+        "cores": workers,
         "kind": "port",
-        "sample": (f"oracle expert_forward (numpy, dequantize-to-fp32, float64 BLAS) on the rows of "
-                   f"{experts_done} routed experts ({rows_done} rows) of the T=8192 prefill, "
-                   f"{t_spent:.1f} s, extrapolated by row count to {total_rows} rows"),
-        "host_cpu": platform.processor() or platform.machine(),
+        "sample": (f"the whole T={pre.T} prefill layer, measured once ({dt:.1f} s): oracle "
+                   f"route_topk + moe_forward over all {E} routed experts and the shared one "
+                   f"(gather, act quant, dequantize-to-fp32 GEMMs in float64 BLAS, SwiGLU, "
+                   f"requant, ascending fp32 combine), experts on {workers} threads x 1 BLAS "
+                   f"thread"),
+        "seconds": round(dt, 2),
+        "host_cpu": cpu_model(),
         "os_cpu_count": os.cpu_count(),
+        "blas": blas,
+        "blas_threads_per_worker": 1,
+        "rel_l2_vs_gpu_layer": round(rel, 6),
     }
 
 
@@ -469,6 +489,16 @@ def main():
         4 * T * H + 4 * T * E
     tok_s = T / (ms / 1e3)
     traffic = read_traffic("moe_gate_up_prefill")
+    # algorithmic bytes of one gate/up launch: every expert's w1 | w3 and
+    # scales, the quantized activations and scales, h and its scales written
+    n_mt = H // 128
+    gu_bytes = (E + 1) * (2 * I * H + 2 * (I // 128) * n_mt * 4) + T * H + T * n_mt * 4 + \
+        rows * I + rows * (I // 128) * 4
+    t_mfma = gu_flops / (PEAK_FP8_TFLOPS * 1e12)
+    t_hbm = gu_bytes / (PEAK_HBM_GBS * 1e9)
+    bound = "hbm" if t_hbm >= t_mfma else "mfma"
+    gu_tflops = gu_flops / (gu_ms / 1e3) / 1e12
+    gu_gbs = gu_bytes / (gu_ms / 1e3) / 1e9
     result = {
         "metric": METRIC,
         "value": round(tok_s, 1),
@@ -492,12 +522,21 @@ def main():
                   "hbm_gbs_algorithmic": round(layer_bytes / (ms / 1e3) / 1e9, 1),
                   "hbm_frac": round(layer_bytes / (ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
                   "stages_ms": {k_: round(v, 4) for k_, v in stages.items()}},
-        "roofline": {"kernel": "gemm_fp8_kernel<gate_up> (grouped gate/up + SwiGLU + requant)",
-                     "bound": "mfma", "achieved": round(gu_flops / (gu_ms / 1e3) / 1e12, 2),
-                     "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(gu_flops / (gu_ms / 1e3) / 1e12 / PEAK_FP8_TFLOPS, 4),
+        # the bound is whichever roof the launch's algorithmic work reaches
+        # later: bytes / 8 TB/s or FLOPs / 5 PF/s
+        "roofline": {"kernel": "gemm_pipe_kernel<gate_up> (grouped gate/up + SwiGLU + requant)",
+                     "bound": bound,
+                     "achieved": round(gu_gbs, 1) if bound == "hbm" else round(gu_tflops, 2),
+                     "peak": PEAK_HBM_GBS if bound == "hbm" else PEAK_FP8_TFLOPS,
+                     "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
+                     "frac": round(gu_gbs / PEAK_HBM_GBS if bound == "hbm" else
+                                   gu_tflops / PEAK_FP8_TFLOPS, 4),
                      "traffic": traffic,
-                     "flops_per_launch": gu_flops, "avg_launch_ms": round(gu_ms, 4)},
+                     "algorithmic_bytes_per_launch": gu_bytes, "flops_per_launch": gu_flops,
+                     "hbm_frac": round(gu_gbs / PEAK_HBM_GBS, 4),
+                     "mfma_frac": round(gu_tflops / PEAK_FP8_TFLOPS, 4),
+                     "roof_us": {"hbm": round(t_hbm * 1e6, 1), "mfma": round(t_mfma * 1e6, 1)},
+                     "avg_launch_ms": round(gu_ms, 4)},
     }
     log(f"prefill {ms:.3f} ms/step -> {tok_s:.0f} tok/s; stages {stages}")
 
@@ -668,8 +707,9 @@ def main():
         result["extra"] = extra
 
     if not args.no_cpu_baseline:
-        log("cpu baseline (oracle) on a bounded sample")
-        result["cpu_baseline"] = cpu_baseline(torch, table, weights, pre)
+        log("cpu baseline: the oracle over the whole prefill layer")
+        pre.step()
+        result["cpu_baseline"] = cpu_baseline(torch, weights, pre)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

@@ -190,24 +190,43 @@ def expert_forward(x_bf16: np.ndarray, w: Dict[str, np.ndarray], weights: Option
 def moe_forward(x_bf16: np.ndarray, ids: np.ndarray, weights: np.ndarray,
                 experts: Sequence[Dict[str, np.ndarray]], shared: Optional[Dict[str, np.ndarray]],
                 swiglu_limit: float = 0.0, mode: int = 0,
-                expert_outputs: Optional[dict] = None) -> np.ndarray:
+                expert_outputs: Optional[dict] = None, workers: int = 1) -> np.ndarray:
     """engine/v4_moe_fast.py:79-106 _moe_forward_activated_only (one rank):
     y = 0 (fp32); for each activated expert ascending: y[tok] += expert(x[tok], w);
-    y += shared(x); return bf16(y)."""
+    y += shared(x); return bf16(y).
+
+    ``workers`` > 1 computes the experts' outputs on that many threads (numpy
+    and BLAS release the GIL) and still sums them in ascending expert order:
+    the result is the same bytes as with one worker."""
     x = np.asarray(x_bf16, dtype=np.float32)
     ids = np.asarray(ids)
-    T = x.shape[0]
     y = np.zeros_like(x, dtype=np.float32)
-    for e in np.unique(ids).tolist():
+
+    def run(e):
         tok, top = np.nonzero(ids == e)
-        if tok.size == 0:
-            continue
-        out = expert_forward(x[tok], experts[e], weights[tok, top][:, None], swiglu_limit, mode)
+        return tok, top, expert_forward(x[tok], experts[e], weights[tok, top][:, None],
+                                        swiglu_limit, mode)
+
+    def run_shared():
+        return expert_forward(x, shared, None, swiglu_limit, mode)
+
+    active = [e for e in np.unique(ids).tolist()]
+    if workers > 1:
+        from concurrent.futures import ThreadPoolExecutor
+
+        with ThreadPoolExecutor(workers) as pool:
+            jobs = [pool.submit(run, e) for e in active]
+            sh_job = pool.submit(run_shared) if shared is not None else None
+            results = [j.result() for j in jobs]
+            sh = sh_job.result() if sh_job is not None else None
+    else:
+        results = [run(e) for e in active]
+        sh = run_shared() if shared is not None else None
+    for e, (tok, top, out) in zip(active, results):
         if expert_outputs is not None:
             expert_outputs[e] = (tok, top, out)
         y[tok] = (y[tok] + out).astype(np.float32)
-    if shared is not None:
-        sh = expert_forward(x, shared, None, swiglu_limit, mode)
+    if sh is not None:
         if expert_outputs is not None:
             expert_outputs["shared"] = sh
         y = (y + sh).astype(np.float32)

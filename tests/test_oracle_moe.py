@@ -45,3 +45,30 @@ def test_router_logits_exact_for_bf16_operands():
     ref = (x.double() @ W.double().T).float().numpy()
     got = OM.router_logits(x.float().numpy(), W.float().numpy())
     np.testing.assert_array_equal(got, ref)
+
+
+def test_moe_forward_workers_same_bytes():
+    """The threaded oracle layer (experts on worker threads, combined in
+    ascending expert order) is the serial layer, byte for byte; the per-expert
+    outputs it reports are the serial ones too."""
+    from oracle import quant as Q
+
+    rng = np.random.default_rng(12)
+    T, H, I, E, k = 48, 256, 128, 8, 2
+    x = Q.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    w, ids = OM.route_topk(rng.standard_normal((T, E)).astype(np.float32), k)
+    experts = [OM.make_expert(rng, H, I) for _ in range(E)]
+    sh = OM.make_expert(rng, H, I)
+    o1, o4 = {}, {}
+    y1 = OM.moe_forward(x, ids, w, experts, sh, swiglu_limit=5.0, expert_outputs=o1)
+    y4 = OM.moe_forward(x, ids, w, experts, sh, swiglu_limit=5.0, expert_outputs=o4, workers=4)
+    np.testing.assert_array_equal(y1.view(np.uint32), y4.view(np.uint32))
+    assert o1.keys() == o4.keys()
+    for key in o1:
+        a, b = o1[key], o4[key]
+        a, b = (a[2], b[2]) if isinstance(a, tuple) else (a, b)
+        np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+    # and the serial layer is the reference's full loop (model.py:629-644)
+    np.testing.assert_array_equal(
+        y1.view(np.uint32),
+        OM.moe_forward_full_loop(x, ids, w, experts, sh, swiglu_limit=5.0).view(np.uint32))
