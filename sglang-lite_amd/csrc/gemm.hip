@@ -35,7 +35,11 @@
 // MoE tiles: an M tile never straddles two experts.  The workgroup first
 // prefix-sums ceil(count_e / BM) over the expert offsets into LDS, so the
 // grid is sized without reading routing data on the host.
+#include <algorithm>
+#include <map>
+#include <mutex>
 #include <type_traits>
+#include <utility>
 
 #include "sgl_gemm.h"
 #include "sgl_numeric.h"
@@ -1602,6 +1606,9 @@ int launch_cfg(GemmArgs& a, hipStream_t stream) {
 #ifndef SGL_LWN
 #define SGL_LWN 4
 #endif
+#ifndef SGL_SPLITK
+#define SGL_SPLITK 1
+#endif
 #ifndef SGL_SKINNY_MAX_M
 #define SGL_SKINNY_MAX_M 64
 #endif
@@ -1792,6 +1799,262 @@ int launch_skinny(GemmArgs& a, hipStream_t stream) {
   return check_launch(WF == WF_FP4 ? "gemm_fp4_skinny" : "gemm_fp8_skinny");
 }
 
+// ---- small-M dense GEMM, split over K
+//
+// 32 < M <= 64 rows against an N x K weight: the work is streaming B (N K
+// bytes from HBM).  A workgroup that spans all of K also reads all of A (M K
+// bytes, twice its B strip at M = 64) from L2, so the grid is N/128 column
+// tiles x S K ranges of KS blocks, about one workgroup per CU, each reading
+// only its M x KS x 128 slice of A.  The slice and the scales go to LDS by LDS
+// DMA (the ring kernels' fragment layout; the DMAs are invisible to the
+// compiler, which would otherwise drain every load in flight before its first
+// LDS write); each of the 8 wavefronts owns 16 columns and loads their B
+// fragments from HBM straight into registers, all KS blocks in flight, then
+// runs the K blocks in order as they land (per block: the MFMA partial
+// promoted with sa sb in fp32, as everywhere).  The fp32 tile partials go to
+// a workspace and splitk_reduce_kernel, over the whole GPU, sums them in split
+// order: C is the same bytes on every run.  (N = 4096, K = 7168 at M = 64: 12
+// us + 4 us, against 22.6 us for the unsplit kernel.  At M <= 32 the unsplit
+// kernel reads less A and already runs near a read-only stream of B, and the
+// reduction does not pay: a last-workgroup sum costs three dependent trips to
+// device-coherent memory, about 3 us.)
+namespace splitk {
+constexpr int NW = 8, NT = 64 * NW, BN = 16 * NW, KSMAX = 8, SMAX = 16, TM = 4, ROWS = 16 * TM;
+}  // namespace splitk
+
+struct SplitKArgs {
+  float* part;  // [S][M][N] fp32 partials
+  int S;
+};
+
+template <int KS>
+__global__ __launch_bounds__(splitk::NT) void gemm_splitk_kernel(const GemmArgs args, const SplitKArgs sk) {
+  using namespace splitk;
+  static_assert(KS >= 1 && KS <= KSMAX, "split-K tile");
+  __shared__ __align__(16) uint8_t sA[KS * TM * 2048];
+  // row scales [ROWS][KS] and the weight scales of the split's blocks (fp32,
+  // or e8m0 bytes at offset idx0 % 4 of the dwords that hold them)
+  __shared__ __align__(16) float sSa[ROWS * KS + 64];
+  __shared__ __align__(16) uint32_t sSk[64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g4 = lane >> 4, r16 = lane & 15;
+  const int64_t M = args.M, N = args.N, K = args.K;
+  const int KB = (int)(K / 128);
+  // workgroup -> (column tile t, split s): consecutive workgroups (which the
+  // dispatcher spreads over the XCDs) take consecutive tiles of one split
+  const int n_tiles = (int)(N / BN);
+  const int s = blockIdx.x / n_tiles;
+  const int t = blockIdx.x - s * n_tiles;
+  const int kb0 = s * KS;
+  const int nkb = min(KS, KB - kb0);  // >= 1: S = ceil(KB / KS)
+  const int64_t n0 = (int64_t)t * BN;
+  const int rr = lane >> 3, pc = lane & 7;
+
+  // the A slice: one DMA moves rows 8h..8h+7 of K block kl (lane: row
+  // 8h + lane/8, 16-byte position lane%8, which holds the row's chunk
+  // position ^ swz(row)); rows past M re-read row M-1 (their outputs are
+  // dropped), blocks past the split's last re-read its first (their products
+  // are skipped)
+  const uint32_t a_lds = __builtin_amdgcn_readfirstlane(lds_u32(sA));
+  constexpr int NDA = (ROWS / 8) * KS;
+#pragma unroll
+  for (int j = 0; j < (NDA + NW - 1) / NW; ++j) {
+    const int q = wave + NW * j;
+    if (q < NDA) {
+      const int kl = q / (ROWS / 8), h8 = q - kl * (ROWS / 8);
+      const int r = h8 * 8 + rr;
+      const int64_t row = r < M ? r : M - 1;
+      const int kb = kb0 + (kl < nkb ? kl : 0);
+      dma16v((uint64_t)(uintptr_t)args.a + (uint64_t)(row * K + (int64_t)kb * 128) +
+                 (uint32_t)((pc ^ swz(r & 15)) << 4),
+             __builtin_amdgcn_readfirstlane(a_lds + (uint32_t)((kl * TM + (h8 >> 1)) * 2048 + (h8 & 1) * 1024)));
+    }
+  }
+  // sa rows x KS, one dword per lane (row M-1 past M, the split's first
+  // block past its last), and the weight scales of blocks kb0 .. kb0 + nkb - 1
+  // of column block n0 / 128 -- fp32, or the dwords holding those e8m0 bytes
+  // (never past the last one's dword, so no read leaves the scales' last page)
+  constexpr int NDS = (ROWS * KS + 63) / 64;
+  const uint32_t sa_lds = __builtin_amdgcn_readfirstlane(lds_u32(sSa));
+#pragma unroll
+  for (int j = 0; j < (NDS + NW - 1) / NW; ++j) {
+    const int q = wave + NW * j;
+    if (q < NDS) {
+      const int i = q * 64 + lane;
+      const int r = i / KS, kl = i - r * KS;
+      const int64_t row = r < M ? r : M - 1;
+      const int kb = kb0 + (kl < nkb ? kl : 0);
+      dma4v((uint64_t)(uintptr_t)args.sa + (uint64_t)(row * KB + kb) * 4u,
+            __builtin_amdgcn_readfirstlane(sa_lds + (uint32_t)(q * 256)));
+    }
+  }
+  const int64_t idx0 = (n0 / 128) * KB + kb0;
+  if (wave == NW - 1) {
+    const uint32_t sk_lds = __builtin_amdgcn_readfirstlane(lds_u32(sSk));
+    if (args.sb_e8m0) {
+      const int nd = (int)((idx0 & 3) + nkb + 3) / 4;
+      if (lane < nd)
+        dma4v((uint64_t)(uintptr_t)args.sb + (uint64_t)((idx0 & ~(int64_t)3) + 4 * lane), sk_lds);
+    } else if (lane < nkb) {
+      dma4v((uint64_t)(uintptr_t)args.sb + (uint64_t)(idx0 + lane) * 4u, sk_lds);
+    }
+  }
+  // B: column n0 + 16 wave + r16, K bytes [32 g4, +32) of each block
+  const uint8_t* brow = args.b + (n0 + 16 * wave + r16) * K + 32 * g4;
+  v8i bf[KS];
+#pragma unroll
+  for (int kl = 0; kl < KS; ++kl) bf[kl] = load_frag_global(brow + (int64_t)(kb0 + (kl < nkb ? kl : 0)) * 128);
+  // the DMAs were issued before the 2 KS B loads: wait for those alone
+  // (vmcnt counts in issue order)
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * KS) : "memory");
+  __syncthreads();
+
+  const FragLane fl = frag_lane(r16, g4);
+  const v4f vzero = {0.0f, 0.0f, 0.0f, 0.0f};
+  v4f acc[TM];
+#pragma unroll
+  for (int mi = 0; mi < TM; ++mi) acc[mi] = vzero;
+#pragma unroll
+  for (int kl = 0; kl < KS; ++kl) {
+    if (kl < nkb) {
+      const float skb = args.sb_e8m0 ? e8m0_value(reinterpret_cast<const uint8_t*>(sSk)[(idx0 & 3) + kl])
+                                     : __uint_as_float(sSk[kl]);
+      v8i af[TM];
+#pragma unroll
+      for (int mi = 0; mi < TM; ++mi) af[mi] = read_frag(sA + (kl * TM + mi) * 2048, fl);
+#pragma unroll
+      for (int mi = 0; mi < TM; ++mi) {
+        const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[mi], bf[kl], vzero, 0, 0, 0, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[mi][r] = fmaf(p[r], sSa[(16 * mi + 4 * g4 + r) * KS + kl] * skb, acc[mi][r]);
+      }
+    }
+  }
+
+  // lane (g4, r16) holds rows 16 mi + 4 g4 + r of column col
+  const int64_t col = n0 + 16 * wave + r16;
+  float* part = sk.part + (int64_t)s * M * N;
+#pragma unroll
+  for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * mi + 4 * g4 + r;
+      if (row < M) part[row * N + col] = acc[mi][r];
+    }
+}
+
+// C = sum over the S split partials in split order (4 consecutive elements
+// of [M, N] per thread; M N % 4 == 0 as N % 128 == 0)
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int S,
+                                                            int64_t MN, void* c, int out_f32) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= MN) return;
+  float4 v[splitk::SMAX];
+#pragma unroll
+  for (int s = 0; s < splitk::SMAX; ++s)
+    if (s < S) v[s] = *reinterpret_cast<const float4*>(part + (int64_t)s * MN + i);
+  float4 a = v[0];
+#pragma unroll
+  for (int s = 1; s < splitk::SMAX; ++s)
+    if (s < S) {
+      a.x += v[s].x;
+      a.y += v[s].y;
+      a.z += v[s].z;
+      a.w += v[s].w;
+    }
+  if (out_f32) {
+    *reinterpret_cast<float4*>(reinterpret_cast<float*>(c) + i) = a;
+  } else {
+    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(c) + i) =
+        make_uint2((uint32_t)bf16_bits_exact(a.x) | ((uint32_t)bf16_bits_exact(a.y) << 16),
+                   (uint32_t)bf16_bits_exact(a.z) | ((uint32_t)bf16_bits_exact(a.w) << 16));
+  }
+}
+
+// Workspace of the split-K kernel (the partials) per (device, stream),
+// allocated outside stream capture: a call on a capturing stream that has
+// none yet takes the unsplit kernels.  Calls on one stream are ordered, so
+// they share it.
+struct SplitKWs {
+  uint8_t* base = nullptr;
+  size_t bytes = 0;
+};
+std::mutex g_splitk_mu;
+std::map<std::pair<int, hipStream_t>, SplitKWs> g_splitk_ws;
+
+uint8_t* splitk_workspace(hipStream_t stream, size_t need) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(g_splitk_mu);
+  SplitKWs& w = g_splitk_ws[{dev, stream}];
+  if (w.bytes >= need) return w.base;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (w.base) {  // grow: the stream's earlier calls finish before the old block goes
+    if (hipStreamSynchronize(stream) != hipSuccess || hipFree(w.base) != hipSuccess) {
+      (void)hipGetLastError();
+      w = SplitKWs{};
+      return nullptr;
+    }
+    w = SplitKWs{};
+  }
+  void* p = nullptr;
+  if (hipMalloc(&p, need) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  w.base = static_cast<uint8_t*>(p);
+  w.bytes = need;
+  return w.base;
+}
+
+template <int KS>
+int launch_splitk_ks(GemmArgs& a, int S, float* part, hipStream_t stream) {
+  const SplitKArgs sk{part, S};
+  const int n_tiles = (int)(a.N / splitk::BN);
+  gemm_splitk_kernel<KS><<<(unsigned)(n_tiles * S), splitk::NT, 0, stream>>>(a, sk);
+  int rc = check_launch("gemm_fp8_splitk");
+  if (rc) return rc;
+  const int64_t MN = a.M * a.N;
+  splitk_reduce_kernel<<<(unsigned)ceil_div(MN / 4, (int64_t)256), 256, 0, stream>>>(part, S, MN, a.c,
+                                                                                    a.out_f32);
+  return check_launch("gemm_fp8_splitk_reduce");
+}
+
+// The split-K path for a dense FP8 GEMM when it applies (32 < M <= 64, N %
+// 128 == 0, at least two splits that fit, a workspace at hand); returns -1
+// when the caller should take the unsplit kernels.
+int try_splitk(GemmArgs& a, hipStream_t stream) {
+  using namespace splitk;
+  if (a.M <= 32 || a.M > ROWS || a.N % BN != 0 || a.wfmt != WF_FP8) return -1;
+  if (a.sb_e8m0 && !aligned(a.sb, 4)) return -1;  // e8m0 scales are read as whole dwords
+  const int KB = (int)(a.K / 128);
+  const int n_tiles = (int)(a.N / BN);
+  // about one workgroup per CU: S <= 16 splits of KS <= 8 blocks
+  const int s_target = n_tiles >= 256 ? 1 : 256 / n_tiles;
+  int KS = (int)ceil_div((int64_t)KB, (int64_t)s_target);
+  KS = (int)std::max<int64_t>(KS, ceil_div((int64_t)KB, (int64_t)SMAX));
+  if (KS > KSMAX) return -1;
+  const int S = (int)ceil_div((int64_t)KB, (int64_t)KS);
+  if (S < 2) return -1;
+  float* part = reinterpret_cast<float*>(splitk_workspace(stream, (size_t)S * (size_t)a.M * (size_t)a.N * 4));
+  if (!part) return -1;
+  switch (KS) {
+    case 1: return launch_splitk_ks<1>(a, S, part, stream);
+    case 2: return launch_splitk_ks<2>(a, S, part, stream);
+    case 3: return launch_splitk_ks<3>(a, S, part, stream);
+    case 4: return launch_splitk_ks<4>(a, S, part, stream);
+    case 5: return launch_splitk_ks<5>(a, S, part, stream);
+    case 6: return launch_splitk_ks<6>(a, S, part, stream);
+    case 7: return launch_splitk_ks<7>(a, S, part, stream);
+    default: return launch_splitk_ks<8>(a, S, part, stream);
+  }
+}
+
 }  // namespace
 
 // FP4 weights: a stage is 256 deep, so two stages fill what three fp8
@@ -1841,7 +2104,9 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
   // (other kernels promote in fp32, exact for such scales too)
   const bool pow2 = a.sa_pow2 && a.sb_pow2;
   switch (kind) {
-    case KIND_DENSE:
+    case KIND_DENSE: {
+      const int rc = SGL_SPLITK ? try_splitk(a, stream) : -1;
+      if (rc >= 0) return rc;
       if (a.M <= kSkinnyMaxM) {
         if (a.M <= 16) return launch_skinny<1>(a, stream);
         if (a.M <= 32) return launch_skinny<2>(a, stream);
@@ -1860,6 +2125,7 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       // in 52 us where 64 x 128 tiles take 64 us
       if (a.M <= 2048) return launch_cfg<KIND_DENSE, 128, 128, 2, 4, 3>(a, stream);
       return launch_cfg<KIND_DENSE, 128, 256, 2, 4, 3>(a, stream);
+    }
     case KIND_GATE_UP:
       if (big && pipe_ok)
         return pow2 ? launch_pipe<KIND_GATE_UP, true>(a, stream) : launch_pipe<KIND_GATE_UP, false>(a, stream);

@@ -101,3 +101,112 @@ def test_fp8_gemm_end_to_end_from_bf16(gpu):
     finally:
         torch.set_default_dtype(prev)
     assert_gemm_close(f32(c), ref, "linear")
+
+
+# The split-K kernel (32 < M <= 64, N % 128 == 0): N/128 column tiles x S
+# K ranges of KS <= 8 blocks, the partials summed in split order by a second
+# kernel.  Shapes beside it take the unsplit kernels.
+@pytest.mark.parametrize("M,N,K", [
+    (33, 1024, 1152),   # 8 tiles, KB = 9: S = 5, ragged last split; 31 rows past M
+    (48, 4096, 896),    # 32 tiles, one block per split
+    (64, 384, 2048),    # 3 tiles
+    (40, 4096, 7168),   # the dense config's N and K: 8 splits of 7 blocks
+    (64, 2048, 4096),
+    (32, 1024, 1152),   # M <= 32 and M > 64: the unsplit kernels
+    (65, 1024, 1152),
+])
+def test_fp8_gemm_splitk_matches_oracle(gpu, M, N, K):
+    from sglang_lite_amd import kernel as K_
+
+    print(f"splitk {M}x{N}x{K}", flush=True)
+    rng = np.random.default_rng(M + N + K)
+    aq, sa, bq, sb = _operands(rng, M, N, K)
+    ref = OM.fp8_gemm(aq, sa, bq, sb, out_bf16=False)
+    args = (to_dev_fp8(aq, gpu), to_dev_f32(sa, gpu), to_dev_fp8(bq, gpu), to_dev_f32(sb, gpu))
+    c32 = K_.fp8_gemm(*args)  # default dtype fp32: fp32 output
+    assert c32.dtype == torch.float32
+    np.testing.assert_allclose(f32(c32), OM.fp8_gemm_promoted(aq, sa, bq, sb), rtol=1e-4,
+                               atol=1e-4 * np.abs(ref).max())
+    prev = torch.get_default_dtype()
+    try:
+        torch.set_default_dtype(torch.bfloat16)
+        c = K_.fp8_gemm(*args)
+        c2 = K_.fp8_gemm(*args)
+    finally:
+        torch.set_default_dtype(prev)
+    assert_gemm_close(f32(c), ref, f"fp8_gemm split-K {M}x{N}x{K}")
+    # the partials are summed in split order: the same bytes on every call
+    np.testing.assert_array_equal(u8(c), u8(c2))
+
+
+def test_fp8_gemm_splitk_e8m0_weight_scales(gpu):
+    from sglang_lite_amd import kernel as K_
+
+    rng = np.random.default_rng(21)
+    M, N, K = 50, 2048, 7168
+    a = bf16_values(rng, (M, K))
+    aq, sa = Q.per_token_cast_to_fp8(a, True, 128)
+    bq, sb = Q.per_block_cast_to_fp8(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02),
+                                     True)
+    ref = OM.fp8_gemm(aq, sa, bq, sb, out_bf16=False)
+    sb_e = torch.from_numpy(Q.e8m0_byte(sb)).view(torch.float8_e8m0fnu).to(gpu)
+    c = K_.fp8_gemm(to_dev_fp8(aq, gpu), to_dev_f32(sa, gpu), to_dev_fp8(bq, gpu), sb_e)
+    assert_gemm_close(f32(c), ref, "fp8_gemm split-K e8m0")
+
+
+def test_fp8_gemm_splitk_concurrent_streams_and_graph(gpu):
+    """Each stream has its own split-K workspace, so GEMMs overlapping on two
+    streams stay exact; a captured GEMM replays the eager result each time
+    (nothing is memset inside the graph), with eager work on the same stream
+    between replays."""
+    from sglang_lite_amd import kernel as K_
+
+    rng = np.random.default_rng(22)
+    M, N, K = 48, 4096, 7168
+    ops = [_operands(rng, M, N, K) for _ in range(2)]
+    dev_ops = [(to_dev_fp8(aq, gpu), to_dev_f32(sa, gpu), to_dev_fp8(bq, gpu), to_dev_f32(sb, gpu))
+               for aq, sa, bq, sb in ops]
+    refs = [OM.fp8_gemm(*o, out_bf16=False) for o in ops]
+    eager = [K_.fp8_gemm(*d) for d in dev_ops]
+    torch.cuda.synchronize()
+    for e, r in zip(eager, refs):
+        assert_gemm_close(f32(e), r, "split-K eager")
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [torch.empty(M, N, dtype=torch.float32, device=gpu) for _ in range(2)]
+    for _ in range(3):
+        for st, d, o in zip(streams, dev_ops, outs):
+            st.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(st):
+                for _ in range(4):
+                    K_.fp8_gemm(*d, out=o)
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            np.testing.assert_array_equal(f32(o).view(np.uint32), f32(e).view(np.uint32))
+    # graph capture on a stream whose workspace exists (warmed up above)
+    g = torch.cuda.CUDAGraph()
+    gout = torch.empty(M, N, dtype=torch.float32, device=gpu)
+    cap = streams[0]
+    with torch.cuda.stream(cap):
+        K_.fp8_gemm(*dev_ops[0], out=gout)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=cap):
+        K_.fp8_gemm(*dev_ops[0], out=gout)
+    for i in range(4):
+        gout.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(f32(gout).view(np.uint32), f32(eager[0]).view(np.uint32))
+        with torch.cuda.stream(cap):
+            K_.fp8_gemm(*dev_ops[1], out=outs[1])  # eager split-K work between replays
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(f32(outs[1]).view(np.uint32), f32(eager[1]).view(np.uint32))
+    # a capture on a fresh stream (no workspace yet) takes the unsplit kernels
+    g2 = torch.cuda.CUDAGraph()
+    fresh = torch.cuda.Stream()
+    gout2 = torch.empty(M, N, dtype=torch.float32, device=gpu)
+    with torch.cuda.graph(g2, stream=fresh):
+        K_.fp8_gemm(*dev_ops[1], out=gout2)
+    for _ in range(2):
+        g2.replay()
+        torch.cuda.synchronize()
+        assert_gemm_close(f32(gout2), refs[1], "captured on a fresh stream")
