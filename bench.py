@@ -179,6 +179,36 @@ def graph_ms(torch, fn, iters=20, warmup=3):
     return a.elapsed_time(b) / iters
 
 
+def replay_ms(torch, calls, reps=8):
+    """Device time per call of ``calls`` run back to back, captured into one
+    HIP graph and replayed ``reps`` times between two events: a serving loop's
+    view of a short kernel, free of the ~12 us an event pair around a single
+    small launch measures even for an empty kernel.  ``calls`` rotate input
+    sets larger together than the 256 MB memory-side cache, so each call reads
+    its inputs from HBM."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for fn in calls:  # allocations and per-stream workspaces before capture
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for fn in calls:
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        g.replay()
+    b.record()
+    b.synchronize()
+    return a.elapsed_time(b) / (reps * len(calls))
+
+
 class Prefill:
     """The staged prefill pipeline with events around each stage."""
 
@@ -320,6 +350,8 @@ def fp4_extra(torch, M, K, weights, dev, args, flush):
     bq = torch.randint(0, 256, (4096, 3584), dtype=torch.uint8, device=dev, generator=gw)
     bs = torch.randint(118, 123, (4096, 224), dtype=torch.uint8, device=dev,
                        generator=gw).view(torch.float8_e8m0fnu)
+    # 20 copies of the weight (311 MB): each back-to-back call streams a cold B
+    wsets = [(bq.clone(), bs.clone()) for _ in range(20)]
     dense = []
     prev = torch.get_default_dtype()
     torch.set_default_dtype(torch.bfloat16)
@@ -332,7 +364,9 @@ def fp4_extra(torch, M, K, weights, dev, args, flush):
                 fn = lambda: K.fp4_gemm(aq, as_, bq, bs, out=c, a_scale_pow2=pow2)  # noqa: E731
                 for _ in range(2):
                     fn()
-                msg = event_avg_ms(torch, fn, 10, flush)
+                msg = replay_ms(torch, [lambda w=w, pow2=pow2: K.fp4_gemm(aq, as_, w[0], w[1], out=c,
+                                                                             a_scale_pow2=pow2)
+                                        for w in wsets])
                 fl = 2.0 * Md * 4096 * 7168
                 byt = Md * 7168 + 4 * Md * 56 + 4096 * 3584 + 4096 * 224 + 2 * Md * 4096
                 dense.append({"M": Md, "N": 4096, "K": 7168, "a_scale_pow2": pow2,
@@ -343,6 +377,7 @@ def fp4_extra(torch, M, K, weights, dev, args, flush):
                 log(f"fp4 dense M={Md} pow2={pow2}: {msg * 1e3:.1f} us")
     finally:
         torch.set_default_dtype(prev)
+    del wsets
     out["dense_gemm"] = dense
     return out
 
@@ -599,30 +634,35 @@ def main():
         gw = torch.Generator(device=dev).manual_seed(2)
         bq, bs = K.per_block_cast_to_fp8(torch.randn(4096, 7168, generator=gw, device=dev) * 0.02,
                                          False)
+        # 12 copies of the weight (353 MB): each back-to-back call streams a
+        # cold B, as the 72-odd linears of a decode step do
+        wsets = [(bq.clone(), bs.clone()) for _ in range(12)]
         dense = []
         prev = torch.get_default_dtype()
         torch.set_default_dtype(torch.bfloat16)
         try:
-            for Md in (16, 128, 1024, 4096):
+            for Md in (16, 64, 128, 1024, 4096):
                 a = torch.randn(Md, 7168, generator=gw, device=dev).to(torch.bfloat16)
                 aq, as_ = K.act_quant(a)
                 c = torch.empty(Md, 4096, dtype=torch.bfloat16, device=dev)
                 for _ in range(2):
                     K.fp8_gemm(aq, as_, bq, bs, out=c)
-                msg = event_avg_ms(torch, lambda: K.fp8_gemm(aq, as_, bq, bs, out=c), 10, flush)
+                msg = replay_ms(torch, [lambda w=w: K.fp8_gemm(aq, as_, w[0], w[1], out=c) for w in wsets])
+                mse = event_avg_ms(torch, lambda: K.fp8_gemm(aq, as_, bq, bs, out=c), 10, flush)
                 fl = 2.0 * Md * 4096 * 7168
                 byt = Md * 7168 + 4 * Md * 56 + 4096 * 7168 + 4 * 32 * 56 + 2 * Md * 4096
                 dense.append({"M": Md, "N": 4096, "K": 7168, "ms": round(msg, 5),
+                              "ms_single_call_events": round(mse, 5),
                               "tflops": round(fl / msg / 1e9, 2),
                               "mfma_frac": round(fl / msg / 1e9 / PEAK_FP8_TFLOPS, 4),
                               "gbs": round(byt / msg / 1e6, 1),
                               "hbm_frac": round(byt / msg / 1e6 / PEAK_HBM_GBS, 4)})
-                log(f"dense M={Md}: {msg * 1e3:.1f} us")
-                aqm = K.act_quant(a)
-                del aqm
-            # act_quant alone at the largest dense shape
-            a = torch.randn(4096, 7168, generator=gw, device=dev).to(torch.bfloat16)
-            msq = event_avg_ms(torch, lambda: K.act_quant(a), 10, flush)
+                log(f"dense M={Md}: {msg * 1e3:.1f} us back to back ({mse * 1e3:.1f} us single call)")
+            del wsets
+            # act_quant alone at the largest dense shape, 6 rotating inputs (352 MB)
+            xs6 = [torch.randn(4096, 7168, generator=gw, device=dev).to(torch.bfloat16) for _ in range(6)]
+            msq = replay_ms(torch, [lambda x=x: K.act_quant(x) for x in xs6])
+            del xs6
             qb = 3 * 4096 * 7168 + 4 * 4096 * 56
             extra["act_quant_4096x7168"] = {"ms": round(msq, 5), "gbs": round(qb / msq / 1e6, 1),
                                             "hbm_frac": round(qb / msq / 1e6 / PEAK_HBM_GBS, 4)}
@@ -633,22 +673,25 @@ def main():
         gk = torch.Generator().manual_seed(5)
         kv = torch.randn(65536, 576, generator=gk).to(torch.bfloat16).to(dev)
         packed = KVP.pack_kv_latent_rope(kv)
-        msp = event_avg_ms(torch, lambda: KVP.pack_kv_latent_rope(kv), 10, flush)
+        kvs = [kv] + [kv.clone() for _ in range(3)]  # 4 x (75 + 43) MB through the pack
+        msp = replay_ms(torch, [lambda x=x: KVP.pack_kv_latent_rope(x) for x in kvs])
+        del kvs
         pb = 65536 * (1152 + 656)
         idx = torch.stack([torch.randperm(65536, generator=gk)[:2048] for _ in range(128)]).to(
             torch.int32).to(dev)
         out = torch.empty(128, 2048, 576, dtype=torch.bfloat16, device=dev)
-        msg_ = event_avg_ms(torch, lambda: KVP.gather_dequant(packed, idx, layout="B", out=out),
-                            10, flush)
+        msg_ = replay_ms(torch, [lambda: KVP.gather_dequant(packed, idx, layout="B", out=out)] * 4)
         gb = 128 * 2048 * (656 + 1152)
         kva = torch.randn(65536, 512, generator=gk).to(torch.bfloat16).to(dev)
-        msa = event_avg_ms(torch, lambda: KVP.pack_dsv4_kv_paged(kva, 64), 10, flush)
+        kvas = [kva] + [kva.clone() for _ in range(3)]
+        msa = replay_ms(torch, [lambda x=x: KVP.pack_dsv4_kv_paged(x, 64) for x in kvas])
+        del kvas
         ab = 65536 * (1024 + 584)
         # gather-dequant of the same 128 x 2048 indices from layout A footer pages
         pages_ga = KVP.pack_dsv4_kv_paged(kva, 64)
         out_a = torch.empty(128, 2048, 512, dtype=torch.bfloat16, device=dev)
-        msga = event_avg_ms(torch, lambda: KVP.gather_dequant(pages_ga, idx, layout="A", page_size=64,
-                                                              out=out_a), 10, flush)
+        msga = replay_ms(torch, [lambda: KVP.gather_dequant(pages_ga, idx, layout="A", page_size=64,
+                                                             out=out_a)] * 4)
         gab = 128 * 2048 * (584 + 1024)
         extra["kv"] = {
             "pack_layout_b_65536": {"ms": round(msp, 5), "gbs": round(pb / msp / 1e6, 1),
