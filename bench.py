@@ -51,7 +51,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extra", action="store_true", help="headline prefill line only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--profile-kernels", nargs="?", const="fp8", choices=("fp8", "fp4"),
+    ap.add_argument("--profile-kernels", nargs="?", const="fp8", choices=("fp8", "fp4", "small"),
                     help="run only 3 prefill steps (FP8 experts, or FP4 routed experts in the "
                          "ue8m0 scale mode) plus a counter-calibration kernel, for rocprofv3 "
                          "runs; prints no JSON")
@@ -252,6 +252,76 @@ class Prefill:
             for i, n in enumerate(names):
                 tot[n] += ev[i].elapsed_time(ev[i + 1])
         return {n: v / iters for n, v in tot.items()}
+
+
+def hbm_ceiling(torch, dev):
+    """HBM rates a plain streaming kernel reaches on this GPU (sgl_hbm_stream:
+    16-byte accesses, four in flight per lane, 2048 x 512 threads), beside the
+    8 TB/s nominal the fractions are quoted against: a copy (read + write) and
+    a read of 2 GiB, and a read of 29.4 MB (the dense GEMM's weight) rotating
+    over 12 buffers, each graph-replayed back to back."""
+    from sglang_lite_amd import _lib
+
+    out = {}
+    sums = torch.empty(2048, dtype=torch.int32, device=dev)
+
+    def stream(src, dst):
+        _lib.call("sgl_hbm_stream", src.data_ptr(), dst.data_ptr() if dst is not None else None,
+                  src.numel(), sums.data_ptr(), _lib.stream_of(src))
+
+    a = torch.ones(1 << 31, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    ms = replay_ms(torch, [lambda: stream(a, b)] * 3, reps=4)
+    out["copy_2GiB_gbs"] = round(2 * a.numel() / ms / 1e6, 1)
+    ms = replay_ms(torch, [lambda: stream(a, None)] * 3, reps=4)
+    out["read_2GiB_gbs"] = round(a.numel() / ms / 1e6, 1)
+    del a, b
+    bufs = [torch.ones(4096 * 7168, dtype=torch.uint8, device=dev) for _ in range(12)]
+    ms = replay_ms(torch, [lambda x=x: stream(x, None) for x in bufs], reps=8)
+    out["read_29MB_gbs"] = round(4096 * 7168 / ms / 1e6, 1)
+    out["read_29MB_us"] = round(ms * 1e3, 2)
+    return out
+
+
+def profile_small(torch, M, K, table, dev):
+    """The short kernels for a profiler run (--profile-kernels small), three
+    launches each: the decode layers (T = 64 / 256 / 512, Zipf(1.1) load), the
+    dense GEMM at M = 16 / 64 / 128 (N = 4096, K = 7168) over 12 rotating
+    weight copies, act_quant 4096 x 7168, and the KV packs (65536 rows)."""
+    from sglang_lite_amd import dsv4_kv_pack as KVP
+
+    for Td, seed in ((64, 31), (256, 32), (512, 33)):
+        logits = zipf_logits(torch, Td, seed).to(dev)
+        xd = torch.randn(Td, H, generator=torch.Generator().manual_seed(seed)).to(torch.bfloat16).to(dev)
+        ws = M.MoEWorkspace()
+        for _ in range(3):
+            w, ids = M.route_topk(logits, K_TOP)
+            M.moe_forward(xd, ids, w, table, workspace=ws)
+    torch.cuda.synchronize()
+    gw = torch.Generator(device=dev).manual_seed(2)
+    bq, bs = K.per_block_cast_to_fp8(torch.randn(4096, 7168, generator=gw, device=dev) * 0.02, False)
+    wsets = [(bq.clone(), bs.clone()) for _ in range(12)]
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        for Md in (16, 64, 128):
+            aq, as_ = K.act_quant(torch.randn(Md, 7168, generator=gw, device=dev).to(torch.bfloat16))
+            c = torch.empty(Md, 4096, dtype=torch.bfloat16, device=dev)
+            for i in range(3 * len(wsets)):
+                K.fp8_gemm(aq, as_, wsets[i % 12][0], wsets[i % 12][1], out=c)
+        xs = [torch.randn(4096, 7168, generator=gw, device=dev).to(torch.bfloat16) for _ in range(3)]
+        for x in xs:
+            K.act_quant(x)
+    finally:
+        torch.set_default_dtype(prev)
+    gk = torch.Generator().manual_seed(5)
+    kvb = [torch.randn(65536, 576, generator=gk).to(torch.bfloat16).to(dev) for _ in range(3)]
+    kva = [torch.randn(65536, 512, generator=gk).to(torch.bfloat16).to(dev) for _ in range(3)]
+    for x in kvb:
+        KVP.pack_kv_latent_rope(x)
+    for x in kva:
+        KVP.pack_dsv4_kv_paged(x, 64)
+    torch.cuda.synchronize()
 
 
 def prefill_entry(torch, M, K, table, dev, args, mode):
@@ -502,8 +572,11 @@ def main():
             shared = (w13[E, 0], w13[E, 1], w2[E], s13[E, 0], s13[E, 1], s2[E])
             pre = Prefill(torch, M, K, make_fp4_weights(torch, M, dev, shared), T, dev, seed=4,
                           mode=3)
-        for _ in range(3):
-            pre.step()
+        if args.profile_kernels == "small":
+            profile_small(torch, M, K, table, dev)
+        else:
+            for _ in range(3):
+                pre.step()
         # counter calibration: e8m0_to_f32 over 64 MiB reads 64 MiB, writes 256 MiB
         src = torch.full((64 << 20,), 127, dtype=torch.uint8, device=dev).view(torch.float8_e8m0fnu)
         for _ in range(3):
@@ -745,6 +818,8 @@ def main():
             "hbm_frac": round(bd / gsd / 1e6 / PEAK_HBM_GBS, 4)}
         log(f"sparse attn packed decode b32: {msd * 1e3:.1f} us eager, {gsd * 1e3:.1f} us graph")
         del pages_d, qd, idd
+        extra["hbm_ceiling"] = hbm_ceiling(torch, dev)
+        log(f"hbm ceiling: {extra['hbm_ceiling']}")
         extra["fp4"] = fp4_extra(torch, M, K, weights, dev, args, flush)
         extra["pow2_scales"] = pow2_extra(torch, M, K, dev, args)
         result["extra"] = extra

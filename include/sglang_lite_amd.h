@@ -157,6 +157,13 @@ int sgl_e8m0_to_f32(const void* src, float* dst, int64_t n, sgl_stream_t stream)
  * All five must stay 0. */
 int sgl_check_conversions(unsigned long long* counts, sgl_stream_t stream);
 
+/* Measurement aid; no counterpart in the reference.  A plain HBM stream over
+ * `bytes` (a positive multiple of 32768) from src with 16-byte accesses: a
+ * copy into dst, or, with dst NULL, a read whose XOR per 1/2048 slice goes to
+ * sums[2048].  The rate it reaches is the achievable bandwidth the kernels'
+ * HBM fractions are read against (the 8 TB/s nominal is not reachable). */
+int sgl_hbm_stream(const void* src, void* dst, int64_t bytes, uint32_t* sums, sgl_stream_t stream);
+
 /* --------------------------------------------------------------- GEMMs */
 
 /* C[M, N] = sum_kb (A[:, kb] . B[:, kb]^T) * sa[m, kb] * sb[n/128, kb], fp32

@@ -33,11 +33,68 @@ int device_cu_count() {
   return cached[dev];
 }
 
+namespace {
+
+// A plain HBM stream: each of kStreamWgs workgroups moves one contiguous
+// slice with 16-byte accesses, four in flight per lane; a copy (dst) or a read
+// that leaves the XOR of its slice in sums[workgroup].
+constexpr int kStreamWgs = 2048, kStreamThreads = 512;
+
+__global__ __launch_bounds__(kStreamThreads) void hbm_stream_kernel(const uint4* __restrict__ src,
+                                                                   uint4* __restrict__ dst, int64_t n16,
+                                                                   uint32_t* __restrict__ sums) {
+  const int64_t per = n16 / kStreamWgs;
+  const uint4* p = src + (int64_t)blockIdx.x * per;
+  uint32_t acc = 0;
+  for (int64_t base = 0; base < per; base += 4 * kStreamThreads) {
+    uint4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t i = base + u * kStreamThreads + threadIdx.x;
+      v[u] = i < per ? p[i] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t i = base + u * kStreamThreads + threadIdx.x;
+      if (dst) {
+        if (i < per) dst[(int64_t)blockIdx.x * per + i] = v[u];
+      } else {
+        acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+      }
+    }
+  }
+  if (!dst) {
+    __shared__ uint32_t red[kStreamThreads / 64];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t a = 0;
+      for (int w = 0; w < kStreamThreads / 64; ++w) a ^= red[w];
+      sums[blockIdx.x] = a;
+    }
+  }
+}
+
+}  // namespace
+
 }  // namespace sgl
 
 extern "C" {
 
 int sgl_abi_version(void) { return SGL_ABI_VERSION; }
+
+int sgl_hbm_stream(const void* src, void* dst, int64_t bytes, uint32_t* sums, sgl_stream_t stream) {
+  SGL_REQUIRE(bytes > 0 && bytes % (16 * (int64_t)sgl::kStreamWgs) == 0,
+              "hbm_stream: bytes=%lld must be a positive multiple of %d", (long long)bytes,
+              16 * sgl::kStreamWgs);
+  SGL_REQUIRE(src && (dst || sums), "hbm_stream: null pointer");
+  SGL_REQUIRE(sgl::aligned(src, 16) && (!dst || sgl::aligned(dst, 16)), "hbm_stream: misaligned");
+  sgl::hbm_stream_kernel<<<sgl::kStreamWgs, sgl::kStreamThreads, 0, (hipStream_t)stream>>>(
+      (const uint4*)src, (uint4*)dst, bytes / 16, sums);
+  return sgl::check_launch("hbm_stream");
+}
 
 const char* sgl_last_error(void) { return sgl::g_last_error; }
 

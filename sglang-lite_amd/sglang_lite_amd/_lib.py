@@ -54,6 +54,7 @@ SIGNATURES = {
     "sgl_weight_quant_128x128": (c_int, [P, c_int, I64, I64, I64, P, I64, P, I64, c_int, P]),
     "sgl_e8m0_to_f32": (c_int, [P, P, I64, P]),
     "sgl_check_conversions": (c_int, [P, P]),
+    "sgl_hbm_stream": (c_int, [P, P, I64, P, P]),
     "sgl_fp8_gemm": (c_int, [P, P, P, P, c_int, P, c_int, I64, I64, I64, P]),
     "sgl_fp4_gemm": (c_int, [P, P, c_int, P, P, P, c_int, I64, I64, I64, P]),
     "sgl_fp4_to_fp8_weight": (c_int, [P, P, I64, I64, P, P, P]),

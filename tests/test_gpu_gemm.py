@@ -210,3 +210,23 @@ def test_fp8_gemm_splitk_concurrent_streams_and_graph(gpu):
         g2.replay()
         torch.cuda.synchronize()
         assert_gemm_close(f32(gout2), refs[1], "captured on a fresh stream")
+
+
+def test_hbm_stream_copies_and_reads(gpu):
+    """sgl_hbm_stream (the bandwidth measurement kernel): the copy is exact and
+    the read leaves the XOR of each 1/2048 slice."""
+    from sglang_lite_amd import _lib
+
+    rng = np.random.default_rng(30)
+    n = 2048 * 64 * 16  # 2 MiB
+    host = rng.integers(0, 256, n, dtype=np.uint8)
+    src = torch.from_numpy(host).to(gpu)
+    dst = torch.zeros_like(src)
+    sums = torch.zeros(2048, dtype=torch.int32, device=gpu)
+    _lib.call("sgl_hbm_stream", src.data_ptr(), dst.data_ptr(), n, sums.data_ptr(), _lib.stream_of(src))
+    _lib.call("sgl_hbm_stream", src.data_ptr(), None, n, sums.data_ptr(), _lib.stream_of(src))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(dst.cpu().numpy(), host)
+    words = host.view(np.uint32).reshape(2048, -1)
+    np.testing.assert_array_equal(sums.cpu().numpy().view(np.uint32),
+                                  np.bitwise_xor.reduce(words, axis=1))
