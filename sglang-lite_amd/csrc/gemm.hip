@@ -40,6 +40,7 @@
 #include <mutex>
 #include <type_traits>
 #include <utility>
+#include <vector>
 
 #include "sgl_gemm.h"
 #include "sgl_numeric.h"
@@ -1974,11 +1975,16 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 
 // Workspace of the split-K kernel (the partials) per (device, stream),
 // allocated outside stream capture: a call on a capturing stream that has
-// none yet takes the unsplit kernels.  Calls on one stream are ordered, so
-// they share it.
+// none yet, or too little, takes the unsplit kernels.  Calls on one stream
+// are ordered, so they share it.  A block is never freed while the library
+// is loaded: a HIP graph that captured a call keeps the block's address and
+// writes there on every replay, so a larger call retires the old block
+// instead of freeing it; growth is at least 1.5x, which bounds the retired
+// bytes by twice the live block.
 struct SplitKWs {
   uint8_t* base = nullptr;
   size_t bytes = 0;
+  std::vector<uint8_t*> retired;
 };
 std::mutex g_splitk_mu;
 std::map<std::pair<int, hipStream_t>, SplitKWs> g_splitk_ws;
@@ -1994,21 +2000,15 @@ uint8_t* splitk_workspace(hipStream_t stream, size_t need) {
     (void)hipGetLastError();
     return nullptr;
   }
-  if (w.base) {  // grow: the stream's earlier calls finish before the old block goes
-    if (hipStreamSynchronize(stream) != hipSuccess || hipFree(w.base) != hipSuccess) {
-      (void)hipGetLastError();
-      w = SplitKWs{};
-      return nullptr;
-    }
-    w = SplitKWs{};
-  }
+  const size_t bytes = std::max(need, w.bytes + w.bytes / 2);
   void* p = nullptr;
-  if (hipMalloc(&p, need) != hipSuccess) {
+  if (hipMalloc(&p, bytes) != hipSuccess) {
     (void)hipGetLastError();
     return nullptr;
   }
+  if (w.base) w.retired.push_back(w.base);
   w.base = static_cast<uint8_t*>(p);
-  w.bytes = need;
+  w.bytes = bytes;
   return w.base;
 }
 

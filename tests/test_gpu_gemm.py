@@ -212,6 +212,46 @@ def test_fp8_gemm_splitk_concurrent_streams_and_graph(gpu):
         assert_gemm_close(f32(gout2), refs[1], "captured on a fresh stream")
 
 
+def test_fp8_gemm_splitk_graph_survives_workspace_growth(gpu):
+    """A graph captured with the stream's split-K workspace keeps its address:
+    a larger eager GEMM on that stream afterwards grows the workspace without
+    freeing the captured block, so replays stay exact with the larger
+    GEMM's eager calls between them."""
+    from sglang_lite_amd import kernel as K_
+
+    rng = np.random.default_rng(23)
+    N, K = 4096, 7168
+    small = _operands(rng, 40, N, K)   # 8 splits x 40 x 4096 fp32 partials
+    large = _operands(rng, 64, N, K)   # 8 splits x 64 x 4096: more than the first block
+    d_small, d_large = [(to_dev_fp8(aq, gpu), to_dev_f32(sa, gpu), to_dev_fp8(bq, gpu), to_dev_f32(sb, gpu))
+                        for aq, sa, bq, sb in (small, large)]
+    cap = torch.cuda.Stream()
+    out_s = torch.empty(40, N, dtype=torch.float32, device=gpu)
+    out_l = torch.empty(64, N, dtype=torch.float32, device=gpu)
+    with torch.cuda.stream(cap):
+        K_.fp8_gemm(*d_small, out=out_s)  # the stream's workspace, sized for M = 40
+    torch.cuda.synchronize()
+    eager_s = f32(out_s).copy()
+    assert_gemm_close(eager_s, OM.fp8_gemm(*small, out_bf16=False), "split-K M=40")
+    g = torch.cuda.CUDAGraph()
+    gout = torch.empty(40, N, dtype=torch.float32, device=gpu)
+    with torch.cuda.graph(g, stream=cap):
+        K_.fp8_gemm(*d_small, out=gout)
+    with torch.cuda.stream(cap):
+        K_.fp8_gemm(*d_large, out=out_l)  # grows the workspace
+    torch.cuda.synchronize()
+    eager_l = f32(out_l).copy()
+    assert_gemm_close(eager_l, OM.fp8_gemm(*large, out_bf16=False), "split-K M=64 after growth")
+    for _ in range(3):
+        gout.zero_()
+        g.replay()
+        with torch.cuda.stream(cap):
+            K_.fp8_gemm(*d_large, out=out_l)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(f32(gout).view(np.uint32), eager_s.view(np.uint32))
+        np.testing.assert_array_equal(f32(out_l).view(np.uint32), eager_l.view(np.uint32))
+
+
 def test_hbm_stream_copies_and_reads(gpu):
     """sgl_hbm_stream (the bandwidth measurement kernel): the copy is exact and
     the read leaves the XOR of each 1/2048 slice."""
