@@ -1556,6 +1556,217 @@ int launch_pipe(GemmArgs& a, hipStream_t stream) {
   return check_launch("gemm_pipe");
 }
 
+// ------------------------------------------------------------ wide tiles
+// Dense products from M = 2048 up: 256 x 256 tiles, eight wavefronts (4 x 2,
+// 64 x 128 each, two per SIMD with 256 registers) and a 2-slot ring of 64 KB
+// stages.  Per 128-deep stage a CU moves 64 KB into LDS for 16.8 MFLOP (the
+// 128 x 256 tile moves 48 KB for 8.4), so the operand path carries two thirds
+// of the bytes per MFMA, and each stage barrier is amortized over 32 MFMAs
+// per wavefront.  Wavefronts 4..7 (one per SIMD) issue the stage DMAs: stage
+// st + 1 right after the barrier of stage st, into the slot stage st - 1
+// used, so one stage's loads fly while the other stage is computed.  The
+// promotion and its order are those of gemm_fp8_kernel, so the output is
+// bit-identical to the 128 x 256 tiles (N = 4096, K = 7168, M = 4096:
+// 175 -> 135 us).
+namespace wide {
+constexpr int BM = 256, BN = 256, WM = 4, WN = 2, TM = 4, TN = 8, NW = 8, NT = 64 * NW;
+constexpr int IW = 4;                                    // DMA issuers: wavefronts 4..7
+constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128, STAGE = A_BYTES + B_BYTES;
+constexpr int RING = 2 * STAGE;
+constexpr int SA_SLOT = BM * 4;                          // row scales of one stage
+constexpr int SMEM = RING + 2 * SA_SLOT;
+constexpr int ACH = BM / 8, BCH = BN / 8;                // 1 KB chunks per stage
+constexpr int QA = ACH / IW, QB = BCH / IW;              // per issuer
+static_assert(WM * TM * 16 == BM && WN * TN * 16 == BN && WM * WN == NW, "wavefront grid");
+static_assert(IW * 64 == BM, "one row-scale DMA per issuer and stage");
+static_assert(TN * 16 == 128, "a wavefront's columns are one 128-column weight-scale block");
+}  // namespace wide
+
+__global__ __launch_bounds__(wide::NT) void gemm_wide_kernel(const GemmArgs args) {
+  using namespace wide;
+  __shared__ __align__(16) uint8_t smem[SMEM];
+  __shared__ float sSb[2][kMaxKB];  // the tile's weight scales: column block j, K block kb
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const bool issuer = wave >= NW - IW;
+  const int iw = issuer ? wave - (NW - IW) : 0;
+  const int g4 = lane >> 4, r16 = lane & 15;
+  const FragLane fl = frag_lane(r16, g4);
+  const int64_t K = args.K, N = args.N, M = args.M;
+  const int KB = (int)(K / 128);
+  const int NST = KB;
+  const int total_mt = (int)((M + BM - 1) / BM);
+  const int total = total_mt * args.n_tiles;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per_xcd = gridDim.x >> 3;
+  const int per = (total + 7) >> 3;
+  const int t_begin = xcd * per;
+  const int t_end = min(t_begin + per, total);
+
+  const uint8_t* baseA = uniform_ptr(args.a);
+  const uint8_t* baseB = uniform_ptr(args.b);
+  const uint8_t* sa_base = uniform_ptr(args.sa);
+  const uint32_t smem_lds = __builtin_amdgcn_readfirstlane(lds_u32(smem));
+  // issuer iw moves chunks iw + IW q of A (rows 8 c ..) and of B; with IW
+  // even every chunk of an issuer has the swizzle parity of iw, so one lane
+  // offset (row rr of the chunk, the lane's swizzled 16-byte piece) serves
+  // all of them; the chunk's first row is a wave-uniform base
+  const int rr = lane >> 3, pc = lane & 7;
+  const uint32_t chunk = (uint32_t)((pc ^ ((rr & 6) | (iw & 1))) << 4);
+  const uint32_t lane_off = (uint32_t)(rr * K) + chunk;
+  const v4f vzero = {0.0f, 0.0f, 0.0f, 0.0f};
+  int gst = 0;  // stages issued before this tile: stage st of the tile uses ring slot (gst + st) & 1
+
+  for (int iter = 0;; ++iter) {
+    const int L = t_begin + slot + iter * per_xcd;
+    if (L >= t_end) break;
+    // N-slice major, the M tiles of a slice adjacent (one XCD's L2 holds the slice)
+    const int nt = L / total_mt;
+    const int mt = L - nt * total_mt;
+    const int row0 = mt * BM;
+    const int rows = (int)min((int64_t)BM, M - row0);
+    const int64_t n0 = (int64_t)nt * BN;
+
+    __syncthreads();  // the previous tile's readers of sSb are done
+    for (int i = tid; i < 2 * KB; i += NT) {
+      const int j = i / KB, kb = i - j * KB;
+      const int64_t nb = (N + 127) / 128;
+      int64_t blk = n0 / 128 + j;
+      if (blk > nb - 1) blk = nb - 1;
+      sSb[j][kb] = load_scale(args.sb, blk * KB + kb, args.sb_e8m0);
+    }
+    // A chunks wholly past the tile's last row and B chunks past N (N % 16
+    // == 0: chunks are wholly in or out) are not loaded: those rows only
+    // feed outputs that are never stored
+    const int sa_r = iw * 64 + lane;
+    const uint32_t sa_off = (uint32_t)((int64_t)(row0 + (sa_r < rows ? sa_r : rows - 1)) * KB * 4);
+    auto issue = [&](int st) {
+      if (!issuer) return;
+      const int s = (gst + st) & 1;
+      const uint32_t sl = smem_lds + (uint32_t)(s * STAGE);
+#pragma unroll
+      for (int q = 0; q < QA; ++q) {
+        const int c = iw + q * IW;
+        if (c * 8 < rows) {
+          const uint32_t vo = c * 8 + 8 <= rows ? lane_off
+                                                : (uint32_t)(min(rr, rows - 1 - c * 8) * K) + chunk;
+          dma16(baseA + ((int64_t)(row0 + c * 8) * K + st * 128), vo, sl + (uint32_t)c * 1024u);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < QB; ++q) {
+        const int b = iw + q * IW;
+        const int64_t nrow = n0 + b * 8;
+        if (nrow < N) dma16(baseB + (nrow * K + st * 128), lane_off, sl + (uint32_t)(A_BYTES + b * 1024));
+      }
+      dma4(sa_base, sa_off + (uint32_t)st * 4u, smem_lds + (uint32_t)(RING + s * SA_SLOT + iw * 256));
+    };
+    __syncthreads();  // sSb published
+    issue(0);
+
+    // wavefront (wm, wn): rows (wm TM + mi) 16 .., columns wn 128 + 16 nj ..
+    v4f acc[TM][TN];
+#pragma unroll
+    for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+      for (int nj = 0; nj < TN; ++nj) acc[mi][nj] = vzero;
+    const bool active = (wm * TM) * 16 < rows;
+
+    for (int st = 0; st < NST; ++st) {
+      // the issuers' stage-st loads are the only ones in flight
+      wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
+      if (st + 1 < NST) issue(st + 1);
+      const int s = (gst + st) & 1;
+      const uint8_t* stg = smem + s * STAGE;
+      const uint8_t* tB = stg + A_BYTES + (wn * TN * 16) * 128;
+      const float* tS = reinterpret_cast<const float*>(smem + RING + s * SA_SLOT);
+      if (active) {
+        // fragments in MFMA order (A0, B0 and the scales, then A1..A3);
+        // the weight fragment of block nj + 1 is read while the MFMAs of
+        // block nj run.  Transposed product (weight fragment = MFMA A
+        // operand): lane (g4, r16) accumulates row r16 of each 16-row block
+        // and columns 4 g4 .. + 3 of each 16-column block, so one row scale
+        // per lane and block and one weight scale per wavefront
+        v8i af[TM];
+        v8i bf[2];
+        float sa1[TM];
+        af[0] = read_frag(stg + (wm * TM) * 16 * 128, fl);
+        bf[0] = read_frag(tB, fl);
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi) sa1[mi] = tS[(wm * TM + mi) * 16 + r16];
+        const float sb = sSb[wn][st];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int mi = 1; mi < TM; ++mi) af[mi] = read_frag(stg + (wm * TM + mi) * 16 * 128, fl);
+        __builtin_amdgcn_sched_barrier(0);
+        float ss[TM];
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi) ss[mi] = sa1[mi] * sb;
+#pragma unroll
+        for (int nj = 0; nj < TN; ++nj) {
+          if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + (nj + 1) * 16 * 128, fl);
+          v4f pr[TM];
+#pragma unroll
+          for (int mi = 0; mi < TM; ++mi)
+            pr[mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[nj & 1], af[mi], vzero, 0, 0, 0,
+                                                                      0, 0, 0);
+          // C += P (sa sb), one FMA per output per K block
+#pragma unroll
+          for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[mi][nj][r] = fmaf(pr[mi][r], ss[mi], acc[mi][nj][r]);
+        }
+      }
+    }
+    gst += NST;
+
+    // lane (g4, r16): row (wm TM + mi) 16 + r16, columns wn 128 + 16 nj + 4 g4 .. + 3
+    const bool f32out = args.out_f32;
+    if (active) {
+#pragma unroll
+      for (int mi = 0; mi < TM; ++mi) {
+        const int row = (wm * TM + mi) * 16 + r16;
+        if (row < rows) {
+          const int64_t drow = row0 + row;
+#pragma unroll
+          for (int nj = 0; nj < TN; ++nj) {
+            const int64_t col = n0 + (wn * TN + nj) * 16 + 4 * g4;
+            if (col < N) {
+              const v4f v = acc[mi][nj];
+              if (f32out)
+                *reinterpret_cast<float4*>(reinterpret_cast<float*>(args.c) + drow * N + col) =
+                    make_float4(v[0], v[1], v[2], v[3]);
+              else
+                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(args.c) + drow * N + col) =
+                    make_uint2(pk2_bf16_exact(v[0], v[1]), pk2_bf16_exact(v[2], v[3]));
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+int launch_wide(GemmArgs& a, hipStream_t stream) {
+  using namespace wide;
+  a.n_tiles = (int)ceil_div(a.N, BN);
+  const int64_t mt = ceil_div(a.M, BM);
+  const int64_t tiles = mt * a.n_tiles;
+  if (tiles == 0) return SGL_OK;
+  constexpr int kLds = SMEM + 2 * kMaxKB * 4;
+  static_assert(kLds <= 160 * 1024, "wide tile exceeds the LDS of a CU");
+  int64_t wgs = (int64_t)device_cu_count();
+  wgs = (wgs + 7) / 8 * 8;
+  const int64_t need = (tiles + 7) / 8 * 8;
+  if (need < wgs) wgs = need;
+  a.m_tiles = (int)mt;
+  gemm_wide_kernel<<<(unsigned)wgs, NT, 0, stream>>>(a);
+  return check_launch("gemm_wide");
+}
+
 template <int KIND, int BM, int BN, int WM, int WN, int NSTAGE, int WF = WF_FP8, bool SAHW = false,
           int LW = 0>
 int launch_cfg(GemmArgs& a, hipStream_t stream) {
@@ -2112,8 +2323,8 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
         if (a.M <= 32) return launch_skinny<2>(a, stream);
         return launch_skinny<4>(a, stream);
       }
-      // 128 x 256 tiles from M = 2048 up; below, 64 x 128 tiles (two
-      // workgroups per CU) so the grid still covers every CU.  A workgroup
+      // 256 x 256 tiles above M = 2048, 128 x 128 from 512, 64 x 128 (two
+      // workgroups per CU) from 256, so the grid still covers every CU.  A workgroup
       // streams its operands at a capped rate (about 35 GB/s measured,
       // whatever the stage depth or wavefront count), so for M <= 256 the
       // tiles shrink until there is about one per CU: N = 4096, K = 7168 at
@@ -2124,7 +2335,9 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       // 128 x 128 with 8 wavefronts (the issuer split) from M = 512: M = 1024
       // in 52 us where 64 x 128 tiles take 64 us
       if (a.M <= 2048) return launch_cfg<KIND_DENSE, 128, 128, 2, 4, 3>(a, stream);
-      return launch_cfg<KIND_DENSE, 128, 256, 2, 4, 3>(a, stream);
+      // 256 x 256 tiles (K <= 16384 by the check above): M = 2049 in 27 us
+      // where 128 x 256 tiles take 33
+      return launch_wide(a, stream);
     }
     case KIND_GATE_UP:
       if (big && pipe_ok)

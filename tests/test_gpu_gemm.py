@@ -270,3 +270,47 @@ def test_hbm_stream_copies_and_reads(gpu):
     words = host.view(np.uint32).reshape(2048, -1)
     np.testing.assert_array_equal(sums.cpu().numpy().view(np.uint32),
                                   np.bitwise_xor.reduce(words, axis=1))
+
+
+# The 256 x 256 tiles (M > 2048): a partial last M tile whose rows end inside
+# a wavefront's 64 (3000 = 11 x 256 + 184), a last row tile of 8 rows
+# (2056), ragged N (a 16-column last tile: chunks past N are not loaded),
+# one 256-deep K range (two stages), and fp32 output against the exact
+# per-128-K promotion emulation.
+@pytest.mark.parametrize("M,N,K,f32_out", [(3000, 1040, 1024, True), (2056, 512, 256, True),
+                                           (2304, 4096, 7168, False), (4100, 272, 640, False)])
+def test_fp8_gemm_wide_tiles(gpu, M, N, K, f32_out):
+    from sglang_lite_amd import kernel as K_
+
+    print(f"wide {M}x{N}x{K}", flush=True)
+    rng = np.random.default_rng(M + 3 * N + K)
+    aq, sa, bq, sb = _operands(rng, M, N, K)
+    args = (to_dev_fp8(aq, gpu), to_dev_f32(sa, gpu), to_dev_fp8(bq, gpu), to_dev_f32(sb, gpu))
+    if f32_out:
+        c = K_.fp8_gemm(*args)
+        assert c.dtype == torch.float32
+        ref = OM.fp8_gemm_promoted(aq, sa, bq, sb)
+        np.testing.assert_allclose(f32(c), ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
+    else:
+        prev = torch.get_default_dtype()
+        try:
+            torch.set_default_dtype(torch.bfloat16)
+            c = K_.fp8_gemm(*args)
+        finally:
+            torch.set_default_dtype(prev)
+        assert_gemm_close(f32(c), OM.fp8_gemm(aq, sa, bq, sb, out_bf16=False), f"wide {M}x{N}x{K}")
+
+
+def test_fp8_gemm_wide_tiles_e8m0_weight_scales(gpu):
+    from sglang_lite_amd import kernel as K_
+
+    rng = np.random.default_rng(23)
+    M, N, K = 2500, 768, 1536
+    a = bf16_values(rng, (M, K))
+    aq, sa = Q.per_token_cast_to_fp8(a, True, 128)
+    bq, sb = Q.per_block_cast_to_fp8(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02),
+                                     True)
+    ref = OM.fp8_gemm(aq, sa, bq, sb, out_bf16=False)
+    sb_e = torch.from_numpy(Q.e8m0_byte(sb)).view(torch.float8_e8m0fnu).to(gpu)
+    c = K_.fp8_gemm(to_dev_fp8(aq, gpu), to_dev_f32(sa, gpu), to_dev_fp8(bq, gpu), sb_e)
+    assert_gemm_close(f32(c), ref, "fp8_gemm wide e8m0")
