@@ -172,7 +172,7 @@ int sgl_hbm_stream(const void* src, void* dst, int64_t bytes, uint32_t* sums, sg
  * (e8m0 activation scales: convert with sgl_e8m0_to_f32 first), B e4m3 [N, K]
  * contiguous, sb [ceil(N/128), K/128] fp32, or one e8m0 byte per scale when
  * b_scale_e8m0 is set.  K % 128 == 0, N % 16 == 0, M*K and N*K < 2^31.
- * For 32 < M <= 64 with N % 128 == 0 the K range is split over workgroups:
+ * For 16 < M <= 64 with N % 128 == 0 the K range is split over workgroups:
  * the fp32 partials go to a buffer the library allocates once per (device,
  * stream) outside stream capture and keeps until the process ends (the only
  * allocation in this library); a capturing stream without one takes the

@@ -2013,7 +2013,7 @@ int launch_skinny(GemmArgs& a, hipStream_t stream) {
 
 // ---- small-M dense GEMM, split over K
 //
-// 32 < M <= 64 rows against an N x K weight: the work is streaming B (N K
+// 16 < M <= 64 rows against an N x K weight: the work is streaming B (N K
 // bytes from HBM).  A workgroup that spans all of K also reads all of A (M K
 // bytes, twice its B strip at M = 64) from L2, so the grid is N/128 column
 // tiles x S K ranges of KS blocks, about one workgroup per CU, each reading
@@ -2031,7 +2031,7 @@ int launch_skinny(GemmArgs& a, hipStream_t stream) {
 // reduction does not pay: a last-workgroup sum costs three dependent trips to
 // device-coherent memory, about 3 us.)
 namespace splitk {
-constexpr int NW = 8, NT = 64 * NW, BN = 16 * NW, KSMAX = 8, SMAX = 16, TM = 4, ROWS = 16 * TM;
+constexpr int NW = 8, NT = 64 * NW, BN = 16 * NW, KSMAX = 8, SMAX = 16, TMMAX = 4;
 }  // namespace splitk
 
 struct SplitKArgs {
@@ -2039,10 +2039,11 @@ struct SplitKArgs {
   int S;
 };
 
-template <int KS>
+template <int KS, int TM>
 __global__ __launch_bounds__(splitk::NT) void gemm_splitk_kernel(const GemmArgs args, const SplitKArgs sk) {
   using namespace splitk;
-  static_assert(KS >= 1 && KS <= KSMAX, "split-K tile");
+  constexpr int ROWS = 16 * TM;
+  static_assert(KS >= 1 && KS <= KSMAX && TM >= 1 && TM <= TMMAX, "split-K tile");
   __shared__ __align__(16) uint8_t sA[KS * TM * 2048];
   // row scales [ROWS][KS] and the weight scales of the split's blocks (fp32,
   // or e8m0 bytes at offset idx0 % 4 of the dwords that hold them)
@@ -2223,11 +2224,11 @@ uint8_t* splitk_workspace(hipStream_t stream, size_t need) {
   return w.base;
 }
 
-template <int KS>
+template <int KS, int TM>
 int launch_splitk_ks(GemmArgs& a, int S, float* part, hipStream_t stream) {
   const SplitKArgs sk{part, S};
   const int n_tiles = (int)(a.N / splitk::BN);
-  gemm_splitk_kernel<KS><<<(unsigned)(n_tiles * S), splitk::NT, 0, stream>>>(a, sk);
+  gemm_splitk_kernel<KS, TM><<<(unsigned)(n_tiles * S), splitk::NT, 0, stream>>>(a, sk);
   int rc = check_launch("gemm_fp8_splitk");
   if (rc) return rc;
   const int64_t MN = a.M * a.N;
@@ -2236,12 +2237,29 @@ int launch_splitk_ks(GemmArgs& a, int S, float* part, hipStream_t stream) {
   return check_launch("gemm_fp8_splitk_reduce");
 }
 
-// The split-K path for a dense FP8 GEMM when it applies (32 < M <= 64, N %
+// The split-K path for a dense FP8 GEMM when it applies (16 < M <= 64, N %
 // 128 == 0, at least two splits that fit, a workspace at hand); returns -1
 // when the caller should take the unsplit kernels.
+template <int TM>
+int launch_splitk_tm(GemmArgs& a, int KS, int S, float* part, hipStream_t stream) {
+  switch (KS) {
+    case 1: return launch_splitk_ks<1, TM>(a, S, part, stream);
+    case 2: return launch_splitk_ks<2, TM>(a, S, part, stream);
+    case 3: return launch_splitk_ks<3, TM>(a, S, part, stream);
+    case 4: return launch_splitk_ks<4, TM>(a, S, part, stream);
+    case 5: return launch_splitk_ks<5, TM>(a, S, part, stream);
+    case 6: return launch_splitk_ks<6, TM>(a, S, part, stream);
+    case 7: return launch_splitk_ks<7, TM>(a, S, part, stream);
+    default: return launch_splitk_ks<8, TM>(a, S, part, stream);
+  }
+}
+
 int try_splitk(GemmArgs& a, hipStream_t stream) {
   using namespace splitk;
-  if (a.M <= 32 || a.M > ROWS || a.N % BN != 0 || a.wfmt != WF_FP8) return -1;
+  // 16 < M <= 64 (N = 4096, K = 7168, graph-replayed over cold weights:
+  // M = 32 12.1 us where the skinny kernel takes 14.3; M = 16 10.9 vs 10.5,
+  // M = 128 with 128-row tiles 23.0 vs 22.0 with 32 x 64 tiles)
+  if (a.M <= 16 || a.M > 16 * TMMAX || a.N % BN != 0 || a.wfmt != WF_FP8) return -1;
   if (a.sb_e8m0 && !aligned(a.sb, 4)) return -1;  // e8m0 scales are read as whole dwords
   const int KB = (int)(a.K / 128);
   const int n_tiles = (int)(a.N / BN);
@@ -2254,16 +2272,8 @@ int try_splitk(GemmArgs& a, hipStream_t stream) {
   if (S < 2) return -1;
   float* part = reinterpret_cast<float*>(splitk_workspace(stream, (size_t)S * (size_t)a.M * (size_t)a.N * 4));
   if (!part) return -1;
-  switch (KS) {
-    case 1: return launch_splitk_ks<1>(a, S, part, stream);
-    case 2: return launch_splitk_ks<2>(a, S, part, stream);
-    case 3: return launch_splitk_ks<3>(a, S, part, stream);
-    case 4: return launch_splitk_ks<4>(a, S, part, stream);
-    case 5: return launch_splitk_ks<5>(a, S, part, stream);
-    case 6: return launch_splitk_ks<6>(a, S, part, stream);
-    case 7: return launch_splitk_ks<7>(a, S, part, stream);
-    default: return launch_splitk_ks<8>(a, S, part, stream);
-  }
+  if (a.M <= 32) return launch_splitk_tm<2>(a, KS, S, part, stream);
+  return launch_splitk_tm<4>(a, KS, S, part, stream);
 }
 
 }  // namespace

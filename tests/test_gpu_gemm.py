@@ -103,16 +103,19 @@ def test_fp8_gemm_end_to_end_from_bf16(gpu):
     assert_gemm_close(f32(c), ref, "linear")
 
 
-# The split-K kernel (32 < M <= 64, N % 128 == 0): N/128 column tiles x S
-# K ranges of KS <= 8 blocks, the partials summed in split order by a second
-# kernel.  Shapes beside it take the unsplit kernels.
+# The split-K kernel (16 < M <= 64, N % 128 == 0; 32-row tiles up to M = 32,
+# 64-row tiles above): N/128 column tiles x S K ranges of KS <= 8 blocks, the
+# partials summed in split order by a second kernel.  Shapes beside it take
+# the unsplit kernels.
 @pytest.mark.parametrize("M,N,K", [
     (33, 1024, 1152),   # 8 tiles, KB = 9: S = 5, ragged last split; 31 rows past M
     (48, 4096, 896),    # 32 tiles, one block per split
     (64, 384, 2048),    # 3 tiles
     (40, 4096, 7168),   # the dense config's N and K: 8 splits of 7 blocks
     (64, 2048, 4096),
-    (32, 1024, 1152),   # M <= 32 and M > 64: the unsplit kernels
+    (32, 1024, 1152),   # 32-row tiles
+    (17, 4096, 7168),   # 32-row tiles, 15 rows past M, the dense config's N and K
+    (16, 1024, 1152),   # M <= 16 and M > 64: the unsplit kernels
     (65, 1024, 1152),
 ])
 def test_fp8_gemm_splitk_matches_oracle(gpu, M, N, K):
