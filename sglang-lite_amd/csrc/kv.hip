@@ -56,6 +56,21 @@ __device__ __forceinline__ void load8(const uint8_t* row, int elem, float* f, ui
   }
 }
 
+// Row t of a footer-paged cache sits in page t / page at slot t % page: a
+// shift and a mask for power-of-two pages (the 64-row pages of the
+// reference), a 64-bit division otherwise.
+struct PageSplit {
+  int64_t pg, l;
+};
+__device__ __forceinline__ int page_shift_of(int page) {
+  return page > 0 && (page & (page - 1)) == 0 ? __builtin_ctz((unsigned)page) : -1;
+}
+__device__ __forceinline__ PageSplit page_split(int64_t t, int page, int shift) {
+  if (shift >= 0) return PageSplit{t >> shift, t & (int64_t)(page - 1)};
+  const int64_t pg = t / page;
+  return PageSplit{pg, t - pg * page};
+}
+
 // Layout A: lanes 0..55 quantize 8 NoPE values each (7 groups of 64 = 8
 // lanes), lanes 56..63 carry the 128 RoPE bytes verbatim.  paged != 0 writes
 // the footer page layout of to_paged_hnd directly (data at l*576 inside the
@@ -80,6 +95,7 @@ __global__ __launch_bounds__(256) void kv_pack_a_kernel(const uint8_t* __restric
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * 4;
   const int64_t w0 = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int shift = page_shift_of(page);
   for (int64_t tb = w0 * R; tb < rows_total; tb += nwaves * R) {
     float f[R][8];
     uint4 raw[R];
@@ -93,16 +109,16 @@ __global__ __launch_bounds__(256) void kv_pack_a_kernel(const uint8_t* __restric
       uint8_t* data;
       uint8_t* foot;
       if (pt.block_table) {
-        const int64_t pos = pt.start + t;
-        const int64_t bid = pt.block_table[pos / page];
+        const PageSplit ps = page_split(pt.start + t, page, shift);
+        const int64_t bid = pt.block_table[ps.pg];
         if (bid < 0 || bid >= pt.num_blocks) continue;  // not a block of this pool
-        data = out + (bid * page + pos % page) * A_ROW;
+        data = out + (bid * page + ps.l) * A_ROW;
         foot = data + A_DATA;
       } else if (paged) {
-        const int64_t pg = t / page, l = t - pg * page;
-        uint8_t* pbase = out + pg * (int64_t)page * A_ROW;
-        data = pbase + l * A_DATA;
-        foot = pbase + (int64_t)page * A_DATA + l * 8;
+        const PageSplit ps = page_split(t, page, shift);
+        uint8_t* pbase = out + ps.pg * (int64_t)page * A_ROW;
+        data = pbase + ps.l * A_DATA;
+        foot = pbase + (int64_t)page * A_DATA + ps.l * 8;
       } else {
         data = out + t * A_ROW;
         foot = data + A_DATA;
@@ -210,8 +226,10 @@ __global__ __launch_bounds__(256) void kv_to_paged_kernel(const uint8_t* __restr
                                                           uint8_t* __restrict__ pages) {
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * 4;
+  const int shift = page_shift_of(page);
   for (int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); t < rows_total; t += nwaves) {
-    const int64_t pg = t / page, l = t - pg * page;
+    const PageSplit ps = page_split(t, page, shift);
+    const int64_t pg = ps.pg, l = ps.l;
     uint8_t* pbase = pages + pg * (int64_t)page * A_ROW;
     // 73 eight-byte words per row: 72 data words, 1 footer word
     for (int w = lane; w < 73; w += 64) {
@@ -240,6 +258,7 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const uint8_t* __restric
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * 4;
   const int64_t w0 = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int shift = page_shift_of(page);
   // lane r < R: index r of the step starting at rb (clamped into the array)
   auto load_idx = [&](int64_t rb) -> int32_t {
     const int64_t i = rb + (lane < R ? lane : 0);
@@ -267,7 +286,8 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const uint8_t* __restric
           const uint8_t* data;
           const uint8_t* foot;
           if (paged) {
-            const int64_t pg = id[r] / page, l = id[r] - pg * page;
+            const PageSplit ps = page_split(id[r], page, shift);
+            const int64_t pg = ps.pg, l = ps.l;
             const uint8_t* pbase = cache + pg * (int64_t)page * A_ROW;
             data = pbase + l * A_DATA;
             foot = pbase + (int64_t)page * A_DATA + l * 8;

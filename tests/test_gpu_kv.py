@@ -53,6 +53,25 @@ def test_pack_layout_a_bit_exact(gpu, dtype, mode, T):
     np.testing.assert_array_equal(pages2.cpu().numpy(), OK.to_paged_hnd(ref, 64))
 
 
+@pytest.mark.parametrize("page,T", [(16, 100), (48, 97), (40, 90), (64, 128), (128, 300)])
+def test_pack_paged_page_sizes_and_strided_rows(gpu, page, T):
+    """Footer pages at several page sizes (multiples of 16 take the
+    16-rows-per-wavefront kernel, 40 the row kernel), a ragged last page, and
+    input rows that are a view of a wider [T, 576] buffer (row stride 576)."""
+    from sglang_lite_amd import dsv4_kv_pack as KVP
+
+    print(f"paged pack page={page} T={T}", flush=True)
+    rng = np.random.default_rng(page * 1000 + T)
+    wide = bf16_values(rng, (T, 576))
+    wt = torch.from_numpy(wide).to(torch.bfloat16)
+    xt = wt[:, :512]
+    xv = xt.float().numpy()
+    rope = xt[:, 448:].contiguous().view(torch.uint8).numpy()
+    ref = OK.to_paged_hnd(OK.pack_layout_a(xv, rope, 4), page)
+    pages = KVP.pack_dsv4_kv_paged(wt.to(gpu)[:, :512], page)
+    np.testing.assert_array_equal(pages.cpu().numpy(), ref)
+
+
 def test_pack_calls_an_injected_quantizer(gpu):
     """dsv4_kv_pack.py:58-61: a quantizer other than the official act_quant is
     called on the NoPE part as (nope, 64, "ue8m0", float8_e8m0fnu, False) and
