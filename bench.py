@@ -286,8 +286,9 @@ def hbm_ceiling(torch, dev):
 def profile_small(torch, M, K, table, dev):
     """The short kernels for a profiler run (--profile-kernels small), three
     launches each: the decode layers (T = 64 / 256 / 512, Zipf(1.1) load), the
-    dense GEMM at M = 16 / 64 / 128 (N = 4096, K = 7168) over 12 rotating
-    weight copies, act_quant 4096 x 7168, and the KV packs (65536 rows)."""
+    dense GEMM at M = 16 / 32 / 64 / 128 (N = 4096, K = 7168) over 12 rotating
+    weight copies (three rounds; M = 4096 one round), act_quant 4096 x 7168,
+    and the KV packs (65536 rows)."""
     from sglang_lite_amd import dsv4_kv_pack as KVP
 
     for Td, seed in ((64, 31), (256, 32), (512, 33)):
@@ -304,10 +305,10 @@ def profile_small(torch, M, K, table, dev):
     prev = torch.get_default_dtype()
     torch.set_default_dtype(torch.bfloat16)
     try:
-        for Md in (16, 64, 128):
+        for Md in (16, 32, 64, 128, 4096):
             aq, as_ = K.act_quant(torch.randn(Md, 7168, generator=gw, device=dev).to(torch.bfloat16))
             c = torch.empty(Md, 4096, dtype=torch.bfloat16, device=dev)
-            for i in range(3 * len(wsets)):
+            for i in range(3 * len(wsets) if Md <= 128 else len(wsets)):
                 K.fp8_gemm(aq, as_, wsets[i % 12][0], wsets[i % 12][1], out=c)
         xs = [torch.randn(4096, 7168, generator=gw, device=dev).to(torch.bfloat16) for _ in range(3)]
         for x in xs:
@@ -714,7 +715,7 @@ def main():
         prev = torch.get_default_dtype()
         torch.set_default_dtype(torch.bfloat16)
         try:
-            for Md in (16, 64, 128, 1024, 4096):
+            for Md in (16, 32, 64, 128, 1024, 4096):
                 a = torch.randn(Md, 7168, generator=gw, device=dev).to(torch.bfloat16)
                 aq, as_ = K.act_quant(a)
                 c = torch.empty(Md, 4096, dtype=torch.bfloat16, device=dev)
