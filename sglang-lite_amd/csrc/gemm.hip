@@ -949,9 +949,6 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
 // (wm 4 + mi) 16 + r16 and columns 16 nj + 4 g4 .. + 3; per 128-deep K
 // block C += P (sa sb); SwiGLU + 1x128 requant (gate/up) or bf16 stores
 // (down) from registers.
-#ifndef SGL_PIPE_PROBE
-#define SGL_PIPE_PROBE 0
-#endif
 namespace pipe {
 constexpr int BM = 128, BN = 256, WM = 2, WN = 4, TM = 4, TN = 4, NWC = 8, LW = 4, NW = 12;
 constexpr int NT = 64 * NW, NSTAGE = 3, HALF = 128, HW = HALF / WN;
@@ -1221,13 +1218,13 @@ __global__ __launch_bounds__(pipe::NT) void gemm_pipe_kernel(const GemmArgs args
     for (int j = 0; j < CPW; ++j) {
       const int c = iw + j * LW;
       if (j < QA) {
-        dma16v(ls.a[j] + (uint64_t)(SGL_PIPE_PROBE == 1 ? 0 : st) * 128u, __builtin_amdgcn_readfirstlane(sl + (uint32_t)c * 1024u));
+        dma16v(ls.a[j] + (uint64_t)st * 128u, __builtin_amdgcn_readfirstlane(sl + (uint32_t)c * 1024u));
       } else {
         const int b = c - BM / 8;
         const bool up_half = KIND == KIND_GATE_UP && b * 8 >= HALF;
         const int64_t nrow = ls.n0 + (up_half ? b * 8 - HALF : b * 8);
         const uint32_t vo = nrow + rr < N ? (uint32_t)(nrow * K) + ls.laneB : ls.clampB;
-        dma16v((up_half ? ls.b1 : ls.b0) + vo + (uint64_t)(SGL_PIPE_PROBE == 2 ? 0 : st) * 128u,
+        dma16v((up_half ? ls.b1 : ls.b0) + vo + (uint64_t)st * 128u,
                __builtin_amdgcn_readfirstlane(sl + (uint32_t)c * 1024u));
       }
     }
