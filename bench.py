@@ -283,6 +283,32 @@ def hbm_ceiling(torch, dev):
     return out
 
 
+def mfma_ceiling(torch, dev, iters=2000):
+    """MFMA rates of the GEMMs' inner-loop instruction mix on this GPU
+    (sgl_mfma_mix: 4 x 4 blocks of 16x16x128 FP8 MFMAs per wavefront from
+    registers, two wavefronts per SIMD on every CU), beside the 5.0 PF/s
+    nominal: accumulating in the MFMA (the power-of-two-scale path) and with
+    each block partial promoted by 4 fp32 FMAs (the fp32-scale path)."""
+    from sglang_lite_amd import _lib
+
+    threads = _lib.load().sgl_mfma_mix_threads()
+    out = torch.empty(threads, dtype=torch.float32, device=dev)
+    res = {}
+    for v, name in ((0, "mfma_only_tflops"), (1, "mfma_plus_fp32_promotion_tflops")):
+        run = lambda n, v=v: _lib.call("sgl_mfma_mix", v, out.data_ptr(), n, _lib.stream_of(out))  # noqa: E731
+        run(10)
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        run(iters)
+        b.record()
+        b.synchronize()
+        flops = (threads // 64) * iters * 16 * 65536.0
+        res[name] = round(flops / a.elapsed_time(b) / 1e9, 1)
+    return res
+
+
 def profile_small(torch, M, K, table, dev):
     """The short kernels for a profiler run (--profile-kernels small), three
     launches each: the decode layers (T = 64 / 256 / 512, Zipf(1.1) load), the
@@ -589,6 +615,8 @@ def main():
     log(f"prefill T={T}: warmup {args.warmup}, timed {args.steps}")
     ms = time_steps(torch, pre.step, args.steps, args.warmup)
     stages = pre.staged(max(3, min(args.steps, 10)))
+    mix = mfma_ceiling(torch, dev)
+    log(f"MFMA instruction-mix ceilings: {mix}")
     rows = T * K_TOP + T
     flops = moe_flops(rows)
     gu_flops = rows * 4.0 * H * I
@@ -645,7 +673,11 @@ def main():
                      "hbm_frac": round(gu_gbs / PEAK_HBM_GBS, 4),
                      "mfma_frac": round(gu_tflops / PEAK_FP8_TFLOPS, 4),
                      "roof_us": {"hbm": round(t_hbm * 1e6, 1), "mfma": round(t_mfma * 1e6, 1)},
-                     "avg_launch_ms": round(gu_ms, 4)},
+                     "avg_launch_ms": round(gu_ms, 4),
+                     # the same launch against what this GPU's MFMAs reach with the
+                     # fp32-scale promotion in the instruction stream (measured now)
+                     "mix_ceiling": {**mix, "frac_of_fp32_promotion_ceiling": round(
+                         gu_tflops / mix["mfma_plus_fp32_promotion_tflops"], 4)}},
     }
     log(f"prefill {ms:.3f} ms/step -> {tok_s:.0f} tok/s; stages {stages}")
 

@@ -164,6 +164,17 @@ int sgl_check_conversions(unsigned long long* counts, sgl_stream_t stream);
  * HBM fractions are read against (the 8 TB/s nominal is not reachable). */
 int sgl_hbm_stream(const void* src, void* dst, int64_t bytes, uint32_t* sums, sgl_stream_t stream);
 
+/* Measurement aid; no counterpart in the reference.  The MFMA rate of the
+ * FP8 GEMMs' inner-loop instruction mix on all CUs, two wavefronts per SIMD:
+ * each wavefront runs `iters` rounds of a 4 x 4 block of 16x16x128 FP8 MFMAs
+ * (65536 FLOP each) from registers, accumulating in the MFMA (variant 0: the
+ * power-of-two-scale path) or promoting each block partial with 4 fp32 FMAs
+ * (variant 1: the fp32-scale path).  out receives one float per thread,
+ * sgl_mfma_mix_threads() of them.  The rate is the ceiling the GEMMs' MFMA
+ * fractions are read against beside the 5.0 PF/s nominal. */
+int sgl_mfma_mix(int variant, float* out, int64_t iters, sgl_stream_t stream);
+int sgl_mfma_mix_threads(void);
+
 /* --------------------------------------------------------------- GEMMs */
 
 /* C[M, N] = sum_kb (A[:, kb] . B[:, kb]^T) * sa[m, kb] * sb[n/128, kb], fp32

@@ -77,6 +77,76 @@ __global__ __launch_bounds__(kStreamThreads) void hbm_stream_kernel(const uint4*
   }
 }
 
+// MFMA rate of the GEMMs' inner-loop instruction mix: each wavefront runs
+// `iters` rounds of a 4 x 4 block of v_mfma_f32_16x16x128_f8f6f4 from
+// registers (the GEMM wavefront's 64 x 64 tile), either accumulating in the
+// MFMA's C operand (variant 0: the power-of-two path) or with each block
+// partial promoted by 4 dependent fp32 FMAs one column block behind
+// (variant 1: the fp32-scale path).  Operands come from the lane id; the
+// sums go to out[thread] so nothing is optimised away.  Two 4-wavefront
+// workgroups per CU: two wavefronts per SIMD, as in the GEMMs.
+typedef int v8i_t __attribute__((ext_vector_type(8)));
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+constexpr int kMixThreads = 256;
+
+template <int V>
+__global__ __launch_bounds__(kMixThreads) void mfma_mix_kernel(float* __restrict__ out, int iters) {
+  const int lane = threadIdx.x & 63;
+  v8i_t a[4], b[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      // e4m3 bytes of small finite values (exponent field below 15)
+      a[i][j] = (int)(0x38383838u ^ (uint32_t)((lane * 29 + i * 7 + j) & 0x07070707));
+      b[i][j] = (int)(0x30303030u ^ (uint32_t)((lane * 13 + i * 5 + j) & 0x07070707));
+    }
+  float ss[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ss[i] = 1.0f + (float)((lane + i) & 3) * 0.25f;
+  const v4f_t z = {0.0f, 0.0f, 0.0f, 0.0f};
+  v4f_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = z;
+  for (int it = 0; it < iters; ++it) {
+    if constexpr (V == 0) {
+#pragma unroll
+      for (int nj = 0; nj < 4; ++nj)
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+          acc[mi][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b[nj], a[mi], acc[mi][nj], 0, 0, 0,
+                                                                         0, 0, 0);
+    } else {
+      v4f_t pr[2][4];
+#pragma unroll
+      for (int nj = 0; nj < 5; ++nj) {
+        if (nj < 4) {
+#pragma unroll
+          for (int mi = 0; mi < 4; ++mi)
+            pr[nj & 1][mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b[nj], a[mi], z, 0, 0, 0, 0, 0, 0);
+        }
+        if (nj >= 1) {
+#pragma unroll
+          for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              acc[mi][nj - 1][r] = fmaf(pr[(nj - 1) & 1][mi][r], ss[mi], acc[mi][nj - 1][r]);
+        }
+      }
+    }
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sum += acc[i][j][r];
+  out[(int64_t)blockIdx.x * kMixThreads + threadIdx.x] = sum;
+}
+
 }  // namespace
 
 }  // namespace sgl
@@ -95,6 +165,20 @@ int sgl_hbm_stream(const void* src, void* dst, int64_t bytes, uint32_t* sums, sg
       (const uint4*)src, (uint4*)dst, bytes / 16, sums);
   return sgl::check_launch("hbm_stream");
 }
+
+int sgl_mfma_mix(int variant, float* out, int64_t iters, sgl_stream_t stream) {
+  SGL_REQUIRE(variant == 0 || variant == 1, "mfma_mix: variant must be 0 or 1");
+  SGL_REQUIRE(iters > 0 && iters < (1 << 30), "mfma_mix: iters=%lld out of range", (long long)iters);
+  SGL_REQUIRE(out, "mfma_mix: null pointer");
+  const unsigned wgs = (unsigned)(2 * sgl::device_cu_count());
+  if (variant == 0)
+    sgl::mfma_mix_kernel<0><<<wgs, sgl::kMixThreads, 0, (hipStream_t)stream>>>(out, (int)iters);
+  else
+    sgl::mfma_mix_kernel<1><<<wgs, sgl::kMixThreads, 0, (hipStream_t)stream>>>(out, (int)iters);
+  return sgl::check_launch("mfma_mix");
+}
+
+int sgl_mfma_mix_threads(void) { return 2 * sgl::device_cu_count() * sgl::kMixThreads; }
 
 const char* sgl_last_error(void) { return sgl::g_last_error; }
 

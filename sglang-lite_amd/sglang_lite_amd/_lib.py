@@ -55,6 +55,8 @@ SIGNATURES = {
     "sgl_e8m0_to_f32": (c_int, [P, P, I64, P]),
     "sgl_check_conversions": (c_int, [P, P]),
     "sgl_hbm_stream": (c_int, [P, P, I64, P, P]),
+    "sgl_mfma_mix": (c_int, [c_int, P, I64, P]),
+    "sgl_mfma_mix_threads": (c_int, []),
     "sgl_fp8_gemm": (c_int, [P, P, P, P, c_int, P, c_int, I64, I64, I64, P]),
     "sgl_fp4_gemm": (c_int, [P, P, c_int, P, P, P, c_int, I64, I64, I64, P]),
     "sgl_fp4_to_fp8_weight": (c_int, [P, P, I64, I64, P, P, P]),

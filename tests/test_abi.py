@@ -159,6 +159,8 @@ def test_invalid_arguments_map_to_value_error_without_launch():
     assert rc == L.SGL_ERR_INVALID_ARG and "multiple of 16" in L.last_error()
     rc = lib.sgl_hbm_stream(None, None, 1000, None, None)
     assert rc == L.SGL_ERR_INVALID_ARG and "multiple of 32768" in L.last_error()
+    rc = lib.sgl_mfma_mix(2, None, 10, None)
+    assert rc == L.SGL_ERR_INVALID_ARG and "variant" in L.last_error()
     rc = lib.sgl_moe_permute(None, 4, 2, 5000, None, None, None, None, None)
     assert rc == L.SGL_ERR_INVALID_ARG
     assert lib.sgl_moe_workspace_size(8192, 4096, 2048, 256, 8, 1) > 8192 * 4096

@@ -275,6 +275,28 @@ def test_hbm_stream_copies_and_reads(gpu):
                                   np.bitwise_xor.reduce(words, axis=1))
 
 
+def test_mfma_mix_measurement_kernel(gpu):
+    """sgl_mfma_mix (the MFMA-rate measurement kernel) runs both instruction
+    mixes on every CU and its per-thread sums are exact multiples of one
+    round (the e4m3 operands have at most 4 significant bits, so every block
+    partial and its promotion by 1, 1.25, 1.5 or 1.75 is exact in fp32)."""
+    from sglang_lite_amd import _lib
+
+    n = _lib.load().sgl_mfma_mix_threads()
+    assert n > 0 and n % 256 == 0
+    outs = {}
+    for v in (0, 1):
+        for it in (1, 2, 4):
+            o = torch.empty(n, dtype=torch.float32, device=gpu)
+            _lib.call("sgl_mfma_mix", v, o.data_ptr(), it, _lib.stream_of(o))
+            outs[v, it] = f32(o)
+    for v in (0, 1):
+        assert np.all(np.isfinite(outs[v, 1])) and np.any(outs[v, 1] != 0)
+        np.testing.assert_array_equal(outs[v, 2], 2 * outs[v, 1])
+        np.testing.assert_array_equal(outs[v, 4], 4 * outs[v, 1])
+    assert not np.array_equal(outs[0, 1], outs[1, 1])  # the promotion scales differ from 1
+
+
 # The 256 x 256 tiles (M > 2048): a partial last M tile whose rows end inside
 # a wavefront's 64 (3000 = 11 x 256 + 184), a last row tile of 8 rows
 # (2056), ragged N (a 16-column last tile: chunks past N are not loaded),
