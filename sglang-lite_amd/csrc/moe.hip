@@ -432,12 +432,16 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(const int32_t* __r
 
 // -------------------------------------------------------------- combine
 
-// One workgroup per token: sum the token's k expert rows (bf16) into fp32 in
-// ascending expert id, add the shared row, round to bf16.  8 columns / thread.
-__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ out,
-                                                      const int32_t* __restrict__ ids, int64_t T,
-                                                      int k, int64_t H, int has_shared, int E,
-                                                      uint16_t* __restrict__ y) {
+// One workgroup per (token, column slice): sum the token's k expert rows
+// (bf16) into fp32 in ascending expert id, add the shared row, round to
+// bf16.  8 columns / thread; workgroup y of gridDim.y takes the column
+// slices y, y + gridDim.y, ... of NT * 8 columns (small batches split the
+// row over several workgroups so the launch still covers the CUs).
+template <int NT>
+__global__ __launch_bounds__(NT) void combine_kernel(const uint16_t* __restrict__ out,
+                                                     const int32_t* __restrict__ ids, int64_t T,
+                                                     int k, int64_t H, int has_shared, int E,
+                                                     uint16_t* __restrict__ y) {
   __shared__ int ord[16];
   __shared__ int nvalid;
   const int64_t t = blockIdx.x;
@@ -461,7 +465,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   const int nv = nvalid;
   const int stride_rows = k + has_shared;
   const uint16_t* base = out + t * stride_rows * H;
-  for (int64_t col = (int64_t)tid * 8; col < H; col += 256 * 8) {
+  for (int64_t col = ((int64_t)blockIdx.y * NT + tid) * 8; col < H; col += (int64_t)gridDim.y * NT * 8) {
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
@@ -487,6 +491,19 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = pk2_bf16_exact(acc[2 * i], acc[2 * i + 1]);
     *reinterpret_cast<uint4*>(y + t * H + col) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// T tokens of H columns: 256-thread workgroups, one per token, from about
+// two per CU; below, 64-thread workgroups over 512-column slices (T = 64,
+// H = 4096: 512 workgroups where one per token gives 64)
+void launch_combine(const uint16_t* out, const int32_t* ids, int64_t T, int k, int64_t H,
+                    int has_shared, int E, uint16_t* y, hipStream_t st) {
+  if (T >= 2 * (int64_t)device_cu_count()) {
+    combine_kernel<256><<<dim3((unsigned)T, 1), 256, 0, st>>>(out, ids, T, k, H, has_shared, E, y);
+  } else {
+    const unsigned slices = (unsigned)ceil_div(H, 64 * 8);
+    combine_kernel<64><<<dim3((unsigned)T, slices), 64, 0, st>>>(out, ids, T, k, H, has_shared, E, y);
   }
 }
 
@@ -824,8 +841,8 @@ int sgl_moe_combine(const void* out, const int32_t* ids, int64_t T, int k, int64
   if (T == 0) return SGL_OK;
   SGL_REQUIRE(out && ids && y, "moe_combine: null pointer");
   SGL_REQUIRE(sgl::aligned(out, 16) && sgl::aligned(y, 16), "moe_combine: out/y misaligned");
-  sgl::combine_kernel<<<(unsigned)T, 256, 0, (hipStream_t)stream>>>(
-      (const uint16_t*)out, ids, T, k, H, has_shared ? 1 : 0, 0x7FFFFFFF, (uint16_t*)y);
+  sgl::launch_combine((const uint16_t*)out, ids, T, k, H, has_shared ? 1 : 0, 0x7FFFFFFF, (uint16_t*)y,
+                      (hipStream_t)stream);
   return sgl::check_launch("moe_combine");
 }
 
@@ -886,8 +903,7 @@ int sgl_moe_forward(const void* x, int64_t T, int64_t H, int64_t I, int E, int k
   if ((rc = sgl::run_down(w.hq, w.hs, T, H, I, E, k, w.offsets, w.sorted_slot, experts, has_shared,
                           expert_format, scale_mode, w.out, w.tile_ctr + 16, st)))
     return rc;
-  sgl::combine_kernel<<<(unsigned)T, 256, 0, st>>>(w.out, ids, T, k, H, has_shared, E,
-                                                    (uint16_t*)y);
+  sgl::launch_combine(w.out, ids, T, k, H, has_shared, E, (uint16_t*)y, st);
   return sgl::check_launch("moe_combine");
 }
 
