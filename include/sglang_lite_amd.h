@@ -94,6 +94,16 @@ enum sgl_expert_format { SGL_EXPERT_FP8_BLOCK128 = 0, SGL_EXPERT_FP4_E2M1 = 1 };
  * exponents inside the MFMA, which accumulates across K blocks in place (no
  * fp32 promotion per 128-deep block). */
 #define SGL_EXPERT_POW2_SCALES 2
+/* Flag OR'ed into expert_format: the experts array holds, after its E routed
+ * (+ shared) records, as many records again for the same experts whose FP8
+ * weight pointers (w_gate, w_up, w_down) address copies in the MFMA fragment
+ * layout written by sgl_fp8_weight_to_frag (scale pointers as in the first
+ * set; records of FP4 routed experts are not read).  The prefill-size FP8
+ * GEMMs with fp32 block scales then load those weights straight into
+ * registers; every other kernel reads the row-major first set.  No
+ * counterpart in the reference: a layout of this build, costing a second copy
+ * of the FP8 expert weights. */
+#define SGL_EXPERT_FRAG_COPY 4
 
 /* Per-expert weight pointers of one MoE layer, stored in DEVICE memory as an
  * array of E routed experts followed by the shared expert; weights and
@@ -214,6 +224,15 @@ int sgl_fp4_gemm(const void* a, const float* sa, int sa_pow2, const void* b, con
  * cast_e2m1fn_to_e4m3fn (the convert.py --expert-dtype fp8 load step). */
 int sgl_fp4_to_fp8_weight(const void* b, const void* sb, int64_t N, int64_t K, void* q,
                           void* s_out, sgl_stream_t stream);
+
+/* e4m3 weight [N, K] row-major -> the MFMA fragment layout that
+ * SGL_EXPERT_FRAG_COPY records point at: one 2 KB block per (16-row block
+ * n16, 128-deep block kb), at block index n16 * (K/128) + kb; byte
+ * j * 1024 + 16 l + b of a block holds w[16 n16 + l % 16][128 kb + 32 (l/16)
+ * + 16 j + b] (l < 64, j < 2, b < 16).  out: N * K bytes, not aliasing w.
+ * N % 16 == 0, K % 128 == 0.  No counterpart in the reference (a one-time
+ * weight layout step of this build, run when the expert table is made). */
+int sgl_fp8_weight_to_frag(const void* w, int64_t N, int64_t K, void* out, sgl_stream_t stream);
 
 /* ------------------------------------------------------------ MoE layer */
 

@@ -1556,6 +1556,601 @@ int launch_pipe(GemmArgs& a, hipStream_t stream) {
   return check_launch("gemm_pipe");
 }
 
+// ------------------------------------------------------------ register-fed weights
+// The grouped FP8 GEMMs at prefill sizes with the expert weights in the MFMA
+// fragment layout (weight_to_frag_kernel below: per 16 rows x 128-deep block,
+// 2 KB that hold lane l's 32 bytes of the block as two 1 KB halves, so each
+// half is one fully coalesced 1 KB load straight into registers).
+//
+// The weight fragments go from memory into registers D = 4 stages ahead of
+// the MFMAs that use them: the register file (512 KB per CU) holds the weight
+// bytes in flight, where the LDS-staged kernels are capped by 160 KB of LDS
+// at two 48 KB stages in flight.  Only the activation rows, which all eight
+// wavefronts share, pass through LDS: loaded into registers four stages
+// ahead, written into one of four 16 KB LDS slots two stages ahead.
+//
+// 128 x 256 tiles (gate/up: 128 rows x (128 gate + 128 up) columns; down:
+// 128 x 256), eight wavefronts side by side along N: wavefront w owns all 128
+// rows and 16 gate + 16 up columns (gate/up) or 32 columns (down), so no
+// weight byte is loaded twice.  Per 128-deep K block the transposed product
+// and fp32 promotion of gemm_pipe_kernel (C += P (sa sb), K blocks in
+// order), so the outputs are bit-identical to it.
+//
+// Every load is an ordinary compiler-visible load, so the compiler's vmcnt
+// waits count them.  The waits stay partial (vmcnt(n) with the younger
+// stages still in flight) only if the count is the same on every path:
+// every stage issues its activation, row-scale and weight loads
+// unconditionally (the last tile re-reads its own first stages for the
+// tile that does not follow), and the output stores are issued outside the
+// compiler's accounting (store_b32 / store_b64: a store the compiler saw
+// would turn its next wait into vmcnt(0), draining the next tile's loads;
+// an extra store in flight can only delay, never satisfy early, a wait for
+// an older load, since loads return in order).  Tiles follow a static order
+// per XCD (no atomic counter, for the same reason; every tile runs all eight
+// row blocks, so the tiles take the same time).  The next tile's tables are
+// prepared at fixed stages of the current tile (K >= 2048: at least 16
+// stages): resolved at stage 5, its row slots and expert record loaded at 6
+// and stored at 10 (with its weight scales and routing weights loaded), its
+// row addresses formed at 11, its weight scales and routing weights stored
+// at 14; its first stages load from stage NST - 4.
+//
+// Stores the compiler does not count (see above).  At most 8 bytes of data:
+// wider stores have a data-overwrite hazard the compiler would not cover.
+__device__ __forceinline__ void store_b32(void* p, uint32_t v) {
+  asm volatile("global_store_dword %0, %1, off" :: "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_b64(void* p, uint2 v) {
+  asm volatile("global_store_dwordx2 %0, %1, off" :: "v"(p), "v"(v) : "memory");
+}
+
+namespace rb {
+constexpr int BM = 128, BN = 256, NW = 8, NT = 64 * NW;
+constexpr int D = 4;      // stages of weight fragments in registers
+constexpr int SLOTS = 4;  // LDS slots of 128-deep activation stages
+constexpr int A_BYTES = BM * 128;
+constexpr int kMinKB = 16, kMaxKBr = 64;
+static_assert(D == 4 && SLOTS == 4, "the stage loop is unrolled by four");
+}  // namespace rb
+
+template <int KIND>
+__global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
+  using namespace rb;
+  static_assert(KIND == KIND_GATE_UP || KIND == KIND_DOWN, "grouped GEMMs only");
+  __shared__ __align__(16) uint8_t sA[SLOTS * A_BYTES];
+  __shared__ __align__(16) float sSa[2][BM * 4];  // row scales of four stages, [row][4]
+  __shared__ int sTstart[kMaxGroups + 1];
+  __shared__ int sOff[kMaxGroups + 1];  // expert row offsets (the shared group's start last)
+  __shared__ int sSlot[2][BM];    // per table buffer: sorted slot of each routed row
+  __shared__ float sRow[2][BM];   // per table buffer: routing weight (gate/up) / output row (down)
+  __shared__ float sAmax[KIND == KIND_GATE_UP ? NW : 1][BM];
+  __shared__ int sTile[2][5];     // per table buffer: valid, e, row0, rows, nt
+  __shared__ float sSb[2][2][kMaxKBr];  // per table buffer: weight scales per K block (gate,
+                                       // up / the blocks of waves 0-3, 4-7)
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g4 = lane >> 4, r16 = lane & 15;
+  const int64_t K = args.K, N = args.N;
+  const int KB = (int)(K / 128);
+  const int NST = KB;
+  const int n_tiles = args.n_tiles;
+  const int G = args.E + (args.has_shared ? 1 : 0);
+  const int64_t shared_base = args.offsets[args.E];
+
+  for (int g = tid; g <= args.E; g += NT) sOff[g] = args.offsets[g];
+  // ---- M-tile prefix over the expert groups (E routed, then the shared one)
+  if (w == 0) {
+    int carry = 0;
+    if (lane == 0) sTstart[0] = 0;
+    for (int base = 0; base < G; base += 64) {
+      const int g = base + lane;
+      int cnt = 0;
+      if (g < args.E)
+        cnt = args.offsets[g + 1] - args.offsets[g];
+      else if (g < G)
+        cnt = (int)args.T;
+      int incl = (cnt + BM - 1) / BM;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += u;
+      }
+      if (g < G) sTstart[g + 1] = carry + incl;
+      carry += __shfl(incl, 63, 64);
+    }
+  }
+  __syncthreads();
+  const int total = sTstart[G] * n_tiles;
+  const int xcd = blockIdx.x & 7, wslot = blockIdx.x >> 3, per_xcd = gridDim.x >> 3;
+  const int per = (total + 7) >> 3;
+  const int t_begin = xcd * per;
+  const int t_end = min(t_begin + per, total);
+
+  // workgroup wslot of an XCD takes its tiles wslot, wslot + per_xcd, ...
+  int static_next = wslot;
+  auto take_tile = [&]() -> int {
+    const int l = static_next;
+    static_next += per_xcd;
+    return l;
+  };
+  struct Tile {
+    int valid, e, row0, rows, nt;
+  };
+  auto resolve = [&](int local) -> Tile {
+    Tile t = {0, 0, 0, 0, 0};
+    const int L = t_begin + local;
+    if (local < 0 || L >= t_end) return t;
+    int lo = 0, hi = G;  // g with sTstart[g] * n_tiles <= L < sTstart[g + 1] * n_tiles
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (sTstart[mid] * n_tiles <= L) lo = mid; else hi = mid;
+    }
+    const int m_in_g = sTstart[lo + 1] - sTstart[lo];
+    const int loc = L - sTstart[lo] * n_tiles;
+    const int nt = loc / m_in_g;
+    const int mt = loc - nt * m_in_g;
+    // LDS only: no global load whose wait would drain the loads in flight
+    const int cnt = lo < args.E ? sOff[lo + 1] - sOff[lo] : (int)args.T;
+    const int base = lo < args.E ? sOff[lo] : (int)shared_base;
+    t.valid = 1;
+    t.e = __builtin_amdgcn_readfirstlane(lo);
+    t.row0 = __builtin_amdgcn_readfirstlane(base + mt * BM);
+    t.rows = __builtin_amdgcn_readfirstlane(min(BM, cnt - mt * BM));
+    t.nt = __builtin_amdgcn_readfirstlane(nt);
+    return t;
+  };
+  auto read_tile = [&](int buf) -> Tile {
+    Tile t;
+    t.valid = __builtin_amdgcn_readfirstlane(sTile[buf][0]);
+    t.e = __builtin_amdgcn_readfirstlane(sTile[buf][1]);
+    t.row0 = __builtin_amdgcn_readfirstlane(sTile[buf][2]);
+    t.rows = __builtin_amdgcn_readfirstlane(sTile[buf][3]);
+    t.nt = __builtin_amdgcn_readfirstlane(sTile[buf][4]);
+    return t;
+  };
+  auto write_tile = [&](int buf, const Tile& t) {
+    sTile[buf][0] = t.valid;
+    sTile[buf][1] = t.e;
+    sTile[buf][2] = t.row0;
+    sTile[buf][3] = t.rows;
+    sTile[buf][4] = t.nt;
+  };
+  // the epilogue value of tile row i (routed rows: of sorted slot sl): down the
+  // output row t (k + shared) + j, as float bits
+  auto out_row = [&](const Tile& t, int i, int sl) -> float {
+    const int p = t.row0 + (i < t.rows ? i : 0);
+    const int tok = t.e < args.E ? sl / args.k : p - (int)shared_base;
+    const int j = t.e < args.E ? sl - tok * args.k : args.k;
+    return __int_as_float(tok * args.out_k + j);
+  };
+  // uniform 64-bit field f of expert record e (scalar loads: the table is
+  // read-only for the kernel)
+  typedef __attribute__((address_space(4))) const uint64_t* cptr64;
+  auto rec_field = [&](const sgl_expert_ptrs* tab, int e, int f) -> uint64_t {
+    return *((cptr64)(uintptr_t)(tab + e) + f);
+  };
+
+  // ---- per-tile load sources of this wavefront
+  const int ra = 16 * w + (lane >> 3), rb_ = ra + 8, ch = lane & 7;
+  const uint32_t lds_a = (uint32_t)(ra * 128 + ((ch ^ swz(ra)) << 4));
+  const uint32_t lds_b = (uint32_t)(rb_ * 128 + ((ch ^ swz(rb_)) << 4));
+  struct Src {
+    uint32_t a0, a1;  // rows ra and ra + 8 of the tile: byte offset of (row, 16 ch) in A
+    uint32_t sa;      // waves 0, 1: offset (floats) of row 64 w + lane's row scales
+    uint64_t b0, b1;  // (uniform) weight fragment blocks (n16, 0): gate / first, up / second
+  };
+  // source row of tile row r (rows past the tile's last re-read its first)
+  auto src_row = [&](const Tile& t, int buf, int r) -> int64_t {
+    const int rc = r < t.rows ? r : 0;
+    const int p = t.row0 + rc;
+    if constexpr (KIND == KIND_GATE_UP) return t.e < args.E ? sSlot[buf][rc] / args.k : p - shared_base;
+    else return p;
+  };
+  // row offsets of tile t (its slots in sSlot[buf]); T K < 2^31 and rows K < 2^31
+  auto rows_of = [&](Src& s, const Tile& t, int buf) {
+    s.a0 = (uint32_t)(src_row(t, buf, ra) * K + ch * 16);
+    s.a1 = (uint32_t)(src_row(t, buf, rb_) * K + ch * 16);
+    s.sa = (uint32_t)((w < 2 ? src_row(t, buf, 64 * w + lane) : 0) * KB);
+  };
+  // a global (not flat) fp32 load: a flat load also counts in lgkmcnt and is
+  // a different kind of event for the compiler's waits, which then fall back
+  // to vmcnt(0)
+  auto ldg_f32 = [&](uint64_t base, int64_t i) -> float {
+    return ((__attribute__((address_space(1))) const float*)(uintptr_t)base)[i];
+  };
+  // weight bases and (loads of) the weight scales of tile t: lane kb gets
+  // those of K block kb in sb0, sb1
+  auto weights_of = [&](Src& s, const Tile& t, float& sb0, float& sb1) {
+    const int kbl = lane < KB ? lane : KB - 1;
+    if constexpr (KIND == KIND_GATE_UP) {
+      const int64_t n16 = (int64_t)t.nt * 8 + w;
+      s.b0 = rec_field(args.frag, t.e, 0) + (uint64_t)(n16 * KB * 2048);
+      s.b1 = rec_field(args.frag, t.e, 1) + (uint64_t)(n16 * KB * 2048);
+      sb0 = ldg_f32(rec_field(args.experts, t.e, 3), (int64_t)t.nt * KB + kbl);
+      sb1 = ldg_f32(rec_field(args.experts, t.e, 4), (int64_t)t.nt * KB + kbl);
+    } else {
+      const int64_t nb16 = N / 16;
+      int64_t n16 = (int64_t)t.nt * 16 + 2 * w;
+      if (n16 > nb16 - 2) n16 = nb16 - 2;  // columns past N (not stored) re-read the last blocks
+      s.b0 = rec_field(args.frag, t.e, 2) + (uint64_t)(n16 * KB * 2048);
+      s.b1 = s.b0 + (uint64_t)KB * 2048;
+      const int64_t nb = (N + 127) / 128;
+      int64_t blk = ((int64_t)t.nt * BN + 32 * w) / 128;
+      if (blk > nb - 1) blk = nb - 1;
+      sb0 = ldg_f32(rec_field(args.experts, t.e, 5), blk * KB + kbl);
+      sb1 = sb0;
+    }
+  };
+  const uint32_t lane16 = (uint32_t)lane * 16;
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  auto ld_sa = [&](uint32_t off) -> float4 {
+    const f4v v = *(__attribute__((address_space(1))) const f4v*)(
+        (__attribute__((address_space(1))) const float*)(uintptr_t)args.sa + off);
+    return make_float4(v.x, v.y, v.z, v.w);
+  };
+  // global (not flat) loads: a flat load would also count in lgkmcnt, which
+  // the LDS waits drain
+  typedef int i4v __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(1))) const uint8_t gbyte;
+  typedef __attribute__((address_space(1))) const i4v gi4v;
+  gbyte* const a_g = (gbyte*)(uintptr_t)args.a;
+  auto ldA = [&](uint32_t off) -> uint4 {
+    const i4v v = *(gi4v*)(a_g + off);
+    return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+  };
+  auto ldB = [&](uint64_t base, uint32_t off) -> v8i {
+    gbyte* p = (gbyte*)(uintptr_t)base;
+    const i4v lo = *(gi4v*)(p + (lane16 + off));
+    const i4v hi = *(gi4v*)(p + (lane16 + off + 1024u));
+    return v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  };
+  // the tile's weight scales into sSb[buf]: gate/up waves 0 (gate) and 1
+  // (up), down waves 0 and 4 (their 128-column blocks)
+  auto put_scales = [&](int buf, float sb0, float sb1) {
+    if (lane < KB) {
+      if constexpr (KIND == KIND_GATE_UP) {
+        if (w == 0) sSb[buf][0][lane] = sb0;
+        if (w == 1) sSb[buf][1][lane] = sb1;
+      } else {
+        if ((w & 3) == 0) sSb[buf][w >> 2][lane] = sb0;
+      }
+    }
+  };
+
+  // ---- the first tile, with plain loads
+  int nidx = 0;  // wave 0 lane 0: the local index of the tile after the current one
+  if (w == 0) {
+    int first = 0;
+    if (lane == 0) {
+      first = take_tile();
+      nidx = take_tile();
+    }
+    const Tile t0 = resolve(__builtin_amdgcn_readfirstlane(__shfl(first, 0, 64)));
+    if (lane == 0) write_tile(0, t0);
+  }
+  __syncthreads();
+  Tile tc = read_tile(0);
+  if (!tc.valid) return;
+  if (lane < 16) {
+    const int i = 16 * w + lane;
+    const int sl = (tc.e < args.E && i < tc.rows) ? args.sorted_slot[tc.row0 + i] : 0;
+    sSlot[0][i] = sl;
+    if constexpr (KIND == KIND_GATE_UP)
+      sRow[0][i] = (tc.e < args.E && args.route_w) ? args.route_w[sl] : 1.0f;
+    else
+      sRow[0][i] = out_row(tc, i, sl);
+  }
+  __syncthreads();
+  Src cs, ns;
+  float nsb0, nsb1;
+  rows_of(cs, tc, 0);
+  weights_of(cs, tc, nsb0, nsb1);
+  put_scales(0, nsb0, nsb1);
+  ns = cs;
+
+  v8i bq[D][2];
+  uint4 aq[2][2];
+  float4 sq = make_float4(0.f, 0.f, 0.f, 0.f);
+  {
+    // stages 0 and 1 into LDS slots 0 and 1, row scales of stages 0..3
+    aq[0][0] = ldA(cs.a0);
+    aq[0][1] = ldA(cs.a1);
+    aq[1][0] = ldA(cs.a0 + 128);
+    aq[1][1] = ldA(cs.a1 + 128);
+    sq = ld_sa(cs.sa);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      *reinterpret_cast<uint4*>(sA + j * A_BYTES + lds_a) = aq[j][0];
+      *reinterpret_cast<uint4*>(sA + j * A_BYTES + lds_b) = aq[j][1];
+    }
+    if (w < 2) *reinterpret_cast<float4*>(&sSa[0][(64 * w + lane) * 4]) = sq;
+    aq[0][0] = ldA(cs.a0 + 2 * 128);
+    aq[0][1] = ldA(cs.a1 + 2 * 128);
+    aq[1][0] = ldA(cs.a0 + 3 * 128);
+    aq[1][1] = ldA(cs.a1 + 3 * 128);
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      bq[s][0] = ldB(cs.b0, s * 2048);
+      bq[s][1] = ldB(cs.b1, s * 2048);
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  const FragLane fl = frag_lane(r16, g4);
+  const v4f vzero = {0.0f, 0.0f, 0.0f, 0.0f};
+  int tb = 0;    // table buffer of the current tile
+  int gpar = 0;  // row-scale buffer of the current tile's first four stages
+  float nrw = 0.0f;
+  int nslot = 0;
+  Tile tn = {0, 0, 0, 0, 0};
+
+  for (;;) {
+    v4f acc[8][2];
+#pragma unroll
+    for (int mi = 0; mi < 8; ++mi) acc[mi][0] = acc[mi][1] = vzero;
+
+    auto stage = [&](auto jc, const int st) {
+      constexpr int J = decltype(jc)::value;
+      // -- 1. consumers of earlier table loads, then table work of this stage
+      if constexpr (J == 1) {
+        if (st == 5 && w == 0) {
+          const Tile t = resolve(__builtin_amdgcn_readfirstlane(__shfl(nidx, 0, 64)));
+          if (lane == 0) write_tile(tb ^ 1, t);
+        }
+      }
+      if constexpr (J == 2) {
+        if (st == 10 && tn.valid && lane < 16) {
+          const int i = 16 * w + lane;
+          sSlot[tb ^ 1][i] = nslot;
+          if constexpr (KIND == KIND_DOWN) sRow[tb ^ 1][i] = out_row(tn, i, nslot);
+        }
+        if (st == 14 && tn.valid) {
+          put_scales(tb ^ 1, nsb0, nsb1);
+          if constexpr (KIND == KIND_GATE_UP)
+            if (lane < 16) sRow[tb ^ 1][16 * w + lane] = (tn.e < args.E && args.route_w) ? nrw : 1.0f;
+        }
+      }
+      if constexpr (J == 3) {
+        if (st == 11 && tn.valid) rows_of(ns, tn, tb ^ 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // -- 2. activation stage st + 2 into LDS slot (J + 2) % 4 (and at J == 2
+      //       the row scales of stages st + 2 .. st + 5)
+      const int s2 = st + 2;
+      {
+        uint8_t* dst = sA + ((J + 2) & 3) * A_BYTES;
+        *reinterpret_cast<uint4*>(dst + lds_a) = aq[J & 1][0];
+        *reinterpret_cast<uint4*>(dst + lds_b) = aq[J & 1][1];
+        if constexpr (J == 2) {
+          const int grp = s2 < NST ? (s2 >> 2) : (NST >> 2);
+          if (w < 2) *reinterpret_cast<float4*>(&sSa[(gpar + grp) & 1][(64 * w + lane) * 4]) = sq;
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // -- 3. loads of activation stage st + 4 (at J == 0 also its row scales)
+      const int s4 = st + 4;
+      const bool cur4 = s4 < NST;
+      {
+        const uint32_t off = (uint32_t)(cur4 ? s4 : s4 - NST) * 128u;
+        aq[J & 1][0] = ldA((cur4 ? cs.a0 : ns.a0) + off);
+        aq[J & 1][1] = ldA((cur4 ? cs.a1 : ns.a1) + off);
+        if constexpr (J == 0) sq = ld_sa(cur4 ? cs.sa + s4 : ns.sa + (s4 - NST));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // -- 4. the MFMAs of stage st
+      {
+        const uint8_t* stg = sA + J * A_BYTES;
+        const float* sS = &sSa[(gpar + (st >> 2)) & 1][0];
+        const float sb0 = sSb[tb][KIND == KIND_GATE_UP ? 0 : (w >> 2)][st];
+        const float sb1 = KIND == KIND_GATE_UP ? sSb[tb][1][st] : sb0;
+        // software-pipelined over the 16-row blocks, each block a scheduling
+        // region of its own (the compiler would otherwise hoist all eight
+        // fragment reads and sixteen products at once and spill): block
+        // mi + 1's fragment is read and block mi - 1 promoted while block
+        // mi's MFMAs run.  Every block is computed, also those past the
+        // tile's rows (a remainder tile's padding rows re-read its first
+        // row; their results are not stored).
+        v8i af[2];
+        v4f pr[2][2];
+        float sv[8];  // block mi's row scale, read one block ahead (three live at most)
+        af[0] = read_frag(stg, fl);
+        sv[0] = sS[r16 * 4 + J];
+        __builtin_amdgcn_sched_barrier(0);
+        auto promote = [&](int mi) {
+          const int b = mi & 1;
+          const float s0 = sv[mi] * sb0, s1 = sv[mi] * sb1;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            acc[mi][0][r] = fmaf(pr[b][0][r], s0, acc[mi][0][r]);
+            acc[mi][1][r] = fmaf(pr[b][1][r], s1, acc[mi][1][r]);
+          }
+          // keep the promotion here: left alone, the compiler sinks the
+          // accumulator chains past the stage, keeps every product and spills
+          asm volatile("" : "+v"(acc[mi][0]), "+v"(acc[mi][1]));
+        };
+#pragma unroll
+        for (int mi = 0; mi < 8; ++mi) {
+          const int b = mi & 1;
+          if (mi < 7) {
+            af[b ^ 1] = read_frag(stg + (mi + 1) * 16 * 128, fl);
+            sv[mi + 1] = sS[((mi + 1) * 16 + r16) * 4 + J];
+          }
+          pr[b][0] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bq[J][0], af[b], vzero, 0, 0, 0, 0, 0, 0);
+          pr[b][1] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bq[J][1], af[b], vzero, 0, 0, 0, 0, 0, 0);
+          if (mi > 0) promote(mi - 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        promote(7);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // -- 5. weight fragments of stage st + 4 into the freed registers
+      {
+        const uint32_t off = (uint32_t)(cur4 ? s4 : s4 - NST) * 2048u;
+        bq[J][0] = ldB(cur4 ? cs.b0 : ns.b0, off);
+        bq[J][1] = ldB(cur4 ? cs.b1 : ns.b1, off);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // -- 6. table loads for the next tile (consumed four stages later; the
+      //       stage-10 block precedes the stage-6 one, so no path runs from
+      //       the slot loads to their use without passing four stages)
+      if constexpr (J == 2) {
+        if (st == 10 && tn.valid) {
+          weights_of(ns, tn, nsb0, nsb1);
+          if constexpr (KIND == KIND_GATE_UP)
+            if (lane < 16 && tn.e < args.E && args.route_w) nrw = args.route_w[nslot];
+        }
+        if (st == 6) {
+          tn = read_tile(tb ^ 1);
+          if (tn.valid && lane < 16) {
+            const int i = 16 * w + lane;
+            nslot = (tn.e < args.E && i < tn.rows) ? args.sorted_slot[tn.row0 + i] : 0;
+          }
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    for (int st0 = 0; st0 < NST; st0 += 4) {
+      stage(std::integral_constant<int, 0>{}, st0);
+      stage(std::integral_constant<int, 1>{}, st0 + 1);
+      stage(std::integral_constant<int, 2>{}, st0 + 2);
+      stage(std::integral_constant<int, 3>{}, st0 + 3);
+    }
+
+    // ---- epilogue from registers
+    const int rows = tc.rows;
+    if constexpr (KIND == KIND_DOWN) {
+      const int64_t n0 = (int64_t)tc.nt * BN + 32 * w;
+#pragma unroll
+      for (int mi = 0; mi < 8; ++mi) {
+        const int row = mi * 16 + r16;
+        if (row < rows) {
+          const int64_t drow = __float_as_int(sRow[tb][row]);
+#pragma unroll
+          for (int f = 0; f < 2; ++f) {
+            const int64_t col = n0 + 16 * f + 4 * g4;
+            if (col < N) {
+              const v4f v = acc[mi][f];
+              store_b64(reinterpret_cast<uint16_t*>(args.c) + drow * N + col,
+                        make_uint2(pk2_bf16_exact(v[0], v[1]), pk2_bf16_exact(v[2], v[3])));
+            }
+          }
+        }
+      }
+    } else {
+      // SwiGLU + 1x128 requant (as gemm_pipe_kernel): h kept as packed bf16
+      // pairs across the barrier that publishes the row maxima
+      const float lim = args.swiglu_limit;
+      uint32_t h2[8][2];
+      auto swiglu = [&](auto clamp_c) {
+        constexpr bool CLAMP = decltype(clamp_c)::value;
+#pragma unroll
+        for (int mi = 0; mi < 8; ++mi) {
+          const int row = mi * 16 + r16;
+          const float wr = sRow[tb][row];
+          float am = 0.0f;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float gt = bf16_round(acc[mi][0][r]);
+            float up = bf16_round(acc[mi][1][r]);
+            if constexpr (CLAMP) {
+              up = clampf_(up, -lim, lim);
+              gt = gt > lim ? lim : gt;
+            }
+            const float ex = __builtin_amdgcn_exp2f(gt * -1.4426950408889634f);
+            const float silu = gt * __builtin_amdgcn_rcpf(1.0f + ex);
+            const uint32_t hb = bf16_bits_exact(wr * (silu * up));
+            if (r & 1)
+              h2[mi][r >> 1] |= hb << 16;
+            else
+              h2[mi][r >> 1] = hb;
+            am = __builtin_elementwise_maximum(am, fabsf(bits_f32(hb << 16)));
+          }
+          am = __builtin_elementwise_maximum(am, __shfl_xor(am, 16, 64));
+          am = __builtin_elementwise_maximum(am, __shfl_xor(am, 32, 64));
+          if (g4 == 0) sAmax[w][row] = am;
+          // one row block at a time: a spill here would be a scratch access,
+          // whose wait drains the next tile's loads in flight
+          asm volatile("" : "+v"(h2[mi][0]), "+v"(h2[mi][1]));
+        }
+      };
+      if (lim > 0.0f) swiglu(std::true_type{});
+      else swiglu(std::false_type{});
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      const int64_t NB = N / 128;
+      const int64_t n0 = (int64_t)tc.nt * 128;
+      auto requant = [&](auto mode_c) {
+        constexpr int MODE = decltype(mode_c)::value;
+#pragma unroll
+        for (int mi = 0; mi < 8; ++mi) {
+          const int row = mi * 16 + r16;
+          if (row < rows) {
+            float am = sAmax[0][row];
+#pragma unroll
+            for (int q = 1; q < NW; ++q) am = __builtin_elementwise_maximum(am, sAmax[q][row]);
+            const float sf = group_scale(MODE, am);
+            float hf[4];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              hf[2 * q] = bits_f32(h2[mi][q] << 16);
+              hf[2 * q + 1] = bits_f32(h2[mi][q] & 0xFFFF0000u);
+            }
+            const int64_t p = tc.row0 + row;
+            store_b32(args.hq + p * N + n0 + 16 * w + 4 * g4, quant4_e4m3(MODE, hf, sf));
+            if (w == 0 && g4 == 0) store_b32(args.hs + p * NB + tc.nt, __float_as_uint(sf));
+          }
+        }
+      };
+      switch (args.scale_mode) {
+        case SCALE_TORCH_FP32: requant(std::integral_constant<int, SCALE_TORCH_FP32>{}); break;
+        case SCALE_TORCH_UE8M0: requant(std::integral_constant<int, SCALE_TORCH_UE8M0>{}); break;
+        case SCALE_TILELANG_FP32: requant(std::integral_constant<int, SCALE_TILELANG_FP32>{}); break;
+        default: requant(std::integral_constant<int, SCALE_TILELANG_UE8M0>{}); break;
+      }
+    }
+    if (!tn.valid) break;
+    if (w == 0 && lane == 0) nidx = take_tile();  // the tile after the next one
+    tc = tn;
+    cs = ns;
+    tb ^= 1;
+    gpar = (gpar + (NST >> 2)) & 1;
+  }
+}
+
+template <int KIND>
+int launch_rb(GemmArgs& a, hipStream_t stream) {
+  using namespace rb;
+  a.n_tiles = (int)ceil_div(a.N, KIND == KIND_GATE_UP ? 128 : BN);
+  const int64_t P = a.E > 0 ? a.T * a.k : 0;
+  const int64_t mt_bound = P / BM + (P < a.E ? P : a.E) + (a.has_shared ? ceil_div(a.T, BM) : 0);
+  const int64_t tiles = mt_bound * a.n_tiles;
+  if (tiles == 0) return SGL_OK;
+  int64_t wgs = (int64_t)device_cu_count();
+  wgs = (wgs + 7) / 8 * 8;
+  const int64_t need = (tiles + 7) / 8 * 8;
+  if (need < wgs) wgs = need;
+  a.m_tiles = (int)mt_bound;
+  gemm_rb_kernel<KIND><<<(unsigned)wgs, NT, 0, stream>>>(a);
+  return check_launch("gemm_rb");
+}
+
+// [N, K] e4m3 row-major -> the MFMA fragment layout: 2 KB per (16-row block
+// n16, 128-deep block kb), block index n16 * K/128 + kb; byte
+// j * 1024 + 16 l + b of a block holds row 16 n16 + l % 16, column
+// 128 kb + 32 (l / 16) + 16 j + b (lane l's bytes of the operand, as
+// read_frag assembles them from an LDS stage).
+__global__ __launch_bounds__(256) void weight_to_frag_kernel(const uint8_t* __restrict__ w, int64_t N,
+                                                             int64_t K, uint8_t* __restrict__ out) {
+  const int64_t chunk = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 16-byte output chunk
+  if (chunk >= N * K / 16) return;
+  const int64_t KB = K / 128;
+  const int64_t blk = chunk >> 7;
+  const int j = (int)((chunk >> 6) & 1), l = (int)(chunk & 63);
+  const int64_t n16 = blk / KB, kb = blk - n16 * KB;
+  const int64_t n = n16 * 16 + (l & 15);
+  const int64_t k = kb * 128 + (l >> 4) * 32 + j * 16;
+  *reinterpret_cast<uint4*>(out + chunk * 16) = *reinterpret_cast<const uint4*>(w + n * K + k);
+}
+
 // ------------------------------------------------------------ wide tiles
 // Dense products from M = 2048 up: 256 x 256 tiles, eight wavefronts (4 x 2,
 // 64 x 128 each, two per SIMD with 256 registers) and a 2-slot ring of 64 KB
@@ -1811,6 +2406,9 @@ int launch_cfg(GemmArgs& a, hipStream_t stream) {
 // enough to keep every CU streaming where the 128 x 256 tiles leave most idle.
 #ifndef SGL_LW
 #define SGL_LW 4
+#endif
+#ifndef SGL_RB
+#define SGL_RB 1
 #endif
 #ifndef SGL_PIPE
 #define SGL_PIPE 1
@@ -2324,6 +2922,12 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
   // both scales powers of two: the pipelined kernel applies them in the MFMA
   // (other kernels promote in fp32, exact for such scales too)
   const bool pow2 = a.sa_pow2 && a.sb_pow2;
+  // register-fed weights: the experts' fragment-layout copies, 16 to 64
+  // stages in multiples of four, fp32 promotion (the power-of-two path stays
+  // on the pipelined kernel), 16-byte aligned row scales for their float4 loads
+  const int64_t kb = a.K / 128;
+  const bool rb_ok = SGL_RB && a.frag && !pow2 && !a.sb_e8m0 && kb >= rb::kMinKB &&
+                     kb <= rb::kMaxKBr && kb % 4 == 0 && aligned(a.sa, 16);
   switch (kind) {
     case KIND_DENSE: {
       const int rc = SGL_SPLITK ? try_splitk(a, stream) : -1;
@@ -2350,11 +2954,13 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       return launch_wide(a, stream);
     }
     case KIND_GATE_UP:
+      if (big && rb_ok) return launch_rb<KIND_GATE_UP>(a, stream);
       if (big && pipe_ok)
         return pow2 ? launch_pipe<KIND_GATE_UP, true>(a, stream) : launch_pipe<KIND_GATE_UP, false>(a, stream);
       return big ? launch_cfg<KIND_GATE_UP, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)
                  : launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 4>(a, stream);
     default:
+      if (big && rb_ok) return launch_rb<KIND_DOWN>(a, stream);
       if (big && pipe_ok)
         return pow2 ? launch_pipe<KIND_DOWN, true>(a, stream) : launch_pipe<KIND_DOWN, false>(a, stream);
       return big ? launch_cfg<KIND_DOWN, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)
@@ -2420,4 +3026,22 @@ extern "C" int sgl_fp4_gemm(const void* a, const float* sa, int sa_pow2, const v
   g.c = c;
   g.out_f32 = out_dtype == SGL_F32;
   return sgl::launch_gemm(sgl::KIND_DENSE, g, M, (hipStream_t)stream);
+}
+
+extern "C" int sgl_fp8_weight_to_frag(const void* w, int64_t N, int64_t K, void* out,
+                                      sgl_stream_t stream) {
+  SGL_REQUIRE(N >= 0 && K >= 0, "fp8_weight_to_frag: negative shape");
+  SGL_REQUIRE(N % 16 == 0 && K % 128 == 0,
+              "fp8_weight_to_frag: N=%lld must be a multiple of 16 and K=%lld of 128", (long long)N,
+              (long long)K);
+  if (N == 0 || K == 0) return SGL_OK;
+  SGL_REQUIRE(w && out, "fp8_weight_to_frag: null pointer");
+  SGL_REQUIRE(w != out, "fp8_weight_to_frag: the output must not alias the input");
+  SGL_REQUIRE(sgl::aligned(w, 16) && sgl::aligned(out, 16),
+              "fp8_weight_to_frag: w and out must be 16-byte aligned");
+  SGL_REQUIRE(N * K < ((int64_t)1 << 36), "fp8_weight_to_frag: matrix too large");
+  const int64_t chunks = N * K / 16;
+  sgl::weight_to_frag_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      (const uint8_t*)w, N, K, (uint8_t*)out);
+  return sgl::check_launch("fp8_weight_to_frag");
 }

@@ -590,8 +590,9 @@ MoeWorkspace carve(void* base, int64_t T, int64_t H, int64_t I, int E, int k, in
 }
 
 // The routed experts' format without the power-of-two flag.
+constexpr int kExpertFlags = SGL_EXPERT_POW2_SCALES | SGL_EXPERT_FRAG_COPY;
 bool fp4_experts(int expert_format) {
-  return (expert_format & ~SGL_EXPERT_POW2_SCALES) == SGL_EXPERT_FP4_E2M1;
+  return (expert_format & ~kExpertFlags) == SGL_EXPERT_FP4_E2M1;
 }
 
 int check_moe_shapes(const char* what, int64_t T, int64_t H, int64_t I, int E, int k,
@@ -599,8 +600,8 @@ int check_moe_shapes(const char* what, int64_t T, int64_t H, int64_t I, int E, i
   SGL_REQUIRE(T >= 0 && H > 0 && I > 0, "%s: bad shape T=%lld H=%lld I=%lld", what, (long long)T,
               (long long)H, (long long)I);
   SGL_REQUIRE(H % 128 == 0 && I % 128 == 0, "%s: H and I must be multiples of 128", what);
-  SGL_REQUIRE((expert_format & ~SGL_EXPERT_POW2_SCALES) == SGL_EXPERT_FP8_BLOCK128 ||
-                  (expert_format & ~SGL_EXPERT_POW2_SCALES) == SGL_EXPERT_FP4_E2M1,
+  SGL_REQUIRE((expert_format & ~kExpertFlags) == SGL_EXPERT_FP8_BLOCK128 ||
+                  (expert_format & ~kExpertFlags) == SGL_EXPERT_FP4_E2M1,
               "%s: bad expert_format %d", what, expert_format);
   SGL_REQUIRE(!fp4_experts(expert_format) || (H % 256 == 0 && I % 256 == 0),
               "%s: FP4 experts need H and I multiples of 256", what);
@@ -690,11 +691,17 @@ int run_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I
   g.sa_pow2 = pow2_scale_mode(scale_mode);
   g.sb_pow2 = split ? 0 : pow2w;
   g.tile_ctr = tile_ctr;
+  // the fragment-layout records follow the E (+ shared) row-major ones; the
+  // routed FP4 experts have none that a kernel reads
+  const sgl_expert_ptrs* frag =
+      (expert_format & SGL_EXPERT_FRAG_COPY) ? experts + E + (has_shared ? 1 : 0) : nullptr;
+  g.frag = split ? nullptr : frag;
   if ((rc = launch_gemm(KIND_GATE_UP, g, T * k / E, stream)) || !split || !has_shared) return rc;
   GemmArgs sh = g;  // the shared expert: one group whose rows start at offsets[E]
   sh.E = 0;
   sh.offsets = offsets + E;
   sh.experts = experts + E;
+  sh.frag = frag ? frag + E : nullptr;
   sh.has_shared = 1;
   sh.wfmt = WF_FP8;
   sh.sb_pow2 = pow2w;
@@ -731,11 +738,15 @@ int run_down(const void* hq, const float* hs, int64_t T, int64_t H, int64_t I, i
   g.sa_pow2 = pow2_scale_mode(scale_mode);
   g.sb_pow2 = split ? 0 : pow2w;
   g.tile_ctr = tile_ctr;
+  const sgl_expert_ptrs* frag =
+      (expert_format & SGL_EXPERT_FRAG_COPY) ? experts + E + (has_shared ? 1 : 0) : nullptr;
+  g.frag = split ? nullptr : frag;
   if ((rc = launch_gemm(KIND_DOWN, g, T * k / E, stream)) || !split || !has_shared) return rc;
   GemmArgs sh = g;
   sh.E = 0;
   sh.offsets = offsets + E;
   sh.experts = experts + E;
+  sh.frag = frag ? frag + E : nullptr;
   sh.has_shared = 1;
   sh.wfmt = WF_FP8;
   sh.sb_pow2 = pow2w;

@@ -245,6 +245,23 @@ __device__ __forceinline__ uint2 quant8_e4m3(int mode, const float* f, float sf)
   }
   return make_uint2(pk4_e4m3_exact(y[0], y[1], y[2], y[3]), pk4_e4m3_exact(y[4], y[5], y[6], y[7]));
 }
+// The same arithmetic for four values (four consecutive e4m3 bytes).
+__device__ __forceinline__ uint32_t quant4_e4m3(int mode, const float* f, float sf) {
+  float y[4];
+  if (mode == SCALE_TILELANG_FP32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = clampf_(f[i] / sf, -448.0f, 448.0f);
+  } else {
+    const float inv = 1.0f / sf;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = f[i] * inv;
+    if (mode != SCALE_TORCH_FP32 && mode != SCALE_TORCH_UE8M0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] = clampf_(y[i], -448.0f, 448.0f);
+    }
+  }
+  return pk4_e4m3_exact(y[0], y[1], y[2], y[3]);
+}
 #endif
 
 }  // namespace sgl

@@ -39,6 +39,7 @@ KV_LAYOUT_A, KV_LAYOUT_B = 0, 1
 # sgl_expert_format
 EXPERT_FP8_BLOCK128, EXPERT_FP4_E2M1 = 0, 1
 EXPERT_POW2_SCALES = 2  # flag: every FP8 block scale is a power of two
+EXPERT_FRAG_COPY = 4  # flag: a second record set with the FP8 weights in the MFMA fragment layout
 # sgl_attn_kv_format
 ATTN_KV_BF16, ATTN_KV_A, ATTN_KV_A_PAGED = 0, 1, 2
 
@@ -60,6 +61,7 @@ SIGNATURES = {
     "sgl_fp8_gemm": (c_int, [P, P, P, P, c_int, P, c_int, I64, I64, I64, P]),
     "sgl_fp4_gemm": (c_int, [P, P, c_int, P, P, P, c_int, I64, I64, I64, P]),
     "sgl_fp4_to_fp8_weight": (c_int, [P, P, I64, I64, P, P, P]),
+    "sgl_fp8_weight_to_frag": (c_int, [P, I64, I64, P, P]),
     "sgl_moe_route_topk": (c_int, [P, I64, c_int, c_int, c_int, P, c_float, P, P, P]),
     "sgl_moe_gate": (
         c_int,

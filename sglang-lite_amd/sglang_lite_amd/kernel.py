@@ -119,6 +119,21 @@ def e8m0_to_f32(s: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def fp8_weight_to_frag(w: torch.Tensor) -> torch.Tensor:
+    """e4m3 weight [N, K] -> a new [N * K] uint8 tensor in the MFMA fragment
+    layout of ``sgl_fp8_weight_to_frag`` (2 KB per 16-row x 128-deep block,
+    lane-major), the layout ``EXPERT_FRAG_COPY`` expert records point at.
+    A layout step of this build with no counterpart in the reference."""
+    _lib.require_device(w, what="fp8_weight_to_frag")
+    if w.dtype != FP8 or w.dim() != 2:
+        raise TypeError("fp8_weight_to_frag: w must be a 2-D float8_e4m3fn tensor")
+    src = w.contiguous()
+    N, K = src.shape
+    out = torch.empty(N * K, dtype=torch.uint8, device=src.device)
+    _lib.call("sgl_fp8_weight_to_frag", src.data_ptr(), N, K, out.data_ptr(), _lib.stream_of(src))
+    return out
+
+
 def _scale_flag(t: torch.Tensor, what: str) -> int:
     if t.dtype == torch.float32:
         return 0

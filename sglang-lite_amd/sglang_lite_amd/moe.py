@@ -23,7 +23,7 @@ from typing import List, Optional, Sequence, Tuple
 import torch
 
 from . import _lib
-from .kernel import FP4, FP8, E8M0, e8m0_to_f32, fp4_bytes, fp4_weight_scale
+from .kernel import FP4, FP8, E8M0, e8m0_to_f32, fp4_bytes, fp4_weight_scale, fp8_weight_to_frag
 
 SCORE_FUNCS = {"softmax": _lib.SCORE_SOFTMAX, "sigmoid": _lib.SCORE_SIGMOID,
                "sqrtsoftplus": _lib.SCORE_SQRTSOFTPLUS}
@@ -65,7 +65,8 @@ class ExpertTable:
 
     @staticmethod
     def build(experts: Sequence[Tuple[torch.Tensor, ...]],
-              shared: Optional[Tuple[torch.Tensor, ...]] = None) -> "ExpertTable":
+              shared: Optional[Tuple[torch.Tensor, ...]] = None,
+              frag_layout: bool = False) -> "ExpertTable":
         """``experts``: per expert ``(w1, w3, w2, s1, s3, s2)``, either FP8 (w1/w3
         e4m3 [I, H], w2 e4m3 [H, I], 128x128 scales fp32 or e8m0) or FP4 (w1/w3
         packed e2m1 [I, H/2], w2 [H, I/2] as float4_e2m1fn_x2 / int8 / uint8,
@@ -75,7 +76,13 @@ class ExpertTable:
         When every FP8 scale is a power of two (e8m0, as model.py:138-142
         stores them, or fp32 without mantissa bits) the table carries
         ``EXPERT_POW2_SCALES``: with a power-of-two activation ``scale_mode``
-        the FP8 GEMMs then apply both scales inside the MFMA."""
+        the FP8 GEMMs then apply both scales inside the MFMA.
+
+        ``frag_layout``: also keep a copy of every FP8 expert weight (routed
+        FP8 and shared) in the MFMA fragment layout (``fp8_weight_to_frag``)
+        and add their records after the first set (``EXPERT_FRAG_COPY``): the
+        prefill-size FP8 GEMMs with fp32 block scales then load those weights
+        straight into registers.  Costs a second copy of the FP8 weights."""
         rows = list(experts) + ([shared] if shared is not None else [])
         if not rows:
             raise ValueError("ExpertTable needs at least one expert")
@@ -111,10 +118,22 @@ class ExpertTable:
             keep += [*ws, *fs]
             vals.append([ws[0].data_ptr(), ws[1].data_ptr(), ws[2].data_ptr(),
                          fs[0].data_ptr(), fs[1].data_ptr(), fs[2].data_ptr()])
+        if frag_layout:
+            if H % 128 or I % 128:
+                raise ValueError("frag_layout needs H and I multiples of 128")
+            for i, r in enumerate(rows):
+                row = list(vals[i])
+                if not (fp4 and i < len(experts)):
+                    frags = [fp8_weight_to_frag(w) for w in r[:3]]
+                    keep += frags
+                    row[:3] = [f.data_ptr() for f in frags]
+                vals.append(row)
         ptrs = torch.tensor(vals, dtype=torch.int64).to(dev)
         fmt = _lib.EXPERT_FP4_E2M1 if fp4 else _lib.EXPERT_FP8_BLOCK128
         if pow2:
             fmt |= _lib.EXPERT_POW2_SCALES
+        if frag_layout:
+            fmt |= _lib.EXPERT_FRAG_COPY
         return ExpertTable(ptrs, len(experts), H, I, shared is not None, keep, fmt)
 
 

@@ -211,7 +211,8 @@ def test_moe_rejects_tokens_beyond_32_bit_operand_offsets(name, T):
 def test_expert_format_pow2_flag():
     """Power-of-two weight scales are recognised (e8m0 by type, fp32 with no
     mantissa bits, positive); the C boundary accepts SGL_EXPERT_POW2_SCALES
-    OR'ed into either weight format and refuses any other bit before a launch."""
+    and SGL_EXPERT_FRAG_COPY OR'ed into either weight format and refuses any
+    other bit before a launch."""
     from sglang_lite_amd import _lib as L
     from sglang_lite_amd import moe as M
 
@@ -222,9 +223,10 @@ def test_expert_format_pow2_flag():
     assert not M._pow2_scale(torch.tensor([1.0, 0.0]))            # zero
     assert not M._pow2_scale(torch.tensor([-1.0, 1.0]))           # sign
     assert not M._pow2_scale(torch.tensor([2.0 ** -130]))         # subnormal
-    assert L.EXPERT_POW2_SCALES == 2
+    assert L.EXPERT_POW2_SCALES == 2 and L.EXPERT_FRAG_COPY == 4
     H, I, E, k = 4096, 2048, 256, 8
-    for fmt, ok in ((0, True), (1, True), (2, True), (3, True), (4, False), (6, False)):
+    for fmt, ok in ((0, True), (1, True), (2, True), (3, True), (4, True), (7, True), (8, False),
+                    (10, False), (2 | 16, False)):
         args = (None, None, 64, H, I, E, k, None, None, None, None, 1, fmt, 0.0, 0, None, None, None)
         with pytest.raises(ValueError, match="null pointer" if ok else "bad expert_format"):
             L.call("sgl_moe_gate_up", *args)

@@ -1,0 +1,109 @@
+"""Expert weights in the MFMA fragment layout (``ExpertTable(frag_layout=True)``).
+
+* ``fp8_weight_to_frag`` against the layout's definition
+  (``frag_layout_ref``, itself checked element by element in
+  tests/test_frag_layout.py).
+* The register-fed prefill GEMMs (gemm_rb_kernel: gate/up with the SwiGLU +
+  1x128 requant epilogue, and down) against the LDS-staged pipelined
+  kernels, which the other MoE tests hold to the oracle.  Both run the same
+  arithmetic (the same MFMA fragments, the per-128-K fp32 promotion in the
+  same order, the same epilogue), so hq, hs, the expert rows and the layer
+  output are compared bit for bit: at the prefill shape (T = 8192, H = 4096,
+  I = 2048, E = 256 top-8 + shared, uniform routing) and at ragged shapes
+  (Zipf load with empty, one-row and remainder M tiles, a down N that is
+  not a multiple of the 256-column tile, gate/up N of 10 column tiles).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_values, to_dev_bf16, to_dev_f32, u8
+from test_frag_layout import frag_layout_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def test_weight_to_frag_matches_layout(gpu):
+    from sglang_lite_amd import kernel as K
+
+    rng = np.random.default_rng(3)
+    for N, K_ in ((16, 128), (48, 384), (2048, 4096)):
+        w = rng.integers(0, 256, size=(N, K_), dtype=np.uint8)
+        wd = torch.from_numpy(w).to(gpu).view(torch.float8_e4m3fn)
+        out = K.fp8_weight_to_frag(wd)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out.cpu().numpy(), frag_layout_ref(w), err_msg=f"{N}x{K_}")
+
+
+def _experts(dev, n, H, I, seed):
+    from sglang_lite_amd import kernel as K
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    ent = []
+    for _ in range(n):
+        row = []
+        for shape in ((I, H), (I, H), (H, I)):
+            q, s = K.per_block_cast_to_fp8(torch.randn(*shape, generator=g, device=dev) * 0.02, False)
+            row.append((q, s))
+        ent.append((row[0][0], row[1][0], row[2][0], row[0][1], row[1][1], row[2][1]))
+    return ent
+
+
+def _zipf_ids(rng, T, E, k, s=1.1):
+    p = np.arange(1, E + 1, dtype=np.float64) ** -s
+    p /= p.sum()
+    perm = rng.permutation(E)
+    logits = (np.log(p)[np.argsort(perm)][None, :] + rng.gumbel(size=(T, E))).astype(np.float32)
+    return logits
+
+
+def _compare(gpu, x, logits, ent, E, k, swiglu_limit=0.0):
+    from sglang_lite_amd import kernel as K
+    from sglang_lite_amd import moe as M
+
+    T = x.shape[0]
+    rows = M.ExpertTable.build(ent[:E], ent[E])
+    frag = M.ExpertTable.build(ent[:E], ent[E], frag_layout=True)
+    assert frag.fmt & 4 and frag.ptrs.shape[0] == 2 * (E + 1)
+    w, ids = M.route_topk(to_dev_f32(logits, gpu), k)
+    xd = to_dev_bf16(x, gpu)
+    xq, xs = K.act_quant(xd)
+    counts, offsets, sorted_slot, _ = M.permute(ids, E)
+    res = {}
+    for name, table in (("rows", rows), ("frag", frag)):
+        hq, hs = M.gate_up(xq, xs, offsets, sorted_slot, w.reshape(-1), table, k,
+                           swiglu_limit=swiglu_limit)
+        out = M.down(hq, hs, offsets, sorted_slot, table, T, k)
+        y = M.moe_forward(xd, ids, w, table, swiglu_limit=swiglu_limit)
+        torch.cuda.synchronize()
+        res[name] = (u8(hq), u8(hs), u8(out), u8(y))
+    for i, what in enumerate(("hq", "hs", "expert rows", "layer")):
+        np.testing.assert_array_equal(res["frag"][i], res["rows"][i], err_msg=what)
+    return counts.cpu().numpy()
+
+
+def test_prefill_shape_bit_identical(gpu):
+    H, I, E, k, T = 4096, 2048, 256, 8, 8192
+    print(f"frag prefill T={T}", flush=True)
+    rng = np.random.default_rng(11)
+    ent = _experts(gpu, E + 1, H, I, seed=5)
+    x = bf16_values(rng, (T, H))
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    counts = _compare(gpu, x, logits, ent, E, k)
+    assert counts.sum() == T * k
+
+
+@pytest.mark.parametrize("H,I", [(2176, 2048), (2048, 1280)])
+def test_ragged_shapes_bit_identical(gpu, H, I):
+    E, k, T = 16, 4, 600
+    print(f"frag ragged H={H} I={I}", flush=True)
+    rng = np.random.default_rng(H + I)
+    ent = _experts(gpu, E + 1, H, I, seed=H)
+    x = bf16_values(rng, (T, H))
+    logits = _zipf_ids(rng, T, E, k)
+    counts = _compare(gpu, x, logits, ent, E, k, swiglu_limit=7.0)
+    assert (counts % 128 != 0).any()  # remainder M tiles were exercised
