@@ -1591,7 +1591,7 @@ int launch_pipe(GemmArgs& a, hipStream_t stream) {
 // prepared at fixed stages of the current tile (K >= 2048: at least 16
 // stages): resolved at stage 5, its row slots and expert record loaded at 6
 // and stored at 10 (with its weight scales and routing weights loaded), its
-// row addresses formed at 11, its weight scales and routing weights stored
+// row addresses formed at 12, its weight scales and routing weights stored
 // at 14; its first stages load from stage NST - 4.
 //
 // Stores the compiler does not count (see above).  At most 8 bytes of data:
@@ -1603,19 +1603,38 @@ __device__ __forceinline__ void store_b64(void* p, uint2 v) {
   asm volatile("global_store_dwordx2 %0, %1, off" :: "v"(p), "v"(v) : "memory");
 }
 
+#ifndef SGL_RB_DBG
+#define SGL_RB_DBG 2
+#endif
 namespace rb {
-constexpr int BM = 128, BN = 256, NW = 8, NT = 64 * NW;
-constexpr int D = 4;      // stages of weight fragments in registers
+constexpr int BM = 128, BN = 256;
 constexpr int SLOTS = 4;  // LDS slots of 128-deep activation stages
 constexpr int A_BYTES = BM * 128;
 constexpr int kMinKB = 16, kMaxKBr = 64;
-static_assert(D == 4 && SLOTS == 4, "the stage loop is unrolled by four");
+static_assert(SLOTS == 4, "the stage loop is unrolled by four");
 }  // namespace rb
 
-template <int KIND>
-__global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
+// Eight wavefronts (two per SIMD), each owning NJ 16-column fragments of the
+// gate and of the up half (gate/up) or 2 NJ fragments (down): a tile is 128
+// rows x 128 NJ gate + 128 NJ up columns (down: 256 NJ columns).  NJ = 2
+// halves the LDS fragment reads per MFMA (each activation fragment feeds
+// four MFMAs, not two) and keeps DB = 2 weight stages in registers; NJ = 1
+// keeps four.
+template <int KIND, int NJ>
+__global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
   using namespace rb;
   static_assert(KIND == KIND_GATE_UP || KIND == KIND_DOWN, "grouped GEMMs only");
+  static_assert(NJ == 1 || NJ == 2, "one or two fragments per half");
+  constexpr int NW = 8, NT = 64 * NW;
+  // stages of weight fragments in registers: four for down; gate/up (whose
+  // epilogue holds more registers across the tile boundary) SGL_RB_DBG
+  constexpr int DB = NJ == 2 ? 2 : (KIND == KIND_GATE_UP ? SGL_RB_DBG : 4);
+  constexpr int GC = 128 * NJ;         // gate/up: gate columns of a tile
+  constexpr int TC = KIND == KIND_GATE_UP ? GC : 256 * NJ;  // output columns of a tile (per half)
+  constexpr int NB = 2 * NJ;           // weight-scale rows of a tile (gate/up: NJ per half)
+  constexpr int NF = 2 * NJ;        // weight fragments per wavefront and stage
+  constexpr int RPW = BM / NW;      // tile rows whose activations a wavefront loads
+  constexpr int AQ = RPW / 8;       // 1 KB activation loads per wavefront and stage
   __shared__ __align__(16) uint8_t sA[SLOTS * A_BYTES];
   __shared__ __align__(16) float sSa[2][BM * 4];  // row scales of four stages, [row][4]
   __shared__ int sTstart[kMaxGroups + 1];
@@ -1624,8 +1643,8 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
   __shared__ float sRow[2][BM];   // per table buffer: routing weight (gate/up) / output row (down)
   __shared__ float sAmax[KIND == KIND_GATE_UP ? NW : 1][BM];
   __shared__ int sTile[2][5];     // per table buffer: valid, e, row0, rows, nt
-  __shared__ float sSb[2][2][kMaxKBr];  // per table buffer: weight scales per K block (gate,
-                                       // up / the blocks of waves 0-3, 4-7)
+  __shared__ float sSb[2][NB][kMaxKBr];  // per table buffer: weight scales per K block
+                                        // (gate/up: gate blocks, then up blocks)
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1731,13 +1750,16 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
   };
 
   // ---- per-tile load sources of this wavefront
-  const int ra = 16 * w + (lane >> 3), rb_ = ra + 8, ch = lane & 7;
-  const uint32_t lds_a = (uint32_t)(ra * 128 + ((ch ^ swz(ra)) << 4));
-  const uint32_t lds_b = (uint32_t)(rb_ * 128 + ((ch ^ swz(rb_)) << 4));
+  const int ch = lane & 7;
+  auto a_row = [&](int q) -> int { return RPW * w + 8 * q + (lane >> 3); };
+  uint32_t lds_a[AQ];
+#pragma unroll
+  for (int q = 0; q < AQ; ++q) lds_a[q] = (uint32_t)(a_row(q) * 128 + ((ch ^ swz(a_row(q))) << 4));
   struct Src {
-    uint32_t a0, a1;  // rows ra and ra + 8 of the tile: byte offset of (row, 16 ch) in A
+    uint32_t a[AQ];   // rows a_row(q) of the tile: byte offset of (row, 16 ch) in A
     uint32_t sa;      // waves 0, 1: offset (floats) of row 64 w + lane's row scales
-    uint64_t b0, b1;  // (uniform) weight fragment blocks (n16, 0): gate / first, up / second
+    uint64_t b0, b1;  // (uniform) weight fragment blocks (n16, 0) of the wavefront's first
+                      // gate / up fragment (down: b0 only); fragment j at + j K/128 2 KB
   };
   // source row of tile row r (rows past the tile's last re-read its first)
   auto src_row = [&](const Tile& t, int buf, int r) -> int64_t {
@@ -1748,8 +1770,8 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
   };
   // row offsets of tile t (its slots in sSlot[buf]); T K < 2^31 and rows K < 2^31
   auto rows_of = [&](Src& s, const Tile& t, int buf) {
-    s.a0 = (uint32_t)(src_row(t, buf, ra) * K + ch * 16);
-    s.a1 = (uint32_t)(src_row(t, buf, rb_) * K + ch * 16);
+#pragma unroll
+    for (int q = 0; q < AQ; ++q) s.a[q] = (uint32_t)(src_row(t, buf, a_row(q)) * K + ch * 16);
     s.sa = (uint32_t)((w < 2 ? src_row(t, buf, 64 * w + lane) : 0) * KB);
   };
   // a global (not flat) fp32 load: a flat load also counts in lgkmcnt and is
@@ -1763,19 +1785,22 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
   auto weights_of = [&](Src& s, const Tile& t, float& sb0, float& sb1) {
     const int kbl = lane < KB ? lane : KB - 1;
     if constexpr (KIND == KIND_GATE_UP) {
-      const int64_t n16 = (int64_t)t.nt * 8 + w;
+      const int64_t nb16 = N / 16;
+      int64_t n16 = (int64_t)t.nt * (GC / 16) + NJ * w;
+      if (n16 > nb16 - NJ) n16 = nb16 - NJ;  // columns past N (not stored) re-read the last blocks
       s.b0 = rec_field(args.frag, t.e, 0) + (uint64_t)(n16 * KB * 2048);
       s.b1 = rec_field(args.frag, t.e, 1) + (uint64_t)(n16 * KB * 2048);
-      sb0 = ldg_f32(rec_field(args.experts, t.e, 3), (int64_t)t.nt * KB + kbl);
-      sb1 = ldg_f32(rec_field(args.experts, t.e, 4), (int64_t)t.nt * KB + kbl);
+      const int64_t blk = n16 / 8;
+      sb0 = ldg_f32(rec_field(args.experts, t.e, 3), blk * KB + kbl);
+      sb1 = ldg_f32(rec_field(args.experts, t.e, 4), blk * KB + kbl);
     } else {
       const int64_t nb16 = N / 16;
-      int64_t n16 = (int64_t)t.nt * 16 + 2 * w;
-      if (n16 > nb16 - 2) n16 = nb16 - 2;  // columns past N (not stored) re-read the last blocks
+      int64_t n16 = (int64_t)t.nt * (TC / 16) + NF * w;
+      if (n16 > nb16 - NF) n16 = nb16 - NF;  // columns past N (not stored) re-read the last blocks
       s.b0 = rec_field(args.frag, t.e, 2) + (uint64_t)(n16 * KB * 2048);
-      s.b1 = s.b0 + (uint64_t)KB * 2048;
+      s.b1 = s.b0;
       const int64_t nb = (N + 127) / 128;
-      int64_t blk = ((int64_t)t.nt * BN + 32 * w) / 128;
+      int64_t blk = ((int64_t)t.nt * TC + 16 * NF * w) / 128;
       if (blk > nb - 1) blk = nb - 1;
       sb0 = ldg_f32(rec_field(args.experts, t.e, 5), blk * KB + kbl);
       sb1 = sb0;
@@ -1798,22 +1823,21 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
     const i4v v = *(gi4v*)(a_g + off);
     return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
   };
-  auto ldB = [&](uint64_t base, uint32_t off) -> v8i {
+  auto ldB = [&](uint64_t base, uint64_t off) -> v8i {
     gbyte* p = (gbyte*)(uintptr_t)base;
-    const i4v lo = *(gi4v*)(p + (lane16 + off));
-    const i4v hi = *(gi4v*)(p + (lane16 + off + 1024u));
+    const i4v lo = *(gi4v*)(p + off + lane16);
+    const i4v hi = *(gi4v*)(p + off + (lane16 + 1024u));
     return v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
   };
-  // the tile's weight scales into sSb[buf]: gate/up waves 0 (gate) and 1
-  // (up), down waves 0 and 4 (their 128-column blocks)
+  // the 128-column weight-scale block (within the tile) of this wavefront's
+  // columns, and the tile's weight scales into sSb[buf], written by the first
+  // wavefront of each block
+  constexpr int WPB = KIND == KIND_GATE_UP ? 8 / NJ : 4 / NJ;  // wavefronts per block
+  const int bi = w / WPB;
   auto put_scales = [&](int buf, float sb0, float sb1) {
-    if (lane < KB) {
-      if constexpr (KIND == KIND_GATE_UP) {
-        if (w == 0) sSb[buf][0][lane] = sb0;
-        if (w == 1) sSb[buf][1][lane] = sb1;
-      } else {
-        if ((w & 3) == 0) sSb[buf][w >> 2][lane] = sb0;
-      }
+    if (lane < KB && w % WPB == 0) {
+      sSb[buf][bi][lane] = sb0;
+      if constexpr (KIND == KIND_GATE_UP) sSb[buf][NJ + bi][lane] = sb1;
     }
   };
 
@@ -1831,8 +1855,8 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
   __syncthreads();
   Tile tc = read_tile(0);
   if (!tc.valid) return;
-  if (lane < 16) {
-    const int i = 16 * w + lane;
+  if (lane < RPW) {
+    const int i = RPW * w + lane;
     const int sl = (tc.e < args.E && i < tc.rows) ? args.sorted_slot[tc.row0 + i] : 0;
     sSlot[0][i] = sl;
     if constexpr (KIND == KIND_GATE_UP)
@@ -1848,31 +1872,36 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
   put_scales(0, nsb0, nsb1);
   ns = cs;
 
-  v8i bq[D][2];
-  uint4 aq[2][2];
+  // weight fragment f of the wavefront at stage offset off (bytes within the block row)
+  auto ldBf = [&](const Src& s, int f, uint32_t off) -> v8i {
+    if constexpr (KIND == KIND_GATE_UP)
+      return ldB(f < NJ ? s.b0 : s.b1, (uint64_t)(f % NJ) * KB * 2048 + off);
+    else
+      return ldB(s.b0, (uint64_t)f * KB * 2048 + off);
+  };
+  v8i bq[DB][NF];
+  uint4 aq[2][AQ];
   float4 sq = make_float4(0.f, 0.f, 0.f, 0.f);
   {
     // stages 0 and 1 into LDS slots 0 and 1, row scales of stages 0..3
-    aq[0][0] = ldA(cs.a0);
-    aq[0][1] = ldA(cs.a1);
-    aq[1][0] = ldA(cs.a0 + 128);
-    aq[1][1] = ldA(cs.a1 + 128);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < AQ; ++q) aq[j][q] = ldA(cs.a[q] + j * 128);
     sq = ld_sa(cs.sa);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      *reinterpret_cast<uint4*>(sA + j * A_BYTES + lds_a) = aq[j][0];
-      *reinterpret_cast<uint4*>(sA + j * A_BYTES + lds_b) = aq[j][1];
-    }
-    if (w < 2) *reinterpret_cast<float4*>(&sSa[0][(64 * w + lane) * 4]) = sq;
-    aq[0][0] = ldA(cs.a0 + 2 * 128);
-    aq[0][1] = ldA(cs.a1 + 2 * 128);
-    aq[1][0] = ldA(cs.a0 + 3 * 128);
-    aq[1][1] = ldA(cs.a1 + 3 * 128);
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int s = 0; s < D; ++s) {
-      bq[s][0] = ldB(cs.b0, s * 2048);
-      bq[s][1] = ldB(cs.b1, s * 2048);
-    }
+      for (int q = 0; q < AQ; ++q) *reinterpret_cast<uint4*>(sA + j * A_BYTES + lds_a[q]) = aq[j][q];
+    if (w < 2) *reinterpret_cast<float4*>(&sSa[0][(64 * w + lane) * 4]) = sq;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < AQ; ++q) aq[j][q] = ldA(cs.a[q] + (2 + j) * 128);
+#pragma unroll
+    for (int s = 0; s < DB; ++s)
+#pragma unroll
+      for (int f = 0; f < NF; ++f) bq[s][f] = ldBf(cs, f, s * 2048);
   }
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
@@ -1885,9 +1914,12 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
   Tile tn = {0, 0, 0, 0, 0};
 
   for (;;) {
-    v4f acc[8][2];
+    const int nmb = (tc.rows + 15) >> 4;  // 16-row blocks holding rows
+    v4f acc[8][NF];
 #pragma unroll
-    for (int mi = 0; mi < 8; ++mi) acc[mi][0] = acc[mi][1] = vzero;
+    for (int mi = 0; mi < 8; ++mi)
+#pragma unroll
+      for (int f = 0; f < NF; ++f) acc[mi][f] = vzero;
 
     auto stage = [&](auto jc, const int st) {
       constexpr int J = decltype(jc)::value;
@@ -1899,19 +1931,20 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
         }
       }
       if constexpr (J == 2) {
-        if (st == 10 && tn.valid && lane < 16) {
-          const int i = 16 * w + lane;
+        if (st == 10 && tn.valid && lane < RPW) {
+          const int i = RPW * w + lane;
           sSlot[tb ^ 1][i] = nslot;
           if constexpr (KIND == KIND_DOWN) sRow[tb ^ 1][i] = out_row(tn, i, nslot);
         }
         if (st == 14 && tn.valid) {
           put_scales(tb ^ 1, nsb0, nsb1);
           if constexpr (KIND == KIND_GATE_UP)
-            if (lane < 16) sRow[tb ^ 1][16 * w + lane] = (tn.e < args.E && args.route_w) ? nrw : 1.0f;
+            if (lane < RPW) sRow[tb ^ 1][RPW * w + lane] = (tn.e < args.E && args.route_w) ? nrw : 1.0f;
         }
       }
-      if constexpr (J == 3) {
-        if (st == 11 && tn.valid) rows_of(ns, tn, tb ^ 1);
+      if constexpr (J == 0) {
+        // the slots stored at stage 10, behind the barrier that ends stage 11
+        if (st == 12 && tn.valid) rows_of(ns, tn, tb ^ 1);
       }
       __builtin_amdgcn_sched_barrier(0);
       // -- 2. activation stage st + 2 into LDS slot (J + 2) % 4 (and at J == 2
@@ -1919,8 +1952,8 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
       const int s2 = st + 2;
       {
         uint8_t* dst = sA + ((J + 2) & 3) * A_BYTES;
-        *reinterpret_cast<uint4*>(dst + lds_a) = aq[J & 1][0];
-        *reinterpret_cast<uint4*>(dst + lds_b) = aq[J & 1][1];
+#pragma unroll
+        for (int q = 0; q < AQ; ++q) *reinterpret_cast<uint4*>(dst + lds_a[q]) = aq[J & 1][q];
         if constexpr (J == 2) {
           const int grp = s2 < NST ? (s2 >> 2) : (NST >> 2);
           if (w < 2) *reinterpret_cast<float4*>(&sSa[(gpar + grp) & 1][(64 * w + lane) * 4]) = sq;
@@ -1932,8 +1965,8 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
       const bool cur4 = s4 < NST;
       {
         const uint32_t off = (uint32_t)(cur4 ? s4 : s4 - NST) * 128u;
-        aq[J & 1][0] = ldA((cur4 ? cs.a0 : ns.a0) + off);
-        aq[J & 1][1] = ldA((cur4 ? cs.a1 : ns.a1) + off);
+#pragma unroll
+        for (int q = 0; q < AQ; ++q) aq[J & 1][q] = ldA((cur4 ? cs.a[q] : ns.a[q]) + off);
         if constexpr (J == 0) sq = ld_sa(cur4 ? cs.sa + s4 : ns.sa + (s4 - NST));
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -1941,53 +1974,66 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
       {
         const uint8_t* stg = sA + J * A_BYTES;
         const float* sS = &sSa[(gpar + (st >> 2)) & 1][0];
-        const float sb0 = sSb[tb][KIND == KIND_GATE_UP ? 0 : (w >> 2)][st];
-        const float sb1 = KIND == KIND_GATE_UP ? sSb[tb][1][st] : sb0;
+        const float sb0 = sSb[tb][bi][st];
+        const float sb1 = KIND == KIND_GATE_UP ? sSb[tb][NJ + bi][st] : sb0;
         // software-pipelined over the 16-row blocks, each block a scheduling
         // region of its own (the compiler would otherwise hoist all eight
         // fragment reads and sixteen products at once and spill): block
         // mi + 1's fragment is read and block mi - 1 promoted while block
-        // mi's MFMAs run.  Every block is computed, also those past the
-        // tile's rows (a remainder tile's padding rows re-read its first
-        // row; their results are not stored).
-        v8i af[2];
-        v4f pr[2][2];
-        float sv[8];  // block mi's row scale, read one block ahead (three live at most)
-        af[0] = read_frag(stg, fl);
-        sv[0] = sS[r16 * 4 + J];
-        __builtin_amdgcn_sched_barrier(0);
-        auto promote = [&](int mi) {
-          const int b = mi & 1;
-          const float s0 = sv[mi] * sb0, s1 = sv[mi] * sb1;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            acc[mi][0][r] = fmaf(pr[b][0][r], s0, acc[mi][0][r]);
-            acc[mi][1][r] = fmaf(pr[b][1][r], s1, acc[mi][1][r]);
-          }
-          // keep the promotion here: left alone, the compiler sinks the
-          // accumulator chains past the stage, keeps every product and spills
-          asm volatile("" : "+v"(acc[mi][0]), "+v"(acc[mi][1]));
-        };
-#pragma unroll
-        for (int mi = 0; mi < 8; ++mi) {
-          const int b = mi & 1;
-          if (mi < 7) {
-            af[b ^ 1] = read_frag(stg + (mi + 1) * 16 * 128, fl);
-            sv[mi + 1] = sS[((mi + 1) * 16 + r16) * 4 + J];
-          }
-          pr[b][0] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bq[J][0], af[b], vzero, 0, 0, 0, 0, 0, 0);
-          pr[b][1] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bq[J][1], af[b], vzero, 0, 0, 0, 0, 0, 0);
-          if (mi > 0) promote(mi - 1);
+        // mi's MFMAs run.  Blocks past the tile's rows but within the body
+        // are computed too (padding rows re-read the tile's first row; their
+        // results are not stored).
+        // NMB 16-row blocks: all eight, or the first four for a tile of at
+        // most 64 rows (an expert's short last tile); the uniform branch picks
+        // one of two straight-line bodies
+        auto blocks = [&](auto nmb_c) {
+          constexpr int NMB = decltype(nmb_c)::value;
+          v8i af[2];
+          v4f pr[2][NF];
+          float sv[NMB];  // block mi's row scale, read one block ahead (three live at most)
+          af[0] = read_frag(stg, fl);
+          sv[0] = sS[r16 * 4 + J];
           __builtin_amdgcn_sched_barrier(0);
-        }
-        promote(7);
+          auto promote = [&](int mi) {
+            const int b = mi & 1;
+            const float s0 = sv[mi] * sb0, s1 = sv[mi] * sb1;
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+              const float sf = f < NJ ? s0 : s1;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[mi][f][r] = fmaf(pr[b][f][r], sf, acc[mi][f][r]);
+              // keep the promotion here: left alone, the compiler sinks the
+              // accumulator chains past the stage, keeps every product and spills
+              asm volatile("" : "+v"(acc[mi][f]));
+            }
+          };
+#pragma unroll
+          for (int mi = 0; mi < NMB; ++mi) {
+            const int b = mi & 1;
+            if (mi + 1 < NMB) {
+              af[b ^ 1] = read_frag(stg + (mi + 1) * 16 * 128, fl);
+              sv[mi + 1] = sS[((mi + 1) * 16 + r16) * 4 + J];
+            }
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+              pr[b][f] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bq[J % DB][f], af[b], vzero, 0, 0,
+                                                                          0, 0, 0, 0);
+            if (mi > 0) promote(mi - 1);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          promote(NMB - 1);
+        };
+        if (nmb > 4) blocks(std::integral_constant<int, 8>{});
+        else blocks(std::integral_constant<int, 4>{});
       }
       __builtin_amdgcn_sched_barrier(0);
-      // -- 5. weight fragments of stage st + 4 into the freed registers
+      // -- 5. weight fragments of stage st + DB into the freed registers
       {
-        const uint32_t off = (uint32_t)(cur4 ? s4 : s4 - NST) * 2048u;
-        bq[J][0] = ldB(cur4 ? cs.b0 : ns.b0, off);
-        bq[J][1] = ldB(cur4 ? cs.b1 : ns.b1, off);
+        const int sb_ = st + DB;
+        const bool curb = sb_ < NST;
+        const uint32_t off = (uint32_t)(curb ? sb_ : sb_ - NST) * 2048u;
+#pragma unroll
+        for (int f = 0; f < NF; ++f) bq[J % DB][f] = ldBf(curb ? cs : ns, f, off);
       }
       __builtin_amdgcn_sched_barrier(0);
       // -- 6. table loads for the next tile (consumed four stages later; the
@@ -1997,17 +2043,23 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
         if (st == 10 && tn.valid) {
           weights_of(ns, tn, nsb0, nsb1);
           if constexpr (KIND == KIND_GATE_UP)
-            if (lane < 16 && tn.e < args.E && args.route_w) nrw = args.route_w[nslot];
+            if (lane < RPW && tn.e < args.E && args.route_w) nrw = args.route_w[nslot];
         }
         if (st == 6) {
           tn = read_tile(tb ^ 1);
-          if (tn.valid && lane < 16) {
-            const int i = 16 * w + lane;
+          if (tn.valid && lane < RPW) {
+            const int i = RPW * w + lane;
             nslot = (tn.e < args.E && i < tn.rows) ? args.sorted_slot[tn.row0 + i] : 0;
           }
         }
       }
-      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      // a barrier every second stage suffices: slot (J + 2) & 3, written in
+      // this stage, was last read two stages ago, and is read two stages
+      // from now; a barrier at the end of every odd stage lies between each
+      // such pair of accesses.  The table stages read what an earlier stage
+      // stored across such a barrier: 6 reads 5's tile, 12 reads 10's slots,
+      // the next tile reads 14's scales and routing weights.
+      if constexpr (J & 1) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     };
     for (int st0 = 0; st0 < NST; st0 += 4) {
       stage(std::integral_constant<int, 0>{}, st0);
@@ -2019,14 +2071,14 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
     // ---- epilogue from registers
     const int rows = tc.rows;
     if constexpr (KIND == KIND_DOWN) {
-      const int64_t n0 = (int64_t)tc.nt * BN + 32 * w;
+      const int64_t n0 = (int64_t)tc.nt * TC + 16 * NF * w;
 #pragma unroll
       for (int mi = 0; mi < 8; ++mi) {
         const int row = mi * 16 + r16;
         if (row < rows) {
           const int64_t drow = __float_as_int(sRow[tb][row]);
 #pragma unroll
-          for (int f = 0; f < 2; ++f) {
+          for (int f = 0; f < NF; ++f) {
             const int64_t col = n0 + 16 * f + 4 * g4;
             if (col < N) {
               const v4f v = acc[mi][f];
@@ -2040,7 +2092,7 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
       // SwiGLU + 1x128 requant (as gemm_pipe_kernel): h kept as packed bf16
       // pairs across the barrier that publishes the row maxima
       const float lim = args.swiglu_limit;
-      uint32_t h2[8][2];
+      uint32_t h2[8][2 * NJ];
       auto swiglu = [&](auto clamp_c) {
         constexpr bool CLAMP = decltype(clamp_c)::value;
 #pragma unroll
@@ -2049,9 +2101,10 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
           const float wr = sRow[tb][row];
           float am = 0.0f;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float gt = bf16_round(acc[mi][0][r]);
-            float up = bf16_round(acc[mi][1][r]);
+          for (int q = 0; q < 4 * NJ; ++q) {
+            const int j = q >> 2, r = q & 3;
+            float gt = bf16_round(acc[mi][j][r]);
+            float up = bf16_round(acc[mi][NJ + j][r]);
             if constexpr (CLAMP) {
               up = clampf_(up, -lim, lim);
               gt = gt > lim ? lim : gt;
@@ -2059,10 +2112,10 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
             const float ex = __builtin_amdgcn_exp2f(gt * -1.4426950408889634f);
             const float silu = gt * __builtin_amdgcn_rcpf(1.0f + ex);
             const uint32_t hb = bf16_bits_exact(wr * (silu * up));
-            if (r & 1)
-              h2[mi][r >> 1] |= hb << 16;
+            if (q & 1)
+              h2[mi][q >> 1] |= hb << 16;
             else
-              h2[mi][r >> 1] = hb;
+              h2[mi][q >> 1] = hb;
             am = __builtin_elementwise_maximum(am, fabsf(bits_f32(hb << 16)));
           }
           am = __builtin_elementwise_maximum(am, __shfl_xor(am, 16, 64));
@@ -2070,33 +2123,40 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
           if (g4 == 0) sAmax[w][row] = am;
           // one row block at a time: a spill here would be a scratch access,
           // whose wait drains the next tile's loads in flight
-          asm volatile("" : "+v"(h2[mi][0]), "+v"(h2[mi][1]));
+#pragma unroll
+          for (int q = 0; q < 2 * NJ; ++q) asm volatile("" : "+v"(h2[mi][q]));
         }
       };
       if (lim > 0.0f) swiglu(std::true_type{});
       else swiglu(std::false_type{});
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      const int64_t NB = N / 128;
-      const int64_t n0 = (int64_t)tc.nt * 128;
+      const int64_t NBK = N / 128;
+      const int64_t n0 = (int64_t)tc.nt * GC;
+      const bool in_n = n0 + 16 * NJ * w < N;  // the wavefront's columns exist
       auto requant = [&](auto mode_c) {
         constexpr int MODE = decltype(mode_c)::value;
 #pragma unroll
         for (int mi = 0; mi < 8; ++mi) {
           const int row = mi * 16 + r16;
-          if (row < rows) {
-            float am = sAmax[0][row];
+          if (row < rows && in_n) {
+            // the row's maximum over the 128 columns of this wavefront's block
+            float am = sAmax[bi * WPB][row];
 #pragma unroll
-            for (int q = 1; q < NW; ++q) am = __builtin_elementwise_maximum(am, sAmax[q][row]);
+            for (int q = 1; q < WPB; ++q) am = __builtin_elementwise_maximum(am, sAmax[bi * WPB + q][row]);
             const float sf = group_scale(MODE, am);
-            float hf[4];
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-              hf[2 * q] = bits_f32(h2[mi][q] << 16);
-              hf[2 * q + 1] = bits_f32(h2[mi][q] & 0xFFFF0000u);
-            }
             const int64_t p = tc.row0 + row;
-            store_b32(args.hq + p * N + n0 + 16 * w + 4 * g4, quant4_e4m3(MODE, hf, sf));
-            if (w == 0 && g4 == 0) store_b32(args.hs + p * NB + tc.nt, __float_as_uint(sf));
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+              float hf[4];
+#pragma unroll
+              for (int q = 0; q < 2; ++q) {
+                hf[2 * q] = bits_f32(h2[mi][2 * j + q] << 16);
+                hf[2 * q + 1] = bits_f32(h2[mi][2 * j + q] & 0xFFFF0000u);
+              }
+              store_b32(args.hq + p * N + n0 + 16 * (NJ * w + j) + 4 * g4, quant4_e4m3(MODE, hf, sf));
+            }
+            if (w % WPB == 0 && g4 == 0)
+              store_b32(args.hs + p * NBK + tc.nt * NJ + bi, __float_as_uint(sf));
           }
         }
       };
@@ -2116,10 +2176,13 @@ __global__ __launch_bounds__(rb::NT) void gemm_rb_kernel(const GemmArgs args) {
   }
 }
 
+#ifndef SGL_RB_NJ
+#define SGL_RB_NJ 1
+#endif
 template <int KIND>
 int launch_rb(GemmArgs& a, hipStream_t stream) {
   using namespace rb;
-  a.n_tiles = (int)ceil_div(a.N, KIND == KIND_GATE_UP ? 128 : BN);
+  a.n_tiles = (int)ceil_div(a.N, (KIND == KIND_GATE_UP ? 128 : 256) * SGL_RB_NJ);
   const int64_t P = a.E > 0 ? a.T * a.k : 0;
   const int64_t mt_bound = P / BM + (P < a.E ? P : a.E) + (a.has_shared ? ceil_div(a.T, BM) : 0);
   const int64_t tiles = mt_bound * a.n_tiles;
@@ -2129,7 +2192,7 @@ int launch_rb(GemmArgs& a, hipStream_t stream) {
   const int64_t need = (tiles + 7) / 8 * 8;
   if (need < wgs) wgs = need;
   a.m_tiles = (int)mt_bound;
-  gemm_rb_kernel<KIND><<<(unsigned)wgs, NT, 0, stream>>>(a);
+  gemm_rb_kernel<KIND, SGL_RB_NJ><<<(unsigned)wgs, 512, 0, stream>>>(a);
   return check_launch("gemm_rb");
 }
 
