@@ -1620,7 +1620,11 @@ static_assert(SLOTS == 4, "the stage loop is unrolled by four");
 // halves the LDS fragment reads per MFMA (each activation fragment feeds
 // four MFMAs, not two) and keeps DB = 2 weight stages in registers; NJ = 1
 // keeps four.
-template <int KIND, int NJ>
+//
+// POW2: every row scale and weight scale is a power of two; both go into the
+// MFMA as e8m0 exponents with the accumulators as its C operand (no fp32
+// promotion), as in gemm_pipe_kernel<POW2>.
+template <int KIND, int NJ, bool POW2>
 __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
   using namespace rb;
   static_assert(KIND == KIND_GATE_UP || KIND == KIND_DOWN, "grouped GEMMs only");
@@ -1976,6 +1980,7 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
         const float* sS = &sSa[(gpar + (st >> 2)) & 1][0];
         const float sb0 = sSb[tb][bi][st];
         const float sb1 = KIND == KIND_GATE_UP ? sSb[tb][NJ + bi][st] : sb0;
+        const int sbe0 = (int)(__float_as_uint(sb0) >> 23), sbe1 = (int)(__float_as_uint(sb1) >> 23);
         // software-pipelined over the 16-row blocks, each block a scheduling
         // region of its own (the compiler would otherwise hoist all eight
         // fragment reads and sixteen products at once and spill): block
@@ -2014,14 +2019,25 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
               af[b ^ 1] = read_frag(stg + (mi + 1) * 16 * 128, fl);
               sv[mi + 1] = sS[((mi + 1) * 16 + r16) * 4 + J];
             }
+            if constexpr (POW2) {
+              // operand A = the weight fragment (the block's scale), operand
+              // B = the activation rows (lane r16's row scale, the same for
+              // its four 32-deep K quarters)
+              const int sae = (int)(__float_as_uint(sv[mi]) >> 23);
 #pragma unroll
-            for (int f = 0; f < NF; ++f)
-              pr[b][f] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bq[J % DB][f], af[b], vzero, 0, 0,
-                                                                          0, 0, 0, 0);
-            if (mi > 0) promote(mi - 1);
+              for (int f = 0; f < NF; ++f)
+                acc[mi][f] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                    bq[J % DB][f], af[b], acc[mi][f], 0, 0, 0, f < NJ ? sbe0 : sbe1, 0, sae);
+            } else {
+#pragma unroll
+              for (int f = 0; f < NF; ++f)
+                pr[b][f] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bq[J % DB][f], af[b], vzero, 0,
+                                                                            0, 0, 0, 0, 0);
+              if (mi > 0) promote(mi - 1);
+            }
             __builtin_amdgcn_sched_barrier(0);
           }
-          promote(NMB - 1);
+          if constexpr (!POW2) promote(NMB - 1);
         };
         if (nmb > 4) blocks(std::integral_constant<int, 8>{});
         else blocks(std::integral_constant<int, 4>{});
@@ -2192,7 +2208,10 @@ int launch_rb(GemmArgs& a, hipStream_t stream) {
   const int64_t need = (tiles + 7) / 8 * 8;
   if (need < wgs) wgs = need;
   a.m_tiles = (int)mt_bound;
-  gemm_rb_kernel<KIND, SGL_RB_NJ><<<(unsigned)wgs, 512, 0, stream>>>(a);
+  if (a.sa_pow2 && a.sb_pow2)
+    gemm_rb_kernel<KIND, SGL_RB_NJ, true><<<(unsigned)wgs, 512, 0, stream>>>(a);
+  else
+    gemm_rb_kernel<KIND, SGL_RB_NJ, false><<<(unsigned)wgs, 512, 0, stream>>>(a);
   return check_launch("gemm_rb");
 }
 
@@ -2986,10 +3005,10 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
   // (other kernels promote in fp32, exact for such scales too)
   const bool pow2 = a.sa_pow2 && a.sb_pow2;
   // register-fed weights: the experts' fragment-layout copies, 16 to 64
-  // stages in multiples of four, fp32 promotion (the power-of-two path stays
-  // on the pipelined kernel), 16-byte aligned row scales for their float4 loads
+  // stages in multiples of four, fp32 weight scales (powers of two or not),
+  // 16-byte aligned row scales for their float4 loads
   const int64_t kb = a.K / 128;
-  const bool rb_ok = SGL_RB && a.frag && !pow2 && !a.sb_e8m0 && kb >= rb::kMinKB &&
+  const bool rb_ok = SGL_RB && a.frag && !a.sb_e8m0 && kb >= rb::kMinKB &&
                      kb <= rb::kMaxKBr && kb % 4 == 0 && aligned(a.sa, 16);
   switch (kind) {
     case KIND_DENSE: {

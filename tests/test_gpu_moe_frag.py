@@ -11,7 +11,9 @@
   output are compared bit for bit: at the prefill shape (T = 8192, H = 4096,
   I = 2048, E = 256 top-8 + shared, uniform routing) and at ragged shapes
   (Zipf load with empty, one-row and remainder M tiles, a down N that is
-  not a multiple of the 256-column tile, gate/up N of 10 column tiles).
+  not a multiple of the 256-column tile, gate/up N of 10 column tiles),
+  with fp32 block scales and with power-of-two scales (e8m0 weight scales,
+  ue8m0 activation scales: both applied inside the MFMA).
 """
 
 from __future__ import annotations
@@ -38,7 +40,7 @@ def test_weight_to_frag_matches_layout(gpu):
         np.testing.assert_array_equal(out.cpu().numpy(), frag_layout_ref(w), err_msg=f"{N}x{K_}")
 
 
-def _experts(dev, n, H, I, seed):
+def _experts(dev, n, H, I, seed, ue8m0=False):
     from sglang_lite_amd import kernel as K
 
     g = torch.Generator(device=dev)
@@ -47,7 +49,7 @@ def _experts(dev, n, H, I, seed):
     for _ in range(n):
         row = []
         for shape in ((I, H), (I, H), (H, I)):
-            q, s = K.per_block_cast_to_fp8(torch.randn(*shape, generator=g, device=dev) * 0.02, False)
+            q, s = K.per_block_cast_to_fp8(torch.randn(*shape, generator=g, device=dev) * 0.02, ue8m0)
             row.append((q, s))
         ent.append((row[0][0], row[1][0], row[2][0], row[0][1], row[1][1], row[2][1]))
     return ent
@@ -61,7 +63,7 @@ def _zipf_ids(rng, T, E, k, s=1.1):
     return logits
 
 
-def _compare(gpu, x, logits, ent, E, k, swiglu_limit=0.0):
+def _compare(gpu, x, logits, ent, E, k, swiglu_limit=0.0, mode=0):
     from sglang_lite_amd import kernel as K
     from sglang_lite_amd import moe as M
 
@@ -69,16 +71,17 @@ def _compare(gpu, x, logits, ent, E, k, swiglu_limit=0.0):
     rows = M.ExpertTable.build(ent[:E], ent[E])
     frag = M.ExpertTable.build(ent[:E], ent[E], frag_layout=True)
     assert frag.fmt & 4 and frag.ptrs.shape[0] == 2 * (E + 1)
+    assert bool(rows.fmt & 2) == (mode == 1)  # power-of-two scales: both scales in the MFMA
     w, ids = M.route_topk(to_dev_f32(logits, gpu), k)
     xd = to_dev_bf16(x, gpu)
-    xq, xs = K.act_quant(xd)
+    xq, xs = K.act_quant(xd, scale_mode=mode)
     counts, offsets, sorted_slot, _ = M.permute(ids, E)
     res = {}
     for name, table in (("rows", rows), ("frag", frag)):
         hq, hs = M.gate_up(xq, xs, offsets, sorted_slot, w.reshape(-1), table, k,
-                           swiglu_limit=swiglu_limit)
-        out = M.down(hq, hs, offsets, sorted_slot, table, T, k)
-        y = M.moe_forward(xd, ids, w, table, swiglu_limit=swiglu_limit)
+                           swiglu_limit=swiglu_limit, scale_mode=mode)
+        out = M.down(hq, hs, offsets, sorted_slot, table, T, k, scale_mode=mode)
+        y = M.moe_forward(xd, ids, w, table, swiglu_limit=swiglu_limit, scale_mode=mode)
         torch.cuda.synchronize()
         res[name] = (u8(hq), u8(hs), u8(out), u8(y))
     for i, what in enumerate(("hq", "hs", "expert rows", "layer")):
@@ -86,24 +89,25 @@ def _compare(gpu, x, logits, ent, E, k, swiglu_limit=0.0):
     return counts.cpu().numpy()
 
 
-def test_prefill_shape_bit_identical(gpu):
+@pytest.mark.parametrize("pow2", [False, True])
+def test_prefill_shape_bit_identical(gpu, pow2):
     H, I, E, k, T = 4096, 2048, 256, 8, 8192
-    print(f"frag prefill T={T}", flush=True)
+    print(f"frag prefill T={T} pow2={pow2}", flush=True)
     rng = np.random.default_rng(11)
-    ent = _experts(gpu, E + 1, H, I, seed=5)
+    ent = _experts(gpu, E + 1, H, I, seed=5, ue8m0=pow2)
     x = bf16_values(rng, (T, H))
     logits = rng.standard_normal((T, E)).astype(np.float32)
-    counts = _compare(gpu, x, logits, ent, E, k)
+    counts = _compare(gpu, x, logits, ent, E, k, mode=1 if pow2 else 0)
     assert counts.sum() == T * k
 
 
-@pytest.mark.parametrize("H,I", [(2176, 2048), (2048, 1280)])
-def test_ragged_shapes_bit_identical(gpu, H, I):
+@pytest.mark.parametrize("H,I,pow2", [(2176, 2048, False), (2048, 1280, False), (2176, 2048, True)])
+def test_ragged_shapes_bit_identical(gpu, H, I, pow2):
     E, k, T = 16, 4, 600
-    print(f"frag ragged H={H} I={I}", flush=True)
+    print(f"frag ragged H={H} I={I} pow2={pow2}", flush=True)
     rng = np.random.default_rng(H + I)
-    ent = _experts(gpu, E + 1, H, I, seed=H)
+    ent = _experts(gpu, E + 1, H, I, seed=H, ue8m0=pow2)
     x = bf16_values(rng, (T, H))
     logits = _zipf_ids(rng, T, E, k)
-    counts = _compare(gpu, x, logits, ent, E, k, swiglu_limit=7.0)
+    counts = _compare(gpu, x, logits, ent, E, k, swiglu_limit=7.0, mode=1 if pow2 else 0)
     assert (counts % 128 != 0).any()  # remainder M tiles were exercised
