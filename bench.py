@@ -88,6 +88,15 @@ def make_weights(torch, M, dev, seed=4, ue8m0=False):
     return table, (w13, s13, w2, s2)
 
 
+def frag_table(M, weights):
+    """The same 257 FP8 experts with fragment-layout copies of their weights
+    (ExpertTable frag_layout: the register-fed prefill GEMMs)."""
+    w13, s13, w2, s2 = weights
+    experts = [(w13[e, 0], w13[e, 1], w2[e], s13[e, 0], s13[e, 1], s2[e]) for e in range(E)]
+    shared = (w13[E, 0], w13[E, 1], w2[E], s13[E, 0], s13[E, 1], s2[E])
+    return M.ExpertTable.build(experts, shared, frag_layout=True)
+
+
 def make_fp4_weights(torch, M, dev, shared, seed=6):
     """256 routed MXFP4 experts (the reference's live routed format: packed
     e2m1 codes drawn uniformly, e8m0 1x32 scales in [2^-9, 2^-5]) plus the
@@ -381,8 +390,13 @@ def pow2_extra(torch, M, K, dev, args):
     assert table2.fmt & _lib.EXPERT_POW2_SCALES
     out = {"fp8_prefill_mode3": prefill_entry(torch, M, K, table2, dev, args, 3)}
     log(f"pow2 fp8 prefill mode 3: {out['fp8_prefill_mode3']['ms']:.3f} ms")
-    shared = (w13[E, 0], w13[E, 1], w2[E], s13[E, 0], s13[E, 1], s2[E])
     del table2
+    # the same experts with fragment-layout weight copies (register-fed GEMMs)
+    tf = frag_table(M, (w13, s13, w2, s2))
+    out["fp8_prefill_mode3_frag_layout"] = prefill_entry(torch, M, K, tf, dev, args, 3)
+    log(f"pow2 fp8 prefill mode 3, fragment layout: {out['fp8_prefill_mode3_frag_layout']['ms']:.3f} ms")
+    del tf
+    shared = (w13[E, 0], w13[E, 1], w2[E], s13[E, 0], s13[E, 1], s2[E])
     table4 = make_fp4_weights(torch, M, dev, shared)
     assert table4.fmt & _lib.EXPERT_POW2_SCALES
     out["fp4_prefill_mode3"] = prefill_entry(torch, M, K, table4, dev, args, 3)
@@ -853,6 +867,11 @@ def main():
         del pages_d, qd, idd
         extra["hbm_ceiling"] = hbm_ceiling(torch, dev)
         log(f"hbm ceiling: {extra['hbm_ceiling']}")
+        # the headline layer with fragment-layout weight copies (register-fed GEMMs)
+        tf = frag_table(M, weights)
+        extra["prefill_frag_layout"] = prefill_entry(torch, M, K, tf, dev, args, 0)
+        log(f"prefill, fragment layout: {extra['prefill_frag_layout']['ms']:.3f} ms")
+        del tf
         extra["fp4"] = fp4_extra(torch, M, K, weights, dev, args, flush)
         extra["pow2_scales"] = pow2_extra(torch, M, K, dev, args)
         result["extra"] = extra
