@@ -3004,9 +3004,12 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
   // both scales powers of two: the pipelined kernel applies them in the MFMA
   // (other kernels promote in fp32, exact for such scales too)
   const bool pow2 = a.sa_pow2 && a.sb_pow2;
-  // register-fed weights: the experts' fragment-layout copies, 16 to 64
-  // stages in multiples of four, fp32 weight scales (powers of two or not),
-  // 16-byte aligned row scales for their float4 loads
+  // register-fed weights, at every batch size: the experts' fragment-layout
+  // copies, 16 to 64 stages in multiples of four, fp32 weight scales (powers
+  // of two or not), 16-byte aligned row scales for their float4 loads.  At
+  // decode sizes the weight stream is the whole cost and registers fed
+  // straight from memory beat the LDS-staged 32-row tiles (T = 64 / 256 /
+  // 512, Zipf load: layer 676 / 1103 / 1255 -> 627 / 1024 / 1170 us)
   const int64_t kb = a.K / 128;
   const bool rb_ok = SGL_RB && a.frag && !a.sb_e8m0 && kb >= rb::kMinKB &&
                      kb <= rb::kMaxKBr && kb % 4 == 0 && aligned(a.sa, 16);
@@ -3036,13 +3039,13 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       return launch_wide(a, stream);
     }
     case KIND_GATE_UP:
-      if (big && rb_ok) return launch_rb<KIND_GATE_UP>(a, stream);
+      if (rb_ok) return launch_rb<KIND_GATE_UP>(a, stream);
       if (big && pipe_ok)
         return pow2 ? launch_pipe<KIND_GATE_UP, true>(a, stream) : launch_pipe<KIND_GATE_UP, false>(a, stream);
       return big ? launch_cfg<KIND_GATE_UP, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)
                  : launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 4>(a, stream);
     default:
-      if (big && rb_ok) return launch_rb<KIND_DOWN>(a, stream);
+      if (rb_ok) return launch_rb<KIND_DOWN>(a, stream);
       if (big && pipe_ok)
         return pow2 ? launch_pipe<KIND_DOWN, true>(a, stream) : launch_pipe<KIND_DOWN, false>(a, stream);
       return big ? launch_cfg<KIND_DOWN, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)

@@ -3,13 +3,15 @@
 * ``fp8_weight_to_frag`` against the layout's definition
   (``frag_layout_ref``, itself checked element by element in
   tests/test_frag_layout.py).
-* The register-fed prefill GEMMs (gemm_rb_kernel: gate/up with the SwiGLU +
-  1x128 requant epilogue, and down) against the LDS-staged pipelined
-  kernels, which the other MoE tests hold to the oracle.  Both run the same
-  arithmetic (the same MFMA fragments, the per-128-K fp32 promotion in the
-  same order, the same epilogue), so hq, hs, the expert rows and the layer
-  output are compared bit for bit: at the prefill shape (T = 8192, H = 4096,
-  I = 2048, E = 256 top-8 + shared, uniform routing) and at ragged shapes
+* The register-fed grouped GEMMs (gemm_rb_kernel: gate/up with the SwiGLU +
+  1x128 requant epilogue, and down) against the LDS-staged kernels (the
+  pipelined prefill kernel, the 32-row decode kernel), which the other MoE
+  tests hold to the oracle.  They run the same arithmetic (the same MFMA
+  fragments, the per-128-K fp32 promotion in the same order, the same
+  epilogue), so hq, hs, the expert rows and the layer output are compared
+  bit for bit: at the prefill shape (T = 8192, H = 4096, I = 2048, E = 256
+  top-8 + shared, uniform routing), at decode batches (T = 64 and 512, Zipf
+  load) and at ragged shapes
   (Zipf load with empty, one-row and remainder M tiles, a down N that is
   not a multiple of the 256-column tile, gate/up N of 10 column tiles),
   with fp32 block scales and with power-of-two scales (e8m0 weight scales,
@@ -99,6 +101,20 @@ def test_prefill_shape_bit_identical(gpu, pow2):
     logits = rng.standard_normal((T, E)).astype(np.float32)
     counts = _compare(gpu, x, logits, ent, E, k, mode=1 if pow2 else 0)
     assert counts.sum() == T * k
+
+
+@pytest.mark.parametrize("T", [64, 512])
+def test_decode_shape_bit_identical(gpu, T):
+    """Decode batches (Zipf(1.1) expert load, most experts with a few rows)
+    against the LDS-staged decode kernel."""
+    H, I, E, k = 4096, 2048, 256, 8
+    print(f"frag decode T={T}", flush=True)
+    rng = np.random.default_rng(T + 1)
+    ent = _experts(gpu, E + 1, H, I, seed=6)
+    x = bf16_values(rng, (T, H))
+    logits = _zipf_ids(rng, T, E, k)
+    counts = _compare(gpu, x, logits, ent, E, k)
+    assert (counts > 0).sum() > E // 2
 
 
 @pytest.mark.parametrize("H,I,pow2", [(2176, 2048, False), (2048, 1280, False), (2176, 2048, True)])
