@@ -51,7 +51,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extra", action="store_true", help="headline prefill line only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--profile-kernels", nargs="?", const="fp8", choices=("fp8", "fp4", "small"),
+    ap.add_argument("--profile-kernels", nargs="?", const="fp8", choices=("fp8", "fp4", "small", "frag"),
                     help="run only 3 prefill steps (FP8 experts, or FP4 routed experts in the "
                          "ue8m0 scale mode) plus a counter-calibration kernel, for rocprofv3 "
                          "runs; prints no JSON")
@@ -613,7 +613,21 @@ def main():
             shared = (w13[E, 0], w13[E, 1], w2[E], s13[E, 0], s13[E, 1], s2[E])
             pre = Prefill(torch, M, K, make_fp4_weights(torch, M, dev, shared), T, dev, seed=4,
                           mode=3)
-        if args.profile_kernels == "small":
+        if args.profile_kernels == "frag":
+            # fragment-layout weight copies: 3 prefill steps, then 3 decode
+            # steps each at T = 64 / 256 / 512 (Zipf load)
+            tf = frag_table(M, weights)
+            pre = Prefill(torch, M, K, tf, T, dev, seed=4)
+            for _ in range(3):
+                pre.step()
+            for Td, seed in ((64, 31), (256, 32), (512, 33)):
+                logits = zipf_logits(torch, Td, seed).to(dev)
+                xd = torch.randn(Td, H, generator=torch.Generator().manual_seed(seed)).to(
+                    torch.bfloat16).to(dev)
+                for _ in range(3):
+                    w, ids = M.route_topk(logits, K_TOP)
+                    M.moe_forward(xd, ids, w, tf)
+        elif args.profile_kernels == "small":
             profile_small(torch, M, K, table, dev)
         else:
             for _ in range(3):
@@ -697,34 +711,41 @@ def main():
 
     if not args.no_extra:
         extra = {}
-        # ---- decode configs
-        dec = []
-        for Td, seed in ((64, 31), (256, 32), (512, 33)):
-            logits = zipf_logits(torch, Td, seed).to(dev)
-            xd = torch.randn(Td, H, generator=torch.Generator().manual_seed(seed)).to(
-                torch.bfloat16).to(dev)
-            ws = M.MoEWorkspace()
-            yd = torch.empty(Td, H, dtype=torch.bfloat16, device=dev)
+        # ---- decode configs: the row-major expert table, and the same experts
+        # with fragment-layout weight copies (register-fed GEMMs)
+        def decode_lines(tab):
+            dec = []
+            for Td, seed in ((64, 31), (256, 32), (512, 33)):
+                logits = zipf_logits(torch, Td, seed).to(dev)
+                xd = torch.randn(Td, H, generator=torch.Generator().manual_seed(seed)).to(
+                    torch.bfloat16).to(dev)
+                ws = M.MoEWorkspace()
+                yd = torch.empty(Td, H, dtype=torch.bfloat16, device=dev)
 
-            def dstep():
-                w, ids = M.route_topk(logits, K_TOP)
-                M.moe_forward(xd, ids, w, table, workspace=ws, out=yd)
+                def dstep():
+                    w, ids = M.route_topk(logits, K_TOP)
+                    M.moe_forward(xd, ids, w, tab, workspace=ws, out=yd)
 
-            msd = time_steps(torch, dstep, max(args.steps, 10), args.warmup)
-            msg_d = graph_ms(torch, dstep, max(args.steps, 10))
-            _, ids = M.route_topk(logits, K_TOP)
-            touched = int(torch.unique(ids).numel())
-            by = (touched + 1) * (W_BYTES_PER_EXPERT + SCALE_BYTES_PER_EXPERT) + 4 * Td * H + \
-                4 * Td * E
-            dec.append({"tokens": Td, "ms": round(msd, 4), "tokens_per_s": round(Td / msd * 1e3, 1),
-                        "experts_touched": touched, "bytes": by,
-                        "gbs": round(by / msd / 1e6, 1),
-                        "hbm_frac": round(by / msd / 1e6 / PEAK_HBM_GBS, 4),
-                        "graph_ms": round(msg_d, 4),
-                        "graph_hbm_frac": round(by / msg_d / 1e6 / PEAK_HBM_GBS, 4)})
-            log(f"decode T={Td}: {msd:.3f} ms eager, {msg_d:.3f} ms graph, touched {touched}, "
-                f"{by / msg_d / 1e6:.0f} GB/s (graph)")
-        extra["decode"] = dec
+                msd = time_steps(torch, dstep, max(args.steps, 10), args.warmup)
+                msg_d = graph_ms(torch, dstep, max(args.steps, 10))
+                _, ids = M.route_topk(logits, K_TOP)
+                touched = int(torch.unique(ids).numel())
+                by = (touched + 1) * (W_BYTES_PER_EXPERT + SCALE_BYTES_PER_EXPERT) + 4 * Td * H + \
+                    4 * Td * E
+                dec.append({"tokens": Td, "ms": round(msd, 4), "tokens_per_s": round(Td / msd * 1e3, 1),
+                            "experts_touched": touched, "bytes": by,
+                            "gbs": round(by / msd / 1e6, 1),
+                            "hbm_frac": round(by / msd / 1e6 / PEAK_HBM_GBS, 4),
+                            "graph_ms": round(msg_d, 4),
+                            "graph_hbm_frac": round(by / msg_d / 1e6 / PEAK_HBM_GBS, 4)})
+                log(f"decode T={Td}: {msd:.3f} ms eager, {msg_d:.3f} ms graph, touched {touched}, "
+                    f"{by / msg_d / 1e6:.0f} GB/s (graph)")
+            return dec
+
+        extra["decode"] = decode_lines(table)
+        tf = frag_table(M, weights)
+        extra["decode_frag_layout"] = decode_lines(tf)
+        del tf
         # ---- fused gate (router projection on bf16 MFMA + score + top-k), model.py:564-584
         gate = []
         gg = torch.Generator(device=dev).manual_seed(8)
