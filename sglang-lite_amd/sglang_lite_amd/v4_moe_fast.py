@@ -45,6 +45,15 @@ def moe_fast_enabled() -> bool:
     return raw not in ("0", "false", "no", "off")
 
 
+def frag_layout_enabled() -> bool:
+    """``SGLANG_LITE_AMD_FRAG_LAYOUT=1``: the MoE layers' expert tables also
+    keep fragment-layout copies of the FP8 expert weights (the register-fed
+    GEMMs; a second copy of those weights).  Off by default.  A switch of this
+    build, not of the reference."""
+    raw = os.environ.get("SGLANG_LITE_AMD_FRAG_LAYOUT", "0").strip().lower()
+    return raw in ("1", "true", "yes", "on")
+
+
 def _official_model():
     M = sys.modules.get("model")
     if M is None:
@@ -83,7 +92,8 @@ def expert_table(moe) -> HM.ExpertTable:
     tab = getattr(moe, "_sgl_table", None)
     if tab is None:
         experts = [_expert_entry(e) for e in moe.experts]
-        tab = HM.ExpertTable.build(experts, _expert_entry(moe.shared_experts))
+        tab = HM.ExpertTable.build(experts, _expert_entry(moe.shared_experts),
+                                   frag_layout=frag_layout_enabled())
         moe._sgl_table = tab
     return tab
 
@@ -203,4 +213,5 @@ def detach_v4_moe_fast() -> None:
             del cls._sgl_orig_forward
 
 
-__all__ = ["attach_v4_moe_fast", "detach_v4_moe_fast", "expert_table", "moe_fast_enabled"]
+__all__ = ["attach_v4_moe_fast", "detach_v4_moe_fast", "expert_table", "frag_layout_enabled",
+           "moe_fast_enabled"]

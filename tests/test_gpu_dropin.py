@@ -293,3 +293,37 @@ def test_graph_replay_after_the_workspace_grows(official, gpu):
     for f in fence:
         assert bool((f == 0xA5).all()), "a graph replay wrote into a tensor allocated after capture"
     assert isinstance(ws, HM.MoEWorkspace)
+
+
+def test_moe_forward_with_frag_layout_switch(official, gpu, monkeypatch):
+    """SGLANG_LITE_AMD_FRAG_LAYOUT=1: the patched MoE.forward builds its expert
+    table with fragment-layout weight copies (the register-fed GEMMs at
+    H = I = 2048) and returns the same bytes as the row-major table; both
+    against the oracle."""
+    from sglang_lite_amd import v4_moe_fast as MF
+
+    M, K = official
+    rng = np.random.default_rng(45)
+    T, H, I, E, k = 40, 2048, 2048, 8, 2
+    x = bf16_values(rng, (T, H))
+    W = (rng.standard_normal((E, H)) * H ** -0.5).astype(np.float32)
+    experts = [OM.make_expert(rng, H, I) for _ in range(E)]
+    sh = OM.make_expert(rng, H, I)
+    gate = M.Gate(to_dev_f32(W, gpu), k)
+    xd = to_dev_bf16(x, gpu)
+    iid = torch.zeros(1, T, dtype=torch.long, device=gpu)
+    ys = {}
+    for on in (False, True):
+        monkeypatch.setenv("SGLANG_LITE_AMD_FRAG_LAYOUT", "1" if on else "0")
+        moe = M.MoE(H, gate, [M.Expert(_dev_expert(e, gpu)) for e in experts],
+                    M.Expert(_dev_expert(sh, gpu)))
+        assert MF.attach_v4_moe_fast(moe)["enabled"]
+        ys[on] = moe(xd.view(1, T, H), iid)
+        assert bool(MF.expert_table(moe).fmt & 4) == on
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(u8(ys[True]), u8(ys[False]))
+    logits = F.linear(xd.float(), gate.weight.float()).cpu().numpy()
+    w_ref, ids_ref = OM.route_topk(logits, k)
+    assert OM.topk_margin(logits, k) > 1e-6
+    y_ref = OM.moe_forward(x, ids_ref, w_ref, experts, sh)
+    assert_gemm_close(f32(ys[True][0]), y_ref, "MoE.forward with fragment-layout weights")
