@@ -199,19 +199,22 @@ def test_moe_forward_with_bf16_and_hash_gates(official, gpu):
         assert_gemm_close(f32(y[0]), y_ref, f"MoE.forward bf16 gate hash={hashed}")
 
 
-def test_moe_layer_captures_into_a_hip_graph(official, gpu):
+@pytest.mark.parametrize("frag", [False, True])
+def test_moe_layer_captures_into_a_hip_graph(official, gpu, monkeypatch, frag):
     """The patched MoE.forward captured the way the reference's decode runner
     captures the model (v4_runner/cuda_graph.py:98-137: warmup, synchronize,
     capture, replay into static buffers).  The official forward cannot be
     captured (bincount().tolist() syncs, model.py:634); this one launches
     only HIP kernels on torch's stream.  Every replay, with eager work and
     syncs between replays, equals the eager forward on the same input bit
-    for bit."""
+    for bit.  ``frag``: with fragment-layout weight copies (the register-fed
+    GEMMs, which need K >= 2048: H = I = 2048)."""
     from sglang_lite_amd import v4_moe_fast as MF
 
     M, K = official
+    monkeypatch.setenv("SGLANG_LITE_AMD_FRAG_LAYOUT", "1" if frag else "0")
     rng = np.random.default_rng(45)
-    T, H, I, E, k = 64, 512, 256, 16, 4
+    T, H, I, E, k = (64, 2048, 2048, 8, 2) if frag else (64, 512, 256, 16, 4)
     Wb = bf16_values(rng, (E, H), scale=H ** -0.5)
     experts = [OM.make_expert(rng, H, I) for _ in range(E)]
     sh = OM.make_expert(rng, H, I)
@@ -220,6 +223,7 @@ def test_moe_layer_captures_into_a_hip_graph(official, gpu):
     moe = M.MoE(H, gate, [M.Expert(_dev_expert(e, gpu)) for e in experts],
                 M.Expert(_dev_expert(sh, gpu)))
     assert MF.attach_v4_moe_fast(moe)["enabled"]
+    assert bool(MF.expert_table(moe).fmt & 4) == frag
     ids0 = torch.zeros(1, T, dtype=torch.long, device=gpu)
     x_static = to_dev_bf16(bf16_values(rng, (T, H)), gpu).view(1, T, H)
     for _ in range(3):
