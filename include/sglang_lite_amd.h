@@ -98,11 +98,12 @@ enum sgl_expert_format { SGL_EXPERT_FP8_BLOCK128 = 0, SGL_EXPERT_FP4_E2M1 = 1 };
  * (+ shared) records, as many records again for the same experts whose FP8
  * weight pointers (w_gate, w_up, w_down) address copies in the MFMA fragment
  * layout written by sgl_fp8_weight_to_frag (scale pointers as in the first
- * set; records of FP4 routed experts are not read).  The prefill-size FP8
- * GEMMs with fp32 block scales then load those weights straight into
- * registers; every other kernel reads the row-major first set.  No
- * counterpart in the reference: a layout of this build, costing a second copy
- * of the FP8 expert weights. */
+ * set); for FP4 routed experts the weight and the scale pointers address the
+ * copies sgl_fp4_weight_to_frag writes.  The grouped GEMMs (K a multiple of
+ * 512, 2048 <= K <= 8192) then load those weights straight into registers;
+ * every other kernel reads the row-major first set.  No counterpart in the
+ * reference: a layout of this build, costing a second copy of the expert
+ * weights. */
 #define SGL_EXPERT_FRAG_COPY 4
 
 /* Per-expert weight pointers of one MoE layer, stored in DEVICE memory as an
@@ -233,6 +234,19 @@ int sgl_fp4_to_fp8_weight(const void* b, const void* sb, int64_t N, int64_t K, v
  * N % 16 == 0, K % 128 == 0.  No counterpart in the reference (a one-time
  * weight layout step of this build, run when the expert table is made). */
 int sgl_fp8_weight_to_frag(const void* w, int64_t N, int64_t K, void* out, sgl_stream_t stream);
+
+/* Packed e2m1 weight [N, K/2] (low nibble = even K) with e8m0 scales
+ * [N, K/32] -> the FP4 fragment layout of SGL_EXPERT_FRAG_COPY records:
+ * out_w (N * K/2 bytes) one 1 KB block per (16-row block n16, 128-deep
+ * block kb), at n16 * (K/128) + kb, byte 16 l + b holding packed byte
+ * 64 kb + 16 (l/16) + b of row 16 n16 + l % 16; out_s (N * K/32 bytes) one
+ * 256-byte block per (n16, group q of four 128-deep blocks), at
+ * n16 * (K/512) + q, byte 4 l + j holding the scale of row 16 n16 + l % 16
+ * for its 32-deep block 16 q + 4 j + l/16.  N % 16 == 0, K % 512 == 0; the
+ * outputs do not alias the inputs.  No counterpart in the reference (a
+ * one-time weight layout step of this build). */
+int sgl_fp4_weight_to_frag(const void* w, const void* s, int64_t N, int64_t K, void* out_w,
+                           void* out_s, sgl_stream_t stream);
 
 /* ------------------------------------------------------------ MoE layer */
 

@@ -1624,15 +1624,25 @@ static_assert(SLOTS == 4, "the stage loop is unrolled by four");
 // POW2: every row scale and weight scale is a power of two; both go into the
 // MFMA as e8m0 exponents with the accumulators as its C operand (no fp32
 // promotion), as in gemm_pipe_kernel<POW2>.
-template <int KIND, int NJ, bool POW2>
+//
+// W4: packed e2m1 weights (the FP4 fragment layout: 16 bytes per lane and
+// 128-deep block, the fp4 MFMA operand) with their e8m0 1 x 32 scales, which
+// the MFMA applies (one dword per lane holds a lane's scales for four
+// stages); the activation fragment pairs its K as the FP4 kernels do (chunks
+// l/16 and 4 + l/16); the row scales as for FP8 (POW2: in the MFMA, else one
+// fp32 promotion per 128-deep block).
+template <int KIND, int NJ, bool POW2, bool W4>
 __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
   using namespace rb;
   static_assert(KIND == KIND_GATE_UP || KIND == KIND_DOWN, "grouped GEMMs only");
   static_assert(NJ == 1 || NJ == 2, "one or two fragments per half");
+  static_assert(!W4 || NJ == 1, "fp4 weights: 16-column fragments per half");
   constexpr int NW = 8, NT = 64 * NW;
-  // stages of weight fragments in registers: four for down; gate/up (whose
-  // epilogue holds more registers across the tile boundary) SGL_RB_DBG
-  constexpr int DB = NJ == 2 ? 2 : (KIND == KIND_GATE_UP ? SGL_RB_DBG : 4);
+  // stages of weight fragments in registers: four for down and for fp4
+  // (half the registers per fragment); fp8 gate/up (whose epilogue holds more
+  // registers across the tile boundary) SGL_RB_DBG
+  constexpr int DB = NJ == 2 ? 2 : ((KIND == KIND_GATE_UP && !W4) ? SGL_RB_DBG : 4);
+  constexpr uint32_t WBLK = W4 ? 1024 : 2048;  // weight bytes per 16-row x 128-deep block
   constexpr int GC = 128 * NJ;         // gate/up: gate columns of a tile
   constexpr int TC = KIND == KIND_GATE_UP ? GC : 256 * NJ;  // output columns of a tile (per half)
   constexpr int NB = 2 * NJ;           // weight-scale rows of a tile (gate/up: NJ per half)
@@ -1763,7 +1773,8 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
     uint32_t a[AQ];   // rows a_row(q) of the tile: byte offset of (row, 16 ch) in A
     uint32_t sa;      // waves 0, 1: offset (floats) of row 64 w + lane's row scales
     uint64_t b0, b1;  // (uniform) weight fragment blocks (n16, 0) of the wavefront's first
-                      // gate / up fragment (down: b0 only); fragment j at + j K/128 2 KB
+                      // gate / up fragment (down: b0 only); fragment j at + j K/128 WBLK
+    uint64_t s0, s1;  // W4: (uniform) scale blocks (n16, 0), fragment j at + j K/512 256
   };
   // source row of tile row r (rows past the tile's last re-read its first)
   auto src_row = [&](const Tile& t, int buf, int r) -> int64_t {
@@ -1792,22 +1803,34 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
       const int64_t nb16 = N / 16;
       int64_t n16 = (int64_t)t.nt * (GC / 16) + NJ * w;
       if (n16 > nb16 - NJ) n16 = nb16 - NJ;  // columns past N (not stored) re-read the last blocks
-      s.b0 = rec_field(args.frag, t.e, 0) + (uint64_t)(n16 * KB * 2048);
-      s.b1 = rec_field(args.frag, t.e, 1) + (uint64_t)(n16 * KB * 2048);
-      const int64_t blk = n16 / 8;
-      sb0 = ldg_f32(rec_field(args.experts, t.e, 3), blk * KB + kbl);
-      sb1 = ldg_f32(rec_field(args.experts, t.e, 4), blk * KB + kbl);
+      s.b0 = rec_field(args.frag, t.e, 0) + (uint64_t)(n16 * KB * WBLK);
+      s.b1 = rec_field(args.frag, t.e, 1) + (uint64_t)(n16 * KB * WBLK);
+      if constexpr (W4) {
+        s.s0 = rec_field(args.frag, t.e, 3) + (uint64_t)(n16 * (KB / 4) * 256);
+        s.s1 = rec_field(args.frag, t.e, 4) + (uint64_t)(n16 * (KB / 4) * 256);
+        sb0 = sb1 = 1.0f;  // the weight scales go into the MFMA
+      } else {
+        const int64_t blk = n16 / 8;
+        sb0 = ldg_f32(rec_field(args.experts, t.e, 3), blk * KB + kbl);
+        sb1 = ldg_f32(rec_field(args.experts, t.e, 4), blk * KB + kbl);
+      }
     } else {
       const int64_t nb16 = N / 16;
       int64_t n16 = (int64_t)t.nt * (TC / 16) + NF * w;
       if (n16 > nb16 - NF) n16 = nb16 - NF;  // columns past N (not stored) re-read the last blocks
-      s.b0 = rec_field(args.frag, t.e, 2) + (uint64_t)(n16 * KB * 2048);
+      s.b0 = rec_field(args.frag, t.e, 2) + (uint64_t)(n16 * KB * WBLK);
       s.b1 = s.b0;
-      const int64_t nb = (N + 127) / 128;
-      int64_t blk = ((int64_t)t.nt * TC + 16 * NF * w) / 128;
-      if (blk > nb - 1) blk = nb - 1;
-      sb0 = ldg_f32(rec_field(args.experts, t.e, 5), blk * KB + kbl);
-      sb1 = sb0;
+      if constexpr (W4) {
+        s.s0 = rec_field(args.frag, t.e, 5) + (uint64_t)(n16 * (KB / 4) * 256);
+        s.s1 = s.s0;
+        sb0 = sb1 = 1.0f;
+      } else {
+        const int64_t nb = (N + 127) / 128;
+        int64_t blk = ((int64_t)t.nt * TC + 16 * NF * w) / 128;
+        if (blk > nb - 1) blk = nb - 1;
+        sb0 = ldg_f32(rec_field(args.experts, t.e, 5), blk * KB + kbl);
+        sb1 = sb0;
+      }
     }
   };
   const uint32_t lane16 = (uint32_t)lane * 16;
@@ -1830,8 +1853,16 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
   auto ldB = [&](uint64_t base, uint64_t off) -> v8i {
     gbyte* p = (gbyte*)(uintptr_t)base;
     const i4v lo = *(gi4v*)(p + off + lane16);
+    if constexpr (W4) return v8i{lo.x, lo.y, lo.z, lo.w, 0, 0, 0, 0};  // 16 packed bytes
     const i4v hi = *(gi4v*)(p + off + (lane16 + 1024u));
     return v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  };
+  // W4: lane's scale dword of fragment f for the four stages of group g
+  auto ldS = [&](const Src& s, int f, int g) -> uint32_t {
+    const uint64_t base = (f < NJ || KIND == KIND_DOWN) ? s.s0 : s.s1;
+    const int j = KIND == KIND_DOWN ? f : f % NJ;
+    return *(__attribute__((address_space(1))) const uint32_t*)(uintptr_t)(
+        base + (uint64_t)j * (KB / 4) * 256 + (uint64_t)g * 256 + (uint64_t)lane * 4);
   };
   // the 128-column weight-scale block (within the tile) of this wavefront's
   // columns, and the tile's weight scales into sSb[buf], written by the first
@@ -1879,10 +1910,11 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
   // weight fragment f of the wavefront at stage offset off (bytes within the block row)
   auto ldBf = [&](const Src& s, int f, uint32_t off) -> v8i {
     if constexpr (KIND == KIND_GATE_UP)
-      return ldB(f < NJ ? s.b0 : s.b1, (uint64_t)(f % NJ) * KB * 2048 + off);
+      return ldB(f < NJ ? s.b0 : s.b1, (uint64_t)(f % NJ) * KB * WBLK + off);
     else
-      return ldB(s.b0, (uint64_t)f * KB * 2048 + off);
+      return ldB(s.b0, (uint64_t)f * KB * WBLK + off);
   };
+  uint32_t swc[NF], swn[NF];  // W4: scale dwords of the current / next group of four stages
   v8i bq[DB][NF];
   uint4 aq[2][AQ];
   float4 sq = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1905,11 +1937,15 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
 #pragma unroll
     for (int s = 0; s < DB; ++s)
 #pragma unroll
-      for (int f = 0; f < NF; ++f) bq[s][f] = ldBf(cs, f, s * 2048);
+      for (int f = 0; f < NF; ++f) bq[s][f] = ldBf(cs, f, s * WBLK);
+#pragma unroll
+    for (int f = 0; f < NF; ++f) swc[f] = swn[f] = W4 ? ldS(cs, f, 0) : 0u;
   }
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-  const FragLane fl = frag_lane(r16, g4);
+  // the activation fragment's K pairing: fp8 x fp8 chunks 2 (l/16), +1; with
+  // fp4 weights chunks l/16 and 4 + l/16
+  const FragLane fl = W4 ? frag_lane_fp4a(r16, g4) : frag_lane(r16, g4);
   const v4f vzero = {0.0f, 0.0f, 0.0f, 0.0f};
   int tb = 0;    // table buffer of the current tile
   int gpar = 0;  // row-scale buffer of the current tile's first four stages
@@ -1971,7 +2007,13 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
         const uint32_t off = (uint32_t)(cur4 ? s4 : s4 - NST) * 128u;
 #pragma unroll
         for (int q = 0; q < AQ; ++q) aq[J & 1][q] = ldA((cur4 ? cs.a[q] : ns.a[q]) + off);
-        if constexpr (J == 0) sq = ld_sa(cur4 ? cs.sa + s4 : ns.sa + (s4 - NST));
+        if constexpr (J == 0) {
+          sq = ld_sa(cur4 ? cs.sa + s4 : ns.sa + (s4 - NST));
+          if constexpr (W4) {
+#pragma unroll
+            for (int f = 0; f < NF; ++f) swn[f] = ldS(cur4 ? cs : ns, f, (cur4 ? s4 : s4 - NST) >> 2);
+          }
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
       // -- 4. the MFMAs of stage st
@@ -2019,7 +2061,23 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
               af[b ^ 1] = read_frag(stg + (mi + 1) * 16 * 128, fl);
               sv[mi + 1] = sS[((mi + 1) * 16 + r16) * 4 + J];
             }
-            if constexpr (POW2) {
+            if constexpr (W4) {
+              // operand A = the fp4 weight fragment with its lane's e8m0
+              // scale for this stage (byte J of the group's dword)
+              const int sae = POW2 ? (int)(__float_as_uint(sv[mi]) >> 23) : 127;
+#pragma unroll
+              for (int f = 0; f < NF; ++f) {
+                const int sw = (int)(swc[f] >> (8 * J));
+                if constexpr (POW2)
+                  acc[mi][f] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                      bq[J % DB][f], af[b], acc[mi][f], 4, 0, 0, sw, 0, sae);
+                else
+                  pr[b][f] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                      bq[J % DB][f], af[b], vzero, 4, 0, 0, sw, 0, sae);
+              }
+              if constexpr (!POW2)
+                if (mi > 0) promote(mi - 1);
+            } else if constexpr (POW2) {
               // operand A = the weight fragment (the block's scale), operand
               // B = the activation rows (lane r16's row scale, the same for
               // its four 32-deep K quarters)
@@ -2047,9 +2105,14 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
       {
         const int sb_ = st + DB;
         const bool curb = sb_ < NST;
-        const uint32_t off = (uint32_t)(curb ? sb_ : sb_ - NST) * 2048u;
+        const uint32_t off = (uint32_t)(curb ? sb_ : sb_ - NST) * WBLK;
 #pragma unroll
         for (int f = 0; f < NF; ++f) bq[J % DB][f] = ldBf(curb ? cs : ns, f, off);
+      }
+      if constexpr (W4 && J == 3) {
+        // the next group's scale dwords (loaded at this group's stage 0)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) swc[f] = swn[f];
       }
       __builtin_amdgcn_sched_barrier(0);
       // -- 6. table loads for the next tile (consumed four stages later; the
@@ -2195,7 +2258,7 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
 #ifndef SGL_RB_NJ
 #define SGL_RB_NJ 1
 #endif
-template <int KIND>
+template <int KIND, bool W4 = false>
 int launch_rb(GemmArgs& a, hipStream_t stream) {
   using namespace rb;
   a.n_tiles = (int)ceil_div(a.N, (KIND == KIND_GATE_UP ? 128 : 256) * SGL_RB_NJ);
@@ -2208,11 +2271,56 @@ int launch_rb(GemmArgs& a, hipStream_t stream) {
   const int64_t need = (tiles + 7) / 8 * 8;
   if (need < wgs) wgs = need;
   a.m_tiles = (int)mt_bound;
-  if (a.sa_pow2 && a.sb_pow2)
-    gemm_rb_kernel<KIND, SGL_RB_NJ, true><<<(unsigned)wgs, 512, 0, stream>>>(a);
-  else
-    gemm_rb_kernel<KIND, SGL_RB_NJ, false><<<(unsigned)wgs, 512, 0, stream>>>(a);
+  if constexpr (W4) {
+    // fp4 weights: their scales always in the MFMA; the row scales too when
+    // they are powers of two
+    if (a.sa_pow2)
+      gemm_rb_kernel<KIND, 1, true, true><<<(unsigned)wgs, 512, 0, stream>>>(a);
+    else
+      gemm_rb_kernel<KIND, 1, false, true><<<(unsigned)wgs, 512, 0, stream>>>(a);
+  } else if (a.sa_pow2 && a.sb_pow2) {
+    gemm_rb_kernel<KIND, SGL_RB_NJ, true, false><<<(unsigned)wgs, 512, 0, stream>>>(a);
+  } else {
+    gemm_rb_kernel<KIND, SGL_RB_NJ, false, false><<<(unsigned)wgs, 512, 0, stream>>>(a);
+  }
   return check_launch("gemm_rb");
+}
+
+// Packed e2m1 [N, K/2] with e8m0 scales [N, K/32] -> the FP4 fragment layout:
+// weights 1 KB per (16-row block n16, 128-deep block kb), block index
+// n16 * K/128 + kb, byte 16 l + b of a block holding packed byte
+// 64 kb + 16 (l / 16) + b of row 16 n16 + l % 16 (lane l's 32 values, K
+// [32 (l / 16), +32) of the block); scales 256 bytes per (n16, group q of
+// four 128-deep blocks), block index n16 * K/512 + q, byte 4 l + j holding
+// the scale of row 16 n16 + l % 16 for its 32-deep block 16 q + 4 j + l / 16
+// (lane l's scale for stage 4 q + j).
+__global__ __launch_bounds__(256) void weight_fp4_to_frag_kernel(const uint8_t* __restrict__ w,
+                                                                 const uint8_t* __restrict__ s,
+                                                                 int64_t N, int64_t K,
+                                                                 uint8_t* __restrict__ ow,
+                                                                 uint8_t* __restrict__ os) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t KB = K / 128, KR = K / 2;
+  const int64_t nw = N * KR / 16;  // 16-byte weight chunks
+  if (i < nw) {
+    const int64_t blk = i >> 6;
+    const int l = (int)(i & 63);
+    const int64_t n16 = blk / KB, kb = blk - n16 * KB;
+    const int64_t n = n16 * 16 + (l & 15);
+    *reinterpret_cast<uint4*>(ow + i * 16) =
+        *reinterpret_cast<const uint4*>(w + n * KR + kb * 64 + (l >> 4) * 16);
+    return;
+  }
+  const int64_t d = i - nw;  // scale dword
+  if (d >= N * KB) return;
+  const int64_t blk = d >> 6;
+  const int l = (int)(d & 63);
+  const int64_t NQ = KB / 4;
+  const int64_t n16 = blk / NQ, q = blk - n16 * NQ;
+  const int64_t n = n16 * 16 + (l & 15);
+  const uint8_t* srow = s + n * (K / 32) + 16 * q + (l >> 4);
+  *reinterpret_cast<uint32_t*>(os + d * 4) =
+      (uint32_t)srow[0] | ((uint32_t)srow[4] << 8) | ((uint32_t)srow[8] << 16) | ((uint32_t)srow[12] << 24);
 }
 
 // [N, K] e4m3 row-major -> the MFMA fragment layout: 2 KB per (16-row block
@@ -2961,6 +3069,14 @@ int try_splitk(GemmArgs& a, hipStream_t stream) {
 // FP4 weights: a stage is 256 deep, so two stages fill what three fp8
 // stages of the same tile would (the 128 x 256 tiles run one workgroup per
 // CU with one stage in flight while the other is computed)
+// fp4 experts with fragment-layout copies: the register-fed kernel (K a
+// multiple of 512, 16 to 64 stages, 16-byte aligned row scales)
+inline bool rb_fp4_ok(const GemmArgs& a) {
+  const int64_t kb = a.K / 128;
+  return SGL_RB && a.frag && kb >= rb::kMinKB && kb <= rb::kMaxKBr && kb % 4 == 0 &&
+         aligned(a.sa, 16);
+}
+
 template <bool SAHW>
 int launch_fp4(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
   const bool big = rows_hint >= 64;
@@ -2976,9 +3092,11 @@ int launch_fp4(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       if (a.M <= 2048) return launch_cfg<KIND_DENSE, 128, 128, 2, 4, 2, WF_FP4, SAHW>(a, stream);
       return launch_cfg<KIND_DENSE, 128, 256, 2, 4, 2, WF_FP4, SAHW>(a, stream);
     case KIND_GATE_UP:
+      if (rb_fp4_ok(a)) return launch_rb<KIND_GATE_UP, true>(a, stream);
       return big ? launch_cfg<KIND_GATE_UP, 128, 256, 2, 4, 2, WF_FP4, SAHW>(a, stream)
                  : launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 3, WF_FP4, SAHW>(a, stream);
     default:
+      if (rb_fp4_ok(a)) return launch_rb<KIND_DOWN, true>(a, stream);
       return big ? launch_cfg<KIND_DOWN, 128, 256, 2, 4, 2, WF_FP4, SAHW>(a, stream)
                  : launch_cfg<KIND_DOWN, 32, 256, 1, 4, 3, WF_FP4, SAHW>(a, stream);
   }
@@ -3129,4 +3247,22 @@ extern "C" int sgl_fp8_weight_to_frag(const void* w, int64_t N, int64_t K, void*
   sgl::weight_to_frag_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, (hipStream_t)stream>>>(
       (const uint8_t*)w, N, K, (uint8_t*)out);
   return sgl::check_launch("fp8_weight_to_frag");
+}
+
+extern "C" int sgl_fp4_weight_to_frag(const void* w, const void* s, int64_t N, int64_t K, void* out_w,
+                                      void* out_s, sgl_stream_t stream) {
+  SGL_REQUIRE(N >= 0 && K >= 0, "fp4_weight_to_frag: negative shape");
+  SGL_REQUIRE(N % 16 == 0 && K % 512 == 0,
+              "fp4_weight_to_frag: N=%lld must be a multiple of 16 and K=%lld of 512", (long long)N,
+              (long long)K);
+  if (N == 0 || K == 0) return SGL_OK;
+  SGL_REQUIRE(w && s && out_w && out_s, "fp4_weight_to_frag: null pointer");
+  SGL_REQUIRE(w != out_w && s != out_s, "fp4_weight_to_frag: the outputs must not alias the inputs");
+  SGL_REQUIRE(sgl::aligned(w, 16) && sgl::aligned(out_w, 16) && sgl::aligned(out_s, 4),
+              "fp4_weight_to_frag: w and out_w must be 16-byte aligned, out_s 4-byte aligned");
+  SGL_REQUIRE(N * K < ((int64_t)1 << 36), "fp4_weight_to_frag: matrix too large");
+  const int64_t items = N * (K / 2) / 16 + N * (K / 128);
+  sgl::weight_fp4_to_frag_kernel<<<(unsigned)((items + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      (const uint8_t*)w, (const uint8_t*)s, N, K, (uint8_t*)out_w, (uint8_t*)out_s);
+  return sgl::check_launch("fp4_weight_to_frag");
 }

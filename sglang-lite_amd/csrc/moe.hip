@@ -691,11 +691,10 @@ int run_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I
   g.sa_pow2 = pow2_scale_mode(scale_mode);
   g.sb_pow2 = split ? 0 : pow2w;
   g.tile_ctr = tile_ctr;
-  // the fragment-layout records follow the E (+ shared) row-major ones; the
-  // routed FP4 experts have none that a kernel reads
+  // the fragment-layout records follow the E (+ shared) row-major ones
   const sgl_expert_ptrs* frag =
       (expert_format & SGL_EXPERT_FRAG_COPY) ? experts + E + (has_shared ? 1 : 0) : nullptr;
-  g.frag = split ? nullptr : frag;
+  g.frag = frag;
   if ((rc = launch_gemm(KIND_GATE_UP, g, T * k / E, stream)) || !split || !has_shared) return rc;
   GemmArgs sh = g;  // the shared expert: one group whose rows start at offsets[E]
   sh.E = 0;
@@ -740,7 +739,7 @@ int run_down(const void* hq, const float* hs, int64_t T, int64_t H, int64_t I, i
   g.tile_ctr = tile_ctr;
   const sgl_expert_ptrs* frag =
       (expert_format & SGL_EXPERT_FRAG_COPY) ? experts + E + (has_shared ? 1 : 0) : nullptr;
-  g.frag = split ? nullptr : frag;
+  g.frag = frag;
   if ((rc = launch_gemm(KIND_DOWN, g, T * k / E, stream)) || !split || !has_shared) return rc;
   GemmArgs sh = g;
   sh.E = 0;

@@ -62,6 +62,7 @@ SIGNATURES = {
     "sgl_fp4_gemm": (c_int, [P, P, c_int, P, P, P, c_int, I64, I64, I64, P]),
     "sgl_fp4_to_fp8_weight": (c_int, [P, P, I64, I64, P, P, P]),
     "sgl_fp8_weight_to_frag": (c_int, [P, I64, I64, P, P]),
+    "sgl_fp4_weight_to_frag": (c_int, [P, P, I64, I64, P, P, P]),
     "sgl_moe_route_topk": (c_int, [P, I64, c_int, c_int, c_int, P, c_float, P, P, P]),
     "sgl_moe_gate": (
         c_int,

@@ -134,6 +134,26 @@ def fp8_weight_to_frag(w: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def fp4_weight_to_frag(b: torch.Tensor, s: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Packed e2m1 weight [N, K/2] with e8m0 scales [N, K/32] -> new uint8
+    tensors (weights [N * K/2], scales [N * K/32]) in the FP4 fragment layout
+    of ``sgl_fp4_weight_to_frag`` (the layout ``EXPERT_FRAG_COPY`` records of
+    FP4 experts point at).  A layout step of this build with no counterpart
+    in the reference."""
+    wb = fp4_bytes(b).contiguous()
+    sc = fp4_weight_scale(s).view(torch.uint8).contiguous()
+    _lib.require_device(wb, sc, what="fp4_weight_to_frag")
+    N, KH = wb.shape
+    K = 2 * KH
+    if tuple(sc.shape) != (N, K // 32):
+        raise ValueError(f"fp4_weight_to_frag: scales must be [{N}, {K // 32}], got {tuple(sc.shape)}")
+    ow = torch.empty(N * KH, dtype=torch.uint8, device=wb.device)
+    os_ = torch.empty(N * (K // 32), dtype=torch.uint8, device=wb.device)
+    _lib.call("sgl_fp4_weight_to_frag", wb.data_ptr(), sc.data_ptr(), N, K, ow.data_ptr(),
+              os_.data_ptr(), _lib.stream_of(wb))
+    return ow, os_
+
+
 def _scale_flag(t: torch.Tensor, what: str) -> int:
     if t.dtype == torch.float32:
         return 0

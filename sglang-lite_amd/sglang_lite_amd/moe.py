@@ -23,7 +23,8 @@ from typing import List, Optional, Sequence, Tuple
 import torch
 
 from . import _lib
-from .kernel import FP4, FP8, E8M0, e8m0_to_f32, fp4_bytes, fp4_weight_scale, fp8_weight_to_frag
+from .kernel import (FP4, FP8, E8M0, e8m0_to_f32, fp4_bytes, fp4_weight_scale, fp4_weight_to_frag,
+                     fp8_weight_to_frag)
 
 SCORE_FUNCS = {"softmax": _lib.SCORE_SOFTMAX, "sigmoid": _lib.SCORE_SIGMOID,
                "sqrtsoftplus": _lib.SCORE_SQRTSOFTPLUS}
@@ -78,11 +79,12 @@ class ExpertTable:
         ``EXPERT_POW2_SCALES``: with a power-of-two activation ``scale_mode``
         the FP8 GEMMs then apply both scales inside the MFMA.
 
-        ``frag_layout``: also keep a copy of every FP8 expert weight (routed
-        FP8 and shared) in the MFMA fragment layout (``fp8_weight_to_frag``)
-        and add their records after the first set (``EXPERT_FRAG_COPY``): the
-        prefill-size FP8 GEMMs with fp32 block scales then load those weights
-        straight into registers.  Costs a second copy of the FP8 weights."""
+        ``frag_layout``: also keep a copy of every expert weight in the MFMA
+        fragment layout (``fp8_weight_to_frag``; FP4 routed experts with their
+        e8m0 scales, ``fp4_weight_to_frag``) and add their records after the
+        first set (``EXPERT_FRAG_COPY``): the grouped GEMMs then load those
+        weights straight into registers.  Costs a second copy of the expert
+        weights."""
         rows = list(experts) + ([shared] if shared is not None else [])
         if not rows:
             raise ValueError("ExpertTable needs at least one expert")
@@ -119,11 +121,15 @@ class ExpertTable:
             vals.append([ws[0].data_ptr(), ws[1].data_ptr(), ws[2].data_ptr(),
                          fs[0].data_ptr(), fs[1].data_ptr(), fs[2].data_ptr()])
         if frag_layout:
-            if H % 128 or I % 128:
-                raise ValueError("frag_layout needs H and I multiples of 128")
+            if H % 128 or I % 128 or (fp4 and (H % 512 or I % 512)):
+                raise ValueError("frag_layout needs H and I multiples of 128 (FP4 experts: of 512)")
             for i, r in enumerate(rows):
                 row = list(vals[i])
-                if not (fp4 and i < len(experts)):
+                if fp4 and i < len(experts):
+                    pairs = [fp4_weight_to_frag(w, sc) for w, sc in zip(r[:3], r[3:])]
+                    keep += [t for pr in pairs for t in pr]
+                    row = [pr[0].data_ptr() for pr in pairs] + [pr[1].data_ptr() for pr in pairs]
+                else:
                     frags = [fp8_weight_to_frag(w) for w in r[:3]]
                     keep += frags
                     row[:3] = [f.data_ptr() for f in frags]

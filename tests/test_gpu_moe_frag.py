@@ -25,7 +25,7 @@ import pytest
 import torch
 
 from helpers import bf16_values, to_dev_bf16, to_dev_f32, u8
-from test_frag_layout import frag_layout_ref
+from test_frag_layout import frag_fp4_layout_ref, frag_layout_ref
 
 pytestmark = pytest.mark.gpu
 
@@ -40,6 +40,39 @@ def test_weight_to_frag_matches_layout(gpu):
         out = K.fp8_weight_to_frag(wd)
         torch.cuda.synchronize()
         np.testing.assert_array_equal(out.cpu().numpy(), frag_layout_ref(w), err_msg=f"{N}x{K_}")
+
+
+def test_fp4_weight_to_frag_matches_layout(gpu):
+    from sglang_lite_amd import kernel as K
+
+    rng = np.random.default_rng(4)
+    for N, K_ in ((16, 512), (48, 1024), (2048, 4096)):
+        w = rng.integers(0, 256, size=(N, K_ // 2), dtype=np.uint8)
+        sc = rng.integers(0, 256, size=(N, K_ // 32), dtype=np.uint8)
+        ow, os_ = K.fp4_weight_to_frag(torch.from_numpy(w).to(gpu),
+                                       torch.from_numpy(sc).to(gpu).view(torch.float8_e8m0fnu))
+        torch.cuda.synchronize()
+        wf, sf = frag_fp4_layout_ref(w, sc)
+        np.testing.assert_array_equal(ow.cpu().numpy(), wf, err_msg=f"weights {N}x{K_}")
+        np.testing.assert_array_equal(os_.cpu().numpy(), sf, err_msg=f"scales {N}x{K_}")
+
+
+def _fp4_experts(dev, E, H, I, seed):
+    """MXFP4 routed experts as the reference's live format stores them:
+    packed e2m1 codes drawn uniformly, e8m0 1 x 32 scales in [2^-9, 2^-5]."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    u8_, e8 = torch.uint8, torch.float8_e8m0fnu
+    ent = []
+    for _ in range(E):
+        w1 = torch.randint(0, 256, (I, H // 2), dtype=u8_, device=dev, generator=g)
+        w3 = torch.randint(0, 256, (I, H // 2), dtype=u8_, device=dev, generator=g)
+        w2 = torch.randint(0, 256, (H, I // 2), dtype=u8_, device=dev, generator=g)
+        s1 = torch.randint(118, 123, (I, H // 32), dtype=u8_, device=dev, generator=g).view(e8)
+        s3 = torch.randint(118, 123, (I, H // 32), dtype=u8_, device=dev, generator=g).view(e8)
+        s2 = torch.randint(118, 123, (H, I // 32), dtype=u8_, device=dev, generator=g).view(e8)
+        ent.append((w1, w3, w2, s1, s3, s2))
+    return ent
 
 
 def _experts(dev, n, H, I, seed, ue8m0=False):
@@ -65,7 +98,7 @@ def _zipf_ids(rng, T, E, k, s=1.1):
     return logits
 
 
-def _compare(gpu, x, logits, ent, E, k, swiglu_limit=0.0, mode=0):
+def _compare(gpu, x, logits, ent, E, k, swiglu_limit=0.0, mode=0, pow2_flag=None):
     from sglang_lite_amd import kernel as K
     from sglang_lite_amd import moe as M
 
@@ -73,7 +106,8 @@ def _compare(gpu, x, logits, ent, E, k, swiglu_limit=0.0, mode=0):
     rows = M.ExpertTable.build(ent[:E], ent[E])
     frag = M.ExpertTable.build(ent[:E], ent[E], frag_layout=True)
     assert frag.fmt & 4 and frag.ptrs.shape[0] == 2 * (E + 1)
-    assert bool(rows.fmt & 2) == (mode == 1)  # power-of-two scales: both scales in the MFMA
+    # power-of-two scales: both scales in the MFMA
+    assert bool(rows.fmt & 2) == ((mode == 1) if pow2_flag is None else pow2_flag)
     w, ids = M.route_topk(to_dev_f32(logits, gpu), k)
     xd = to_dev_bf16(x, gpu)
     xq, xs = K.act_quant(xd, scale_mode=mode)
@@ -127,3 +161,19 @@ def test_ragged_shapes_bit_identical(gpu, H, I, pow2):
     logits = _zipf_ids(rng, T, E, k)
     counts = _compare(gpu, x, logits, ent, E, k, swiglu_limit=7.0, mode=1 if pow2 else 0)
     assert (counts % 128 != 0).any()  # remainder M tiles were exercised
+
+
+@pytest.mark.parametrize("T,mode", [(64, 3), (64, 0), (8192, 3), (8192, 0)])
+def test_fp4_experts_bit_identical(gpu, T, mode):
+    """FP4 routed experts (the live format) with the FP8 shared expert: the
+    register-fed fp4 kernels (weight scales in the MFMA; row scales in the
+    MFMA in the ue8m0 mode 3, promoted in fp32 in mode 0) against the
+    LDS-staged FP4 kernels, at decode (Zipf) and prefill (uniform) batches."""
+    H, I, E, k = 4096, 2048, 256, 8
+    print(f"frag fp4 T={T} mode={mode}", flush=True)
+    rng = np.random.default_rng(T + mode)
+    ent = _fp4_experts(gpu, E, H, I, seed=9) + _experts(gpu, 1, H, I, seed=10, ue8m0=(mode == 3))
+    x = bf16_values(rng, (T, H))
+    logits = _zipf_ids(rng, T, E, k) if T <= 512 else rng.standard_normal((T, E)).astype(np.float32)
+    counts = _compare(gpu, x, logits, ent, E, k, mode=mode, pow2_flag=(mode == 3))
+    assert counts.sum() == T * k
