@@ -2030,9 +2030,10 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
         // mi's MFMAs run.  Blocks past the tile's rows but within the body
         // are computed too (padding rows re-read the tile's first row; their
         // results are not stored).
-        // NMB 16-row blocks: all eight, or the first four for a tile of at
-        // most 64 rows (an expert's short last tile); the uniform branch picks
-        // one of two straight-line bodies
+        // NMB 16-row blocks: all eight, or the first four, two or one for a
+        // tile of at most 64, 32 or 16 rows (an expert's short last tile; at
+        // decode most tiles hold a few rows); the uniform branch picks one of
+        // four straight-line bodies
         auto blocks = [&](auto nmb_c) {
           constexpr int NMB = decltype(nmb_c)::value;
           v8i af[2];
@@ -2098,7 +2099,9 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
           if constexpr (!POW2) promote(NMB - 1);
         };
         if (nmb > 4) blocks(std::integral_constant<int, 8>{});
-        else blocks(std::integral_constant<int, 4>{});
+        else if (nmb > 2) blocks(std::integral_constant<int, 4>{});
+        else if (nmb > 1) blocks(std::integral_constant<int, 2>{});
+        else blocks(std::integral_constant<int, 1>{});
       }
       __builtin_amdgcn_sched_barrier(0);
       // -- 5. weight fragments of stage st + DB into the freed registers

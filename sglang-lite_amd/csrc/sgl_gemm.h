@@ -31,8 +31,9 @@ struct GemmArgs {
   int sb_pow2;        // fp8 weight scales (fp32) are powers of two: with sa_pow2, both
                       // scales go into the MFMA and no fp32 promotion runs
   const sgl_expert_ptrs* experts;  // moe: device array [E (+1)]
-  const sgl_expert_ptrs* frag;     // moe (or null): the same experts with their FP8 weights in
-                                   // the MFMA fragment layout (sgl_fp8_weight_to_frag)
+  const sgl_expert_ptrs* frag;     // moe (or null): the same experts with their weights (and
+                                   // FP4 scales) in the MFMA fragment layout
+                                   // (sgl_fp8_weight_to_frag, sgl_fp4_weight_to_frag)
   const int32_t* offsets;          // moe: [E + 1]
   const int32_t* sorted_slot;      // moe: [T * k]
   const float* route_w;            // gate_up: [T * k] slot-indexed (may be null)
