@@ -51,10 +51,12 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extra", action="store_true", help="headline prefill line only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--profile-kernels", nargs="?", const="fp8", choices=("fp8", "fp4", "small", "frag"),
-                    help="run only 3 prefill steps (FP8 experts, or FP4 routed experts in the "
-                         "ue8m0 scale mode) plus a counter-calibration kernel, for rocprofv3 "
-                         "runs; prints no JSON")
+    ap.add_argument("--profile-kernels", nargs="?", const="fp8", choices=("fp8", "fp4", "small", "frag", "fp4frag"),
+                    help="for rocprofv3 runs: only 3 prefill steps (fp8: FP8 experts; fp4: FP4 "
+                         "routed experts in the ue8m0 scale mode; frag / fp4frag: the same with "
+                         "fragment-layout weight copies, then 3 decode steps at T = 64/256/512; "
+                         "small: the short kernels) plus a counter-calibration kernel; prints no "
+                         "JSON")
     return ap.parse_args()
 
 
@@ -97,10 +99,11 @@ def frag_table(M, weights):
     return M.ExpertTable.build(experts, shared, frag_layout=True)
 
 
-def make_fp4_weights(torch, M, dev, shared, seed=6):
+def make_fp4_weights(torch, M, dev, shared, seed=6, frag_layout=False):
     """256 routed MXFP4 experts (the reference's live routed format: packed
     e2m1 codes drawn uniformly, e8m0 1x32 scales in [2^-9, 2^-5]) plus the
-    given FP8 shared expert."""
+    given FP8 shared expert; with frag_layout the table also carries
+    fragment-layout copies (the register-fed GEMMs)."""
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     u8 = torch.uint8
@@ -111,7 +114,7 @@ def make_fp4_weights(torch, M, dev, shared, seed=6):
     e8 = torch.float8_e8m0fnu
     experts = [(w13[e, 0], w13[e, 1], w2[e], s13[e, 0].view(e8), s13[e, 1].view(e8), s2[e].view(e8))
                for e in range(E)]
-    return M.ExpertTable.build(experts, shared)
+    return M.ExpertTable.build(experts, shared, frag_layout=frag_layout)
 
 
 def zipf_logits(torch, T, seed, s=1.1):
@@ -431,32 +434,50 @@ def fp4_extra(torch, M, K, weights, dev, args, flush):
         if mode == 3:
             out["prefill_mode3"]["gate_up_traffic_bytes"] = read_traffic("moe_fp4_gate_up_prefill")
         log(f"fp4 prefill mode {mode}: {ms:.3f} ms, gate_up {gu:.0f} TF, down {dn:.0f} TF")
-    dec = []
     wb = 3 * I * H // 2 + 3 * I * H // 32  # packed e2m1 + e8m0 bytes per routed expert
     sb_ = 3 * I * H + 3 * 4 * (I // 128) * (H // 128)  # the FP8 shared expert
-    for Td, seed in ((64, 31), (256, 32), (512, 33)):
-        logits = zipf_logits(torch, Td, seed).to(dev)
-        xd = torch.randn(Td, H, generator=torch.Generator().manual_seed(seed)).to(
-            torch.bfloat16).to(dev)
-        ws = M.MoEWorkspace()
-        yd = torch.empty(Td, H, dtype=torch.bfloat16, device=dev)
 
-        def dstep():
-            w, ids = M.route_topk(logits, K_TOP)
-            M.moe_forward(xd, ids, w, table4, workspace=ws, out=yd, scale_mode=3)
+    def decode_lines(tab, what):
+        dec = []
+        for Td, seed in ((64, 31), (256, 32), (512, 33)):
+            logits = zipf_logits(torch, Td, seed).to(dev)
+            xd = torch.randn(Td, H, generator=torch.Generator().manual_seed(seed)).to(
+                torch.bfloat16).to(dev)
+            ws = M.MoEWorkspace()
+            yd = torch.empty(Td, H, dtype=torch.bfloat16, device=dev)
 
-        msd = time_steps(torch, dstep, max(args.steps, 10), args.warmup)
-        msg_d = graph_ms(torch, dstep, max(args.steps, 10))
-        _, ids = M.route_topk(logits, K_TOP)
-        touched = int(torch.unique(ids).numel())
-        by = touched * wb + sb_ + 4 * Td * H + 4 * Td * E
-        dec.append({"tokens": Td, "ms": round(msd, 4), "tokens_per_s": round(Td / msd * 1e3, 1),
-                    "experts_touched": touched, "bytes": by, "gbs": round(by / msd / 1e6, 1),
-                    "hbm_frac": round(by / msd / 1e6 / PEAK_HBM_GBS, 4),
-                    "graph_ms": round(msg_d, 4),
-                    "graph_hbm_frac": round(by / msg_d / 1e6 / PEAK_HBM_GBS, 4)})
-        log(f"fp4 decode T={Td}: {msd:.3f} ms, {by / msd / 1e6:.0f} GB/s")
+            def dstep():
+                w, ids = M.route_topk(logits, K_TOP)
+                M.moe_forward(xd, ids, w, tab, workspace=ws, out=yd, scale_mode=3)
+
+            msd = time_steps(torch, dstep, max(args.steps, 10), args.warmup)
+            msg_d = graph_ms(torch, dstep, max(args.steps, 10))
+            _, ids = M.route_topk(logits, K_TOP)
+            touched = int(torch.unique(ids).numel())
+            by = touched * wb + sb_ + 4 * Td * H + 4 * Td * E
+            dec.append({"tokens": Td, "ms": round(msd, 4), "tokens_per_s": round(Td / msd * 1e3, 1),
+                        "experts_touched": touched, "bytes": by, "gbs": round(by / msd / 1e6, 1),
+                        "hbm_frac": round(by / msd / 1e6 / PEAK_HBM_GBS, 4),
+                        "graph_ms": round(msg_d, 4),
+                        "graph_hbm_frac": round(by / msg_d / 1e6 / PEAK_HBM_GBS, 4)})
+            log(f"fp4 decode{what} T={Td}: {msd:.3f} ms, graph {msg_d:.3f} ms, "
+                f"{by / msg_d / 1e6:.0f} GB/s")
+        return dec
+
+    dec = decode_lines(table4, "")
     out["decode_mode3"] = dec
+    # the same routed experts with fragment-layout copies (register-fed GEMMs)
+    del table4
+    table4f = make_fp4_weights(torch, M, dev, shared, frag_layout=True)
+    pre = Prefill(torch, M, K, table4f, T, dev, seed=4, mode=3)
+    ms = time_steps(torch, pre.step, args.steps, args.warmup)
+    st = pre.staged(max(3, min(args.steps, 10)))
+    out["prefill_mode3_frag_layout"] = {
+        "tokens": T, "ms": round(ms, 4), "tokens_per_s": round(T / ms * 1e3, 1),
+        "stages_ms": {k_: round(v, 4) for k_, v in st.items()}}
+    log(f"fp4 prefill mode 3 with fragment-layout copies: {ms:.3f} ms")
+    out["decode_mode3_frag_layout"] = decode_lines(table4f, " (fragment layout)")
+    del table4f
     gw = torch.Generator(device=dev).manual_seed(7)
     bq = torch.randint(0, 256, (4096, 3584), dtype=torch.uint8, device=dev, generator=gw)
     bs = torch.randint(118, 123, (4096, 224), dtype=torch.uint8, device=dev,
@@ -613,7 +634,23 @@ def main():
             shared = (w13[E, 0], w13[E, 1], w2[E], s13[E, 0], s13[E, 1], s2[E])
             pre = Prefill(torch, M, K, make_fp4_weights(torch, M, dev, shared), T, dev, seed=4,
                           mode=3)
-        if args.profile_kernels == "frag":
+        if args.profile_kernels == "fp4frag":
+            # FP4 routed experts with fragment-layout copies, ue8m0 mode 3: 3
+            # prefill steps, then 3 decode steps each at T = 64 / 256 / 512
+            w13, s13, w2, s2 = weights
+            shared = (w13[E, 0], w13[E, 1], w2[E], s13[E, 0], s13[E, 1], s2[E])
+            tf = make_fp4_weights(torch, M, dev, shared, frag_layout=True)
+            pre = Prefill(torch, M, K, tf, T, dev, seed=4, mode=3)
+            for _ in range(3):
+                pre.step()
+            for Td, seed in ((64, 31), (256, 32), (512, 33)):
+                logits = zipf_logits(torch, Td, seed).to(dev)
+                xd = torch.randn(Td, H, generator=torch.Generator().manual_seed(seed)).to(
+                    torch.bfloat16).to(dev)
+                for _ in range(3):
+                    w, ids = M.route_topk(logits, K_TOP)
+                    M.moe_forward(xd, ids, w, tf, scale_mode=3)
+        elif args.profile_kernels == "frag":
             # fragment-layout weight copies: 3 prefill steps, then 3 decode
             # steps each at T = 64 / 256 / 512 (Zipf load)
             tf = frag_table(M, weights)
