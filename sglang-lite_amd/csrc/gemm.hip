@@ -2261,6 +2261,15 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
 #ifndef SGL_RB_NJ
 #define SGL_RB_NJ 1
 #endif
+// CUs a grouped launch may fill: all, or what spare_cus / max_cus leave it
+// (a multiple of 8, so every XCD gets the same number)
+int64_t cu_budget(const GemmArgs& a) {
+  int64_t n = device_cu_count();
+  if (a.max_cus > 0 && n > a.max_cus) n = a.max_cus;
+  n -= a.spare_cus;
+  return std::max<int64_t>(8, (n + (a.spare_cus || a.max_cus ? 0 : 7)) / 8 * 8);
+}
+
 template <int KIND, bool W4 = false>
 int launch_rb(GemmArgs& a, hipStream_t stream) {
   using namespace rb;
@@ -2269,8 +2278,7 @@ int launch_rb(GemmArgs& a, hipStream_t stream) {
   const int64_t mt_bound = P / BM + (P < a.E ? P : a.E) + (a.has_shared ? ceil_div(a.T, BM) : 0);
   const int64_t tiles = mt_bound * a.n_tiles;
   if (tiles == 0) return SGL_OK;
-  int64_t wgs = (int64_t)device_cu_count();
-  wgs = (wgs + 7) / 8 * 8;
+  int64_t wgs = cu_budget(a);
   const int64_t need = (tiles + 7) / 8 * 8;
   if (need < wgs) wgs = need;
   a.m_tiles = (int)mt_bound;
@@ -2578,8 +2586,7 @@ int launch_cfg(GemmArgs& a, hipStream_t stream) {
                          (KIND == KIND_GATE_UP && LW > 0 ? WN * BM * 4 : 4);
   static_assert(C::SMEM + kExtra <= kLdsPerCU, "tile configuration exceeds the LDS of a CU");
   constexpr int per_cu = kLdsPerCU / (C::SMEM + kExtra) >= 2 ? 2 : 1;
-  int64_t wgs = (int64_t)device_cu_count() * per_cu;
-  wgs = (wgs + 7) / 8 * 8;
+  int64_t wgs = cu_budget(a) * per_cu;
   const int64_t need = (tiles + 7) / 8 * 8;
   if (need < wgs) wgs = need;
   a.m_tiles = (int)mt_bound;

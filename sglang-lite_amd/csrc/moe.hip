@@ -650,6 +650,74 @@ bool pow2_scale_mode(int scale_mode) {
   return scale_mode == SGL_SCALE_TORCH_UE8M0 || scale_mode == SGL_SCALE_TILELANG_UE8M0;
 }
 
+// FP4 layers run the FP8 shared expert in launches of their own: at decode
+// sizes a few column tiles, i.e. a few workgroups each at one workgroup's
+// stream rate.  Up to kSideMaxT tokens they run on a second stream of the
+// device beside the routed launch, which leaves them kSharedCus CUs (fork and
+// join by events, so a graph captured on the caller's stream holds both
+// branches).  The enqueue sequence holds a mutex: the events are shared.
+#ifndef SGL_SIDE_MAX_T
+#define SGL_SIDE_MAX_T 512
+#endif
+constexpr int64_t kSideMaxT = SGL_SIDE_MAX_T;
+constexpr int kSharedCus = 16;
+struct SideStream {
+  hipStream_t s;
+  hipEvent_t fork, join;
+};
+std::mutex g_side_mu;
+SideStream g_side[64];
+
+// The device's side stream, created on first use outside graph capture;
+// null when there is none (the caller then runs the launches in order).
+SideStream* side_stream(hipStream_t stream) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  SideStream& ss = g_side[dev];
+  if (ss.s) return &ss;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  SideStream n = {};
+  if (hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreateWithFlags(&n.fork, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&n.join, hipEventDisableTiming) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  ss = n;
+  return &ss;
+}
+
+// routed launch g on `stream` and the shared launch sh: side by side when a
+// side stream exists and T <= kSideMaxT, else one after the other
+int run_routed_and_shared(int kind, GemmArgs& g, GemmArgs& sh, int64_t T, hipStream_t stream) {
+  const int64_t hint = g.T * g.k / g.E;
+  if (T <= kSideMaxT) {
+    std::lock_guard<std::mutex> lock(g_side_mu);
+    SideStream* ss = side_stream(stream);
+    if (ss) {
+      sh.max_cus = kSharedCus;
+      g.spare_cus = kSharedCus;
+      int rc;
+      if (hipEventRecord(ss->fork, stream) != hipSuccess ||
+          hipStreamWaitEvent(ss->s, ss->fork, 0) != hipSuccess)
+        return check_launch("moe side stream fork");
+      if ((rc = launch_gemm(kind, sh, T, ss->s))) return rc;
+      if (hipEventRecord(ss->join, ss->s) != hipSuccess) return check_launch("moe side stream join");
+      rc = launch_gemm(kind, g, hint, stream);
+      if (hipStreamWaitEvent(stream, ss->join, 0) != hipSuccess && !rc)
+        return check_launch("moe side stream join");
+      return rc;
+    }
+  }
+  int rc = launch_gemm(kind, g, hint, stream);
+  return rc ? rc : launch_gemm(kind, sh, T, stream);
+}
+
+
 // The routed experts in `expert_format`; the shared expert (experts[E]) is
 // always FP8 128 x 128 (deepseek_infer/model.py:623-626 builds it without the
 // routed experts' dtype).  FP4 routed experts run in a launch of their own,
@@ -695,7 +763,7 @@ int run_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I
   const sgl_expert_ptrs* frag =
       (expert_format & SGL_EXPERT_FRAG_COPY) ? experts + E + (has_shared ? 1 : 0) : nullptr;
   g.frag = frag;
-  if ((rc = launch_gemm(KIND_GATE_UP, g, T * k / E, stream)) || !split || !has_shared) return rc;
+  if (!split || !has_shared) return launch_gemm(KIND_GATE_UP, g, T * k / E, stream);
   GemmArgs sh = g;  // the shared expert: one group whose rows start at offsets[E]
   sh.E = 0;
   sh.offsets = offsets + E;
@@ -705,7 +773,7 @@ int run_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I
   sh.wfmt = WF_FP8;
   sh.sb_pow2 = pow2w;
   sh.tile_ctr = tile_ctr ? tile_ctr + 8 : nullptr;
-  return launch_gemm(KIND_GATE_UP, sh, T, stream);
+  return run_routed_and_shared(KIND_GATE_UP, g, sh, T, stream);
 }
 
 int run_down(const void* hq, const float* hs, int64_t T, int64_t H, int64_t I, int E, int k,
@@ -740,7 +808,7 @@ int run_down(const void* hq, const float* hs, int64_t T, int64_t H, int64_t I, i
   const sgl_expert_ptrs* frag =
       (expert_format & SGL_EXPERT_FRAG_COPY) ? experts + E + (has_shared ? 1 : 0) : nullptr;
   g.frag = frag;
-  if ((rc = launch_gemm(KIND_DOWN, g, T * k / E, stream)) || !split || !has_shared) return rc;
+  if (!split || !has_shared) return launch_gemm(KIND_DOWN, g, T * k / E, stream);
   GemmArgs sh = g;
   sh.E = 0;
   sh.offsets = offsets + E;
@@ -750,7 +818,7 @@ int run_down(const void* hq, const float* hs, int64_t T, int64_t H, int64_t I, i
   sh.wfmt = WF_FP8;
   sh.sb_pow2 = pow2w;
   sh.tile_ctr = tile_ctr ? tile_ctr + 8 : nullptr;
-  return launch_gemm(KIND_DOWN, sh, T, stream);
+  return run_routed_and_shared(KIND_DOWN, g, sh, T, stream);
 }
 
 int launch_route(const char* what, const float* logits, int64_t T, int E, int k, int score_func,

@@ -50,6 +50,8 @@ struct GemmArgs {
   int m_tiles;      // grid rows (upper bound of M tiles)
   int n_tiles;      // tiles along N
   int* tile_ctr;    // moe: 8 zeroed per-XCD tile counters -> dynamic tile order (null: static)
+  int spare_cus;    // grouped launches: leave this many CUs to a concurrent launch (0: none)
+  int max_cus;      // grouped launches: use at most this many CUs (0: all)
 };
 
 int launch_gemm(int kind, GemmArgs& args, int64_t rows_hint, hipStream_t stream);

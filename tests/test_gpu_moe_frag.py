@@ -177,3 +177,37 @@ def test_fp4_experts_bit_identical(gpu, T, mode):
     logits = _zipf_ids(rng, T, E, k) if T <= 512 else rng.standard_normal((T, E)).astype(np.float32)
     counts = _compare(gpu, x, logits, ent, E, k, mode=mode, pow2_flag=(mode == 3))
     assert counts.sum() == T * k
+
+
+@pytest.mark.parametrize("frag", [False, True])
+def test_fp4_layer_in_a_graph_replays_equal_eager(gpu, frag):
+    """The FP4 layer at a decode batch runs its FP8 shared expert on a second
+    stream beside the routed launch (fork and join by events): captured into
+    a HIP graph on the caller's stream, every replay, with eager layers and
+    synchronizations between them, equals the eager layer bit for bit."""
+    from sglang_lite_amd import moe as M
+
+    H, I, E, k, T = 4096, 2048, 256, 8, 64
+    print(f"fp4 graph frag={frag}", flush=True)
+    rng = np.random.default_rng(21)
+    ent = _fp4_experts(gpu, E, H, I, seed=12) + _experts(gpu, 1, H, I, seed=13, ue8m0=True)
+    table = M.ExpertTable.build(ent[:E], ent[E], frag_layout=frag)
+    x = to_dev_bf16(bf16_values(rng, (T, H)), gpu)
+    w, ids = M.route_topk(to_dev_f32(_zipf_ids(rng, T, E, k), gpu), k)
+    x2 = to_dev_bf16(bf16_values(rng, (T, H)), gpu)
+    ws = M.MoEWorkspace()
+    y = torch.empty(T, H, dtype=torch.bfloat16, device=gpu)
+    M.moe_forward(x, ids, w, table, workspace=ws, out=y, scale_mode=3)
+    torch.cuda.synchronize()
+    eager = u8(y).copy()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        M.moe_forward(x, ids, w, table, workspace=ws, out=y, scale_mode=3)
+    for i in range(4):
+        y.fill_(0)
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(u8(y), eager, err_msg=f"replay {i}")
+        # eager work between replays, on its own workspace
+        M.moe_forward(x2, ids, w, table, scale_mode=3)
+        torch.cuda.synchronize()
