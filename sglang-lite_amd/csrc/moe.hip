@@ -667,6 +667,9 @@ struct SideStream {
 };
 std::mutex g_side_mu;
 SideStream g_side[64];
+// set while sgl_moe_forward_noalloc runs: its calls create no stream (an
+// existing side stream is still used)
+thread_local bool t_no_new_side = false;
 
 // The device's side stream, created on first use outside graph capture;
 // null when there is none (the caller then runs the launches in order).
@@ -675,6 +678,7 @@ SideStream* side_stream(hipStream_t stream) {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
   SideStream& ss = g_side[dev];
   if (ss.s) return &ss;
+  if (t_no_new_side) return nullptr;
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
     (void)hipGetLastError();
@@ -947,8 +951,11 @@ int sgl_moe_forward_noalloc(const void* x, int64_t T, int64_t H, int64_t I, int 
   if ((rc = sgl::moe_scratch_ptr(&ws))) return rc;
   // every buffer the layer reads is written first inside the call (the
   // permute kernel zeroes the GEMM tile counters), so the array needs no clear
-  return sgl_moe_forward(x, T, H, I, E, k, ids, weights, experts, has_shared, expert_format,
-                         swiglu_limit, scale_mode, ws, sgl::kScratchBytes, y, stream);
+  sgl::t_no_new_side = true;
+  rc = sgl_moe_forward(x, T, H, I, E, k, ids, weights, experts, has_shared, expert_format,
+                       swiglu_limit, scale_mode, ws, sgl::kScratchBytes, y, stream);
+  sgl::t_no_new_side = false;
+  return rc;
 }
 
 int sgl_moe_forward(const void* x, int64_t T, int64_t H, int64_t I, int E, int k,
