@@ -335,11 +335,12 @@ size_t sgl_moe_workspace_size(int64_t T, int64_t H, int64_t I, int E, int k, int
  * (ids int32 [T, k], weights fp32 [T, k]): act quant -> permute -> gate/up
  * -> down -> combine, y bf16 [T, H]; routed experts in expert_format.
  * Replaces engine/v4_moe_fast.py:79-106 _moe_forward_activated_only after
- * the gate.  With FP4 routed experts and T <= 512, sgl_moe_gate_up /
- * sgl_moe_down / sgl_moe_forward run the FP8 shared expert's GEMMs on a
- * second stream of the device (created on the first such call made outside
- * graph capture), forked from and joined back into `stream` by events, so
- * the results are ordered on `stream` as if it ran them all. */
+ * the gate.  With FP4 routed experts and T <= 512, when `stream` is being
+ * captured into a graph, sgl_moe_gate_up / sgl_moe_down / sgl_moe_forward
+ * run the FP8 shared expert's GEMMs on a second stream of the device
+ * (created by the first such call made outside capture), forked from and
+ * joined back into `stream` by events, so the graph orders the results as if
+ * `stream` ran them all; eager calls run everything on `stream`. */
 int sgl_moe_forward(const void* x, int64_t T, int64_t H, int64_t I, int E, int k,
                     const int32_t* ids, const float* weights, const sgl_expert_ptrs* experts,
                     int has_shared, int expert_format, float swiglu_limit, int scale_mode,

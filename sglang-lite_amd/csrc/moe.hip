@@ -652,10 +652,14 @@ bool pow2_scale_mode(int scale_mode) {
 
 // FP4 layers run the FP8 shared expert in launches of their own: at decode
 // sizes a few column tiles, i.e. a few workgroups each at one workgroup's
-// stream rate.  Up to kSideMaxT tokens they run on a second stream of the
-// device beside the routed launch, which leaves them kSharedCus CUs (fork and
-// join by events, so a graph captured on the caller's stream holds both
-// branches).  The enqueue sequence holds a mutex: the events are shared.
+// stream rate.  Up to kSideMaxT tokens, when the caller's stream is being
+// captured into a graph, they run on a second stream of the device beside the
+// routed launch, which leaves them kSharedCus CUs (fork and join by events:
+// the graph holds both branches).  Eager calls run them in order: there the
+// cross-stream event waits cost more than the overlap gains (measured: FP4
+// decode T = 64 / 256 / 512 0.415 / 0.667 / 0.777 -> 0.467 / 0.774 / 0.943
+// ms).  The side stream is created by the first such call made outside
+// capture.  The enqueue sequence holds a mutex: the events are shared.
 #ifndef SGL_SIDE_MAX_T
 #define SGL_SIDE_MAX_T 512
 #endif
@@ -671,19 +675,19 @@ SideStream g_side[64];
 // existing side stream is still used)
 thread_local bool t_no_new_side = false;
 
-// The device's side stream, created on first use outside graph capture;
-// null when there is none (the caller then runs the launches in order).
+// The device's side stream when `stream` is being captured (null
+// otherwise, or when none exists yet); created by calls outside capture.
 SideStream* side_stream(hipStream_t stream) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
   SideStream& ss = g_side[dev];
-  if (ss.s) return &ss;
-  if (t_no_new_side) return nullptr;
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess) {
     (void)hipGetLastError();
     return nullptr;
   }
+  if (cs != hipStreamCaptureStatusNone) return ss.s ? &ss : nullptr;
+  if (ss.s || t_no_new_side) return nullptr;
   SideStream n = {};
   if (hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking) != hipSuccess ||
       hipEventCreateWithFlags(&n.fork, hipEventDisableTiming) != hipSuccess ||
@@ -692,11 +696,12 @@ SideStream* side_stream(hipStream_t stream) {
     return nullptr;
   }
   ss = n;
-  return &ss;
+  return nullptr;
 }
 
-// routed launch g on `stream` and the shared launch sh: side by side when a
-// side stream exists and T <= kSideMaxT, else one after the other
+// routed launch g on `stream` and the shared launch sh: side by side in a
+// graph being captured (T <= kSideMaxT, a side stream exists), else one after
+// the other
 int run_routed_and_shared(int kind, GemmArgs& g, GemmArgs& sh, int64_t T, hipStream_t stream) {
   const int64_t hint = g.T * g.k / g.E;
   if (T <= kSideMaxT) {
