@@ -369,8 +369,10 @@ int sgl_moe_forward_noalloc(const void* x, int64_t T, int64_t H, int64_t I, int 
 
 /* Pack KV rows.  Layout A: kv [T, 512] (bf16 / f16 / f32, row stride ldkv)
  * with scale_mode SGL_SCALE_KV_UE8M0 (the torch fallback,
- * dsv4_kv_pack.py:78-101) or SGL_SCALE_TILELANG_UE8M0 (act_quant_fn
- * injected, dsv4_kv_pack.py:58-61), out [T, 584] uint8; with paged != 0 the
+ * dsv4_kv_pack.py:78-101), SGL_SCALE_TILELANG_UE8M0 (the official TileLang
+ * act_quant injected, dsv4_kv_pack.py:58-61) or SGL_SCALE_TORCH_UE8M0 (this
+ * library's act_quant with its default torch formula injected), out [T, 584]
+ * uint8; with paged != 0 the
  * output is the footer-paged [ceil(T/page)*page*584] bytes of to_paged_hnd,
  * zero-filled padding rows included.  Layout B: kv [T, 576], out [T, 656]
  * (scale_mode ignored: SGL_SCALE_TORCH_FP32), paged must be 0.

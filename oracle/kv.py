@@ -21,7 +21,9 @@ def pack_layout_a(kv: np.ndarray, rope_bytes: np.ndarray, scale_mode: int = 4) -
     ``kv``: float32 [T, 512] holding the input values; ``rope_bytes``: uint8
     [T, 128], the RoPE part's raw 16-bit bytes (copied verbatim, :69-71).
     scale_mode 4 = the torch fallback (:78-101); 3 = the injected
-    ``act_quant(..., "ue8m0", float8_e8m0fnu)`` (:58-61, kernel.py:22-37,79-96).
+    ``act_quant(..., "ue8m0", float8_e8m0fnu)`` (:58-61, kernel.py:22-37,79-96);
+    1 = an injected quantizer with the torch ue8m0 formula
+    (deep_gemm_sm120/utils/math.py:13-37, group 64).
     """
     kv = np.asarray(kv, dtype=np.float32)
     T = kv.shape[0]
@@ -30,6 +32,8 @@ def pack_layout_a(kv: np.ndarray, rope_bytes: np.ndarray, scale_mode: int = 4) -
         q, s = Q.kv_ue8m0_quant(nope, 64)
     elif scale_mode == 3:
         q, s = Q.act_quant_tilelang(nope, 64, round_scale=True)
+    elif scale_mode == 1:
+        q, s = Q.per_token_cast_to_fp8(nope, True, 64)
     else:
         raise ValueError(scale_mode)
     out = np.zeros((T, ROW_A), dtype=np.uint8)

@@ -386,15 +386,22 @@ unsigned grid_for_rows(int64_t rows, int rows_per_wave = 1) {
   return (unsigned)(blocks < 1 ? 1 : blocks);
 }
 
-// layout A launch for the two ue8m0 scale modes (compile-time in the kernel)
+// layout A launch for the three ue8m0 scale modes (compile-time in the kernel)
 template <int DT>
 void launch_pack_a(unsigned g, hipStream_t st, int mode, const uint8_t* kv, int64_t T, int64_t ld_bytes,
                    int paged, int page, int64_t rows, uint8_t* out, const PageTable& pt) {
   if (mode == SGL_SCALE_KV_UE8M0)
     kv_pack_a_kernel<DT, kKvRows, SGL_SCALE_KV_UE8M0><<<g, 256, 0, st>>>(kv, T, ld_bytes, paged, page, rows, out, pt);
+  else if (mode == SGL_SCALE_TORCH_UE8M0)
+    kv_pack_a_kernel<DT, kKvRows, SGL_SCALE_TORCH_UE8M0><<<g, 256, 0, st>>>(kv, T, ld_bytes, paged, page, rows,
+                                                                          out, pt);
   else
     kv_pack_a_kernel<DT, kKvRows, SGL_SCALE_TILELANG_UE8M0><<<g, 256, 0, st>>>(kv, T, ld_bytes, paged, page, rows,
                                                                              out, pt);
+}
+
+bool ue8m0_mode(int m) {
+  return m == SGL_SCALE_KV_UE8M0 || m == SGL_SCALE_TILELANG_UE8M0 || m == SGL_SCALE_TORCH_UE8M0;
 }
 
 }  // namespace
@@ -410,8 +417,8 @@ int sgl_kv_pack(const void* kv, int dtype, int64_t T, int64_t ldkv, int layout, 
   hipStream_t st = (hipStream_t)stream;
   const int es = dtype == SGL_F32 ? 4 : 2;
   if (layout == SGL_KV_LAYOUT_A) {
-    SGL_REQUIRE(scale_mode == SGL_SCALE_KV_UE8M0 || scale_mode == SGL_SCALE_TILELANG_UE8M0,
-                "kv_pack: layout A needs a ue8m0 scale mode (got %d)", scale_mode);
+    SGL_REQUIRE(sgl::ue8m0_mode(scale_mode), "kv_pack: layout A needs a ue8m0 scale mode (got %d)",
+                scale_mode);
     SGL_REQUIRE(dtype != SGL_F32, "kv_pack: layout A stores the rope as 16-bit values; fp32 "
                                   "input is not representable in the 584-byte row");
     SGL_REQUIRE(ldkv >= 512, "kv_pack: layout A row stride %lld < 512", (long long)ldkv);
@@ -457,7 +464,7 @@ int sgl_kv_pack_to_pages(const void* kv, int dtype, int64_t T, int64_t ldkv, int
               "kv_pack_to_pages: bad T / start_pos / page_size / num_blocks");
   SGL_REQUIRE(dtype == SGL_BF16 || dtype == SGL_F16,
               "kv_pack_to_pages: kv must be bf16 or f16 (the 584-byte row stores 16-bit rope)");
-  SGL_REQUIRE(scale_mode == SGL_SCALE_KV_UE8M0 || scale_mode == SGL_SCALE_TILELANG_UE8M0,
+  SGL_REQUIRE(sgl::ue8m0_mode(scale_mode),
               "kv_pack_to_pages: layout A needs a ue8m0 scale mode (got %d)", scale_mode);
   SGL_REQUIRE(layer_idx >= 0 && layer_idx < num_layers, "kv_pack_to_pages: layer_idx %d out of range (%d)",
               layer_idx, num_layers);

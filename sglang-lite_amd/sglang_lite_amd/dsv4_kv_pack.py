@@ -70,7 +70,9 @@ def _fused_quant_mode(act_quant_fn) -> Optional[int]:
         return _lib.SCALE_KV_UE8M0
     from . import kernel as HK
 
-    if act_quant_fn is HK.act_quant:
+    # this package's act_quant, or a wrapper of it such as the kernel.act_quant
+    # that attach_v4_deep_gemm installs (v4_sparse_mla.py:85,91 resolves that name)
+    if act_quant_fn is HK.act_quant or getattr(act_quant_fn, HK.FUSED_ACT_QUANT, False):
         return HK.scale_mode_for("ue8m0")
     if getattr(act_quant_fn, "__module__", None) == "kernel" and \
             getattr(act_quant_fn, "__name__", None) == "act_quant":

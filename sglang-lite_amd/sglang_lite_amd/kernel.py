@@ -29,6 +29,11 @@ FP8 = torch.float8_e4m3fn
 E8M0 = torch.float8_e8m0fnu
 FP4 = torch.float4_e2m1fn_x2  # two e2m1 codes per byte, low nibble = even K
 
+# Attribute set on functions that compute exactly this module's ``act_quant``
+# (``act_quant`` itself and wrappers of it): a quantizer injected into the KV
+# pack that carries it is computed by the fused pack kernel instead of called.
+FUSED_ACT_QUANT = "_sglang_lite_amd_act_quant"
+
 
 def act_quant_formula() -> str:
     raw = os.environ.get("SGLANG_LITE_AMD_ACT_QUANT", "torch").strip().lower()
@@ -81,6 +86,9 @@ def act_quant(
         x.copy_(y)
         return x
     return y, s
+
+
+setattr(act_quant, FUSED_ACT_QUANT, True)
 
 
 def per_token_cast_to_fp8(x: torch.Tensor, use_ue8m0: bool, gran_k: int = 128):

@@ -249,6 +249,11 @@ def _act_quant_dropin(x: torch.Tensor, block_size: int = 128, scale_fmt: Optiona
     return HK.act_quant(x, block_size, scale_fmt, scale_dtype, inplace)
 
 
+# the KV pack (dsv4_kv_pack.py:58-61 injects kernel.act_quant, which after the
+# attach is this function) computes this function's formula in its fused kernel
+setattr(_act_quant_dropin, HK.FUSED_ACT_QUANT, True)
+
+
 def prewarm_model_scales(model: Any) -> int:
     """Materialize the scale cache of every FP8 (fp32 scales) and FP4 (uint8
     view + e8m0 scales) weight (v4_deep_gemm.py:267-281)."""

@@ -84,3 +84,23 @@ def test_scale_formula_switch(monkeypatch):
     monkeypatch.setenv("SGLANG_LITE_AMD_ACT_QUANT", "bogus")
     with pytest.raises(ValueError):
         K.scale_mode_for(None)
+
+
+def test_kv_pack_fuses_the_attached_act_quant():
+    """After attach_v4_deep_gemm, kernel.act_quant is the package's drop-in
+    wrapper; the live KV pack injects that name (engine/v4_sparse_mla.py:85,91),
+    so the pack must compute its formula in the fused kernel (not call it
+    through the unfused path), like the package's own act_quant."""
+    from sglang_lite_amd import dsv4_kv_pack as KVP
+    from sglang_lite_amd import kernel as HK
+    from sglang_lite_amd import v4_deep_gemm as D
+
+    want = HK.scale_mode_for("ue8m0")
+    assert KVP._fused_quant_mode(HK.act_quant) == want
+    assert KVP._fused_quant_mode(D._act_quant_dropin) == want
+    assert KVP._fused_quant_mode(None) == KVP._lib.SCALE_KV_UE8M0
+
+    def other(*a, **k):
+        raise AssertionError
+
+    assert KVP._fused_quant_mode(other) is None

@@ -331,3 +331,34 @@ def test_moe_forward_with_frag_layout_switch(official, gpu, monkeypatch):
     assert OM.topk_margin(logits, k) > 1e-6
     y_ref = OM.moe_forward(x, ids_ref, w_ref, experts, sh)
     assert_gemm_close(f32(ys[True][0]), y_ref, "MoE.forward with fragment-layout weights")
+
+
+def test_kv_pack_with_the_attached_act_quant_takes_the_fused_kernel(official, gpu, monkeypatch):
+    """attach_v4_deep_gemm replaces kernel.act_quant by the package's wrapper;
+    pack_dsv4_kv_bf16 / pack_dsv4_kv_paged / write_packed_kv_bf16 given that
+    function (as engine/v4_sparse_mla.py:85,91 passes it) run the fused kernel
+    and produce the bytes of the package's own act_quant."""
+    from sglang_lite_amd import dsv4_kv_pack as KVP
+    from sglang_lite_amd import kernel as HK
+    from sglang_lite_amd import v4_deep_gemm as D
+
+    M, K = official
+    assert D.attach_v4_deep_gemm(None)["enabled"]
+    assert K.act_quant is not HK.act_quant
+    rng = np.random.default_rng(42)
+    kv = to_dev_bf16(bf16_values(rng, (130, 512)), gpu)
+    want = KVP.pack_dsv4_kv_bf16(kv, act_quant_fn=HK.act_quant)
+
+    def unfused(*a, **k):
+        raise AssertionError("the attached act_quant took the unfused path")
+
+    monkeypatch.setattr(KVP, "_pack_rows_with", unfused)
+    got = KVP.pack_dsv4_kv_bf16(kv, act_quant_fn=K.act_quant)
+    assert torch.equal(got, want)
+    pages = KVP.pack_dsv4_kv_paged(kv, 64, act_quant_fn=K.act_quant)
+    assert torch.equal(pages, KVP.to_paged_hnd(want, 64))
+    pool = torch.zeros(1, 4, 1, 64, 584, dtype=torch.uint8, device=gpu)
+    KVP.write_packed_kv_bf16(pool, [2, 0, 3], 0, kv, act_quant_fn=K.act_quant)
+    torch.cuda.synchronize()
+    assert torch.equal(pool[0, 2, 0], want[:64]) and torch.equal(pool[0, 0, 0], want[64:128])
+    assert torch.equal(pool[0, 3, 0, :2], want[128:130])

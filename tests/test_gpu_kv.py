@@ -31,12 +31,22 @@ def _kv(rng, T, dim, dtype):
     return t.float().numpy(), t
 
 
+def _quantizer(mode):
+    """The act_quant_fn whose formula is scale mode ``mode``: None (the torch
+    fallback), the official TileLang act_quant, or this package's act_quant
+    with its default torch formula."""
+    from sglang_lite_amd import kernel as HK
+
+    return {4: None, 3: _official_act_quant(), 1: HK.act_quant}[mode]
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("mode", [4, 3])
+@pytest.mark.parametrize("mode", [4, 3, 1])
 @pytest.mark.parametrize("T", [1, 70, 4096])
-def test_pack_layout_a_bit_exact(gpu, dtype, mode, T):
+def test_pack_layout_a_bit_exact(gpu, dtype, mode, T, monkeypatch):
     from sglang_lite_amd import dsv4_kv_pack as KVP
 
+    monkeypatch.delenv("SGLANG_LITE_AMD_ACT_QUANT", raising=False)
     rng = np.random.default_rng(T + mode)
     xv, xt = _kv(rng, T, 512, dtype)
     if T > 2:
@@ -45,9 +55,9 @@ def test_pack_layout_a_bit_exact(gpu, dtype, mode, T):
     rope = xt[:, 448:].contiguous().view(torch.uint8).numpy()
     ref = OK.pack_layout_a(xv, rope, mode)
     d = xt.to(gpu)
-    out = KVP.pack_dsv4_kv_bf16(d, act_quant_fn=None if mode == 4 else _official_act_quant())
+    out = KVP.pack_dsv4_kv_bf16(d, act_quant_fn=_quantizer(mode))
     np.testing.assert_array_equal(out.cpu().numpy(), ref)
-    pages = KVP.pack_dsv4_kv_paged(d, 64, act_quant_fn=None if mode == 4 else _official_act_quant())
+    pages = KVP.pack_dsv4_kv_paged(d, 64, act_quant_fn=_quantizer(mode))
     np.testing.assert_array_equal(pages.cpu().numpy(), OK.to_paged_hnd(ref, 64))
     pages2 = KVP.to_paged_hnd(out, 64)
     np.testing.assert_array_equal(pages2.cpu().numpy(), OK.to_paged_hnd(ref, 64))
