@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 2
+#define SGL_ABI_VERSION 3
 
 typedef void* sgl_stream_t; /* hipStream_t */
 
@@ -194,15 +194,22 @@ int sgl_mfma_mix_threads(void);
  * (e8m0 activation scales: convert with sgl_e8m0_to_f32 first), B e4m3 [N, K]
  * contiguous, sb [ceil(N/128), K/128] fp32, or one e8m0 byte per scale when
  * b_scale_e8m0 is set.  K % 128 == 0, N % 16 == 0, M*K and N*K < 2^31.
- * For 16 < M <= 64 with N % 128 == 0 the K range is split over workgroups:
- * the fp32 partials go to a buffer the library allocates once per (device,
- * stream) outside stream capture and keeps until the process ends (the only
- * allocation in this library); a capturing stream without one takes the
- * unsplit kernel.
+ * Shapes for which sgl_fp8_gemm_workspace_size is non-zero (16 < M <= 64
+ * with N % 128 == 0) split the K range over workgroups and keep the fp32
+ * partials in the caller's workspace (16-byte aligned, at least that many
+ * bytes; a smaller one is SGL_ERR_WORKSPACE).  Whether a shape splits
+ * depends on the shape alone, so eager and graph-captured calls sum in the
+ * same order.  Calls that overlap in time need workspaces of their own.
  * Replaces deepseek_infer/kernel.py:257-273 fp8_gemm (kernel :203-254) and the
- * call-site adapter engine/v4_deep_gemm.py:169-218 fp4_gemm_nt. */
+ * call-site adapter engine/v4_deep_gemm.py:169-218 fp4_gemm_nt (whose
+ * workspace-free call the reference's adapter allocates with torch at
+ * :186-188, as the caller does here). */
 int sgl_fp8_gemm(const void* a, const void* sa, const void* b, const void* sb, int b_scale_e8m0,
-                 void* c, int out_dtype, int64_t M, int64_t N, int64_t K, sgl_stream_t stream);
+                 void* c, int out_dtype, int64_t M, int64_t N, int64_t K, void* workspace,
+                 size_t workspace_bytes, sgl_stream_t stream);
+
+/* Workspace bytes sgl_fp8_gemm needs for an M x N x K product (0: none). */
+size_t sgl_fp8_gemm_workspace_size(int64_t M, int64_t N, int64_t K);
 
 /* C[M, N] = A_e4m3[M, K] . B_e2m1[N, K]^T with A scaled per (row, 128-deep K
  * block) by sa and B per (row, 32-deep K block) by sb; fp32 accumulation,
@@ -335,16 +342,40 @@ size_t sgl_moe_workspace_size(int64_t T, int64_t H, int64_t I, int E, int k, int
  * (ids int32 [T, k], weights fp32 [T, k]): act quant -> permute -> gate/up
  * -> down -> combine, y bf16 [T, H]; routed experts in expert_format.
  * Replaces engine/v4_moe_fast.py:79-106 _moe_forward_activated_only after
- * the gate.  With FP4 routed experts and T <= 512, when `stream` is being
- * captured into a graph, sgl_moe_gate_up / sgl_moe_down / sgl_moe_forward
- * run the FP8 shared expert's GEMMs on a second stream of the device
- * (created by the first such call made outside capture), forked from and
- * joined back into `stream` by events, so the graph orders the results as if
- * `stream` ran them all; eager calls run everything on `stream`. */
+ * the gate.  Every launch goes to `stream`. */
 int sgl_moe_forward(const void* x, int64_t T, int64_t H, int64_t I, int E, int k,
                     const int32_t* ids, const float* weights, const sgl_expert_ptrs* experts,
                     int has_shared, int expert_format, float swiglu_limit, int scale_mode,
                     void* workspace, size_t workspace_bytes, void* y, sgl_stream_t stream);
+
+/* One rank's share of an expert-sharded MoE layer (the expert split of
+ * deepseek_infer/model.py:616-625: the rank holds the routed experts
+ * [expert_begin, expert_end) and sees every token).  act quant -> permute of
+ * the slots routed to a local expert -> gate/up -> down, then
+ *   y_local fp32 [T, H] = sum over the token's routed experts inside the
+ *   range, in ascending expert id and fp32, of their bf16 outputs (0 for a
+ *   token with none), the shared expert left out.
+ * Records of experts outside the range are never read (they may hold null
+ * pointers).  With has_shared the shared expert's rows run in the same
+ * launches and stay in the workspace for sgl_moe_add_shared.  Workspace as
+ * for sgl_moe_forward.  Replaces engine/v4_moe_fast.py:79-102
+ * _moe_forward_activated_only up to its all_reduce (the range test :93-97)
+ * and deepseek_infer/model.py:629-640. */
+int sgl_moe_forward_local(const void* x, int64_t T, int64_t H, int64_t I, int E, int k,
+                          const int32_t* ids, const float* weights, const sgl_expert_ptrs* experts,
+                          int expert_begin, int expert_end, int has_shared, int expert_format,
+                          float swiglu_limit, int scale_mode, void* workspace,
+                          size_t workspace_bytes, float* y_local, sgl_stream_t stream);
+
+/* y bf16 [T, H] = bf16(y_local + the shared expert's row), an fp32 addition,
+ * where y_local is the caller's all-reduced sum of the ranks'
+ * sgl_moe_forward_local outputs and workspace the one this rank's
+ * sgl_moe_forward_local call (same T, H, I, E, k, has_shared set) filled.
+ * y may alias nothing the call reads.  Replaces engine/v4_moe_fast.py:103-106
+ * and deepseek_infer/model.py:641-644 (y += shared_experts(x); y.type_as(x)). */
+int sgl_moe_add_shared(const float* y_local, const void* workspace, size_t workspace_bytes,
+                       int64_t T, int64_t H, int64_t I, int E, int k, void* y,
+                       sgl_stream_t stream);
 
 /* Size of the static device workspace of sgl_moe_forward_noalloc: 64 MiB
  * per GPU, held from library load to process end (T <= 690 tokens at hidden

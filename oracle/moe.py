@@ -233,6 +233,25 @@ def moe_forward(x_bf16: np.ndarray, ids: np.ndarray, weights: np.ndarray,
     return Q.bf16_round(y)
 
 
+def moe_local_partial(x_bf16: np.ndarray, ids: np.ndarray, weights: np.ndarray,
+                      experts: Sequence[Optional[Dict[str, np.ndarray]]], expert_begin: int,
+                      expert_end: int, swiglu_limit: float = 0.0, mode: int = 0) -> np.ndarray:
+    """engine/v4_moe_fast.py:79-102 on one rank of an expert-sharded layer, up
+    to its all_reduce: y = 0 (fp32); for each activated expert ascending, skip
+    it unless expert_begin <= e < expert_end (:93-97), y[tok] += expert(x[tok],
+    w).  Returns the fp32 y (the value the rank hands to all_reduce)."""
+    x = np.asarray(x_bf16, dtype=np.float32)
+    ids = np.asarray(ids)
+    y = np.zeros_like(x, dtype=np.float32)
+    for e in np.unique(ids).tolist():
+        if e < expert_begin or e >= expert_end or experts[e] is None:
+            continue
+        tok, top = np.nonzero(ids == e)
+        out = expert_forward(x[tok], experts[e], weights[tok, top][:, None], swiglu_limit, mode)
+        y[tok] = (y[tok] + out).astype(np.float32)
+    return y
+
+
 def moe_forward_full_loop(x_bf16, ids, weights, experts, shared, swiglu_limit=0.0, mode=0):
     """The official MoE.forward loop (model.py:629-644): all experts, bincount skip."""
     x = np.asarray(x_bf16, dtype=np.float32)

@@ -36,11 +36,7 @@
 // prefix-sums ceil(count_e / BM) over the expert offsets into LDS, so the
 // grid is sized without reading routing data on the host.
 #include <algorithm>
-#include <map>
-#include <mutex>
 #include <type_traits>
-#include <utility>
-#include <vector>
 
 #include "sgl_gemm.h"
 #include "sgl_numeric.h"
@@ -2261,13 +2257,11 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
 #ifndef SGL_RB_NJ
 #define SGL_RB_NJ 1
 #endif
-// CUs a grouped launch may fill: all, or what spare_cus / max_cus leave it
-// (a multiple of 8, so every XCD gets the same number)
-int64_t cu_budget(const GemmArgs& a) {
-  int64_t n = device_cu_count();
-  if (a.max_cus > 0 && n > a.max_cus) n = a.max_cus;
-  n -= a.spare_cus;
-  return std::max<int64_t>(8, (n + (a.spare_cus || a.max_cus ? 0 : 7)) / 8 * 8);
+// CUs a grouped launch fills, rounded up to a multiple of 8 so every XCD
+// gets the same number
+int64_t cu_budget(const GemmArgs&) {
+  const int64_t n = device_cu_count();
+  return std::max<int64_t>(8, (n + 7) / 8 * 8);
 }
 
 template <int KIND, bool W4 = false>
@@ -2983,45 +2977,6 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
-// Workspace of the split-K kernel (the partials) per (device, stream),
-// allocated outside stream capture: a call on a capturing stream that has
-// none yet, or too little, takes the unsplit kernels.  Calls on one stream
-// are ordered, so they share it.  A block is never freed while the library
-// is loaded: a HIP graph that captured a call keeps the block's address and
-// writes there on every replay, so a larger call retires the old block
-// instead of freeing it; growth is at least 1.5x, which bounds the retired
-// bytes by twice the live block.
-struct SplitKWs {
-  uint8_t* base = nullptr;
-  size_t bytes = 0;
-  std::vector<uint8_t*> retired;
-};
-std::mutex g_splitk_mu;
-std::map<std::pair<int, hipStream_t>, SplitKWs> g_splitk_ws;
-
-uint8_t* splitk_workspace(hipStream_t stream, size_t need) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-  std::lock_guard<std::mutex> lock(g_splitk_mu);
-  SplitKWs& w = g_splitk_ws[{dev, stream}];
-  if (w.bytes >= need) return w.base;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  const size_t bytes = std::max(need, w.bytes + w.bytes / 2);
-  void* p = nullptr;
-  if (hipMalloc(&p, bytes) != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  if (w.base) w.retired.push_back(w.base);
-  w.base = static_cast<uint8_t*>(p);
-  w.bytes = bytes;
-  return w.base;
-}
-
 template <int KS, int TM>
 int launch_splitk_ks(GemmArgs& a, int S, float* part, hipStream_t stream) {
   const SplitKArgs sk{part, S};
@@ -3052,29 +3007,57 @@ int launch_splitk_tm(GemmArgs& a, int KS, int S, float* part, hipStream_t stream
   }
 }
 
-int try_splitk(GemmArgs& a, hipStream_t stream) {
+// The split of a dense FP8 GEMM over K, a function of the shape alone (so an
+// eager call and a captured one sum in the same order): 16 < M <= 64
+// (N = 4096, K = 7168, graph-replayed over cold weights: M = 32 12.1 us where
+// the skinny kernel takes 14.3; M = 16 10.9 vs 10.5, M = 128 with 128-row
+// tiles 23.0 vs 22.0 with 32 x 64 tiles), N % 128 == 0, about one workgroup
+// per CU: S <= 16 splits of KS <= 8 K blocks.  Returns false when the shape
+// does not split.
+bool splitk_plan(int64_t M, int64_t N, int64_t K, int* ks_out, int* s_out) {
   using namespace splitk;
-  // 16 < M <= 64 (N = 4096, K = 7168, graph-replayed over cold weights:
-  // M = 32 12.1 us where the skinny kernel takes 14.3; M = 16 10.9 vs 10.5,
-  // M = 128 with 128-row tiles 23.0 vs 22.0 with 32 x 64 tiles)
-  if (a.M <= 16 || a.M > 16 * TMMAX || a.N % BN != 0 || a.wfmt != WF_FP8) return -1;
-  if (a.sb_e8m0 && !aligned(a.sb, 4)) return -1;  // e8m0 scales are read as whole dwords
-  const int KB = (int)(a.K / 128);
-  const int n_tiles = (int)(a.N / BN);
-  // about one workgroup per CU: S <= 16 splits of KS <= 8 blocks
+  if (M <= 16 || M > 16 * TMMAX || N % BN != 0 || K % 128 != 0) return false;
+  const int KB = (int)(K / 128);
+  const int n_tiles = (int)(N / BN);
   const int s_target = n_tiles >= 256 ? 1 : 256 / n_tiles;
   int KS = (int)ceil_div((int64_t)KB, (int64_t)s_target);
   KS = (int)std::max<int64_t>(KS, ceil_div((int64_t)KB, (int64_t)SMAX));
-  if (KS > KSMAX) return -1;
+  if (KS > KSMAX) return false;
   const int S = (int)ceil_div((int64_t)KB, (int64_t)KS);
-  if (S < 2) return -1;
-  float* part = reinterpret_cast<float*>(splitk_workspace(stream, (size_t)S * (size_t)a.M * (size_t)a.N * 4));
-  if (!part) return -1;
+  if (S < 2) return false;
+  *ks_out = KS;
+  *s_out = S;
+  return true;
+}
+
+// The split-K path when the shape splits: the fp32 partials go to the
+// caller's workspace (too small: an error, never a different summation
+// order); returns kNoSplit when the caller should take the unsplit kernels,
+// else the launch status.
+constexpr int kNoSplit = 1;
+int try_splitk(GemmArgs& a, hipStream_t stream) {
+  int KS = 0, S = 0;
+  if (a.wfmt != WF_FP8 || !splitk_plan(a.M, a.N, a.K, &KS, &S)) return kNoSplit;
+  if (a.sb_e8m0 && !aligned(a.sb, 4)) return kNoSplit;  // e8m0 scales are read as whole dwords
+  const size_t need = (size_t)S * (size_t)a.M * (size_t)a.N * 4;
+  if (!a.ws || a.ws_bytes < need || !aligned(a.ws, 16)) {
+    set_error("fp8_gemm: M=%lld N=%lld K=%lld splits K %d ways and needs a 16-byte aligned "
+              "workspace of %zu bytes (sgl_fp8_gemm_workspace_size), got %zu",
+              (long long)a.M, (long long)a.N, (long long)a.K, S, need, a.ws ? a.ws_bytes : (size_t)0);
+    return SGL_ERR_WORKSPACE;
+  }
+  float* part = reinterpret_cast<float*>(a.ws);
   if (a.M <= 32) return launch_splitk_tm<2>(a, KS, S, part, stream);
   return launch_splitk_tm<4>(a, KS, S, part, stream);
 }
 
 }  // namespace
+
+size_t dense_fp8_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  int KS = 0, S = 0;
+  if (!SGL_SPLITK || !splitk_plan(M, N, K, &KS, &S)) return 0;
+  return (size_t)S * (size_t)M * (size_t)N * 4;
+}
 
 // FP4 weights: a stage is 256 deep, so two stages fill what three fp8
 // stages of the same tile would (the 128 x 256 tiles run one workgroup per
@@ -3143,8 +3126,8 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
                      kb <= rb::kMaxKBr && kb % 4 == 0 && aligned(a.sa, 16);
   switch (kind) {
     case KIND_DENSE: {
-      const int rc = SGL_SPLITK ? try_splitk(a, stream) : -1;
-      if (rc >= 0) return rc;
+      const int rc = SGL_SPLITK ? try_splitk(a, stream) : kNoSplit;
+      if (rc != kNoSplit) return rc;
       if (a.M <= kSkinnyMaxM) {
         if (a.M <= 16) return launch_skinny<1>(a, stream);
         if (a.M <= 32) return launch_skinny<2>(a, stream);
@@ -3183,9 +3166,15 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
 
 }  // namespace sgl
 
+extern "C" size_t sgl_fp8_gemm_workspace_size(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return sgl::dense_fp8_workspace_bytes(M, N, K);
+}
+
 extern "C" int sgl_fp8_gemm(const void* a, const void* sa, const void* b, const void* sb,
                             int b_scale_e8m0, void* c, int out_dtype, int64_t M, int64_t N,
-                            int64_t K, sgl_stream_t stream) {
+                            int64_t K, void* workspace, size_t workspace_bytes,
+                            sgl_stream_t stream) {
   SGL_REQUIRE(M >= 0 && N >= 0 && K >= 0, "fp8_gemm: negative shape");
   SGL_REQUIRE(out_dtype == SGL_BF16 || out_dtype == SGL_F32, "fp8_gemm: out_dtype must be bf16/f32");
   SGL_REQUIRE(K % 128 == 0, "fp8_gemm: K=%lld must be a multiple of 128", (long long)K);
@@ -3209,6 +3198,8 @@ extern "C" int sgl_fp8_gemm(const void* a, const void* sa, const void* b, const 
   g.K = K;
   g.c = c;
   g.out_f32 = out_dtype == SGL_F32;
+  g.ws = workspace;
+  g.ws_bytes = workspace ? workspace_bytes : 0;
   return sgl::launch_gemm(sgl::KIND_DENSE, g, M, (hipStream_t)stream);
 }
 

@@ -252,17 +252,18 @@ __global__ __launch_bounds__(64 * NWV) void router_logits_kernel(const uint16_t*
 // lower peers), per-wavefront counts in LDS give the offset of each wavefront
 // inside the round, and run[e] (the next free position of expert e) carries
 // rounds forward, so equal ids keep slot order.  Writes slot_pos, and
-// sorted_slot when it is non-null.
+// sorted_slot when it is non-null.  Only ids in [elo, ehi) are placed (a rank's
+// local experts of an expert-sharded layer); the other slots get slot_pos -1.
 __device__ void rank_slots(const int32_t* __restrict__ ids, int64_t lo, int64_t hi, int E,
-                           int* run, int (*wcnt)[kMaxPermE], int32_t* __restrict__ sorted_slot,
-                           int32_t* __restrict__ slot_pos) {
+                           int elo, int ehi, int* run, int (*wcnt)[kMaxPermE],
+                           int32_t* __restrict__ sorted_slot, int32_t* __restrict__ slot_pos) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nbits = E > 1 ? 32 - __clz(E - 1) : 0;
   const unsigned long long lt_mask = (1ull << lane) - 1ull;
   for (int64_t base = lo; base < hi; base += kPermThreads) {
     const int64_t i = base + tid;
     const int e = i < hi ? ids[i] : -1;
-    const bool valid = e >= 0 && e < E;
+    const bool valid = e >= elo && e < ehi;
     unsigned long long peers = __ballot(valid);
     for (int b = 0; b < nbits; ++b) {
       const bool bit = valid && ((e >> b) & 1);
@@ -319,7 +320,8 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* __
                                                                int32_t* __restrict__ offsets,
                                                                int32_t* __restrict__ sorted_slot,
                                                                int32_t* __restrict__ slot_pos,
-                                                               int32_t* __restrict__ zero, int nzero) {
+                                                               int32_t* __restrict__ zero, int nzero,
+                                                               int elo, int ehi) {
   __shared__ int cnt[kMaxPermE];
   __shared__ int run[kMaxPermE];
   __shared__ int wcnt[kPermWaves][kMaxPermE];
@@ -333,7 +335,7 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* __
   __syncthreads();
   for (int64_t i = tid; i < P; i += kPermThreads) {
     const int e = ids[i];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    if (e >= elo && e < ehi) atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
   {
@@ -347,7 +349,7 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* __
     if (tid == E - 1) offsets[E] = excl + v;
   }
   __syncthreads();
-  rank_slots(ids, 0, P, E, run, wcnt, sorted_slot, slot_pos);
+  rank_slots(ids, 0, P, E, elo, ehi, run, wcnt, sorted_slot, slot_pos);
 }
 
 // Large inputs: chunks of kPermChunk slots, one workgroup each, in four
@@ -360,7 +362,8 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* __
 constexpr int kPermChunk = 4096;
 
 __global__ __launch_bounds__(kPermThreads) void permute_hist_kernel(const int32_t* __restrict__ ids,
-                                                                    int64_t P, int E,
+                                                                    int64_t P, int E, int elo,
+                                                                    int ehi,
                                                                     int32_t* __restrict__ hist) {
   __shared__ int cnt[kMaxPermE];
   const int tid = threadIdx.x;
@@ -370,7 +373,7 @@ __global__ __launch_bounds__(kPermThreads) void permute_hist_kernel(const int32_
   __syncthreads();
   for (int64_t i = lo + tid; i < hi; i += kPermThreads) {
     const int e = ids[i];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    if (e >= elo && e < ehi) atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
   for (int e = tid; e < E; e += kPermThreads) hist[(int64_t)blockIdx.x * E + e] = cnt[e];
@@ -404,7 +407,8 @@ __global__ __launch_bounds__(kPermThreads) void permute_scan_kernel(const int32_
 }
 
 __global__ __launch_bounds__(kPermThreads) void permute_rank_kernel(const int32_t* __restrict__ ids,
-                                                                    int64_t P, int E,
+                                                                    int64_t P, int E, int elo,
+                                                                    int ehi,
                                                                     const int32_t* __restrict__ starts,
                                                                     int32_t* __restrict__ slot_pos) {
   __shared__ int run[kMaxPermE];
@@ -417,7 +421,7 @@ __global__ __launch_bounds__(kPermThreads) void permute_rank_kernel(const int32_
     for (int w = 0; w < kPermWaves; ++w) wcnt[w][e] = 0;
   }
   __syncthreads();
-  rank_slots(ids, lo, hi, E, run, wcnt, nullptr, slot_pos);
+  rank_slots(ids, lo, hi, E, elo, ehi, run, wcnt, nullptr, slot_pos);
 }
 
 __global__ __launch_bounds__(256) void permute_scatter_kernel(const int32_t* __restrict__ slot_pos,
@@ -432,16 +436,19 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(const int32_t* __r
 
 // -------------------------------------------------------------- combine
 
-// One workgroup per (token, column slice): sum the token's k expert rows
-// (bf16) into fp32 in ascending expert id, add the shared row, round to
-// bf16.  8 columns / thread; workgroup y of gridDim.y takes the column
-// slices y, y + gridDim.y, ... of NT * 8 columns (small batches split the
-// row over several workgroups so the launch still covers the CUs).
-template <int NT>
+// One workgroup per (token, column slice): sum the token's expert rows (bf16)
+// whose expert id lies in [elo, ehi) into fp32 in ascending expert id, then
+// either add the shared row and round to bf16 (PARTIAL false: the whole
+// layer) or store the fp32 sum (PARTIAL true: one rank's share of an
+// expert-sharded layer, before the caller's all-reduce; the shared row is
+// not added).  8 columns / thread; workgroup y of gridDim.y takes the column
+// slices y, y + gridDim.y, ... of NT * 8 columns (small batches split the row
+// over several workgroups so the launch still covers the CUs).
+template <int NT, bool PARTIAL>
 __global__ __launch_bounds__(NT) void combine_kernel(const uint16_t* __restrict__ out,
                                                      const int32_t* __restrict__ ids, int64_t T,
-                                                     int k, int64_t H, int has_shared, int E,
-                                                     uint16_t* __restrict__ y) {
+                                                     int k, int64_t H, int has_shared, int elo,
+                                                     int ehi, void* __restrict__ y) {
   __shared__ int ord[16];
   __shared__ int nvalid;
   const int64_t t = blockIdx.x;
@@ -450,11 +457,11 @@ __global__ __launch_bounds__(NT) void combine_kernel(const uint16_t* __restrict_
   __syncthreads();
   if (tid < k) {
     const int my = ids[t * k + tid];
-    if (my >= 0 && my < E) {
+    if (my >= elo && my < ehi) {
       int rank = 0;
       for (int j = 0; j < k; ++j) {
         const int o = ids[t * k + j];
-        if (o < 0 || o >= E) continue;
+        if (o < elo || o >= ehi) continue;
         if (o < my || (o == my && j < tid)) ++rank;
       }
       ord[rank] = tid;
@@ -478,32 +485,65 @@ __global__ __launch_bounds__(NT) void combine_kernel(const uint16_t* __restrict_
         acc[2 * i + 1] += bits_f32(w[i] & 0xFFFF0000u);
       }
     }
-    if (has_shared) {
-      const uint4 v = *reinterpret_cast<const uint4*>(base + (int64_t)k * H + col);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    if constexpr (PARTIAL) {
+      float4* yo = reinterpret_cast<float4*>(reinterpret_cast<float*>(y) + t * H + col);
+      yo[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      yo[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    } else {
+      if (has_shared) {
+        const uint4 v = *reinterpret_cast<const uint4*>(base + (int64_t)k * H + col);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[2 * i] += bits_f32(w[i] << 16);
-        acc[2 * i + 1] += bits_f32(w[i] & 0xFFFF0000u);
+        for (int i = 0; i < 4; ++i) {
+          acc[2 * i] += bits_f32(w[i] << 16);
+          acc[2 * i + 1] += bits_f32(w[i] & 0xFFFF0000u);
+        }
       }
-    }
-    uint32_t o[4];
+      uint32_t o[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = pk2_bf16_exact(acc[2 * i], acc[2 * i + 1]);
-    *reinterpret_cast<uint4*>(y + t * H + col) = make_uint4(o[0], o[1], o[2], o[3]);
+      for (int i = 0; i < 4; ++i) o[i] = pk2_bf16_exact(acc[2 * i], acc[2 * i + 1]);
+      *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(y) + t * H + col) =
+          make_uint4(o[0], o[1], o[2], o[3]);
+    }
   }
 }
 
 // T tokens of H columns: 256-thread workgroups, one per token, from about
 // two per CU; below, 64-thread workgroups over 512-column slices (T = 64,
 // H = 4096: 512 workgroups where one per token gives 64)
+template <bool PARTIAL>
 void launch_combine(const uint16_t* out, const int32_t* ids, int64_t T, int k, int64_t H,
-                    int has_shared, int E, uint16_t* y, hipStream_t st) {
+                    int has_shared, int elo, int ehi, void* y, hipStream_t st) {
   if (T >= 2 * (int64_t)device_cu_count()) {
-    combine_kernel<256><<<dim3((unsigned)T, 1), 256, 0, st>>>(out, ids, T, k, H, has_shared, E, y);
+    combine_kernel<256, PARTIAL><<<dim3((unsigned)T, 1), 256, 0, st>>>(out, ids, T, k, H, has_shared,
+                                                                       elo, ehi, y);
   } else {
     const unsigned slices = (unsigned)ceil_div(H, 64 * 8);
-    combine_kernel<64><<<dim3((unsigned)T, slices), 64, 0, st>>>(out, ids, T, k, H, has_shared, E, y);
+    combine_kernel<64, PARTIAL><<<dim3((unsigned)T, slices), 64, 0, st>>>(out, ids, T, k, H,
+                                                                          has_shared, elo, ehi, y);
+  }
+}
+
+// y[t] = bf16(y_local[t] + shared row t), the shared expert's output added
+// after the caller's all-reduce of the ranks' fp32 partial sums
+// (engine/v4_moe_fast.py:103-106).  One thread per 8 columns.
+__global__ __launch_bounds__(256) void add_shared_kernel(const float* __restrict__ y_local,
+                                                         const uint16_t* __restrict__ out, int64_t T,
+                                                         int k, int64_t H,
+                                                         uint16_t* __restrict__ y) {
+  const int64_t n8 = T * H / 8;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (int64_t)gridDim.x * 256) {
+    const int64_t t = i * 8 / H, col = i * 8 - t * H;
+    const float4 a = reinterpret_cast<const float4*>(y_local + t * H + col)[0];
+    const float4 b = reinterpret_cast<const float4*>(y_local + t * H + col)[1];
+    const uint4 v = *reinterpret_cast<const uint4*>(out + (t * (k + 1) + k) * H + col);
+    const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      o[q] = pk2_bf16_exact(f[2 * q] + bits_f32(w[q] << 16), f[2 * q + 1] + bits_f32(w[q] & 0xFFFF0000u));
+    *reinterpret_cast<uint4*>(y + t * H + col) = make_uint4(o[0], o[1], o[2], o[3]);
   }
 }
 
@@ -618,13 +658,17 @@ int check_moe_shapes(const char* what, int64_t T, int64_t H, int64_t I, int E, i
 }
 
 // Also zeroes zero[0, nzero) (nzero <= 1024) on the way, for the caller's
-// tile counters.
+// tile counters.  Only the slots whose expert lies in [elo, ehi) are placed
+// (0 <= elo <= ehi <= E; the whole range for a layer on one rank).
 int launch_permute(const int32_t* ids, int64_t T, int k, int E, int32_t* counts, int32_t* offsets,
                    int32_t* sorted_slot, int32_t* slot_pos, int32_t* zero, int nzero,
-                   hipStream_t st) {
+                   hipStream_t st, int elo = 0, int ehi = -1) {
+  if (ehi < 0) ehi = E;
   SGL_REQUIRE(T >= 0 && k >= 1, "moe_permute: bad T=%lld k=%d", (long long)T, k);
   SGL_REQUIRE(E >= 1 && E <= kMaxPermE, "moe_permute: E=%d not in [1, %d]", E,
               kMaxPermE);
+  SGL_REQUIRE(0 <= elo && elo <= ehi && ehi <= E, "moe_permute: expert range [%d, %d) not in [0, %d]",
+              elo, ehi, E);
   SGL_REQUIRE(T * k < 0x7FFFFFFF, "moe_permute: T*k too large");
   SGL_REQUIRE(counts && offsets && (T == 0 || (ids && sorted_slot && slot_pos)),
               "moe_permute: null pointer");
@@ -632,14 +676,14 @@ int launch_permute(const int32_t* ids, int64_t T, int k, int E, int32_t* counts,
   const int64_t chunks = ceil_div(P, (int64_t)kPermChunk);
   if (P < 4 * kPermChunk || chunks * E > P) {
     permute_kernel<<<1, kPermThreads, 0, st>>>(ids, P, E, counts, offsets, sorted_slot, slot_pos,
-                                               zero, nzero);
+                                               zero, nzero, elo, ehi);
     return check_launch("moe_permute");
   }
-  permute_hist_kernel<<<(unsigned)chunks, kPermThreads, 0, st>>>(ids, P, E, slot_pos);
+  permute_hist_kernel<<<(unsigned)chunks, kPermThreads, 0, st>>>(ids, P, E, elo, ehi, slot_pos);
   permute_scan_kernel<<<1, kPermThreads, 0, st>>>(slot_pos, (int)chunks, E, counts, offsets,
                                                        sorted_slot, zero, nzero);
-  permute_rank_kernel<<<(unsigned)chunks, kPermThreads, 0, st>>>(ids, P, E, sorted_slot,
-                                                                           slot_pos);
+  permute_rank_kernel<<<(unsigned)chunks, kPermThreads, 0, st>>>(ids, P, E, elo, ehi, sorted_slot,
+                                                                  slot_pos);
   int64_t sblocks = ceil_div(P, (int64_t)256);
   if (sblocks > 4096) sblocks = 4096;
   permute_scatter_kernel<<<(unsigned)sblocks, 256, 0, st>>>(slot_pos, P, sorted_slot);
@@ -650,82 +694,12 @@ bool pow2_scale_mode(int scale_mode) {
   return scale_mode == SGL_SCALE_TORCH_UE8M0 || scale_mode == SGL_SCALE_TILELANG_UE8M0;
 }
 
-// FP4 layers run the FP8 shared expert in launches of their own: at decode
-// sizes a few column tiles, i.e. a few workgroups each at one workgroup's
-// stream rate.  Up to kSideMaxT tokens, when the caller's stream is being
-// captured into a graph, they run on a second stream of the device beside the
-// routed launch, which leaves them kSharedCus CUs (fork and join by events:
-// the graph holds both branches).  Eager calls run them in order: there the
-// cross-stream event waits cost more than the overlap gains (measured: FP4
-// decode T = 64 / 256 / 512 0.415 / 0.667 / 0.777 -> 0.467 / 0.774 / 0.943
-// ms).  The side stream is created by the first such call made outside
-// capture.  The enqueue sequence holds a mutex: the events are shared.
-#ifndef SGL_SIDE_MAX_T
-#define SGL_SIDE_MAX_T 512
-#endif
-constexpr int64_t kSideMaxT = SGL_SIDE_MAX_T;
-constexpr int kSharedCus = 16;
-struct SideStream {
-  hipStream_t s;
-  hipEvent_t fork, join;
-};
-std::mutex g_side_mu;
-SideStream g_side[64];
-// set while sgl_moe_forward_noalloc runs: its calls create no stream (an
-// existing side stream is still used)
-thread_local bool t_no_new_side = false;
-
-// The device's side stream when `stream` is being captured (null
-// otherwise, or when none exists yet); created by calls outside capture.
-SideStream* side_stream(hipStream_t stream) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  SideStream& ss = g_side[dev];
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &cs) != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  if (cs != hipStreamCaptureStatusNone) return ss.s ? &ss : nullptr;
-  if (ss.s || t_no_new_side) return nullptr;
-  SideStream n = {};
-  if (hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking) != hipSuccess ||
-      hipEventCreateWithFlags(&n.fork, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&n.join, hipEventDisableTiming) != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  ss = n;
-  return nullptr;
-}
-
-// routed launch g on `stream` and the shared launch sh: side by side in a
-// graph being captured (T <= kSideMaxT, a side stream exists), else one after
-// the other
+// FP4 layers run the FP8 shared expert in a launch of its own after the
+// routed launch, on the same stream.
 int run_routed_and_shared(int kind, GemmArgs& g, GemmArgs& sh, int64_t T, hipStream_t stream) {
-  const int64_t hint = g.T * g.k / g.E;
-  if (T <= kSideMaxT) {
-    std::lock_guard<std::mutex> lock(g_side_mu);
-    SideStream* ss = side_stream(stream);
-    if (ss) {
-      sh.max_cus = kSharedCus;
-      g.spare_cus = kSharedCus;
-      int rc;
-      if (hipEventRecord(ss->fork, stream) != hipSuccess ||
-          hipStreamWaitEvent(ss->s, ss->fork, 0) != hipSuccess)
-        return check_launch("moe side stream fork");
-      if ((rc = launch_gemm(kind, sh, T, ss->s))) return rc;
-      if (hipEventRecord(ss->join, ss->s) != hipSuccess) return check_launch("moe side stream join");
-      rc = launch_gemm(kind, g, hint, stream);
-      if (hipStreamWaitEvent(stream, ss->join, 0) != hipSuccess && !rc)
-        return check_launch("moe side stream join");
-      return rc;
-    }
-  }
-  int rc = launch_gemm(kind, g, hint, stream);
+  const int rc = launch_gemm(kind, g, g.T * g.k / g.E, stream);
   return rc ? rc : launch_gemm(kind, sh, T, stream);
 }
-
 
 // The routed experts in `expert_format`; the shared expert (experts[E]) is
 // always FP8 128 x 128 (deepseek_infer/model.py:623-626 builds it without the
@@ -928,8 +902,8 @@ int sgl_moe_combine(const void* out, const int32_t* ids, int64_t T, int k, int64
   if (T == 0) return SGL_OK;
   SGL_REQUIRE(out && ids && y, "moe_combine: null pointer");
   SGL_REQUIRE(sgl::aligned(out, 16) && sgl::aligned(y, 16), "moe_combine: out/y misaligned");
-  sgl::launch_combine((const uint16_t*)out, ids, T, k, H, has_shared ? 1 : 0, 0x7FFFFFFF, (uint16_t*)y,
-                      (hipStream_t)stream);
+  sgl::launch_combine<false>((const uint16_t*)out, ids, T, k, H, has_shared ? 1 : 0, 0, 0x7FFFFFFF, y,
+                             (hipStream_t)stream);
   return sgl::check_launch("moe_combine");
 }
 
@@ -956,11 +930,8 @@ int sgl_moe_forward_noalloc(const void* x, int64_t T, int64_t H, int64_t I, int 
   if ((rc = sgl::moe_scratch_ptr(&ws))) return rc;
   // every buffer the layer reads is written first inside the call (the
   // permute kernel zeroes the GEMM tile counters), so the array needs no clear
-  sgl::t_no_new_side = true;
-  rc = sgl_moe_forward(x, T, H, I, E, k, ids, weights, experts, has_shared, expert_format,
-                       swiglu_limit, scale_mode, ws, sgl::kScratchBytes, y, stream);
-  sgl::t_no_new_side = false;
-  return rc;
+  return sgl_moe_forward(x, T, H, I, E, k, ids, weights, experts, has_shared, expert_format,
+                         swiglu_limit, scale_mode, ws, sgl::kScratchBytes, y, stream);
 }
 
 int sgl_moe_forward(const void* x, int64_t T, int64_t H, int64_t I, int E, int k,
@@ -993,8 +964,70 @@ int sgl_moe_forward(const void* x, int64_t T, int64_t H, int64_t I, int E, int k
   if ((rc = sgl::run_down(w.hq, w.hs, T, H, I, E, k, w.offsets, w.sorted_slot, experts, has_shared,
                           expert_format, scale_mode, w.out, w.tile_ctr + 16, st)))
     return rc;
-  sgl::launch_combine(w.out, ids, T, k, H, has_shared, E, (uint16_t*)y, st);
+  sgl::launch_combine<false>(w.out, ids, T, k, H, has_shared, 0, E, y, st);
   return sgl::check_launch("moe_combine");
+}
+
+int sgl_moe_forward_local(const void* x, int64_t T, int64_t H, int64_t I, int E, int k,
+                          const int32_t* ids, const float* weights, const sgl_expert_ptrs* experts,
+                          int expert_begin, int expert_end, int has_shared, int expert_format,
+                          float swiglu_limit, int scale_mode, void* workspace,
+                          size_t workspace_bytes, float* y_local, sgl_stream_t stream) {
+  int rc = sgl::check_moe_shapes("moe_forward_local", T, H, I, E, k, expert_format);
+  if (rc) return rc;
+  SGL_REQUIRE(scale_mode >= 0 && scale_mode <= 3, "moe_forward_local: bad scale_mode %d", scale_mode);
+  SGL_REQUIRE(0 <= expert_begin && expert_begin <= expert_end && expert_end <= E,
+              "moe_forward_local: expert range [%d, %d) not in [0, %d]", expert_begin, expert_end, E);
+  if (T == 0) return SGL_OK;
+  SGL_REQUIRE(x && ids && weights && experts && workspace && y_local,
+              "moe_forward_local: null pointer");
+  has_shared = has_shared ? 1 : 0;
+  const sgl::MoeWorkspace w = sgl::carve(workspace, T, H, I, E, k, has_shared);
+  if (workspace_bytes < w.bytes) {
+    sgl::set_error("moe_forward_local: workspace %zu bytes < %zu needed", workspace_bytes, w.bytes);
+    return SGL_ERR_WORKSPACE;
+  }
+  SGL_REQUIRE(sgl::aligned(workspace, 256) && sgl::aligned(y_local, 16),
+              "moe_forward_local: workspace must be 256-byte and y_local 16-byte aligned");
+  if ((rc = sgl_act_quant(x, T, H, H, w.xq, H, w.xs, H / 128, 128, scale_mode, 0, 0, stream)))
+    return rc;
+  hipStream_t st = (hipStream_t)stream;
+  // only the local experts' slots are placed; offsets[E] counts them, and the
+  // shared expert's rows follow them as in the whole layer
+  if ((rc = sgl::launch_permute(ids, T, k, E, w.counts, w.offsets, w.sorted_slot, w.slot_pos,
+                                w.tile_ctr, sgl::kTileCtrs, st, expert_begin, expert_end)))
+    return rc;
+  if ((rc = sgl::run_gate_up(w.xq, w.xs, T, H, I, E, k, w.offsets, w.sorted_slot, weights, experts,
+                             has_shared, expert_format, swiglu_limit, scale_mode, w.hq, w.hs,
+                             w.tile_ctr, st)))
+    return rc;
+  if ((rc = sgl::run_down(w.hq, w.hs, T, H, I, E, k, w.offsets, w.sorted_slot, experts, has_shared,
+                          expert_format, scale_mode, w.out, w.tile_ctr + 16, st)))
+    return rc;
+  sgl::launch_combine<true>(w.out, ids, T, k, H, has_shared, expert_begin, expert_end, y_local, st);
+  return sgl::check_launch("moe_forward_local");
+}
+
+int sgl_moe_add_shared(const float* y_local, const void* workspace, size_t workspace_bytes,
+                       int64_t T, int64_t H, int64_t I, int E, int k, void* y,
+                       sgl_stream_t stream) {
+  SGL_REQUIRE(T >= 0 && H > 0 && H % 128 == 0 && I > 0 && E >= 1 && k >= 1 && k <= 16,
+              "moe_add_shared: bad shape");
+  if (T == 0) return SGL_OK;
+  SGL_REQUIRE(y_local && workspace && y, "moe_add_shared: null pointer");
+  const sgl::MoeWorkspace w = sgl::carve(const_cast<void*>(workspace), T, H, I, E, k, 1);
+  if (workspace_bytes < w.bytes) {
+    sgl::set_error("moe_add_shared: workspace %zu bytes < %zu needed", workspace_bytes, w.bytes);
+    return SGL_ERR_WORKSPACE;
+  }
+  SGL_REQUIRE(sgl::aligned(y_local, 16) && sgl::aligned(y, 16),
+              "moe_add_shared: y_local and y must be 16-byte aligned");
+  int64_t blocks = sgl::ceil_div(T * H / 8, (int64_t)256);
+  const int64_t cap = 16 * (int64_t)sgl::device_cu_count();
+  if (blocks > cap) blocks = cap;
+  sgl::add_shared_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(
+      y_local, w.out, T, k, H, (uint16_t*)y);
+  return sgl::check_launch("moe_add_shared");
 }
 
 }  // extern "C"

@@ -50,10 +50,14 @@ struct GemmArgs {
   int m_tiles;      // grid rows (upper bound of M tiles)
   int n_tiles;      // tiles along N
   int* tile_ctr;    // moe: 8 zeroed per-XCD tile counters -> dynamic tile order (null: static)
-  int spare_cus;    // grouped launches: leave this many CUs to a concurrent launch (0: none)
-  int max_cus;      // grouped launches: use at most this many CUs (0: all)
+  void* ws;         // dense: the caller's workspace (split-K partials), or null
+  size_t ws_bytes;
 };
 
 int launch_gemm(int kind, GemmArgs& args, int64_t rows_hint, hipStream_t stream);
+
+// Bytes of workspace the dense FP8 GEMM of this shape uses (its split-K
+// partials; 0 when the shape does not split).  A function of the shape only.
+size_t dense_fp8_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 }  // namespace sgl

@@ -16,7 +16,7 @@ from typing import Optional
 LIB_DIR = Path(__file__).resolve().parent / "lib"
 LIB_PATH = LIB_DIR / "libsglang_lite_amd.so"
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 SGL_OK = 0
 SGL_ERR_INVALID_ARG = -1
@@ -58,7 +58,8 @@ SIGNATURES = {
     "sgl_hbm_stream": (c_int, [P, P, I64, P, P]),
     "sgl_mfma_mix": (c_int, [c_int, P, I64, P]),
     "sgl_mfma_mix_threads": (c_int, []),
-    "sgl_fp8_gemm": (c_int, [P, P, P, P, c_int, P, c_int, I64, I64, I64, P]),
+    "sgl_fp8_gemm": (c_int, [P, P, P, P, c_int, P, c_int, I64, I64, I64, P, c_size_t, P]),
+    "sgl_fp8_gemm_workspace_size": (c_size_t, [I64, I64, I64]),
     "sgl_fp4_gemm": (c_int, [P, P, c_int, P, P, P, c_int, I64, I64, I64, P]),
     "sgl_fp4_to_fp8_weight": (c_int, [P, P, I64, I64, P, P, P]),
     "sgl_fp8_weight_to_frag": (c_int, [P, I64, I64, P, P]),
@@ -82,6 +83,12 @@ SIGNATURES = {
         c_int,
         [P, I64, I64, I64, c_int, c_int, P, P, P, c_int, c_int, c_float, c_int, P, c_size_t, P, P],
     ),
+    "sgl_moe_forward_local": (
+        c_int,
+        [P, I64, I64, I64, c_int, c_int, P, P, P, c_int, c_int, c_int, c_int, c_float, c_int, P,
+         c_size_t, P, P],
+    ),
+    "sgl_moe_add_shared": (c_int, [P, P, c_size_t, I64, I64, I64, c_int, c_int, P, P]),
     "sgl_moe_forward_noalloc": (
         c_int, [P, I64, I64, I64, c_int, c_int, P, P, P, c_int, c_int, c_float, c_int, P, P],
     ),

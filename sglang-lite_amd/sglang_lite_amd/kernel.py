@@ -201,12 +201,17 @@ def fp8_gemm(
         assert out.is_contiguous() and out.dtype == odt and out.numel() == M * N
     if _scale_flag(a_s, "fp8_gemm a_s"):
         a_s = e8m0_to_f32(a_s)  # the kernel streams fp32 activation scales
+    # split-K shapes keep their fp32 partials in a workspace allocated here with
+    # torch (inside a graph capture it comes from the graph's pool), as the
+    # reference's adapter allocates its output (engine/v4_deep_gemm.py:186-188)
+    nws = int(_lib.load().sgl_fp8_gemm_workspace_size(M, N, K)) if M else 0
+    ws = torch.empty(nws, dtype=torch.uint8, device=a.device) if nws else None
     _lib.call(
         "sgl_fp8_gemm",
         a.data_ptr(), a_s.data_ptr(), b.data_ptr(), b_s.data_ptr(),
         _scale_flag(b_s, "fp8_gemm b_s"),
         out.data_ptr(), _lib.SGL_BF16 if odt == torch.bfloat16 else _lib.SGL_F32,
-        M, N, K, _lib.stream_of(a),
+        M, N, K, _lib.ptr(ws), nws, _lib.stream_of(a),
     )
     return out
 

@@ -84,19 +84,30 @@ class ExpertTable:
         e8m0 scales, ``fp4_weight_to_frag``) and add their records after the
         first set (``EXPERT_FRAG_COPY``): the grouped GEMMs then load those
         weights straight into registers.  Costs a second copy of the expert
-        weights."""
+        weights.
+
+        A routed expert given as None (an expert another rank holds, as
+        deepseek_infer/model.py:616-625 builds them) gets a record of null
+        pointers; only :func:`moe_forward_local` with a range that excludes
+        it may run such a table."""
         rows = list(experts) + ([shared] if shared is not None else [])
-        if not rows:
+        live = [r for r in rows if r is not None]
+        if not live:
             raise ValueError("ExpertTable needs at least one expert")
-        fp4 = bool(experts) and experts[0][0].dtype in (FP4, torch.int8, torch.uint8)
-        w1 = rows[0][0]
+        routed = [r for r in experts if r is not None]
+        fp4 = bool(routed) and routed[0][0].dtype in (FP4, torch.int8, torch.uint8)
+        first = routed[0] if routed else live[0]
+        w1 = first[0]
         I = int(w1.shape[0])
-        H = int(w1.shape[1]) * (2 if fp4 else 1)  # packed e2m1 rows hold two inputs per byte
+        H = int(w1.shape[1]) * (2 if fp4 and routed else 1)  # packed e2m1 rows hold two inputs per byte
         dev = w1.device
         keep: List[torch.Tensor] = []
         vals = []
         pow2 = True
         for i, r in enumerate(rows):
+            if r is None:
+                vals.append([0] * 6)
+                continue
             w1, w3, w2, s1, s3, s2 = r
             if fp4 and i < len(experts):
                 ws = [fp4_bytes(w) for w in (w1, w3, w2)]
@@ -125,6 +136,9 @@ class ExpertTable:
                 raise ValueError("frag_layout needs H and I multiples of 128 (FP4 experts: of 512)")
             for i, r in enumerate(rows):
                 row = list(vals[i])
+                if r is None:
+                    vals.append(row)
+                    continue
                 if fp4 and i < len(experts):
                     pairs = [fp4_weight_to_frag(w, sc) for w, sc in zip(r[:3], r[3:])]
                     keep += [t for pr in pairs for t in pr]
@@ -331,9 +345,57 @@ def moe_forward(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, table
     return y
 
 
+def moe_forward_local(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
+                      table: ExpertTable, expert_begin: int, expert_end: int,
+                      swiglu_limit: float = 0.0, scale_mode: int = _lib.SCALE_TORCH_FP32,
+                      workspace: Optional[MoEWorkspace] = None) -> torch.Tensor:
+    """One rank's share of an expert-sharded layer (engine/v4_moe_fast.py:79-102
+    up to the all-reduce): fp32 [T, H] = the sum, in ascending expert id, of
+    each token's outputs from the routed experts in ``[expert_begin,
+    expert_end)``.  The shared expert runs in the same launches and its rows
+    stay in ``workspace`` for :func:`moe_add_shared` (pass the same object)."""
+    _lib.require_device(x, ids, weights, what="moe_forward_local")
+    if x.dtype != torch.bfloat16 or x.dim() != 2:
+        raise TypeError("moe_forward_local: x must be bfloat16 [T, H]")
+    x = x.contiguous()
+    ids = _ids32(ids)
+    w = weights.to(torch.float32).contiguous()
+    T, H = x.shape
+    k = ids.shape[1]
+    if H != table.H:
+        raise ValueError(f"moe_forward_local: x has H={H}, experts have H={table.H}")
+    ws = (workspace or MoEWorkspace()).get(workspace_size(T, H, table.I, table.E, k,
+                                                          table.has_shared), x.device)
+    y = torch.empty(T, H, dtype=torch.float32, device=x.device)
+    _lib.call("sgl_moe_forward_local", x.data_ptr(), T, H, table.I, table.E, k, ids.data_ptr(),
+              w.data_ptr(), table.ptrs.data_ptr(), int(expert_begin), int(expert_end),
+              int(table.has_shared), table.fmt, float(swiglu_limit), int(scale_mode),
+              ws.data_ptr(), ws.numel(), y.data_ptr(), _lib.stream_of(x))
+    return y
+
+
+def moe_add_shared(y_local: torch.Tensor, table: ExpertTable, k: int,
+                   workspace: MoEWorkspace) -> torch.Tensor:
+    """``bf16(y_local + shared(x))`` (engine/v4_moe_fast.py:103-106) with the
+    shared expert's rows that :func:`moe_forward_local` left in ``workspace``."""
+    _lib.require_device(y_local, what="moe_add_shared")
+    if not table.has_shared:
+        raise ValueError("moe_add_shared: the table has no shared expert")
+    if y_local.dtype != torch.float32 or y_local.dim() != 2 or not y_local.is_contiguous():
+        raise TypeError("moe_add_shared: y_local must be contiguous float32 [T, H]")
+    T, H = y_local.shape
+    ws = workspace.buf
+    if ws is None:
+        raise ValueError("moe_add_shared: the workspace holds no moe_forward_local result")
+    y = torch.empty(T, H, dtype=torch.bfloat16, device=y_local.device)
+    _lib.call("sgl_moe_add_shared", y_local.data_ptr(), ws.data_ptr(), ws.numel(), T, H, table.I,
+              table.E, int(k), y.data_ptr(), _lib.stream_of(y_local))
+    return y
+
+
 def workspace_size(T: int, H: int, I: int, E: int, k: int, has_shared: bool) -> int:
     return int(_lib.load().sgl_moe_workspace_size(T, H, I, E, k, int(has_shared)))
 
 
-__all__ = ["ExpertTable", "MoEWorkspace", "combine", "down", "gate", "gate_up", "moe_forward",
-           "permute", "route_topk", "workspace_size"]
+__all__ = ["ExpertTable", "MoEWorkspace", "combine", "down", "gate", "gate_up", "moe_add_shared",
+           "moe_forward", "moe_forward_local", "permute", "route_topk", "workspace_size"]

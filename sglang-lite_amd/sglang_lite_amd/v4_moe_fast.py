@@ -88,10 +88,11 @@ def _scale_mode():
 
 
 def expert_table(moe) -> HM.ExpertTable:
-    """Device pointer table of a MoE module's experts + shared expert (cached)."""
+    """Device pointer table of a MoE module's experts + shared expert (cached);
+    the experts another rank holds (None, model.py:616-625) get null records."""
     tab = getattr(moe, "_sgl_table", None)
     if tab is None:
-        experts = [_expert_entry(e) for e in moe.experts]
+        experts = [None if e is None else _expert_entry(e) for e in moe.experts]
         tab = HM.ExpertTable.build(experts, _expert_entry(moe.shared_experts),
                                    frag_layout=frag_layout_enabled())
         moe._sgl_table = tab
@@ -139,15 +140,39 @@ def _gate_topk(gate, x: torch.Tensor, input_ids: torch.Tensor):
     return weights, ids
 
 
+def _local_range(moe):
+    """``(ok, lo, hi)`` of a MoE module, decided once and cached: the rank's
+    expert range ``[experts_start_idx, experts_end_idx)`` (model.py:616-625),
+    and whether the device path can run it -- every expert in the range
+    present and quantized alike (all FP8 or all FP4) and an FP8 shared expert."""
+    st = getattr(moe, "_sgl_range", None)
+    if st is None:
+        E = len(moe.experts)
+        lo = int(getattr(moe, "experts_start_idx", 0))
+        hi = int(getattr(moe, "experts_end_idx", E))
+        local = list(moe.experts[lo:hi]) if 0 <= lo <= hi <= E else []
+        ok = bool(local) and all(e is not None for e in local) and \
+            _is_fp8(moe.shared_experts.w1) and _quantized(moe.shared_experts) and \
+            (all(_is_fp8(e.w1) and _quantized(e) for e in local) or
+             all(_is_fp4(e.w1) and _quantized(e) for e in local))
+        st = (ok, lo, hi)
+        moe._sgl_range = st
+    return st
+
+
 def _moe_forward_fused(self, x: torch.Tensor, input_ids: torch.Tensor):
-    """The whole MoE layer (v4_moe_fast.py:79-106) on the device, no host sync."""
-    M = sys.modules.get("model")
-    if (M is not None and getattr(M, "world_size", 1) > 1) or \
-            any(e is None for e in self.experts) or \
-            not all(_quantized(e) for e in (self.experts[0], self.shared_experts)) or \
-            not _is_fp8(self.shared_experts.w1):
-        # expert-sharded ranks / bf16 experts are not this path
+    """The whole MoE layer (v4_moe_fast.py:79-106) on the device, no host sync.
+
+    An expert-sharded rank (``world_size > 1``, or a module that holds only
+    the experts ``[experts_start_idx, experts_end_idx)``) computes the fp32 sum
+    of its local experts' outputs, calls ``dist.all_reduce`` on it exactly
+    where the reference does (v4_moe_fast.py:103-104), then adds the shared
+    expert and rounds to bf16."""
+    ok, lo, hi = _local_range(self)
+    if not ok:  # bf16 experts, mixed formats, missing local experts: not this path
         return self._sgl_orig_forward(x, input_ids)
+    M = sys.modules.get("model")
+    world = int(getattr(M, "world_size", 1) or 1) if M is not None else 1
     shape = x.size()
     x2 = x.view(-1, self.dim)
     weights, ids = _gate_topk(self.gate, x2, input_ids)
@@ -157,8 +182,16 @@ def _moe_forward_fused(self, x: torch.Tensor, input_ids: torch.Tensor):
     if ws is None:
         ws = HM.MoEWorkspace()
         self._sgl_ws = ws
-    y = HM.moe_forward(xb, ids, weights, expert_table(self), swiglu_limit=lim,
-                       scale_mode=_scale_mode(), workspace=ws)
+    tab = expert_table(self)
+    if world == 1 and lo == 0 and hi == len(self.experts):
+        y = HM.moe_forward(xb, ids, weights, tab, swiglu_limit=lim, scale_mode=_scale_mode(),
+                           workspace=ws)
+        return y.type_as(x).view(shape)
+    y32 = HM.moe_forward_local(xb, ids, weights, tab, lo, hi, swiglu_limit=lim,
+                               scale_mode=_scale_mode(), workspace=ws)
+    if world > 1:
+        M.dist.all_reduce(y32)
+    y = HM.moe_add_shared(y32, tab, ids.shape[1], ws)
     return y.type_as(x).view(shape)
 
 

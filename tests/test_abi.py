@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     from sglang_lite_amd import _lib as L
 
-    assert lib.sgl_abi_version() == L.ABI_VERSION == 2
+    assert lib.sgl_abi_version() == L.ABI_VERSION == 3
 
 
 def test_probe_without_gpu_reports_why():
@@ -155,7 +155,7 @@ def test_invalid_arguments_map_to_value_error_without_launch():
     assert "divisible" in L.last_error()
     with pytest.raises(ValueError, match="group"):
         L.call("sgl_act_quant", None, 4, 128, 128, None, 128, None, 1, 96, 0, 0, 0, None)
-    rc = lib.sgl_fp8_gemm(None, None, None, None, 0, None, 0, 4, 100, 256, None)
+    rc = lib.sgl_fp8_gemm(None, None, None, None, 0, None, 0, 4, 100, 256, None, 0, None)
     assert rc == L.SGL_ERR_INVALID_ARG and "multiple of 16" in L.last_error()
     rc = lib.sgl_hbm_stream(None, None, 1000, None, None)
     assert rc == L.SGL_ERR_INVALID_ARG and "multiple of 32768" in L.last_error()
@@ -230,3 +230,26 @@ def test_expert_format_pow2_flag():
         args = (None, None, 64, H, I, E, k, None, None, None, None, 1, fmt, 0.0, 0, None, None, None)
         with pytest.raises(ValueError, match="null pointer" if ok else "bad expert_format"):
             L.call("sgl_moe_gate_up", *args)
+
+
+def test_fp8_gemm_split_decision_is_a_function_of_the_shape():
+    """sgl_fp8_gemm_workspace_size depends on (M, N, K) only: split-K for
+    16 < M <= 64 with N % 128 == 0, S splits of fp32 [M, N] partials; a call
+    whose shape splits and whose workspace is missing or short is refused with
+    SGL_ERR_WORKSPACE before anything is launched (the pointers below are
+    never dereferenced), rather than summed in another order."""
+    from sglang_lite_amd import _lib as L
+
+    lib = _lib()
+    ws = lib.sgl_fp8_gemm_workspace_size
+    assert ws(40, 4096, 7168) == 8 * 40 * 4096 * 4  # 56 K blocks in 8 splits of 7
+    assert ws(17, 4096, 7168) == 8 * 17 * 4096 * 4
+    assert ws(64, 384, 2048) > 0
+    for M, N, K in ((16, 4096, 7168), (65, 4096, 7168), (1024, 4096, 7168), (40, 4096 + 16, 7168)):
+        assert ws(M, N, K) == 0, (M, N, K)
+    fake = 1 << 20  # aligned, never read: the workspace check comes first
+    need = ws(40, 4096, 7168)
+    for buf, n in ((None, 0), (fake, need - 16)):
+        rc = lib.sgl_fp8_gemm(fake, fake, fake, fake, 0, fake, 0, 40, 4096, 7168, buf, n, None)
+        assert rc == L.SGL_ERR_WORKSPACE, rc
+        assert str(need) in L.last_error()

@@ -11,7 +11,8 @@ import torch
 import torch.nn.functional as F
 
 import fake_official
-from helpers import assert_gemm_close, bf16_values, f32, to_dev_bf16, to_dev_f32, to_dev_fp8, u8
+from helpers import (assert_gemm_close, assert_layer_close, bf16_values, f32, to_dev_bf16, to_dev_f32,
+                     to_dev_fp8, u8)
 from oracle import fp4 as F4
 from oracle import moe as OM
 from oracle import quant as Q
@@ -362,3 +363,148 @@ def test_kv_pack_with_the_attached_act_quant_takes_the_fused_kernel(official, gp
     torch.cuda.synchronize()
     assert torch.equal(pool[0, 2, 0], want[:64]) and torch.equal(pool[0, 0, 0], want[64:128])
     assert torch.equal(pool[0, 3, 0, :2], want[128:130])
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "fp4"])
+def test_expert_sharded_ranks(official, gpu, fmt):
+    """The layer as the reference runs it on an expert-sharded world
+    (deepseek_infer/model.py:616-625: rank r builds experts [r E/W, (r+1) E/W)
+    and None elsewhere; engine/v4_moe_fast.py:79-106): each of W = 4 ranks is
+    built in turn with world_size = 4 and dist.all_reduce stubbed.
+    * The fp32 sum each rank hands to all_reduce equals, bit for bit, the
+      ascending fp32 sum of the device's own expert rows of that rank's
+      experts (the unsharded grouped launches' rows), and the oracle's rank
+      sum (moe_local_partial) within the layer tolerance.
+    * With all_reduce as identity, the rank's output is bf16(partial + shared
+      row) exactly.
+    * With all_reduce summing the four ranks' partials, the output matches the
+      whole layer's oracle."""
+    import types
+
+    from sglang_lite_amd import moe as HM
+    from sglang_lite_amd import v4_moe_fast as MF
+
+    M, K = official
+    rng = np.random.default_rng(44 if fmt == "fp8" else 45)
+    T, H, I, E, k, W = 48, 512, 256, 16, 4, 4
+    x = bf16_values(rng, (T, H))
+    Wg = (rng.standard_normal((E, H)) * H ** -0.5).astype(np.float32)
+    if fmt == "fp8":
+        experts = [OM.make_expert(rng, H, I) for _ in range(E)]
+        dev = [_dev_expert(e, gpu) for e in experts]
+    else:
+        experts = [OM.make_fp4_expert(rng, H, I) for _ in range(E)]
+        dev = [_dev_fp4_expert(e, gpu) for e in experts]
+    sh = OM.make_expert(rng, H, I)
+    sh_dev = _dev_expert(sh, gpu)
+    gate = M.Gate(to_dev_f32(Wg, gpu), k)
+    xd = to_dev_bf16(x, gpu).view(1, T, H)
+    in_ids = torch.zeros(1, T, dtype=torch.long, device=gpu)
+    # routing and the device's own expert rows from the unsharded launches
+    logits = F.linear(xd[0].float(), gate.weight.float()).cpu().numpy()
+    w_ref, ids_ref = OM.route_topk(logits, k)
+    assert OM.topk_margin(logits, k) > 1e-6
+    full_tab = HM.ExpertTable.build(dev, sh_dev)
+    from sglang_lite_amd import kernel as HK
+
+    w_d, ids_d = HM.route_topk(F.linear(xd[0].float(), gate.weight.float()), k)
+    xq, xs = HK.act_quant(xd[0])
+    _, offsets, sorted_slot, _ = HM.permute(ids_d, E)
+    hq, hs = HM.gate_up(xq, xs, offsets, sorted_slot, w_d.reshape(-1), full_tab, k)
+    rows = f32(HM.down(hq, hs, offsets, sorted_slot, full_tab, T, k))  # [T, k+1, H]
+    ids_np = ids_d.cpu().numpy()
+    np.testing.assert_array_equal(ids_np, ids_ref)
+
+    M.world_size = W
+    partials = []
+
+    def record(t):
+        partials.append(t.clone())
+
+    M.dist = types.SimpleNamespace(all_reduce=record)
+    MF.attach_v4_moe_fast(torch.nn.Module())
+    per = E // W
+    mods = []
+    for r in range(W):
+        lo, hi = r * per, (r + 1) * per
+        moe = M.MoE(H, gate, [M.Expert(dev[e]) if lo <= e < hi else None for e in range(E)],
+                    M.Expert(sh_dev))
+        moe.experts_start_idx, moe.experts_end_idx = lo, hi
+        mods.append(moe)
+        y_r = moe(xd, in_ids)
+        part = partials[-1]
+        assert part.dtype == torch.float32 and part.shape == (T, H)
+        p_np = part.cpu().numpy()
+        # bit for bit: the ascending fp32 sum of the device's rows of local experts
+        want = np.zeros((T, H), np.float32)
+        for t in range(T):
+            for j in np.argsort(ids_np[t], kind="stable"):
+                if lo <= ids_np[t, j] < hi:
+                    want[t] = (want[t] + rows[t, j]).astype(np.float32)
+        np.testing.assert_array_equal(p_np.view(np.uint32), want.view(np.uint32))
+        ref = OM.moe_local_partial(x, ids_ref, w_ref, experts, lo, hi)
+        assert_layer_close(p_np, ref, f"rank {r} partial ({fmt})")
+        # identity all_reduce: the rank's output is bf16(partial + shared row)
+        y_want = Q.bf16_round((p_np + rows[:, k]).astype(np.float32))
+        np.testing.assert_array_equal(f32(y_r[0]).view(np.uint32), y_want.view(np.uint32))
+    # all ranks' partials summed by the collective
+    total = partials[0].clone()
+    for p_ in partials[1:W]:
+        total += p_
+
+    def reduce_sum(t):
+        t.copy_(total)
+
+    M.dist = types.SimpleNamespace(all_reduce=reduce_sum)
+    y = mods[1](xd, in_ids)
+    y_ref = OM.moe_forward(x, ids_ref, w_ref, experts, sh)
+    assert_layer_close(f32(y[0]), y_ref, f"expert-sharded layer, {W} ranks ({fmt})")
+    np.testing.assert_array_equal(
+        f32(y[0]).view(np.uint32),
+        Q.bf16_round((total.cpu().numpy() + rows[:, k]).astype(np.float32)).view(np.uint32))
+    M.world_size = 1
+
+
+@pytest.mark.parametrize("T", [2049, 40])
+def test_local_range_partial_is_the_ordered_sum_of_the_rows(gpu, T):
+    """moe_forward_local over several expert ranges -- the whole range, an
+    inner one, an empty one -- at a size that takes the chunked permute (T*k
+    = 16392 slots) and a small one: the fp32 partial equals, bit for bit, the
+    ascending fp32 sum of the device's own expert rows whose expert lies in
+    the range, and moe_add_shared adds the shared row in fp32 and rounds."""
+    from sglang_lite_amd import kernel as HK
+    from sglang_lite_amd import moe as HM
+
+    print(f"local-range partial T={T}", flush=True)
+    rng = np.random.default_rng(46 + T)
+    H, I, E, k = 512, 256, 16, 8
+    x = bf16_values(rng, (T, H))
+    experts = [OM.make_expert(rng, H, I) for _ in range(E)]
+    sh = OM.make_expert(rng, H, I)
+    tab = HM.ExpertTable.build([_dev_expert(e, gpu) for e in experts], _dev_expert(sh, gpu))
+    logits = to_dev_f32(rng.standard_normal((T, E)).astype(np.float32), gpu)
+    w_d, ids_d = HM.route_topk(logits, k)
+    xd = to_dev_bf16(x, gpu)
+    xq, xs = HK.act_quant(xd)
+    _, offsets, sorted_slot, _ = HM.permute(ids_d, E)
+    hq, hs = HM.gate_up(xq, xs, offsets, sorted_slot, w_d.reshape(-1), tab, k)
+    rows = f32(HM.down(hq, hs, offsets, sorted_slot, tab, T, k))
+    ids_np = ids_d.cpu().numpy()
+    order = np.argsort(ids_np, axis=1, kind="stable")
+    ws = HM.MoEWorkspace()
+    for lo, hi in ((0, E), (3, 11), (5, 5)):
+        part = HM.moe_forward_local(xd, ids_d, w_d, tab, lo, hi, workspace=ws)
+        want = np.zeros((T, H), np.float32)
+        for j in range(k):
+            e = np.take_along_axis(ids_np, order[:, j:j + 1], axis=1)[:, 0]
+            r = rows[np.arange(T), order[:, j]]
+            local = (e >= lo) & (e < hi)
+            want[local] = (want[local] + r[local]).astype(np.float32)
+        np.testing.assert_array_equal(part.cpu().numpy().view(np.uint32), want.view(np.uint32))
+        y = HM.moe_add_shared(part, tab, k, ws)
+        y_want = Q.bf16_round((want + rows[:, k]).astype(np.float32))
+        np.testing.assert_array_equal(f32(y).view(np.uint32), y_want.view(np.uint32))
+    # the whole range is the whole layer
+    y_full = HM.moe_forward(xd, ids_d, w_d, tab)
+    part = HM.moe_forward_local(xd, ids_d, w_d, tab, 0, E, workspace=ws)
+    assert torch.equal(HM.moe_add_shared(part, tab, k, ws), y_full)

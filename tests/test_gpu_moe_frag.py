@@ -181,10 +181,10 @@ def test_fp4_experts_bit_identical(gpu, T, mode):
 
 @pytest.mark.parametrize("frag", [False, True])
 def test_fp4_layer_in_a_graph_replays_equal_eager(gpu, frag):
-    """The FP4 layer at a decode batch runs its FP8 shared expert on a second
-    stream beside the routed launch (fork and join by events): captured into
-    a HIP graph on the caller's stream, every replay, with eager layers and
-    synchronizations between them, equals the eager layer bit for bit."""
+    """The FP4 layer at a decode batch (routed FP4 launch, then the FP8 shared
+    expert's launch) captured into a HIP graph on the caller's stream: every
+    replay, with eager layers and synchronizations between them, equals the
+    eager layer bit for bit."""
     from sglang_lite_amd import moe as M
 
     H, I, E, k, T = 4096, 2048, 256, 8, 64
