@@ -1627,18 +1627,28 @@ static_assert(SLOTS == 4, "the stage loop is unrolled by four");
 // stages); the activation fragment pairs its K as the FP4 kernels do (chunks
 // l/16 and 4 + l/16); the row scales as for FP8 (POW2: in the MFMA, else one
 // fp32 promotion per 128-deep block).
-template <int KIND, int NJ, bool POW2, bool W4>
+//
+// RM: FP8 weights read from the experts' row-major [N, K] arrays (no
+// fragment-layout copy): lane (r16, g4) of a 16-row fragment loads bytes
+// [32 g4, +16) and [32 g4 + 16, +16) of its row's 128-byte K segment, the
+// same bytes the fragment layout puts in that lane, so the products are
+// bit-identical to the fragment-layout kernel's.
+template <int KIND, int NJ, bool POW2, bool W4, bool RM = false>
 __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
   using namespace rb;
   static_assert(KIND == KIND_GATE_UP || KIND == KIND_DOWN, "grouped GEMMs only");
   static_assert(NJ == 1 || NJ == 2, "one or two fragments per half");
   static_assert(!W4 || NJ == 1, "fp4 weights: 16-column fragments per half");
+  static_assert(!(W4 && RM), "row-major weights: FP8 only");
   constexpr int NW = 8, NT = 64 * NW;
   // stages of weight fragments in registers: four for down and for fp4
   // (half the registers per fragment); fp8 gate/up (whose epilogue holds more
   // registers across the tile boundary) SGL_RB_DBG
   constexpr int DB = NJ == 2 ? 2 : ((KIND == KIND_GATE_UP && !W4) ? SGL_RB_DBG : 4);
   constexpr uint32_t WBLK = W4 ? 1024 : 2048;  // weight bytes per 16-row x 128-deep block
+  // byte distance between the K stages of a fragment: a fragment-layout
+  // block, or one 128-byte K segment of a row-major row
+  constexpr uint32_t SSTR = RM ? 128u : WBLK;
   constexpr int GC = 128 * NJ;         // gate/up: gate columns of a tile
   constexpr int TC = KIND == KIND_GATE_UP ? GC : 256 * NJ;  // output columns of a tile (per half)
   constexpr int NB = 2 * NJ;           // weight-scale rows of a tile (gate/up: NJ per half)
@@ -1799,8 +1809,13 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
       const int64_t nb16 = N / 16;
       int64_t n16 = (int64_t)t.nt * (GC / 16) + NJ * w;
       if (n16 > nb16 - NJ) n16 = nb16 - NJ;  // columns past N (not stored) re-read the last blocks
-      s.b0 = rec_field(args.frag, t.e, 0) + (uint64_t)(n16 * KB * WBLK);
-      s.b1 = rec_field(args.frag, t.e, 1) + (uint64_t)(n16 * KB * WBLK);
+      if constexpr (RM) {
+        s.b0 = rec_field(args.experts, t.e, 0) + (uint64_t)(n16 * 16 * K);
+        s.b1 = rec_field(args.experts, t.e, 1) + (uint64_t)(n16 * 16 * K);
+      } else {
+        s.b0 = rec_field(args.frag, t.e, 0) + (uint64_t)(n16 * KB * WBLK);
+        s.b1 = rec_field(args.frag, t.e, 1) + (uint64_t)(n16 * KB * WBLK);
+      }
       if constexpr (W4) {
         s.s0 = rec_field(args.frag, t.e, 3) + (uint64_t)(n16 * (KB / 4) * 256);
         s.s1 = rec_field(args.frag, t.e, 4) + (uint64_t)(n16 * (KB / 4) * 256);
@@ -1814,7 +1829,8 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
       const int64_t nb16 = N / 16;
       int64_t n16 = (int64_t)t.nt * (TC / 16) + NF * w;
       if (n16 > nb16 - NF) n16 = nb16 - NF;  // columns past N (not stored) re-read the last blocks
-      s.b0 = rec_field(args.frag, t.e, 2) + (uint64_t)(n16 * KB * WBLK);
+      s.b0 = RM ? rec_field(args.experts, t.e, 2) + (uint64_t)(n16 * 16 * K)
+                : rec_field(args.frag, t.e, 2) + (uint64_t)(n16 * KB * WBLK);
       s.b1 = s.b0;
       if constexpr (W4) {
         s.s0 = rec_field(args.frag, t.e, 5) + (uint64_t)(n16 * (KB / 4) * 256);
@@ -1846,11 +1862,18 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
     const i4v v = *(gi4v*)(a_g + off);
     return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
   };
+  // the lane's two 16-byte pieces of a weight fragment: in the fragment
+  // layout at 16 l and 1024 + 16 l of the block, row-major at row r16, bytes
+  // 32 g4 and 32 g4 + 16 of the K segment
+  const uint32_t wlo = RM ? (uint32_t)(r16 * K + 32 * g4) : lane16;
+  const uint32_t whi = RM ? wlo + 16u : lane16 + 1024u;
+  // distance between a wavefront's consecutive 16-row weight fragments
+  const uint64_t fstr = RM ? (uint64_t)16 * K : (uint64_t)KB * WBLK;
   auto ldB = [&](uint64_t base, uint64_t off) -> v8i {
     gbyte* p = (gbyte*)(uintptr_t)base;
-    const i4v lo = *(gi4v*)(p + off + lane16);
+    const i4v lo = *(gi4v*)(p + off + wlo);
     if constexpr (W4) return v8i{lo.x, lo.y, lo.z, lo.w, 0, 0, 0, 0};  // 16 packed bytes
-    const i4v hi = *(gi4v*)(p + off + (lane16 + 1024u));
+    const i4v hi = *(gi4v*)(p + off + whi);
     return v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
   };
   // W4: lane's scale dword of fragment f for the four stages of group g
@@ -1906,9 +1929,9 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
   // weight fragment f of the wavefront at stage offset off (bytes within the block row)
   auto ldBf = [&](const Src& s, int f, uint32_t off) -> v8i {
     if constexpr (KIND == KIND_GATE_UP)
-      return ldB(f < NJ ? s.b0 : s.b1, (uint64_t)(f % NJ) * KB * WBLK + off);
+      return ldB(f < NJ ? s.b0 : s.b1, (uint64_t)(f % NJ) * fstr + off);
     else
-      return ldB(s.b0, (uint64_t)f * KB * WBLK + off);
+      return ldB(s.b0, (uint64_t)f * fstr + off);
   };
   uint32_t swc[NF], swn[NF];  // W4: scale dwords of the current / next group of four stages
   v8i bq[DB][NF];
@@ -1933,7 +1956,7 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
 #pragma unroll
     for (int s = 0; s < DB; ++s)
 #pragma unroll
-      for (int f = 0; f < NF; ++f) bq[s][f] = ldBf(cs, f, s * WBLK);
+      for (int f = 0; f < NF; ++f) bq[s][f] = ldBf(cs, f, s * SSTR);
 #pragma unroll
     for (int f = 0; f < NF; ++f) swc[f] = swn[f] = W4 ? ldS(cs, f, 0) : 0u;
   }
@@ -2104,7 +2127,7 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
       {
         const int sb_ = st + DB;
         const bool curb = sb_ < NST;
-        const uint32_t off = (uint32_t)(curb ? sb_ : sb_ - NST) * WBLK;
+        const uint32_t off = (uint32_t)(curb ? sb_ : sb_ - NST) * SSTR;
 #pragma unroll
         for (int f = 0; f < NF; ++f) bq[J % DB][f] = ldBf(curb ? cs : ns, f, off);
       }
@@ -2264,7 +2287,7 @@ int64_t cu_budget(const GemmArgs&) {
   return std::max<int64_t>(8, (n + 7) / 8 * 8);
 }
 
-template <int KIND, bool W4 = false>
+template <int KIND, bool W4 = false, bool RM = false>
 int launch_rb(GemmArgs& a, hipStream_t stream) {
   using namespace rb;
   a.n_tiles = (int)ceil_div(a.N, (KIND == KIND_GATE_UP ? 128 : 256) * SGL_RB_NJ);
@@ -2284,9 +2307,9 @@ int launch_rb(GemmArgs& a, hipStream_t stream) {
     else
       gemm_rb_kernel<KIND, 1, false, true><<<(unsigned)wgs, 512, 0, stream>>>(a);
   } else if (a.sa_pow2 && a.sb_pow2) {
-    gemm_rb_kernel<KIND, SGL_RB_NJ, true, false><<<(unsigned)wgs, 512, 0, stream>>>(a);
+    gemm_rb_kernel<KIND, SGL_RB_NJ, true, false, RM><<<(unsigned)wgs, 512, 0, stream>>>(a);
   } else {
-    gemm_rb_kernel<KIND, SGL_RB_NJ, false, false><<<(unsigned)wgs, 512, 0, stream>>>(a);
+    gemm_rb_kernel<KIND, SGL_RB_NJ, false, false, RM><<<(unsigned)wgs, 512, 0, stream>>>(a);
   }
   return check_launch("gemm_rb");
 }
@@ -2609,6 +2632,11 @@ int launch_cfg(GemmArgs& a, hipStream_t stream) {
 #endif
 #ifndef SGL_LWN
 #define SGL_LWN 4
+#endif
+// the register-fed kernel on the experts' row-major FP8 weights (no
+// fragment-layout copy) for the grouped GEMMs
+#ifndef SGL_RB_RM
+#define SGL_RB_RM 1
 #endif
 #ifndef SGL_SPLITK
 #define SGL_SPLITK 1
@@ -3122,8 +3150,19 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
   // straight from memory beat the LDS-staged 32-row tiles (T = 64 / 256 /
   // 512, Zipf load: layer 676 / 1103 / 1255 -> 627 / 1024 / 1170 us)
   const int64_t kb = a.K / 128;
-  const bool rb_ok = SGL_RB && a.frag && !a.sb_e8m0 && kb >= rb::kMinKB &&
-                     kb <= rb::kMaxKBr && kb % 4 == 0 && aligned(a.sa, 16);
+  const bool rb_shape = SGL_RB && !a.sb_e8m0 && kb >= rb::kMinKB && kb <= rb::kMaxKBr &&
+                        kb % 4 == 0 && aligned(a.sa, 16);
+  const bool rb_ok = rb_shape && a.frag;
+  // the row-major weights straight into registers at decode sizes (fewer
+  // than 64 rows per expert on average); prefill batches take the pipelined
+  // LDS-staged kernel, which reads row-major weights faster (T = 8192:
+  // gate/up 1.97 ms there, 2.08 ms register-fed; decode T = 64 / 256 / 512
+  // layer 0.67 / 1.04 / 1.22 ms register-fed, 0.67 / 1.07 / 1.25 LDS-staged)
+  const bool rb_rm = rb_shape && !a.frag && SGL_RB_RM && !big;
+  // the FP8 shared expert of an FP4 layer in a launch of its own at decode
+  // batch sizes: 32-row tiles, so ceil(T / 32) x N / 256 workgroups share
+  // its weight stream (128-row tiles give N / 256 = 16 at T <= 128)
+  const bool shared_small = a.E == 0 && a.has_shared && a.T <= 512;
   switch (kind) {
     case KIND_DENSE: {
       const int rc = SGL_SPLITK ? try_splitk(a, stream) : kNoSplit;
@@ -3150,13 +3189,17 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       return launch_wide(a, stream);
     }
     case KIND_GATE_UP:
+      if (shared_small) return launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 4>(a, stream);
       if (rb_ok) return launch_rb<KIND_GATE_UP>(a, stream);
+      if (rb_rm) return launch_rb<KIND_GATE_UP, false, true>(a, stream);
       if (big && pipe_ok)
         return pow2 ? launch_pipe<KIND_GATE_UP, true>(a, stream) : launch_pipe<KIND_GATE_UP, false>(a, stream);
       return big ? launch_cfg<KIND_GATE_UP, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)
                  : launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 4>(a, stream);
     default:
+      if (shared_small) return launch_cfg<KIND_DOWN, 32, 256, 1, 4, 4>(a, stream);
       if (rb_ok) return launch_rb<KIND_DOWN>(a, stream);
+      if (rb_rm) return launch_rb<KIND_DOWN, false, true>(a, stream);
       if (big && pipe_ok)
         return pow2 ? launch_pipe<KIND_DOWN, true>(a, stream) : launch_pipe<KIND_DOWN, false>(a, stream);
       return big ? launch_cfg<KIND_DOWN, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)

@@ -14,7 +14,9 @@ from pathlib import Path
 from typing import Optional
 
 LIB_DIR = Path(__file__).resolve().parent / "lib"
-LIB_PATH = LIB_DIR / "libsglang_lite_amd.so"
+# SGLANG_LITE_AMD_LIB names another build of the same library (an A/B build
+# of a kernel variant); by default the in-tree build is loaded
+LIB_PATH = Path(os.environ.get("SGLANG_LITE_AMD_LIB") or (LIB_DIR / "libsglang_lite_amd.so"))
 
 ABI_VERSION = 3
 
