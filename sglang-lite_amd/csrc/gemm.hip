@@ -1239,6 +1239,8 @@ __global__ __launch_bounds__(pipe::NT) void gemm_pipe_kernel(const GemmArgs args
         const bool up_half = KIND == KIND_GATE_UP && b * 8 >= HALF;
         const int64_t nrow = ls.n0 + (up_half ? b * 8 - HALF : b * 8);
         const uint32_t vo = nrow + rr < N ? (uint32_t)(nrow * K) + ls.laneB : ls.clampB;
+        // plain loads: the two or three M tiles of an expert share its weight
+        // slice through L2 (nontemporal DMAs here: gate/up 1.82 -> 2.26 ms)
         dma16v((up_half ? ls.b1 : ls.b0) + vo + (uint64_t)st * 128u,
                __builtin_amdgcn_readfirstlane(sl + (uint32_t)c * 1024u));
       }
@@ -1462,6 +1464,7 @@ __global__ __launch_bounds__(pipe::NT) void gemm_pipe_kernel(const GemmArgs args
               const int64_t col = n0 + tile_col(nj) + 4 * g4;
               if (col < N) {
                 const v4f v = acc[mi][nj];
+                // plain stores (nontemporal ones: down 1.01 -> 1.17 ms)
                 *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(args.c) + drow * N + col) =
                     make_uint2(pk2_bf16_exact(v[0], v[1]), pk2_bf16_exact(v[2], v[3]));
               }
