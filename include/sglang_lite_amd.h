@@ -190,10 +190,11 @@ int sgl_mfma_mix_threads(void);
 
 /* C[M, N] = sum_kb (A[:, kb] . B[:, kb]^T) * sa[m, kb] * sb[n/128, kb], fp32
  * accumulation promoted once per 128-deep K block, output bf16 (out_dtype
- * SGL_BF16) or fp32 (SGL_F32).  A e4m3 [M, K] contiguous, sa fp32 [M, K/128]
- * (e8m0 activation scales: convert with sgl_e8m0_to_f32 first), B e4m3 [N, K]
- * contiguous, sb [ceil(N/128), K/128] fp32, or one e8m0 byte per scale when
- * b_scale_e8m0 is set.  K % 128 == 0, N % 16 == 0, M*K and N*K < 2^31.
+ * SGL_BF16) or fp32 (SGL_F32).  A e4m3 [M, K] contiguous, sa [M, K/128] fp32,
+ * or one e8m0 byte per scale when a_scale_e8m0 is set (the reference's
+ * ue8m0 act_quant output, read as it is), B e4m3 [N, K] contiguous, sb
+ * [ceil(N/128), K/128] fp32, or one e8m0 byte per scale when b_scale_e8m0 is
+ * set.  K % 128 == 0, N % 16 == 0, M*K and N*K < 2^31.
  * Shapes for which sgl_fp8_gemm_workspace_size is non-zero (16 < M <= 64
  * with N % 128 == 0) split the K range over workgroups and keep the fp32
  * partials in the caller's workspace (16-byte aligned, at least that many
@@ -204,25 +205,28 @@ int sgl_mfma_mix_threads(void);
  * call-site adapter engine/v4_deep_gemm.py:169-218 fp4_gemm_nt (whose
  * workspace-free call the reference's adapter allocates with torch at
  * :186-188, as the caller does here). */
-int sgl_fp8_gemm(const void* a, const void* sa, const void* b, const void* sb, int b_scale_e8m0,
-                 void* c, int out_dtype, int64_t M, int64_t N, int64_t K, void* workspace,
-                 size_t workspace_bytes, sgl_stream_t stream);
+int sgl_fp8_gemm(const void* a, const void* sa, int a_scale_e8m0, const void* b, const void* sb,
+                 int b_scale_e8m0, void* c, int out_dtype, int64_t M, int64_t N, int64_t K,
+                 void* workspace, size_t workspace_bytes, sgl_stream_t stream);
 
 /* Workspace bytes sgl_fp8_gemm needs for an M x N x K product (0: none). */
 size_t sgl_fp8_gemm_workspace_size(int64_t M, int64_t N, int64_t K);
 
+/* Formats of the activation (row) scales of sgl_fp4_gemm. */
+#define SGL_ASCALE_F32 0      /* fp32, any value: each 128-deep partial promoted in fp32 */
+#define SGL_ASCALE_F32_POW2 1 /* fp32 powers of two (mantissa bits ignored): in the MFMA */
+#define SGL_ASCALE_E8M0 2     /* one e8m0 byte per scale: in the MFMA */
+
 /* C[M, N] = A_e4m3[M, K] . B_e2m1[N, K]^T with A scaled per (row, 128-deep K
  * block) by sa and B per (row, 32-deep K block) by sb; fp32 accumulation,
  * output bf16 (SGL_BF16) or fp32 (SGL_F32).  A e4m3 [M, K] contiguous, sa
- * fp32 [M, K/128] (e8m0 activation scales: convert with sgl_e8m0_to_f32
- * first), B packed e2m1 [N, K/2] (low nibble = even K), sb e8m0 [N, K/32].
- * The weight scales are applied inside the MFMA; the row scales too when
- * sa_pow2 != 0, which declares every sa entry a power of two (its mantissa
- * bits are then ignored), else each 128-deep partial is promoted with sa in
- * fp32.  K % 256 == 0, N % 16 == 0, M*K and N*K/2 < 2^31.
+ * [M, K/128] in the SGL_ASCALE_* format sa_format, B packed e2m1 [N, K/2]
+ * (low nibble = even K), sb e8m0 [N, K/32].  The weight scales are applied
+ * inside the MFMA; the row scales too unless sa_format is SGL_ASCALE_F32.
+ * K % 256 == 0, N % 16 == 0, M*K and N*K/2 < 2^31.
  * Replaces deepseek_infer/kernel.py:519-536 fp4_gemm (kernel :441-516) and
  * engine/v4_deep_gemm.py:169-218 fp4_gemm_nt (DeepGEMM fp8_fp4_gemm_nt). */
-int sgl_fp4_gemm(const void* a, const float* sa, int sa_pow2, const void* b, const void* sb,
+int sgl_fp4_gemm(const void* a, const void* sa, int sa_format, const void* b, const void* sb,
                  void* c, int out_dtype, int64_t M, int64_t N, int64_t K, sgl_stream_t stream);
 
 /* Lossless FP4 -> FP8 weight repack: per 128 x 128 block, s = (max of the

@@ -84,6 +84,14 @@ __device__ __forceinline__ void dma4(const uint8_t* base, uint32_t voff, uint32_
                :: "v"(voff), "s"(base), "s"(lds) : "memory");
 }
 
+// Lane i copies the byte at base + voff into LDS m0 + 4 i, zero-extended to a
+// dword (global_load_lds_ubyte; the lane layout checked on gfx950): e8m0
+// row scales land where fp32 ones would, as the integer 0..255.
+__device__ __forceinline__ void dma1(const uint8_t* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_ubyte %0, %1"
+               :: "v"(voff), "s"(base), "s"(lds) : "memory");
+}
+
 // The same with a per-lane 64-bit address (no scalar base): lane i copies 16
 // (dma16v) or 4 (dma4v) bytes from addr to LDS m0 + 16 i (4 i).
 __device__ __forceinline__ void dma16v(uint64_t addr, uint32_t lds) {
@@ -94,6 +102,10 @@ __device__ __forceinline__ void dma4v(uint64_t addr, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
                :: "v"(addr), "s"(lds) : "memory");
 }
+__device__ __forceinline__ void dma1v(uint64_t addr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_ubyte %0, off"
+               :: "v"(addr), "s"(lds) : "memory");
+}
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -102,6 +114,11 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 __device__ __forceinline__ float e8m0_value(uint32_t b) {
   return b == 0xFFu ? bits_f32(0x7FC00000u) : (b == 0 ? bits_f32(0x00400000u) : bits_f32(b << 23));
+}
+
+// a row scale as staged in LDS: fp32, or an e8m0 byte widened to a dword
+__device__ __forceinline__ float staged_scale(float v, int e8m0) {
+  return e8m0 ? e8m0_value(__float_as_uint(v)) : v;
 }
 
 __device__ __forceinline__ float load_scale(const void* s, int64_t idx, int e8m0) {
@@ -194,6 +211,7 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
                 HW = C::HW;
   constexpr int KS = C::KS;
   constexpr bool FP4 = WF == WF_FP4;
+  const int sa_e8 = KIND == KIND_DENSE ? args.sa_e8m0 : 0;  // e8m0 row scales (bytes)
 
   __shared__ __align__(16) uint8_t smem[C::SMEM];
   __shared__ int sTstart[KIND == KIND_DENSE ? 1 : kMaxGroups + 1];
@@ -420,7 +438,8 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
     for (int q = 0; q < C::SAI; ++q) {
       const int sa_row = (iw + q * C::IW) * C::SA_ROWS + sa_l % C::SA_ROWS;
       const int sa_src = sSrc[sa_row] >= 0 ? sSrc[sa_row] : src0;
-      sa_off[q] = (uint32_t)(((int64_t)sa_src * KB + sa_l / C::SA_ROWS) * 4);
+      // byte offsets of e8m0 scales (one byte each), else of fp32 ones
+      sa_off[q] = (uint32_t)(((int64_t)sa_src * KB + sa_l / C::SA_ROWS) * (sa_e8 ? 1 : 4));
     }
     const uint8_t* sa_base = uniform_ptr(args.sa);
     const uint32_t smem_lds = __builtin_amdgcn_readfirstlane(lds_u32(smem));
@@ -478,7 +497,11 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
       }
 #pragma unroll
       for (int q = 0; q < C::SAI; ++q)
-        dma4(sa_base, sa_off[q] + (uint32_t)st * (4u * KS),
+        if (sa_e8)
+          dma1(sa_base, sa_off[q] + (uint32_t)st * KS,
+               smem_lds + (uint32_t)(C::RING + sa_slot * C::SA_SLOT + (iw + q * C::IW) * 256));
+        else
+          dma4(sa_base, sa_off[q] + (uint32_t)st * (4u * KS),
              smem_lds + (uint32_t)(C::RING + sa_slot * C::SA_SLOT + (iw + q * C::IW) * 256));
     };
 
@@ -512,7 +535,7 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
       const float* tS = reinterpret_cast<const float*>(smem + C::RING + (st % C::NSA) * C::SA_SLOT);
       // row scale of tile row `row`, K step ks of the stage
       auto row_scale = [&](int row, int ks) -> float {
-        return tS[(row / C::SA_ROWS) * 64 + ks * C::SA_ROWS + row % C::SA_ROWS];
+        return staged_scale(tS[(row / C::SA_ROWS) * 64 + ks * C::SA_ROWS + row % C::SA_ROWS], sa_e8);
       };
 
       // a wavefront whose rows all lie past the tile's last row has no work
@@ -546,7 +569,7 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
             static_assert(C::SA_ROWS == 16, "row-scale slot layout");
             float sa1[TM];
 #pragma unroll
-            for (int mi = 0; mi < TM; ++mi) sa1[mi] = tS[(wm * TM + mi) * 64 + r16];
+            for (int mi = 0; mi < TM; ++mi) sa1[mi] = staged_scale(tS[(wm * TM + mi) * 64 + r16], sa_e8);
             float sbh[HALVES];
 #pragma unroll
             for (int hv = 0; hv < HALVES; ++hv) sbh[hv] = sSb[KIND == KIND_GATE_UP ? hv : wave_blk][kb];
@@ -2475,7 +2498,8 @@ __global__ __launch_bounds__(wide::NT) void gemm_wide_kernel(const GemmArgs args
     // == 0: chunks are wholly in or out) are not loaded: those rows only
     // feed outputs that are never stored
     const int sa_r = iw * 64 + lane;
-    const uint32_t sa_off = (uint32_t)((int64_t)(row0 + (sa_r < rows ? sa_r : rows - 1)) * KB * 4);
+    const int sa_e8 = args.sa_e8m0;  // e8m0 row scales: one byte each
+    const uint32_t sa_off = (uint32_t)((int64_t)(row0 + (sa_r < rows ? sa_r : rows - 1)) * KB * (sa_e8 ? 1 : 4));
     auto issue = [&](int st) {
       if (!issuer) return;
       const int s = (gst + st) & 1;
@@ -2495,7 +2519,10 @@ __global__ __launch_bounds__(wide::NT) void gemm_wide_kernel(const GemmArgs args
         const int64_t nrow = n0 + b * 8;
         if (nrow < N) dma16(baseB + (nrow * K + st * 128), lane_off, sl + (uint32_t)(A_BYTES + b * 1024));
       }
-      dma4(sa_base, sa_off + (uint32_t)st * 4u, smem_lds + (uint32_t)(RING + s * SA_SLOT + iw * 256));
+      if (sa_e8)
+        dma1(sa_base, sa_off + (uint32_t)st, smem_lds + (uint32_t)(RING + s * SA_SLOT + iw * 256));
+      else
+        dma4(sa_base, sa_off + (uint32_t)st * 4u, smem_lds + (uint32_t)(RING + s * SA_SLOT + iw * 256));
     };
     __syncthreads();  // sSb published
     issue(0);
@@ -2530,7 +2557,7 @@ __global__ __launch_bounds__(wide::NT) void gemm_wide_kernel(const GemmArgs args
         af[0] = read_frag(stg + (wm * TM) * 16 * 128, fl);
         bf[0] = read_frag(tB, fl);
 #pragma unroll
-        for (int mi = 0; mi < TM; ++mi) sa1[mi] = tS[(wm * TM + mi) * 16 + r16];
+        for (int mi = 0; mi < TM; ++mi) sa1[mi] = staged_scale(tS[(wm * TM + mi) * 16 + r16], sa_e8);
         const float sb = sSb[wn][st];
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -2709,14 +2736,13 @@ __global__ __launch_bounds__(64 * Skinny<TM>::WAVES) void gemm_skinny_kernel(con
   // after, so waiting for the scales (to stage them in LDS) leaves the
   // operand loads in flight: loads retire in issue order.
   constexpr int SPT = (ROWS * kMaxKB + 64 * kSkinnyWaves - 1) / (64 * kSkinnyWaves);
-  const float* sa = reinterpret_cast<const float*>(args.sa);
   float sv[SPT];
 #pragma unroll
   for (int j = 0; j < SPT; ++j) {
     const int i = tid + j * 64 * kSkinnyWaves;
     const int r = i / KB, kb = i - r * KB;
     const int64_t row = m0 + r;
-    sv[j] = (i < ROWS * KB && row < M) ? sa[row * KB + kb] : 0.0f;
+    sv[j] = (i < ROWS * KB && row < M) ? load_scale(args.sa, row * KB + kb, args.sa_e8m0) : 0.0f;
   }
   float skv = 0.0f;
   constexpr int BPT = FP4 ? (16 * kMaxKB + 64 * kSkinnyWaves - 1) / (64 * kSkinnyWaves) : 1;
@@ -2934,8 +2960,12 @@ __global__ __launch_bounds__(splitk::NT) void gemm_splitk_kernel(const GemmArgs 
       const int r = i / KS, kl = i - r * KS;
       const int64_t row = r < M ? r : M - 1;
       const int kb = kb0 + (kl < nkb ? kl : 0);
-      dma4v((uint64_t)(uintptr_t)args.sa + (uint64_t)(row * KB + kb) * 4u,
-            __builtin_amdgcn_readfirstlane(sa_lds + (uint32_t)(q * 256)));
+      if (args.sa_e8m0)  // e8m0 scales: one byte each, widened to a dword in LDS
+        dma1v((uint64_t)(uintptr_t)args.sa + (uint64_t)(row * KB + kb),
+              __builtin_amdgcn_readfirstlane(sa_lds + (uint32_t)(q * 256)));
+      else
+        dma4v((uint64_t)(uintptr_t)args.sa + (uint64_t)(row * KB + kb) * 4u,
+              __builtin_amdgcn_readfirstlane(sa_lds + (uint32_t)(q * 256)));
     }
   }
   const int64_t idx0 = (n0 / 128) * KB + kb0;
@@ -2976,7 +3006,8 @@ __global__ __launch_bounds__(splitk::NT) void gemm_splitk_kernel(const GemmArgs 
       for (int mi = 0; mi < TM; ++mi) {
         const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[mi], bf[kl], vzero, 0, 0, 0, 0, 0, 0);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[mi][r] = fmaf(p[r], sSa[(16 * mi + 4 * g4 + r) * KS + kl] * skb, acc[mi][r]);
+        for (int r = 0; r < 4; ++r)
+          acc[mi][r] = fmaf(p[r], staged_scale(sSa[(16 * mi + 4 * g4 + r) * KS + kl], args.sa_e8m0) * skb, acc[mi][r]);
       }
     }
   }
@@ -3229,9 +3260,9 @@ extern "C" size_t sgl_fp8_gemm_workspace_size(int64_t M, int64_t N, int64_t K) {
   return sgl::dense_fp8_workspace_bytes(M, N, K);
 }
 
-extern "C" int sgl_fp8_gemm(const void* a, const void* sa, const void* b, const void* sb,
-                            int b_scale_e8m0, void* c, int out_dtype, int64_t M, int64_t N,
-                            int64_t K, void* workspace, size_t workspace_bytes,
+extern "C" int sgl_fp8_gemm(const void* a, const void* sa, int a_scale_e8m0, const void* b,
+                            const void* sb, int b_scale_e8m0, void* c, int out_dtype, int64_t M,
+                            int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
                             sgl_stream_t stream) {
   SGL_REQUIRE(M >= 0 && N >= 0 && K >= 0, "fp8_gemm: negative shape");
   SGL_REQUIRE(out_dtype == SGL_BF16 || out_dtype == SGL_F32, "fp8_gemm: out_dtype must be bf16/f32");
@@ -3243,11 +3274,12 @@ extern "C" int sgl_fp8_gemm(const void* a, const void* sa, const void* b, const 
               "fp8_gemm: operands above 2 GiB are not supported");
   SGL_REQUIRE(sgl::aligned(a, 16) && sgl::aligned(b, 16) && sgl::aligned(c, 16),
               "fp8_gemm: A, B and C must be 16-byte aligned");
-  SGL_REQUIRE(sgl::aligned(sa, 4), "fp8_gemm: sa must be 4-byte aligned fp32");
+  SGL_REQUIRE(a_scale_e8m0 || sgl::aligned(sa, 4), "fp8_gemm: fp32 sa must be 4-byte aligned");
   SGL_REQUIRE(b_scale_e8m0 || sgl::aligned(sb, 4), "fp8_gemm: fp32 sb must be 4-byte aligned");
   sgl::GemmArgs g = {};
   g.a = (const uint8_t*)a;
   g.sa = sa;
+  g.sa_e8m0 = a_scale_e8m0 ? 1 : 0;
   g.b = (const uint8_t*)b;
   g.sb = sb;
   g.sb_e8m0 = b_scale_e8m0;
@@ -3261,7 +3293,7 @@ extern "C" int sgl_fp8_gemm(const void* a, const void* sa, const void* b, const 
   return sgl::launch_gemm(sgl::KIND_DENSE, g, M, (hipStream_t)stream);
 }
 
-extern "C" int sgl_fp4_gemm(const void* a, const float* sa, int sa_pow2, const void* b,
+extern "C" int sgl_fp4_gemm(const void* a, const void* sa, int sa_format, const void* b,
                             const void* sb, void* c, int out_dtype, int64_t M, int64_t N,
                             int64_t K, sgl_stream_t stream) {
   SGL_REQUIRE(M >= 0 && N >= 0 && K >= 0, "fp4_gemm: negative shape");
@@ -3274,14 +3306,19 @@ extern "C" int sgl_fp4_gemm(const void* a, const float* sa, int sa_pow2, const v
               "fp4_gemm: operands above 2 GiB are not supported");
   SGL_REQUIRE(sgl::aligned(a, 16) && sgl::aligned(b, 16) && sgl::aligned(c, 16),
               "fp4_gemm: A, B and C must be 16-byte aligned");
-  SGL_REQUIRE(sgl::aligned(sa, 4) && sgl::aligned(sb, 4), "fp4_gemm: sa and sb must be 4-byte aligned");
+  SGL_REQUIRE(sa_format >= SGL_ASCALE_F32 && sa_format <= SGL_ASCALE_E8M0,
+              "fp4_gemm: sa_format=%d is not an SGL_ASCALE_* value", sa_format);
+  SGL_REQUIRE((sa_format == SGL_ASCALE_E8M0 || sgl::aligned(sa, 4)) && sgl::aligned(sb, 4),
+              "fp4_gemm: fp32 sa and sb must be 4-byte aligned");
   sgl::GemmArgs g = {};
   g.a = (const uint8_t*)a;
   g.sa = sa;
   g.b = (const uint8_t*)b;
   g.sb = sb;
   g.wfmt = sgl::WF_FP4;
-  g.sa_pow2 = sa_pow2 ? 1 : 0;
+  // e8m0 row scales are powers of two: applied inside the MFMA
+  g.sa_pow2 = sa_format != SGL_ASCALE_F32 ? 1 : 0;
+  g.sa_e8m0 = sa_format == SGL_ASCALE_E8M0 ? 1 : 0;
   g.M = M;
   g.N = N;
   g.K = K;

@@ -22,10 +22,11 @@ enum WeightFmt : int { WF_FP8 = 0, WF_FP4 = 1 };
 //             to the token-major output of sgl_moe_down.
 struct GemmArgs {
   const uint8_t* a;   // dense: A [M, K]; gate_up: xq [T, K]; down: hq [rows, K]
-  const void* sa;     // fp32 row scales [*, K/128]
+  const void* sa;     // row scales [*, K/128]: fp32, or e8m0 bytes (dense, sa_e8m0)
   const uint8_t* b;   // dense only: B [N, K]
   const void* sb;     // dense only: fp8 [ceil(N/128), K/128]; fp4 e8m0 [N, K/32]
   int sb_e8m0;
+  int sa_e8m0;        // dense only: sa holds e8m0 bytes (DMA'd as bytes, widened in LDS)
   int wfmt;           // WeightFmt of B (moe: of every expert in the launch)
   int sa_pow2;        // activation scales are powers of two: applied inside the MFMA
   int sb_pow2;        // fp8 weight scales (fp32) are powers of two: with sa_pow2, both

@@ -28,6 +28,8 @@ SGL_ERR_WORKSPACE = -4
 
 # sgl_dtype
 SGL_BF16, SGL_F16, SGL_F32 = 0, 1, 2
+# activation-scale formats of sgl_fp4_gemm (SGL_ASCALE_*)
+ASCALE_F32, ASCALE_F32_POW2, ASCALE_E8M0 = 0, 1, 2
 # sgl_scale_mode
 SCALE_TORCH_FP32 = 0
 SCALE_TORCH_UE8M0 = 1
@@ -60,7 +62,7 @@ SIGNATURES = {
     "sgl_hbm_stream": (c_int, [P, P, I64, P, P]),
     "sgl_mfma_mix": (c_int, [c_int, P, I64, P]),
     "sgl_mfma_mix_threads": (c_int, []),
-    "sgl_fp8_gemm": (c_int, [P, P, P, P, c_int, P, c_int, I64, I64, I64, P, c_size_t, P]),
+    "sgl_fp8_gemm": (c_int, [P, P, c_int, P, P, c_int, P, c_int, I64, I64, I64, P, c_size_t, P]),
     "sgl_fp8_gemm_workspace_size": (c_size_t, [I64, I64, I64]),
     "sgl_fp4_gemm": (c_int, [P, P, c_int, P, P, P, c_int, I64, I64, I64, P]),
     "sgl_fp4_to_fp8_weight": (c_int, [P, P, I64, I64, P, P, P]),

@@ -199,8 +199,6 @@ def fp8_gemm(
         out = a.new_empty(*a.size()[:-1], N, dtype=odt)
     else:
         assert out.is_contiguous() and out.dtype == odt and out.numel() == M * N
-    if _scale_flag(a_s, "fp8_gemm a_s"):
-        a_s = e8m0_to_f32(a_s)  # the kernel streams fp32 activation scales
     # split-K shapes keep their fp32 partials in a workspace allocated here with
     # torch (inside a graph capture it comes from the graph's pool), as the
     # reference's adapter allocates its output (engine/v4_deep_gemm.py:186-188)
@@ -208,7 +206,7 @@ def fp8_gemm(
     ws = torch.empty(nws, dtype=torch.uint8, device=a.device) if nws else None
     _lib.call(
         "sgl_fp8_gemm",
-        a.data_ptr(), a_s.data_ptr(), b.data_ptr(), b_s.data_ptr(),
+        a.data_ptr(), a_s.data_ptr(), _scale_flag(a_s, "fp8_gemm a_s"), b.data_ptr(), b_s.data_ptr(),
         _scale_flag(b_s, "fp8_gemm b_s"),
         out.data_ptr(), _lib.SGL_BF16 if odt == torch.bfloat16 else _lib.SGL_F32,
         M, N, K, _lib.ptr(ws), nws, _lib.stream_of(a),
@@ -270,13 +268,14 @@ def fp4_gemm(
         out = a.new_empty(*a.size()[:-1], N, dtype=odt)
     else:
         assert out.is_contiguous() and out.dtype == odt and out.numel() == M * N
-    pow2 = bool(a_scale_pow2) if a_scale_pow2 is not None else a_s.dtype == E8M0
     if _scale_flag(a_s, "fp4_gemm a_s"):
-        a_s = e8m0_to_f32(a_s)  # the kernel streams fp32 activation scales
+        fmt = _lib.ASCALE_E8M0  # read as bytes, applied in the MFMA
+    else:
+        fmt = _lib.ASCALE_F32_POW2 if a_scale_pow2 else _lib.ASCALE_F32
     bs = fp4_weight_scale(b_s)
     _lib.call(
         "sgl_fp4_gemm",
-        a.data_ptr(), a_s.data_ptr(), int(pow2), bq.data_ptr(), bs.data_ptr(),
+        a.data_ptr(), a_s.data_ptr(), fmt, bq.data_ptr(), bs.data_ptr(),
         out.data_ptr(), _lib.SGL_BF16 if odt == torch.bfloat16 else _lib.SGL_F32,
         M, N, K, _lib.stream_of(a),
     )

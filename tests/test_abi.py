@@ -155,7 +155,7 @@ def test_invalid_arguments_map_to_value_error_without_launch():
     assert "divisible" in L.last_error()
     with pytest.raises(ValueError, match="group"):
         L.call("sgl_act_quant", None, 4, 128, 128, None, 128, None, 1, 96, 0, 0, 0, None)
-    rc = lib.sgl_fp8_gemm(None, None, None, None, 0, None, 0, 4, 100, 256, None, 0, None)
+    rc = lib.sgl_fp8_gemm(None, None, 0, None, None, 0, None, 0, 4, 100, 256, None, 0, None)
     assert rc == L.SGL_ERR_INVALID_ARG and "multiple of 16" in L.last_error()
     rc = lib.sgl_hbm_stream(None, None, 1000, None, None)
     assert rc == L.SGL_ERR_INVALID_ARG and "multiple of 32768" in L.last_error()
@@ -250,6 +250,6 @@ def test_fp8_gemm_split_decision_is_a_function_of_the_shape():
     fake = 1 << 20  # aligned, never read: the workspace check comes first
     need = ws(40, 4096, 7168)
     for buf, n in ((None, 0), (fake, need - 16)):
-        rc = lib.sgl_fp8_gemm(fake, fake, fake, fake, 0, fake, 0, 40, 4096, 7168, buf, n, None)
+        rc = lib.sgl_fp8_gemm(fake, fake, 0, fake, fake, 0, fake, 0, 40, 4096, 7168, buf, n, None)
         assert rc == L.SGL_ERR_WORKSPACE, rc
         assert str(need) in L.last_error()

@@ -60,7 +60,7 @@ def test_fp4_gemm_matches_oracle(gpu, M, N, K, pow2):
     assert_gemm_close(f32(c), ref, f"fp4_gemm {M}x{N}x{K} pow2={pow2}")
 
 
-@pytest.mark.parametrize("M", [8, 200, 2100])
+@pytest.mark.parametrize("M", [8, 40, 200, 600, 2100])
 def test_fp4_gemm_fp32_out_tracks_the_blocked_structure(gpu, M):
     """fp32 output against the reference kernel's own accumulation order
     (kernel.py:485-513) with e8m0 activation scales (the live scale_dtype):
@@ -73,6 +73,10 @@ def test_fp4_gemm_fp32_out_tracks_the_blocked_structure(gpu, M):
     c = _gemm(gpu, aq, sa_e8m0, bp, sb, out_dtype=torch.float32)
     assert c.dtype == torch.float32
     np.testing.assert_allclose(f32(c), ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
+    # the e8m0 bytes, read by the kernel itself, give what the same powers of
+    # two given as fp32 give
+    c32 = _gemm(gpu, aq, to_dev_f32(sa, gpu), bp, sb, out_dtype=torch.float32, a_scale_pow2=True)
+    assert torch.equal(c, c32)
 
 
 def test_fp4_gemm_accepts_fp32_weight_scales_and_3d_input(gpu):

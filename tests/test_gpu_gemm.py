@@ -80,6 +80,34 @@ def test_fp8_gemm_e8m0_scales(gpu):
     assert_gemm_close(f32(c), ref, "fp8_gemm e8m0")
 
 
+@pytest.mark.parametrize("M,N,K", [(16, 256, 1024), (40, 4096, 7168), (128, 384, 1024),
+                                   (300, 256, 1024), (1024, 512, 2048), (2100, 512, 1024)])
+def test_fp8_gemm_reads_e8m0_activation_scales_as_bytes(gpu, M, N, K):
+    """The live format (model.py:138-142,777-778: act_quant with ue8m0 e8m0
+    scales, e8m0 weight scales) without a conversion launch: every dense
+    kernel (skinny M <= 16, split-K 16 < M <= 64, 32 x 64 / 32 x 128 /
+    64 x 128 / 128 x 128 tiles, 256 x 256 tiles above M = 2048) reads the
+    activation scale bytes itself, so its output equals the fp32-scale call
+    bit for bit (the same powers of two, promoted in the same order) and the
+    oracle within the GEMM bound."""
+    from sglang_lite_amd import kernel as K_
+
+    print(f"fp8_gemm e8m0 activations M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M + 7 * N)
+    a = bf16_values(rng, (M, K))
+    aq, sa = Q.per_token_cast_to_fp8(a, True, 128)
+    b = (rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+    bq, sb = Q.per_block_cast_to_fp8(b, True)
+    sa_e = torch.from_numpy(Q.e8m0_byte(sa)).view(torch.float8_e8m0fnu).to(gpu)
+    sb_e = torch.from_numpy(Q.e8m0_byte(sb)).view(torch.float8_e8m0fnu).to(gpu)
+    aqd, bqd = to_dev_fp8(aq, gpu), to_dev_fp8(bq, gpu)
+    c8 = K_.fp8_gemm(aqd, sa_e, bqd, sb_e)
+    c32 = K_.fp8_gemm(aqd, torch.from_numpy(sa).to(gpu), bqd, sb_e)
+    torch.cuda.synchronize()
+    assert torch.equal(c8, c32)
+    assert_gemm_close(f32(c8), OM.fp8_gemm(aq, sa, bq, sb, out_bf16=False), f"fp8_gemm e8m0 a {M}")
+
+
 def test_fp8_gemm_end_to_end_from_bf16(gpu):
     """act_quant -> fp8_gemm (model.py:116-118 linear()) against the oracle of
     the same pipeline, at the dense config's K and N."""
