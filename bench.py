@@ -842,6 +842,31 @@ def main():
                               "hbm_frac": round(byt / msg / 1e6 / PEAK_HBM_GBS, 4)})
                 log(f"dense M={Md}: {msg * 1e3:.1f} us back to back ({mse * 1e3:.1f} us single call)")
             del wsets
+            # the live format (model.py:138-142,777-778): e8m0 weight scales and
+            # ue8m0 act_quant scales as e8m0 bytes, read by the GEMM as they are;
+            # the tiled kernels apply both inside the MFMA
+            bq8, bs8f = K.per_block_cast_to_fp8(torch.randn(4096, 7168, generator=gw, device=dev) * 0.02,
+                                                True)
+            bs8 = (bs8f.view(torch.int32) >> 23).to(torch.uint8).view(torch.float8_e8m0fnu)
+            wsets = [(bq8.clone(), bs8.clone()) for _ in range(12)]
+            live = []
+            for Md in (16, 128, 1024, 4096):
+                a = torch.randn(Md, 7168, generator=gw, device=dev).to(torch.bfloat16)
+                aq, as8 = K.act_quant(a, 128, "ue8m0", torch.float8_e8m0fnu)
+                c = torch.empty(Md, 4096, dtype=torch.bfloat16, device=dev)
+                for _ in range(2):
+                    K.fp8_gemm(aq, as8, bq8, bs8, out=c)
+                msg = replay_ms(torch, [lambda w=w: K.fp8_gemm(aq, as8, w[0], w[1], out=c) for w in wsets])
+                fl = 2.0 * Md * 4096 * 7168
+                byt = Md * 7168 + Md * 56 + 4096 * 7168 + 32 * 56 + 2 * Md * 4096
+                live.append({"M": Md, "N": 4096, "K": 7168, "ms": round(msg, 5),
+                             "tflops": round(fl / msg / 1e9, 2),
+                             "mfma_frac": round(fl / msg / 1e9 / PEAK_FP8_TFLOPS, 4),
+                             "gbs": round(byt / msg / 1e6, 1),
+                             "hbm_frac": round(byt / msg / 1e6 / PEAK_HBM_GBS, 4)})
+                log(f"dense e8m0 scales M={Md}: {msg * 1e3:.1f} us back to back")
+            del wsets
+            extra["dense_gemm_live_e8m0"] = live
             # act_quant alone at the largest dense shape, 6 rotating inputs (352 MB)
             xs6 = [torch.randn(4096, 7168, generator=gw, device=dev).to(torch.bfloat16) for _ in range(6)]
             msq = replay_ms(torch, [lambda x=x: K.act_quant(x) for x in xs6])

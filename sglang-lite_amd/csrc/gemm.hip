@@ -84,14 +84,6 @@ __device__ __forceinline__ void dma4(const uint8_t* base, uint32_t voff, uint32_
                :: "v"(voff), "s"(base), "s"(lds) : "memory");
 }
 
-// Lane i copies the byte at base + voff into LDS m0 + 4 i, zero-extended to a
-// dword (global_load_lds_ubyte; the lane layout checked on gfx950): e8m0
-// row scales land where fp32 ones would, as the integer 0..255.
-__device__ __forceinline__ void dma1(const uint8_t* base, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_ubyte %0, %1"
-               :: "v"(voff), "s"(base), "s"(lds) : "memory");
-}
-
 // The same with a per-lane 64-bit address (no scalar base): lane i copies 16
 // (dma16v) or 4 (dma4v) bytes from addr to LDS m0 + 16 i (4 i).
 __device__ __forceinline__ void dma16v(uint64_t addr, uint32_t lds) {
@@ -102,10 +94,7 @@ __device__ __forceinline__ void dma4v(uint64_t addr, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
                :: "v"(addr), "s"(lds) : "memory");
 }
-__device__ __forceinline__ void dma1v(uint64_t addr, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_ubyte %0, off"
-               :: "v"(addr), "s"(lds) : "memory");
-}
+
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -116,10 +105,7 @@ __device__ __forceinline__ float e8m0_value(uint32_t b) {
   return b == 0xFFu ? bits_f32(0x7FC00000u) : (b == 0 ? bits_f32(0x00400000u) : bits_f32(b << 23));
 }
 
-// a row scale as staged in LDS: fp32, or an e8m0 byte widened to a dword
-__device__ __forceinline__ float staged_scale(float v, int e8m0) {
-  return e8m0 ? e8m0_value(__float_as_uint(v)) : v;
-}
+
 
 __device__ __forceinline__ float load_scale(const void* s, int64_t idx, int e8m0) {
   if (e8m0) return e8m0_value(reinterpret_cast<const uint8_t*>(s)[idx]);
@@ -201,7 +187,7 @@ struct Cfg {
   static_assert(LW > 0 || (KIND == KIND_GATE_UP ? BM * HALF * 2 <= RING : BM * BN * 4 <= RING),
                 "epilogue staging must fit in the stage ring");
   static_assert(NSTAGE >= 2 && NSTAGE <= 6, "stages");
-  static_assert(WF == WF_FP4 || !SAHW, "in-MFMA activation scales are an FP4-weight path");
+  static_assert(WF == WF_FP4 || !SAHW || KIND == KIND_DENSE, "e8m0 activation scales: dense only");
 };
 
 template <int KIND, int BM, int BN, int WM, int WN, int NSTAGE, int WF, bool SAHW, int LW>
@@ -211,7 +197,12 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
                 HW = C::HW;
   constexpr int KS = C::KS;
   constexpr bool FP4 = WF == WF_FP4;
-  const int sa_e8 = KIND == KIND_DENSE ? args.sa_e8m0 : 0;  // e8m0 row scales (bytes)
+  // SAHW: FP4 weights, power-of-two row scales applied inside the MFMA
+  // (fp32, or e8m0 bytes when sa_e8m0); FP8 weights (dense), e8m0 row scales
+  // as bytes, with e8m0 weight scales both applied inside the MFMA, else
+  // promoted in fp32.  The other instantiations read fp32 row scales.
+  const int sa_e8 = SAHW ? (FP4 ? args.sa_e8m0 : 1) : 0;
+  const bool pow2 = KIND == KIND_DENSE && !FP4 && SAHW && args.sb_e8m0;
 
   __shared__ __align__(16) uint8_t smem[C::SMEM];
   __shared__ int sTstart[KIND == KIND_DENSE ? 1 : kMaxGroups + 1];
@@ -497,8 +488,8 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
       }
 #pragma unroll
       for (int q = 0; q < C::SAI; ++q)
-        if (sa_e8)
-          dma1(sa_base, sa_off[q] + (uint32_t)st * KS,
+        if (sa_e8)  // the aligned dword holding the byte
+          dma4(sa_base, (sa_off[q] + (uint32_t)st * KS) & ~3u,
                smem_lds + (uint32_t)(C::RING + sa_slot * C::SA_SLOT + (iw + q * C::IW) * 256));
         else
           dma4(sa_base, sa_off[q] + (uint32_t)st * (4u * KS),
@@ -534,8 +525,19 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
       const uint8_t* tB = stg + C::A_BYTES;
       const float* tS = reinterpret_cast<const float*>(smem + C::RING + (st % C::NSA) * C::SA_SLOT);
       // row scale of tile row `row`, K step ks of the stage
-      auto row_scale = [&](int row, int ks) -> float {
-        return staged_scale(tS[(row / C::SA_ROWS) * 64 + ks * C::SA_ROWS + row % C::SA_ROWS], sa_e8);
+      auto row_scale = [&](int row, int ks) -> float {  // fp32 row scales
+        return tS[(row / C::SA_ROWS) * 64 + ks * C::SA_ROWS + row % C::SA_ROWS];
+      };
+      // SAHW: the row scale's exponent, for the MFMA's scale operand: the
+      // e8m0 byte (source row) KB + K step of the scale tensor, taken from
+      // the aligned dword the DMA staged (dense rows past the tile's last
+      // read the tile's first; their outputs are dropped), or the exponent
+      // field of a power-of-two fp32 scale
+      auto row_exp = [&](int row, int ks) -> int {
+        const uint32_t raw = __float_as_uint(row_scale(row, ks));
+        if (!sa_e8) return (int)(raw >> 23);
+        const int src = row0 + (row < rows ? row : 0);
+        return (int)((raw >> (((uint32_t)(src * KB + st * KS + ks) & 3u) * 8u)) & 0xFFu);
       };
 
       // a wavefront whose rows all lie past the tile's last row has no work
@@ -569,7 +571,7 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
             static_assert(C::SA_ROWS == 16, "row-scale slot layout");
             float sa1[TM];
 #pragma unroll
-            for (int mi = 0; mi < TM; ++mi) sa1[mi] = staged_scale(tS[(wm * TM + mi) * 64 + r16], sa_e8);
+            for (int mi = 0; mi < TM; ++mi) sa1[mi] = tS[(wm * TM + mi) * 64 + r16];  // fp32 (grouped)
             float sbh[HALVES];
 #pragma unroll
             for (int hv = 0; hv < HALVES; ++hv) sbh[hv] = sSb[KIND == KIND_GATE_UP ? hv : wave_blk][kb];
@@ -599,6 +601,45 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
             const int kb = st;
             const float sbv0 = sSb[wave_blk][kb];
             const float sbv1 = KIND == KIND_GATE_UP ? sSb[1][kb] : 0.0f;
+            if constexpr (KIND == KIND_DENSE && SAHW) {
+              // e8m0 row scales: the exponent goes into the MFMA (activation
+              // rows = operand A, lane r16's row), exact for a power of two.
+              // e8m0 weight scales too (operand B, one per wavefront's
+              // 128-column block): the MFMA accumulates in place, no
+              // promotion; fp32 weight scales: C += P' sb, which is the
+              // promotion's C += P (sa sb) to the bit
+              int sae[TM];
+#pragma unroll
+              for (int mi = 0; mi < TM; ++mi) sae[mi] = row_exp((wm * TM + mi) * 16 + r16, 0);
+              v8i bf[2];
+              bf[0] = read_frag(tB + tile_col(0) * 128, fl);
+              if (pow2) {
+                const int sbe = (int)(__float_as_uint(sbv0) >> 23);
+#pragma unroll
+                for (int nj = 0; nj < TN; ++nj) {
+                  if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + tile_col(nj + 1) * 128, fl);
+#pragma unroll
+                  for (int mi = 0; mi < TM; ++mi)
+                    acc[mi][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        af[mi], bf[nj & 1], acc[mi][nj], 0, 0, 0, sae[mi], 0, sbe);
+                }
+              } else {
+#pragma unroll
+                for (int nj = 0; nj < TN; ++nj) {
+                  if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + tile_col(nj + 1) * 128, fl);
+                  v4f pr[TM];
+#pragma unroll
+                  for (int mi = 0; mi < TM; ++mi)
+                    pr[mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[mi], bf[nj & 1], vzero, 0, 0,
+                                                                              0, sae[mi], 0, 127);
+#pragma unroll
+                  for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[mi][nj][r] = fmaf(pr[mi][r], sbv0, acc[mi][nj][r]);
+                }
+              }
+              continue;
+            }
             float sav[TM][4];
 #pragma unroll
             for (int mi = 0; mi < TM; ++mi)
@@ -657,8 +698,7 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
               // scales are applied inside the MFMA, which accumulates in place
               int sae[TM];
 #pragma unroll
-              for (int mi = 0; mi < TM; ++mi)
-                sae[mi] = (int)(__float_as_uint(row_scale((wm * TM + mi) * 16 + r16, ks)) >> 23);
+              for (int mi = 0; mi < TM; ++mi) sae[mi] = row_exp((wm * TM + mi) * 16 + r16, ks);
 #pragma unroll
               for (int nj = 0; nj < TN; ++nj) {
                 if (nj + 1 < TN) {
@@ -2439,7 +2479,12 @@ static_assert(IW * 64 == BM, "one row-scale DMA per issuer and stage");
 static_assert(TN * 16 == 128, "a wavefront's columns are one 128-column weight-scale block");
 }  // namespace wide
 
+// SAF: the scale formats, one instantiation each (their register allocations
+// stay apart): 0 fp32 row scales, promoted; 1 e8m0 row scales (bytes),
+// promoted; 2 e8m0 row and weight scales, both applied inside the MFMA
+template <int SAF>
 __global__ __launch_bounds__(wide::NT) void gemm_wide_kernel(const GemmArgs args) {
+  constexpr bool POW2 = SAF == 2;
   using namespace wide;
   __shared__ __align__(16) uint8_t smem[SMEM];
   __shared__ float sSb[2][kMaxKB];  // the tile's weight scales: column block j, K block kb
@@ -2498,7 +2543,7 @@ __global__ __launch_bounds__(wide::NT) void gemm_wide_kernel(const GemmArgs args
     // == 0: chunks are wholly in or out) are not loaded: those rows only
     // feed outputs that are never stored
     const int sa_r = iw * 64 + lane;
-    const int sa_e8 = args.sa_e8m0;  // e8m0 row scales: one byte each
+    constexpr bool sa_e8 = SAF != 0;  // e8m0 row scales: the aligned dwords that hold them
     const uint32_t sa_off = (uint32_t)((int64_t)(row0 + (sa_r < rows ? sa_r : rows - 1)) * KB * (sa_e8 ? 1 : 4));
     auto issue = [&](int st) {
       if (!issuer) return;
@@ -2519,8 +2564,8 @@ __global__ __launch_bounds__(wide::NT) void gemm_wide_kernel(const GemmArgs args
         const int64_t nrow = n0 + b * 8;
         if (nrow < N) dma16(baseB + (nrow * K + st * 128), lane_off, sl + (uint32_t)(A_BYTES + b * 1024));
       }
-      if (sa_e8)
-        dma1(sa_base, sa_off + (uint32_t)st, smem_lds + (uint32_t)(RING + s * SA_SLOT + iw * 256));
+      if (sa_e8)  // the aligned dword holding the byte
+        dma4(sa_base, (sa_off + (uint32_t)st) & ~3u, smem_lds + (uint32_t)(RING + s * SA_SLOT + iw * 256));
       else
         dma4(sa_base, sa_off + (uint32_t)st * 4u, smem_lds + (uint32_t)(RING + s * SA_SLOT + iw * 256));
     };
@@ -2557,12 +2602,49 @@ __global__ __launch_bounds__(wide::NT) void gemm_wide_kernel(const GemmArgs args
         af[0] = read_frag(stg + (wm * TM) * 16 * 128, fl);
         bf[0] = read_frag(tB, fl);
 #pragma unroll
-        for (int mi = 0; mi < TM; ++mi) sa1[mi] = staged_scale(tS[(wm * TM + mi) * 16 + r16], sa_e8);
+        for (int mi = 0; mi < TM; ++mi) sa1[mi] = tS[(wm * TM + mi) * 16 + r16];
         const float sb = sSb[wn][st];
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int mi = 1; mi < TM; ++mi) af[mi] = read_frag(stg + (wm * TM + mi) * 16 * 128, fl);
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (sa_e8) {
+          // e8m0 row scales: the byte (source row) KB + st of the scale
+          // tensor, from the aligned dword the DMA staged, is the exponent
+          // the MFMA takes (activation rows = operand B, lane r16's row).
+          // SAF 2: the weight scale's too (operand A, one per wavefront),
+          // accumulating in place; SAF 1: C += P' sb, which is the
+          // promotion's C += P (sa sb) to the bit
+          int sae[TM];
+#pragma unroll
+          for (int mi = 0; mi < TM; ++mi) {
+            const int row = (wm * TM + mi) * 16 + r16;
+            const int src = row0 + (row < rows ? row : rows - 1);
+            sae[mi] = (int)((__float_as_uint(sa1[mi]) >> (((uint32_t)(src * KB + st) & 3u) * 8u)) & 0xFFu);
+          }
+          const int sbe = POW2 ? (int)(__float_as_uint(sb) >> 23) : 127;
+#pragma unroll
+          for (int nj = 0; nj < TN; ++nj) {
+            if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + (nj + 1) * 16 * 128, fl);
+            if constexpr (POW2) {
+#pragma unroll
+              for (int mi = 0; mi < TM; ++mi)
+                acc[mi][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[nj & 1], af[mi], acc[mi][nj],
+                                                                               0, 0, 0, sbe, 0, sae[mi]);
+            } else {
+              v4f pr[TM];
+#pragma unroll
+              for (int mi = 0; mi < TM; ++mi)
+                pr[mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[nj & 1], af[mi], vzero, 0, 0, 0,
+                                                                          sbe, 0, sae[mi]);
+#pragma unroll
+              for (int mi = 0; mi < TM; ++mi)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[mi][nj][r] = fmaf(pr[mi][r], sb, acc[mi][nj][r]);
+            }
+          }
+          continue;
+        }
         float ss[TM];
 #pragma unroll
         for (int mi = 0; mi < TM; ++mi) ss[mi] = sa1[mi] * sb;
@@ -2624,7 +2706,12 @@ int launch_wide(GemmArgs& a, hipStream_t stream) {
   const int64_t need = (tiles + 7) / 8 * 8;
   if (need < wgs) wgs = need;
   a.m_tiles = (int)mt;
-  gemm_wide_kernel<<<(unsigned)wgs, NT, 0, stream>>>(a);
+  if (a.sa_e8m0 && a.sb_e8m0)
+    gemm_wide_kernel<2><<<(unsigned)wgs, NT, 0, stream>>>(a);
+  else if (a.sa_e8m0)
+    gemm_wide_kernel<1><<<(unsigned)wgs, NT, 0, stream>>>(a);
+  else
+    gemm_wide_kernel<0><<<(unsigned)wgs, NT, 0, stream>>>(a);
   return check_launch("gemm_wide");
 }
 
@@ -2960,8 +3047,8 @@ __global__ __launch_bounds__(splitk::NT) void gemm_splitk_kernel(const GemmArgs 
       const int r = i / KS, kl = i - r * KS;
       const int64_t row = r < M ? r : M - 1;
       const int kb = kb0 + (kl < nkb ? kl : 0);
-      if (args.sa_e8m0)  // e8m0 scales: one byte each, widened to a dword in LDS
-        dma1v((uint64_t)(uintptr_t)args.sa + (uint64_t)(row * KB + kb),
+      if (args.sa_e8m0)  // e8m0 scales: the aligned dword holding the byte
+        dma4v((uint64_t)(uintptr_t)args.sa + (uint64_t)((row * KB + kb) & ~(int64_t)3),
               __builtin_amdgcn_readfirstlane(sa_lds + (uint32_t)(q * 256)));
       else
         dma4v((uint64_t)(uintptr_t)args.sa + (uint64_t)(row * KB + kb) * 4u,
@@ -3002,12 +3089,30 @@ __global__ __launch_bounds__(splitk::NT) void gemm_splitk_kernel(const GemmArgs 
       v8i af[TM];
 #pragma unroll
       for (int mi = 0; mi < TM; ++mi) af[mi] = read_frag(sA + (kl * TM + mi) * 2048, fl);
+      if (args.sa_e8m0) {
+        // e8m0 row scales: the byte (source row) KB + kb of the scale tensor,
+        // from the aligned dword the DMA staged, is the exponent the MFMA
+        // takes (activation rows = operand A, lane r16's row; rows past M
+        // read row M - 1, dropped); C += P' sb is the promotion's
+        // C += P (sa sb) to the bit
+#pragma unroll
+        for (int mi = 0; mi < TM; ++mi) {
+          const int row = 16 * mi + r16;
+          const int src = row < M ? row : (int)M - 1;
+          const int sae = (int)((__float_as_uint(sSa[row * KS + kl]) >>
+                                 (((uint32_t)(src * KB + kb0 + kl) & 3u) * 8u)) & 0xFFu);
+          const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[mi], bf[kl], vzero, 0, 0, 0, sae, 0,
+                                                                         127);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[mi][r] = fmaf(p[r], skb, acc[mi][r]);
+        }
+        continue;
+      }
 #pragma unroll
       for (int mi = 0; mi < TM; ++mi) {
         const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[mi], bf[kl], vzero, 0, 0, 0, 0, 0, 0);
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          acc[mi][r] = fmaf(p[r], staged_scale(sSa[(16 * mi + 4 * g4 + r) * KS + kl], args.sa_e8m0) * skb, acc[mi][r]);
+        for (int r = 0; r < 4; ++r) acc[mi][r] = fmaf(p[r], sSa[(16 * mi + 4 * g4 + r) * KS + kl] * skb, acc[mi][r]);
       }
     }
   }
@@ -3170,6 +3275,20 @@ int launch_fp4(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
   }
 }
 
+// The tiled dense FP8 kernels above the skinny / split-K sizes (SAHW: e8m0
+// row scales; the tile choice is explained in launch_gemm).  M = 2049 with
+// 256 x 256 tiles in 27 us where 128 x 256 tiles take 33; 128 x 128 with 8
+// wavefronts (the issuer split) from M = 512: M = 1024 in 52 us where
+// 64 x 128 tiles take 64 us.
+template <bool SAHW>
+int launch_dense_tiles(GemmArgs& a, hipStream_t stream) {
+  if (a.M <= 128) return launch_cfg<KIND_DENSE, 32, 64, 1, 4, 4, WF_FP8, SAHW>(a, stream);
+  if (a.M <= 256) return launch_cfg<KIND_DENSE, 32, 128, 1, 4, 4, WF_FP8, SAHW>(a, stream);
+  if (a.M <= 512) return launch_cfg<KIND_DENSE, 64, 128, 2, 2, 3, WF_FP8, SAHW>(a, stream);
+  if (a.M <= 2048) return launch_cfg<KIND_DENSE, 128, 128, 2, 4, 3, WF_FP8, SAHW>(a, stream);
+  return launch_wide(a, stream);  // 256 x 256 tiles (K <= 16384 by the check in launch_gemm)
+}
+
 int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
   if (a.K > 128 * kMaxKB) {
     set_error("gemm: K=%lld above the supported %d", (long long)a.K, 128 * kMaxKB);
@@ -3226,15 +3345,10 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       // M = 128 takes 23 us with 32 x 64 tiles, 39 us with 64 x 128, 36 us
       // with the skinny kernel's 128-row tiles (every workgroup re-reads all
       // of A from L2)
-      if (a.M <= 128) return launch_cfg<KIND_DENSE, 32, 64, 1, 4, 4>(a, stream);
-      if (a.M <= 256) return launch_cfg<KIND_DENSE, 32, 128, 1, 4, 4>(a, stream);
-      if (a.M <= 512) return launch_cfg<KIND_DENSE, 64, 128, 2, 2, 3>(a, stream);
-      // 128 x 128 with 8 wavefronts (the issuer split) from M = 512: M = 1024
-      // in 52 us where 64 x 128 tiles take 64 us
-      if (a.M <= 2048) return launch_cfg<KIND_DENSE, 128, 128, 2, 4, 3>(a, stream);
-      // 256 x 256 tiles (K <= 16384 by the check above): M = 2049 in 27 us
-      // where 128 x 256 tiles take 33
-      return launch_wide(a, stream);
+      // e8m0 row scales: the SAHW instantiations (bytes; with e8m0 weight
+      // scales too, both in the MFMA)
+      if (a.sa_e8m0) return launch_dense_tiles<true>(a, stream);
+      return launch_dense_tiles<false>(a, stream);
     }
     case KIND_GATE_UP:
       if (shared_small) return launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 4>(a, stream);

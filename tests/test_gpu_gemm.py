@@ -84,12 +84,16 @@ def test_fp8_gemm_e8m0_scales(gpu):
                                    (300, 256, 1024), (1024, 512, 2048), (2100, 512, 1024)])
 def test_fp8_gemm_reads_e8m0_activation_scales_as_bytes(gpu, M, N, K):
     """The live format (model.py:138-142,777-778: act_quant with ue8m0 e8m0
-    scales, e8m0 weight scales) without a conversion launch: every dense
+    scales, e8m0 weight scales) without a conversion launch.  Every dense
     kernel (skinny M <= 16, split-K 16 < M <= 64, 32 x 64 / 32 x 128 /
     64 x 128 / 128 x 128 tiles, 256 x 256 tiles above M = 2048) reads the
-    activation scale bytes itself, so its output equals the fp32-scale call
-    bit for bit (the same powers of two, promoted in the same order) and the
-    oracle within the GEMM bound."""
+    activation scale bytes itself.  With fp32 weight scales the split-K and
+    tiled kernels put the row scale's exponent into the MFMA and promote by
+    the weight scale alone: the output equals the all-fp32 call bit for bit
+    (a power-of-two scale inside the MFMA rounds as the promotion does).
+    With e8m0 weight scales too, the tiled kernels apply both inside the
+    MFMA (no promotion; a different rounding of the same sum), within the
+    GEMM bound of the oracle."""
     from sglang_lite_amd import kernel as K_
 
     print(f"fp8_gemm e8m0 activations M={M} N={N} K={K}", flush=True)
@@ -101,11 +105,15 @@ def test_fp8_gemm_reads_e8m0_activation_scales_as_bytes(gpu, M, N, K):
     sa_e = torch.from_numpy(Q.e8m0_byte(sa)).view(torch.float8_e8m0fnu).to(gpu)
     sb_e = torch.from_numpy(Q.e8m0_byte(sb)).view(torch.float8_e8m0fnu).to(gpu)
     aqd, bqd = to_dev_fp8(aq, gpu), to_dev_fp8(bq, gpu)
-    c8 = K_.fp8_gemm(aqd, sa_e, bqd, sb_e)
-    c32 = K_.fp8_gemm(aqd, torch.from_numpy(sa).to(gpu), bqd, sb_e)
+    sb32 = torch.from_numpy(sb).to(gpu)
+    c8 = K_.fp8_gemm(aqd, sa_e, bqd, sb32)
+    c32 = K_.fp8_gemm(aqd, torch.from_numpy(sa).to(gpu), bqd, sb32)
+    c88 = K_.fp8_gemm(aqd, sa_e, bqd, sb_e)
     torch.cuda.synchronize()
     assert torch.equal(c8, c32)
-    assert_gemm_close(f32(c8), OM.fp8_gemm(aq, sa, bq, sb, out_bf16=False), f"fp8_gemm e8m0 a {M}")
+    ref = OM.fp8_gemm(aq, sa, bq, sb, out_bf16=False)
+    assert_gemm_close(f32(c8), ref, f"fp8_gemm e8m0 a {M}")
+    assert_gemm_close(f32(c88), ref, f"fp8_gemm e8m0 a and b {M}")
 
 
 def test_fp8_gemm_end_to_end_from_bf16(gpu):
