@@ -861,10 +861,16 @@ int sgl_moe_gate(const void* x, const void* w, int64_t T, int64_t H, int E, int 
   const uint16_t* wb = (const uint16_t*)w;
   // decode-sized batches: 16 tokens x 16 experts per workgroup, 16
   // wavefronts with all their K steps in flight (many small workgroups
-  // spread the weight read); prefill: 64 x 64, 8 wavefronts, 4 steps in flight
+  // spread the weight read); prefill: 64 x 64, 8 wavefronts, 4 steps in
+  // flight; from T = 4096 64 x 128 with 4 wavefronts (T = 8192, H = 4096,
+  // E = 256, the gate with its top-k: 94 -> 83 us; at T = 512 / 2048 it is
+  // the slower one, 64 / 67 against 47 / 50 us)
   if (T <= 256) {
     dim3 grid((unsigned)E / 16 + (E % 16 != 0), (unsigned)sgl::ceil_div(T, 16));
     sgl::router_logits_kernel<1, 1, 16, 8><<<grid, 1024, 0, st>>>(xb, wb, T, (int)H, E, logits);
+  } else if (T >= 4096) {
+    dim3 grid((unsigned)sgl::ceil_div((int64_t)E, 128), (unsigned)sgl::ceil_div(T, 64));
+    sgl::router_logits_kernel<4, 8, 4, 2><<<grid, 256, 0, st>>>(xb, wb, T, (int)H, E, logits);
   } else {
     dim3 grid((unsigned)sgl::ceil_div((int64_t)E, 64), (unsigned)sgl::ceil_div(T, 64));
     sgl::router_logits_kernel<4, 4, 8, 4><<<grid, 512, 0, st>>>(xb, wb, T, (int)H, E, logits);

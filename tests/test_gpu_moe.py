@@ -263,6 +263,7 @@ def _gate_case(rng, T, H, E, scale=None):
     (32, 256, 8, 2, "sigmoid", True),
     (1000, 512, 256, 8, "sqrtsoftplus", False),
     (7, 4096, 256, 8, "softmax", True),
+    (4100, 1024, 256, 8, "sqrtsoftplus", True),  # the 64 x 128 tiles (T >= 4096), a ragged last tile
 ])
 def test_gate_kernel_matches_oracle(gpu, T, H, E, k, score_func, use_bias):
     """model.py:564-584 from the hidden states: the bf16-MFMA projection within
