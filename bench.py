@@ -325,8 +325,9 @@ def profile_small(torch, M, K, table, dev):
     """The short kernels for a profiler run (--profile-kernels small), three
     launches each: the decode layers (T = 64 / 256 / 512, Zipf(1.1) load), the
     dense GEMM at M = 16 / 32 / 64 / 128 (N = 4096, K = 7168) over 12 rotating
-    weight copies (three rounds; M = 4096 one round), act_quant 4096 x 7168,
-    and the KV packs (65536 rows)."""
+    weight copies (three rounds; M = 4096 one round), the same GEMM in the
+    live format (e8m0 weight and activation scales) at M = 128 / 1024 / 4096
+    (one round), act_quant 4096 x 7168, and the KV packs (65536 rows)."""
     from sglang_lite_amd import dsv4_kv_pack as KVP
 
     for Td, seed in ((64, 31), (256, 32), (512, 33)):
@@ -348,6 +349,18 @@ def profile_small(torch, M, K, table, dev):
             c = torch.empty(Md, 4096, dtype=torch.bfloat16, device=dev)
             for i in range(3 * len(wsets) if Md <= 128 else len(wsets)):
                 K.fp8_gemm(aq, as_, wsets[i % 12][0], wsets[i % 12][1], out=c)
+        # the live format: e8m0 weight scales and ue8m0 activation scales as e8m0
+        # bytes, M = 128 / 1024 / 4096, 12 calls each over 12 weight copies
+        del wsets
+        bq8, bs8f = K.per_block_cast_to_fp8(torch.randn(4096, 7168, generator=gw, device=dev) * 0.02, True)
+        bs8 = (bs8f.view(torch.int32) >> 23).to(torch.uint8).view(torch.float8_e8m0fnu)
+        wsets = [(bq8.clone(), bs8.clone()) for _ in range(12)]
+        for Md in (128, 1024, 4096):
+            aq, as8 = K.act_quant(torch.randn(Md, 7168, generator=gw, device=dev).to(torch.bfloat16), 128,
+                                  "ue8m0", torch.float8_e8m0fnu)
+            c = torch.empty(Md, 4096, dtype=torch.bfloat16, device=dev)
+            for i in range(len(wsets)):
+                K.fp8_gemm(aq, as8, wsets[i][0], wsets[i][1], out=c)
         xs = [torch.randn(4096, 7168, generator=gw, device=dev).to(torch.bfloat16) for _ in range(3)]
         for x in xs:
             K.act_quant(x)

@@ -201,7 +201,7 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
   // (fp32, or e8m0 bytes when sa_e8m0); FP8 weights (dense), e8m0 row scales
   // as bytes, with e8m0 weight scales both applied inside the MFMA, else
   // promoted in fp32.  The other instantiations read fp32 row scales.
-  const int sa_e8 = SAHW ? (FP4 ? args.sa_e8m0 : 1) : 0;
+  const int sa_e8 = (KIND == KIND_DENSE && SAHW) ? (FP4 ? args.sa_e8m0 : 1) : 0;
   const bool pow2 = KIND == KIND_DENSE && !FP4 && SAHW && args.sb_e8m0;
 
   __shared__ __align__(16) uint8_t smem[C::SMEM];
