@@ -1442,76 +1442,91 @@ __global__ __launch_bounds__(pipe::NT) void gemm_pipe_kernel(const GemmArgs args
 #pragma unroll
       for (int nj = 0; nj < TN; ++nj) acc[mi][nj] = vzero;
 
-    for (int st = 0; st < NST; ++st) {
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      const uint8_t* stg = smem + (st % NSTAGE) * STAGE;
-      const uint8_t* tB = stg + A_BYTES;
-      const float* tS = reinterpret_cast<const float*>(smem + RING + (st % NSTAGE) * SA_SLOT);
-      if ((wm * TM) * 16 < rows) {
-        // LDS reads in the order the MFMAs consume them (A0, B0 and the
-        // scales, then A1..A3): the reads complete in order, so the first
-        // MFMA waits for two fragments, not for the whole stage's burst of
-        // all eight wavefronts
-        v8i af[TM];
-        v8i bf[2];
-        constexpr int HALVES = KIND == KIND_GATE_UP ? 2 : 1;
-        float sa1[TM];
-        float sbh[HALVES];
-        af[0] = read_frag(stg + (wm * TM) * 16 * 128, fl);
-        bf[0] = read_frag(tB + tile_col(0) * 128, fl);
+    // The wavefront's 16-row blocks that hold rows of the tile (an expert's
+    // last M tile is partly padding): only those get fragment reads and
+    // MFMAs (TML of the TM blocks, a compile-time count per K loop), so the
+    // padding costs whole 16-row blocks, not the wavefront's 64 rows.
+    const int tml = min(TM, max(0, (rows - wm * TM * 16 + 15) >> 4));
+    auto kloop = [&](auto tml_c) {
+      constexpr int TML = decltype(tml_c)::value;
+      for (int st = 0; st < NST; ++st) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        if constexpr (TML > 0) {
+          const uint8_t* stg = smem + (st % NSTAGE) * STAGE;
+          const uint8_t* tB = stg + A_BYTES;
+          const float* tS = reinterpret_cast<const float*>(smem + RING + (st % NSTAGE) * SA_SLOT);
+          // LDS reads in the order the MFMAs consume them (A0, B0 and the
+          // scales, then A1..): the reads complete in order, so the first
+          // MFMA waits for two fragments, not for the whole stage's burst of
+          // all eight wavefronts
+          v8i af[TML];
+          v8i bf[2];
+          constexpr int HALVES = KIND == KIND_GATE_UP ? 2 : 1;
+          float sa1[TML];
+          float sbh[HALVES];
+          af[0] = read_frag(stg + (wm * TM) * 16 * 128, fl);
+          bf[0] = read_frag(tB + tile_col(0) * 128, fl);
 #pragma unroll
-        for (int mi = 0; mi < TM; ++mi) sa1[mi] = tS[(wm * TM + mi) * 64 + r16];
+          for (int mi = 0; mi < TML; ++mi) sa1[mi] = tS[(wm * TM + mi) * 64 + r16];
 #pragma unroll
-        for (int hv = 0; hv < HALVES; ++hv) sbh[hv] = sSb[cur][KIND == KIND_GATE_UP ? hv : wave_blk][st];
-        __builtin_amdgcn_sched_barrier(0);
+          for (int hv = 0; hv < HALVES; ++hv) sbh[hv] = sSb[cur][KIND == KIND_GATE_UP ? hv : wave_blk][st];
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int mi = 1; mi < TM; ++mi) af[mi] = read_frag(stg + (wm * TM + mi) * 16 * 128, fl);
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (POW2) {
-          // operand A = the weight fragment (one scale per 16-column
-          // fragment: the 128 x 128 block), operand B = the activation rows
-          // (lane r16's row scale); the scale of lane (g4, r16) covers its
-          // 32-deep K quarter, the same for all four quarters here
-          int sae[TM], sbe[HALVES];
+          for (int mi = 1; mi < TML; ++mi) af[mi] = read_frag(stg + (wm * TM + mi) * 16 * 128, fl);
+          __builtin_amdgcn_sched_barrier(0);
+          if constexpr (POW2) {
+            // operand A = the weight fragment (one scale per 16-column
+            // fragment: the 128 x 128 block), operand B = the activation rows
+            // (lane r16's row scale); the scale of lane (g4, r16) covers its
+            // 32-deep K quarter, the same for all four quarters here
+            int sae[TML], sbe[HALVES];
 #pragma unroll
-          for (int mi = 0; mi < TM; ++mi) sae[mi] = (int)(__float_as_uint(sa1[mi]) >> 23);
+            for (int mi = 0; mi < TML; ++mi) sae[mi] = (int)(__float_as_uint(sa1[mi]) >> 23);
 #pragma unroll
-          for (int hv = 0; hv < HALVES; ++hv) sbe[hv] = (int)(__float_as_uint(sbh[hv]) >> 23);
+            for (int hv = 0; hv < HALVES; ++hv) sbe[hv] = (int)(__float_as_uint(sbh[hv]) >> 23);
 #pragma unroll
-          for (int hv = 0; hv < HALVES; ++hv)
+            for (int hv = 0; hv < HALVES; ++hv)
 #pragma unroll
-            for (int nh = 0; nh < TN / HALVES; ++nh) {
-              const int nj = hv * (TN / HALVES) + nh;
-              if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + tile_col(nj + 1) * 128, fl);
+              for (int nh = 0; nh < TN / HALVES; ++nh) {
+                const int nj = hv * (TN / HALVES) + nh;
+                if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + tile_col(nj + 1) * 128, fl);
 #pragma unroll
-              for (int mi = 0; mi < TM; ++mi)
-                acc[mi][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                    bf[nj & 1], af[mi], acc[mi][nj], 0, 0, 0, sbe[hv], 0, sae[mi]);
+                for (int mi = 0; mi < TML; ++mi)
+                  acc[mi][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                      bf[nj & 1], af[mi], acc[mi][nj], 0, 0, 0, sbe[hv], 0, sae[mi]);
+              }
+          } else {
+#pragma unroll
+            for (int hv = 0; hv < HALVES; ++hv) {
+              float ss[TML];
+#pragma unroll
+              for (int mi = 0; mi < TML; ++mi) ss[mi] = sa1[mi] * sbh[hv];
+#pragma unroll
+              for (int nh = 0; nh < TN / HALVES; ++nh) {
+                const int nj = hv * (TN / HALVES) + nh;
+                if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + tile_col(nj + 1) * 128, fl);
+                v4f pr[TML];
+#pragma unroll
+                for (int mi = 0; mi < TML; ++mi)
+                  pr[mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[nj & 1], af[mi], vzero, 0, 0,
+                                                                            0, 0, 0, 0);
+#pragma unroll
+                for (int mi = 0; mi < TML; ++mi)
+#pragma unroll
+                  for (int r = 0; r < 4; ++r) acc[mi][nj][r] = fmaf(pr[mi][r], ss[mi], acc[mi][nj][r]);
+              }
             }
-          continue;
-        }
-#pragma unroll
-        for (int hv = 0; hv < HALVES; ++hv) {
-          float ss[TM];
-#pragma unroll
-          for (int mi = 0; mi < TM; ++mi) ss[mi] = sa1[mi] * sbh[hv];
-#pragma unroll
-          for (int nh = 0; nh < TN / HALVES; ++nh) {
-            const int nj = hv * (TN / HALVES) + nh;
-            if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + tile_col(nj + 1) * 128, fl);
-            v4f pr[TM];
-#pragma unroll
-            for (int mi = 0; mi < TM; ++mi)
-              pr[mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[nj & 1], af[mi], vzero, 0, 0,
-                                                                        0, 0, 0, 0);
-#pragma unroll
-            for (int mi = 0; mi < TM; ++mi)
-#pragma unroll
-              for (int r = 0; r < 4; ++r) acc[mi][nj][r] = fmaf(pr[mi][r], ss[mi], acc[mi][nj][r]);
           }
         }
       }
+    };
+    switch (tml) {
+      case 0: kloop(std::integral_constant<int, 0>{}); break;
+      case 1: kloop(std::integral_constant<int, 1>{}); break;
+      case 2: kloop(std::integral_constant<int, 2>{}); break;
+      case 3: kloop(std::integral_constant<int, 3>{}); break;
+      default: kloop(std::integral_constant<int, TM>{}); break;
     }
     __syncthreads();  // the ring is free; the next tile's tables are in LDS
 
