@@ -86,15 +86,14 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
     const int e = lane + 64 * q;
     sel[q] = !ok[q] ? NEG_INF : (bias ? sc[q] + bias[e] : lg[q]);
   }
-  unsigned taken = 0u;
-  float wsum = 0.0f;
-  int my_e = 0;      // lane j keeps the j-th pick
-  float my_s = 0.0f;
   if (hash.tid2eid) {
     // weights = the original scores gathered at the table's experts, in table order
     int64_t tok = hash.ids64 ? reinterpret_cast<const int64_t*>(hash.input_ids)[t]
                              : (int64_t) reinterpret_cast<const int32_t*>(hash.input_ids)[t];
     tok = tok < 0 ? 0 : (tok >= hash.vocab ? hash.vocab - 1 : tok);
+    float wsum = 0.0f;
+    int my_e = 0;
+    float my_s = 0.0f;
     for (int j = 0; j < k; ++j) {
       int e = hash.tid2eid[tok * k + j];
       e = (e < 0 || e >= E) ? 0 : e;
@@ -116,43 +115,78 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
     }
     return;
   }
-  for (int j = 0; j < k; ++j) {
-    float bv = NEG_INF;
-    int be = 0x7FFFFFFF;
-    float bs = 0.0f;
+  // Top-k as a radix select.  Each key becomes an unsigned image that keeps
+  // the float order (-0 taken as +0, a NaN above +inf as torch.topk places it,
+  // slots past E below every key); 32 rounds fix the k-th largest image bit
+  // by bit from ballot counts, which are the same in every lane, so the
+  // rounds run on scalar registers.  The keys above that threshold are taken
+  // and the ties at it go to the lowest expert ids; the k picks, staged in LDS
+  // in id order, then rank themselves by (key descending, id ascending):
+  // torch.topk's order, ties to the lower expert id.
+  __shared__ uint32_t sKey[4][16];
+  __shared__ int32_t sId[4][16], sOrd[4][16];
+  __shared__ float sSc[4][16];
+  const int wv = threadIdx.x >> 6;
+  uint32_t key[EPL];
 #pragma unroll
-    for (int q = 0; q < EPL; ++q) {
-      const int e = lane + 64 * q;
-      const bool avail = ok[q] && !((taken >> q) & 1u);
-      if (avail && (be == 0x7FFFFFFF || sel[q] > bv || (sel[q] == bv && e < be))) {
-        bv = sel[q];
-        be = e;
-        bs = sc[q];
-      }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oe = __shfl_xor(be, o, 64);
-      const float os = __shfl_xor(bs, o, 64);
-      if (oe != 0x7FFFFFFF && (be == 0x7FFFFFFF || ov > bv || (ov == bv && oe < be))) {
-        bv = ov;
-        be = oe;
-        bs = os;
-      }
-    }
-    if (be != 0x7FFFFFFF && (be & 63) == lane) taken |= 1u << (be >> 6);
-    if (lane == j) {
-      my_e = be;
-      my_s = bs;
-    }
-    wsum += bs;
+  for (int q = 0; q < EPL; ++q) {
+    uint32_t u = __float_as_uint(sel[q]);
+    u = u == 0x80000000u ? 0u : u;
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    u = sel[q] != sel[q] ? 0xFFFFFFFFu : u;
+    key[q] = ok[q] ? u : 0u;
   }
+  uint32_t th = 0u;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = th | (1u << b);
+    int cnt = 0;
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) cnt += __popcll(__ballot(key[q] >= cand));
+    th = cnt >= k ? cand : th;
+  }
+  int need = k;
+#pragma unroll
+  for (int q = 0; q < EPL; ++q) need -= __popcll(__ballot(key[q] > th));
+  const unsigned long long lt_mask = (1ull << lane) - 1ull;
+  int base = 0;
+#pragma unroll
+  for (int q = 0; q < EPL; ++q) {
+    const unsigned long long eq = __ballot(key[q] == th);
+    const bool pick = key[q] > th || (key[q] == th && __popcll(eq & lt_mask) < need);
+    const int neq = __popcll(eq);
+    need -= neq < need ? neq : need;
+    const unsigned long long pm = __ballot(pick);
+    if (pick) {
+      const int pos = base + __popcll(pm & lt_mask);
+      sKey[wv][pos] = key[q];
+      sId[wv][pos] = lane + 64 * q;
+      sSc[wv][pos] = sc[q];
+    }
+    base += __popcll(pm);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  int rank = 0;
   if (lane < k) {
-    float w = my_s;
+    const uint32_t kj = sKey[wv][lane];
+    for (int i = 0; i < k; ++i) {
+      const uint32_t ki = sKey[wv][i];
+      rank += (ki > kj || (ki == kj && i < lane)) ? 1 : 0;
+    }
+    sOrd[wv][rank] = lane;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // the weight sum accumulated in rank order
+  float wsum = 0.0f;
+  for (int r = 0; r < k; ++r) wsum += sSc[wv][sOrd[wv][r]];
+  if (lane < k) {
+    float w = sSc[wv][lane];
     if (score_func != SGL_SCORE_SOFTMAX) w = w / wsum;
-    ids[t * k + lane] = my_e;
-    weights[t * k + lane] = w * route_scale;
+    ids[t * k + rank] = sId[wv][lane];
+    weights[t * k + rank] = w * route_scale;
   }
 }
 

@@ -66,6 +66,29 @@ def test_route_topk(gpu, score_func, use_bias, T, E, k):
     np.testing.assert_allclose(w.cpu().numpy(), w_ref, rtol=2e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("score_func,use_bias", [("softmax", False), ("sigmoid", True),
+                                                 ("sqrtsoftplus", False)])
+@pytest.mark.parametrize("E,k", [(256, 8), (200, 16), (8, 8), (70, 3)])
+def test_route_topk_exact_ties_go_to_lower_ids(gpu, score_func, use_bias, E, k):
+    """Logits on a coarse grid, so most picks tie exactly (-0.0 beside +0.0
+    among them): the picks and their order are the oracle's stable descending
+    sort, ties to the lower expert id; E = 200 and 70 leave lanes past E."""
+    from sglang_lite_amd import moe as M
+
+    rng = np.random.default_rng(E * 31 + k)
+    T = 300
+    logits = (rng.integers(-3, 3, (T, E)) * 0.5).astype(np.float32)
+    zeros = logits == 0
+    logits[zeros] = np.where(rng.random(int(zeros.sum())) < 0.5, np.float32(-0.0), np.float32(0.0))
+    assert np.signbit(logits[zeros]).any() and (~np.signbit(logits[zeros])).any()
+    bias = np.zeros(E, np.float32) if use_bias else None
+    w_ref, ids_ref = OM.route_topk(logits, k, score_func, bias, route_scale=1.5)
+    w, ids = M.route_topk(to_dev_f32(logits, gpu), k, score_func,
+                          to_dev_f32(bias, gpu) if use_bias else None, route_scale=1.5)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_allclose(w.cpu().numpy(), w_ref, rtol=2e-6, atol=1e-7)
+
+
 def test_route_topk_matches_torch_topk(gpu):
     """Library routine pin: torch.topk on torch.softmax scores (CPU)."""
     from sglang_lite_amd import moe as M
