@@ -56,10 +56,6 @@ constexpr int kMaxGroups = 1025;  // 1024 routed experts + shared
 
 constexpr int kMaxKB = 128;       // K <= 16384: weight scales of a tile staged in LDS
 
-__device__ __forceinline__ uint32_t lds_u32(const void* p) {
-  return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const uint8_t*)p);
-}
-
 __device__ __forceinline__ const uint8_t* uniform_ptr(const void* p) {
   const uint64_t v = (uint64_t)(uintptr_t)p;
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
@@ -84,12 +80,8 @@ __device__ __forceinline__ void dma4(const uint8_t* base, uint32_t voff, uint32_
                :: "v"(voff), "s"(base), "s"(lds) : "memory");
 }
 
-// The same with a per-lane 64-bit address (no scalar base): lane i copies 16
-// (dma16v) or 4 (dma4v) bytes from addr to LDS m0 + 16 i (4 i).
-__device__ __forceinline__ void dma16v(uint64_t addr, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(addr), "s"(lds) : "memory");
-}
+// The same with a per-lane 64-bit address (no scalar base): lane i copies 4
+// bytes from addr to LDS m0 + 4 i (dma16v, 16 bytes, is in sgl_common.h).
 __device__ __forceinline__ void dma4v(uint64_t addr, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
                :: "v"(addr), "s"(lds) : "memory");
@@ -111,8 +103,6 @@ __device__ __forceinline__ float load_scale(const void* s, int64_t idx, int e8m0
   if (e8m0) return e8m0_value(reinterpret_cast<const uint8_t*>(s)[idx]);
   return reinterpret_cast<const float*>(s)[idx];
 }
-
-__device__ __forceinline__ int swz(int row) { return (row & 6) | ((row >> 3) & 1); }
 
 // Lane l's two 16-byte chunks of a 16-row operand block: row l % 16, logical
 // chunks 2 (l / 16) and 2 (l / 16) + 1.  Blocks start at multiples of 16 rows,

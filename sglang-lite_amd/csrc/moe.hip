@@ -44,13 +44,21 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const float NEG_INF = -__builtin_huge_valf();
-  float lg[EPL], sc[EPL], sel[EPL];
+  float lg[EPL], sc[EPL], sel[EPL], bv[EPL];
   bool ok[EPL];
+  // every load issued up front (indices past E clamped, their values dropped)
+  // so the logits and the bias arrive in one memory round trip
 #pragma unroll
   for (int q = 0; q < EPL; ++q) {
     const int e = lane + 64 * q;
-    ok[q] = e < E;
-    lg[q] = ok[q] ? logits[t * E + e] : NEG_INF;
+    const int ec = e < E ? e : E - 1;
+    lg[q] = logits[t * E + ec];
+    bv[q] = bias ? bias[ec] : 0.0f;
+  }
+#pragma unroll
+  for (int q = 0; q < EPL; ++q) {
+    ok[q] = lane + 64 * q < E;
+    lg[q] = ok[q] ? lg[q] : NEG_INF;
   }
   if (score_func == SGL_SCORE_SOFTMAX) {
     float m = NEG_INF;
@@ -82,10 +90,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
   // a bias the logits select exactly the experts torch.topk picks on the
   // scores (barring exact score ties); with a bias the biased scores are used.
 #pragma unroll
-  for (int q = 0; q < EPL; ++q) {
-    const int e = lane + 64 * q;
-    sel[q] = !ok[q] ? NEG_INF : (bias ? sc[q] + bias[e] : lg[q]);
-  }
+  for (int q = 0; q < EPL; ++q) sel[q] = !ok[q] ? NEG_INF : (bias ? sc[q] + bv[q] : lg[q]);
   if (hash.tid2eid) {
     // weights = the original scores gathered at the table's experts, in table order
     int64_t tok = hash.ids64 ? reinterpret_cast<const int64_t*>(hash.input_ids)[t]
@@ -117,9 +122,10 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
   }
   // Top-k as a radix select.  Each key becomes an unsigned image that keeps
   // the float order (-0 taken as +0, a NaN above +inf as torch.topk places it,
-  // slots past E below every key); 32 rounds fix the k-th largest image bit
-  // by bit from ballot counts, which are the same in every lane, so the
-  // rounds run on scalar registers.  The keys above that threshold are taken
+  // slots past E below every key); up to 32 rounds fix the k-th largest image
+  // bit by bit from ballot counts, which are the same in every lane, so the
+  // rounds run on scalar registers; they stop early once exactly k keys lie
+  // at or above the threshold.  The keys above that threshold are taken
   // and the ties at it go to the lowest expert ids; the k picks, staged in LDS
   // in id order, then rank themselves by (key descending, id ascending):
   // torch.topk's order, ties to the lower expert id.
@@ -142,7 +148,10 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
     int cnt = 0;
 #pragma unroll
     for (int q = 0; q < EPL; ++q) cnt += __popcll(__ballot(key[q] >= cand));
-    th = cnt >= k ? cand : th;
+    if (cnt >= k) {
+      th = cand;
+      if (cnt == k) break;  // exactly the k largest keys lie at or above th
+    }
   }
   int need = k;
 #pragma unroll
@@ -276,6 +285,144 @@ __global__ __launch_bounds__(64 * NWV) void router_logits_kernel(const uint16_t*
     const int e = e0 + i % RE;
     if (t < T && e < E) logits[t * E + e] = v;
   }
+}
+
+// Router projection for prefill-sized batches (H % 64 == 0).  A workgroup
+// of four wavefronts owns TT tokens x TE experts; the x and W rows stream
+// through an NS-deep ring of 64-deep LDS stages (TT + TE rows of 128 bytes)
+// by global_load_lds_dwordx4, one instruction filling 8 rows x 128 bytes, the
+// 16-byte chunks swizzled (chunk c of row r at c ^ swz(r)), NS - 1 stages in
+// flight.  Whole 128-byte row segments per instruction are what the L2 serves
+// fastest; the register-loaded kernel above reads 16 rows x 64 bytes per
+// instruction.  A wavefront computes a (TT/WT) x (TE/WE) block with
+// v_mfma_f32_16x16x32_bf16: lane (g, r) reads chunks 2g and 2g + 1 of its row,
+// the first MFMA takes chunk 2g's eight values and the second chunk 2g + 1's;
+// x and W lanes hold the same K indices, so every MFMA sums 32 whole
+// products (the 64 of a stage in two MFMAs, in the MFMA's own order).
+// Tiles are numbered token-tile major, expert tile fastest, and the tiles of
+// one XCD (workgroup b runs on XCD b % 8) are consecutive, so the workgroups
+// reading one x tile run together on one L2.  Rows past T / E re-read the
+// last row; their outputs are dropped.
+template <int NI, int L>
+__device__ __forceinline__ void router_wait(int later) {
+  if constexpr (L == 0) {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  } else {
+    if (later >= L)
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(L * NI) : "memory");
+    else
+      router_wait<NI, L - 1>(later);
+  }
+}
+
+template <int TT, int TE, int NS>
+__global__ __launch_bounds__(256) void router_lds_kernel(const uint16_t* __restrict__ x,
+                                                         const uint16_t* __restrict__ w, int64_t T,
+                                                         int H, int E, int ntile_e, int64_t ntiles,
+                                                         int64_t per_xcd, float* __restrict__ logits) {
+  constexpr int WT = TT >= 32 ? 2 : 1, WE = 4 / WT;
+  constexpr int ST = TT / WT, SE = TE / WE;  // a wavefront's block
+  constexpr int MB = ST / 16, NB = SE / 16;
+  constexpr int ROWS = TT + TE;
+  constexpr int SBYTES = ROWS * 128;
+  constexpr int NI = ROWS / 32;  // DMA instructions per wavefront per stage
+  static_assert(ROWS % 32 == 0 && TT % 8 == 0 && ST % 16 == 0 && SE % 16 == 0, "tile shape");
+  static_assert(NS >= 2 && (NS - 2) * NI <= 63, "vmcnt range");
+  __shared__ __align__(16) uint8_t ring[NS * SBYTES];
+
+  const int64_t tile = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (tile >= ntiles) return;
+  const int64_t t0 = (tile / ntile_e) * TT;
+  const int e0 = (int)(tile % ntile_e) * TE;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+  // instruction j of this wavefront fills stage rows 8 (wave + 4 j) + lane / 8
+  uint64_t src[NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int R = 8 * (wave + 4 * j) + (lane >> 3);
+    const int c = (lane & 7) ^ swz(R);
+    const uint16_t* row;
+    if (R < TT) {
+      const int64_t t = t0 + R < T ? t0 + R : T - 1;
+      row = x + t * H;
+    } else {
+      const int e = e0 + R - TT < E ? e0 + R - TT : E - 1;
+      row = w + (int64_t)e * H;
+    }
+    src[j] = (uint64_t)(uintptr_t)row + 16u * (uint32_t)c;
+  }
+  const uint32_t ring0 = __builtin_amdgcn_readfirstlane(lds_u32(ring));
+  const int nst = H / 64;
+  auto issue = [&](int s) {
+    const uint32_t slot = ring0 + (uint32_t)(s % NS) * SBYTES;
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+      dma16v(src[j] + (uint64_t)s * 128u,
+             __builtin_amdgcn_readfirstlane(slot + (uint32_t)(8 * (wave + 4 * j)) * 128u));
+  };
+  for (int s = 0; s < NS - 1 && s < nst; ++s) issue(s);
+
+  const int g4 = lane >> 4, r16 = lane & 15;
+  const uint32_t flo = (uint32_t)(r16 * 128 + (((2 * g4) ^ swz(r16)) << 4));
+  const uint32_t fhi = (uint32_t)(r16 * 128 + (((2 * g4 + 1) ^ swz(r16)) << 4));
+  const int wt = wave / WE, we = wave % WE;
+  v4f_r acc[MB][NB];
+#pragma unroll
+  for (int mi = 0; mi < MB; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < NB; ++nj) acc[mi][nj] = v4f_r{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s = 0; s < nst; ++s) {
+    // stage s has landed once at most min(NS - 2, nst - 1 - s) later stages are outstanding
+    const int later = nst - 1 - s < NS - 2 ? nst - 1 - s : NS - 2;
+    router_wait<NI, NS - 2>(later);
+    __builtin_amdgcn_s_barrier();
+    if (s + NS - 1 < nst) issue(s + NS - 1);
+    const uint8_t* st = ring + (s % NS) * SBYTES;
+    v8bf alo[MB], ahi[MB], blo[NB], bhi[NB];
+#pragma unroll
+    for (int mi = 0; mi < MB; ++mi) {
+      const uint8_t* blk = st + (wt * ST + 16 * mi) * 128;
+      alo[mi] = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(blk + flo));
+      ahi[mi] = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(blk + fhi));
+    }
+#pragma unroll
+    for (int nj = 0; nj < NB; ++nj) {
+      const uint8_t* blk = st + (TT + we * SE + 16 * nj) * 128;
+      blo[nj] = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(blk + flo));
+      bhi[nj] = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(blk + fhi));
+    }
+#pragma unroll
+    for (int mi = 0; mi < MB; ++mi)
+#pragma unroll
+      for (int nj = 0; nj < NB; ++nj) {
+        acc[mi][nj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo[mi], blo[nj], acc[mi][nj], 0, 0, 0);
+        acc[mi][nj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi[mi], bhi[nj], acc[mi][nj], 0, 0, 0);
+      }
+  }
+  // lane (g4, r16) holds tokens 4 g4 + r, expert r16 of each 16 x 16 block
+#pragma unroll
+  for (int mi = 0; mi < MB; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < NB; ++nj) {
+      const int e = e0 + we * SE + 16 * nj + r16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t t = t0 + wt * ST + 16 * mi + 4 * g4 + r;
+        if (t < T && e < E) logits[t * E + e] = acc[mi][nj][r];
+      }
+    }
+}
+
+template <int TT, int TE, int NS>
+void launch_router_lds(const uint16_t* x, const uint16_t* w, int64_t T, int H, int E,
+                       float* logits, hipStream_t st) {
+  const int ntile_e = (int)ceil_div(E, TE);
+  const int64_t ntiles = ceil_div(T, TT) * ntile_e;
+  const int64_t per_xcd = ceil_div(ntiles, 8);
+  router_lds_kernel<TT, TE, NS><<<(unsigned)(8 * per_xcd), 256, 0, st>>>(x, w, T, H, E, ntile_e, ntiles,
+                                                                          per_xcd, logits);
 }
 
 // -------------------------------------------------------------- permute
@@ -893,13 +1040,22 @@ int sgl_moe_gate(const void* x, const void* w, int64_t T, int64_t H, int E, int 
   hipStream_t st = (hipStream_t)stream;
   const uint16_t* xb = (const uint16_t*)x;
   const uint16_t* wb = (const uint16_t*)w;
-  // decode-sized batches: 16 tokens x 16 experts per workgroup, 16
-  // wavefronts with all their K steps in flight (many small workgroups
-  // spread the weight read); prefill: 64 x 64, 8 wavefronts, 4 steps in
-  // flight; from T = 4096 64 x 128 with 4 wavefronts (T = 8192, H = 4096,
-  // E = 256, the gate with its top-k: 94 -> 83 us; at T = 512 / 2048 it is
-  // the slower one, 64 / 67 against 47 / 50 us)
-  if (T <= 256) {
+  // T > 256 with H % 64 == 0: the LDS-staged kernel, the largest of its tiles
+  // that still gives about a workgroup per CU.  Decode-sized batches: the
+  // register-loaded kernel with 16 tokens x 16 experts per workgroup and 16
+  // wavefronts with all their K steps in flight (many small workgroups spread
+  // the weight read); it also serves H % 64 != 0 (64 x 64 or 64 x 128 tiles).
+  auto tiles = [&](int64_t tt, int64_t te) { return sgl::ceil_div(T, tt) * sgl::ceil_div(E, te); };
+  if (T > 256 && H % 64 == 0) {
+    if (tiles(64, 128) >= 240)
+      sgl::launch_router_lds<64, 128, 4>(xb, wb, T, (int)H, E, logits, st);
+    else if (tiles(32, 128) >= 240)
+      sgl::launch_router_lds<32, 128, 4>(xb, wb, T, (int)H, E, logits, st);
+    else if (tiles(32, 64) >= 240)
+      sgl::launch_router_lds<32, 64, 6>(xb, wb, T, (int)H, E, logits, st);
+    else
+      sgl::launch_router_lds<32, 32, 8>(xb, wb, T, (int)H, E, logits, st);
+  } else if (T <= 256) {
     dim3 grid((unsigned)E / 16 + (E % 16 != 0), (unsigned)sgl::ceil_div(T, 16));
     sgl::router_logits_kernel<1, 1, 16, 8><<<grid, 1024, 0, st>>>(xb, wb, T, (int)H, E, logits);
   } else if (T >= 4096) {

@@ -49,6 +49,25 @@ __device__ __forceinline__ uint4 ld16_stream(const void* p) {
   const u4v_ v = SGL_NT_STREAMS ? __builtin_nontemporal_load(q) : *q;
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+
+// LDS byte address of a __shared__ object (what an LDS DMA's m0 takes).
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+  return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const uint8_t*)p);
+}
+
+// LDS DMA with a per-lane 64-bit address: lane i copies 16 bytes from addr to
+// LDS m0 + 16 i (global_load_lds_dwordx4; counted by vmcnt).
+__device__ __forceinline__ void dma16v(uint64_t addr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(addr), "s"(lds) : "memory");
+}
+
+// Chunk swizzle of the LDS-staged operand tiles: a 128-byte stage row's
+// 16-byte chunk c sits at c ^ swz(row).  A ds_read_b128 of an MFMA operand
+// has 16 lanes read one chunk column of 16 consecutive rows; with this
+// swizzle those reads are conflict-free on gfx950's 64-bank LDS.  swz depends
+// on row bits 1-3 only, so it repeats every 16 rows.
+__device__ __forceinline__ int swz(int row) { return (row & 6) | ((row >> 3) & 1); }
 #endif
 
 }  // namespace sgl
