@@ -3331,8 +3331,15 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
                      kb % 4 == 0 && aligned(a.sa, 16);
   // the FP8 shared expert of an FP4 layer in a launch of its own at decode
   // batch sizes: 32-row tiles, so ceil(T / 32) x N / 256 workgroups share
-  // its weight stream (128-row tiles give N / 256 = 16 at T <= 128)
+  // its weight stream (128-row tiles give N / 256 = 16 at T <= 128); the
+  // down projection, with no requant groups to keep whole, in 32 x 64 tiles
+  // while 256-column tiles would leave half the CUs idle: a workgroup streams
+  // its weight slice at a capped rate, so more workgroups finish sooner
+  // (H = 4096, I = 2048, FP4 decode layer: T = 64 / 256 -5 / -11 us; at
+  // T = 512, 256 tiles of 32 x 256 already cover the CUs and the 64-column
+  // tiles' extra activation re-reads cost 15 us)
   const bool shared_small = a.E == 0 && a.has_shared && a.T <= 512;
+  const bool shared_narrow = shared_small && ceil_div(a.T, 32) * ceil_div(a.N, 256) <= 128;
   switch (kind) {
     case KIND_DENSE: {
       const int rc = SGL_SPLITK ? try_splitk(a, stream) : kNoSplit;
@@ -3363,6 +3370,7 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       return big ? launch_cfg<KIND_GATE_UP, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)
                  : launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 4>(a, stream);
     default:
+      if (shared_narrow) return launch_cfg<KIND_DOWN, 32, 64, 1, 4, 4>(a, stream);
       if (shared_small) return launch_cfg<KIND_DOWN, 32, 256, 1, 4, 4>(a, stream);
       if (rb_ok) return launch_rb<KIND_DOWN>(a, rows_hint, stream);
       if (big && pipe_ok)
