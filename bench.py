@@ -327,7 +327,9 @@ def profile_small(torch, M, K, table, dev):
     dense GEMM at M = 16 / 32 / 64 / 128 (N = 4096, K = 7168) over 12 rotating
     weight copies (three rounds; M = 4096 one round), the same GEMM in the
     live format (e8m0 weight and activation scales) at M = 128 / 1024 / 4096
-    (one round), act_quant 4096 x 7168, and the KV packs (65536 rows)."""
+    (one round), act_quant 4096 x 7168, the KV packs (65536 rows), and the
+    router gate (projection + sqrtsoftplus/bias top-k, E = 256) at T = 64 /
+    512 / 2048 / 8192."""
     from sglang_lite_amd import dsv4_kv_pack as KVP
 
     for Td, seed in ((64, 31), (256, 32), (512, 33)):
@@ -337,6 +339,15 @@ def profile_small(torch, M, K, table, dev):
         for _ in range(3):
             w, ids = M.route_topk(logits, K_TOP)
             M.moe_forward(xd, ids, w, table, workspace=ws)
+    torch.cuda.synchronize()
+    gg = torch.Generator(device=dev).manual_seed(8)
+    wr = (torch.randn(E, H, generator=gg, device=dev) * H ** -0.5).to(torch.bfloat16)
+    br = torch.randn(E, generator=gg, device=dev) * 0.05
+    for Tg in (64, 512, 2048, 8192):
+        xg = torch.randn(Tg, H, generator=gg, device=dev).to(torch.bfloat16)
+        lg = torch.empty(Tg, E, dtype=torch.float32, device=dev)
+        for _ in range(3):
+            M.gate(xg, wr, K_TOP, "sqrtsoftplus", br, 1.5, logits=lg)
     torch.cuda.synchronize()
     gw = torch.Generator(device=dev).manual_seed(2)
     bq, bs = K.per_block_cast_to_fp8(torch.randn(4096, 7168, generator=gw, device=dev) * 0.02, False)
