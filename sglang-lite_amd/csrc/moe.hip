@@ -86,11 +86,12 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
       sc[q] = sqrtf(x > 20.0f ? x : log1pf(expf(x)));
     }
   }
-  // Selection key: every score function is monotone in the logit, so without
-  // a bias the logits select exactly the experts torch.topk picks on the
-  // scores (barring exact score ties); with a bias the biased scores are used.
+  // Selection key: the scores (+ bias), which deepseek_infer/model.py:574-579
+  // runs torch.topk on.  Not the logits, though every score function is
+  // monotone in them: two logits can round to one fp32 score, and that tie
+  // goes to the lower expert id, not to the larger logit.
 #pragma unroll
-  for (int q = 0; q < EPL; ++q) sel[q] = !ok[q] ? NEG_INF : (bias ? sc[q] + bv[q] : lg[q]);
+  for (int q = 0; q < EPL; ++q) sel[q] = !ok[q] ? NEG_INF : (bias ? sc[q] + bv[q] : sc[q]);
   if (hash.tid2eid) {
     // weights = the original scores gathered at the table's experts, in table order
     int64_t tok = hash.ids64 ? reinterpret_cast<const int64_t*>(hash.input_ids)[t]
@@ -413,6 +414,124 @@ __global__ __launch_bounds__(256) void router_lds_kernel(const uint16_t* __restr
         if (t < T && e < E) logits[t * E + e] = acc[mi][nj][r];
       }
     }
+}
+
+// The same projection with K split over the four wavefronts (H % 128 == 0):
+// 128-deep stages of 256-byte rows (one 1 KB DMA instruction fills 4 rows,
+// chunk c of row r stored at c ^ (r & 15)), and wavefront w reads only its
+// quarter of every row (bytes [64 w, +64): lane (g, r) the 16 bytes of chunk
+// 4 w + g), one MFMA per block pair per stage over the whole TT x TE tile.
+// Each stage's fragment reads then total its DMA bytes, half of what the
+// 2 x 2 wavefront split reads.  After the K loop the four partial tiles meet
+// in LDS and wavefront w sums rows [w TT / 4, +TT / 4) in the order
+// ((p0 + p1) + p2) + p3.
+template <int TT, int TE, int NS>
+__global__ __launch_bounds__(256) void router_ks_kernel(const uint16_t* __restrict__ x,
+                                                        const uint16_t* __restrict__ w, int64_t T,
+                                                        int H, int E, int ntile_e, int64_t ntiles,
+                                                        int64_t per_xcd, float* __restrict__ logits) {
+  constexpr int MB = TT / 16, NB = TE / 16;
+  constexpr int ROWS = TT + TE;
+  constexpr int SBYTES = ROWS * 256;
+  constexpr int NI = ROWS / 16;  // DMA instructions per wavefront per stage (4 rows each)
+  constexpr int RING = NS * SBYTES;
+  constexpr int PART = TT * TE * 4;  // one wavefront's partial tile, fp32
+  constexpr int SMEM = RING > 4 * PART ? RING : 4 * PART;
+  static_assert(ROWS % 16 == 0 && TT % 16 == 0 && TE % 16 == 0 && TT % 4 == 0, "tile shape");
+  static_assert(NS >= 2 && (NS - 2) * NI <= 63, "vmcnt range");
+  __shared__ __align__(16) uint8_t smem[SMEM];
+
+  const int64_t tile = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (tile >= ntiles) return;
+  const int64_t t0 = (tile / ntile_e) * TT;
+  const int e0 = (int)(tile % ntile_e) * TE;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+  // instruction j of this wavefront fills stage rows 4 (wave + 4 j) + lane / 16
+  uint64_t src[NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int R = 4 * (wave + 4 * j) + (lane >> 4);
+    const int c = (lane & 15) ^ (R & 15);
+    const uint16_t* row;
+    if (R < TT) {
+      const int64_t t = t0 + R < T ? t0 + R : T - 1;
+      row = x + t * H;
+    } else {
+      const int e = e0 + R - TT < E ? e0 + R - TT : E - 1;
+      row = w + (int64_t)e * H;
+    }
+    src[j] = (uint64_t)(uintptr_t)row + 16u * (uint32_t)c;
+  }
+  const uint32_t ring0 = __builtin_amdgcn_readfirstlane(lds_u32(smem));
+  const int nst = H / 128;
+  auto issue = [&](int s) {
+    const uint32_t slot = ring0 + (uint32_t)(s % NS) * SBYTES;
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+      dma16v(src[j] + (uint64_t)s * 256u,
+             __builtin_amdgcn_readfirstlane(slot + (uint32_t)(4 * (wave + 4 * j)) * 256u));
+  };
+  for (int s = 0; s < NS - 1 && s < nst; ++s) issue(s);
+
+  const int g4 = lane >> 4, r16 = lane & 15;
+  // this lane's 16 bytes of any 16-row block (blocks start at multiples of 16 rows)
+  const uint32_t fo = (uint32_t)(r16 * 256 + (((4 * wave + g4) ^ r16) << 4));
+  v4f_r acc[MB][NB];
+#pragma unroll
+  for (int mi = 0; mi < MB; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < NB; ++nj) acc[mi][nj] = v4f_r{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s = 0; s < nst; ++s) {
+    const int later = nst - 1 - s < NS - 2 ? nst - 1 - s : NS - 2;
+    router_wait<NI, NS - 2>(later);
+    __builtin_amdgcn_s_barrier();
+    if (s + NS - 1 < nst) issue(s + NS - 1);
+    const uint8_t* st = smem + (s % NS) * SBYTES;
+    v8bf a[MB], b[NB];
+#pragma unroll
+    for (int mi = 0; mi < MB; ++mi)
+      a[mi] = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(st + 16 * mi * 256 + fo));
+#pragma unroll
+    for (int nj = 0; nj < NB; ++nj)
+      b[nj] = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(st + (TT + 16 * nj) * 256 + fo));
+#pragma unroll
+    for (int mi = 0; mi < MB; ++mi)
+#pragma unroll
+      for (int nj = 0; nj < NB; ++nj)
+        acc[mi][nj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mi], b[nj], acc[mi][nj], 0, 0, 0);
+  }
+  // the partial tiles meet in LDS (the ring is free once every wavefront is past its last stage)
+  __syncthreads();
+  float* part = reinterpret_cast<float*>(smem) + wave * (TT * TE);
+#pragma unroll
+  for (int mi = 0; mi < MB; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < NB; ++nj)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) part[(16 * mi + 4 * g4 + r) * TE + 16 * nj + r16] = acc[mi][nj][r];
+  __syncthreads();
+  const float* p = reinterpret_cast<const float*>(smem);
+  constexpr int RW = TT / 4;  // rows summed per wavefront
+  for (int i = lane; i < RW * TE; i += 64) {
+    const int row = wave * RW + i / TE, col = i % TE;
+    const int o = row * TE + col;
+    const float v = ((p[o] + p[TT * TE + o]) + p[2 * TT * TE + o]) + p[3 * TT * TE + o];
+    const int64_t t = t0 + row;
+    const int e = e0 + col;
+    if (t < T && e < E) logits[t * E + e] = v;
+  }
+}
+
+template <int TT, int TE, int NS>
+void launch_router_ks(const uint16_t* x, const uint16_t* w, int64_t T, int H, int E,
+                      float* logits, hipStream_t st) {
+  const int ntile_e = (int)ceil_div(E, TE);
+  const int64_t ntiles = ceil_div(T, TT) * ntile_e;
+  const int64_t per_xcd = ceil_div(ntiles, 8);
+  router_ks_kernel<TT, TE, NS><<<(unsigned)(8 * per_xcd), 256, 0, st>>>(x, w, T, H, E, ntile_e, ntiles,
+                                                                         per_xcd, logits);
 }
 
 template <int TT, int TE, int NS>
@@ -1040,13 +1159,22 @@ int sgl_moe_gate(const void* x, const void* w, int64_t T, int64_t H, int E, int 
   hipStream_t st = (hipStream_t)stream;
   const uint16_t* xb = (const uint16_t*)x;
   const uint16_t* wb = (const uint16_t*)w;
-  // T > 256 with H % 64 == 0: the LDS-staged kernel, the largest of its tiles
-  // that still gives about a workgroup per CU.  Decode-sized batches: the
+  // T > 256 with H % 64 == 0: the LDS-staged kernels, the largest of their
+  // tiles that still gives about a workgroup per CU; K split over the four
+  // wavefronts for the 32 x 64 and 32 x 32 tiles when H % 128 == 0 (H = 4096,
+  // E = 256 projection: T = 512 13.0 -> 9.4 us, T = 2048 18.3 -> 15.0 us; for
+  // 32 x 128 even, for 64 x 128 31.4 -> 33.6 us, so those keep 2 x 2
+  // wavefronts over 64-deep stages).  Decode-sized batches: the
   // register-loaded kernel with 16 tokens x 16 experts per workgroup and 16
   // wavefronts with all their K steps in flight (many small workgroups spread
   // the weight read); it also serves H % 64 != 0 (64 x 64 or 64 x 128 tiles).
   auto tiles = [&](int64_t tt, int64_t te) { return sgl::ceil_div(T, tt) * sgl::ceil_div(E, te); };
-  if (T > 256 && H % 64 == 0) {
+  if (T > 256 && H % 128 == 0 && tiles(32, 128) < 240) {
+    if (tiles(32, 64) >= 240)
+      sgl::launch_router_ks<32, 64, 6>(xb, wb, T, (int)H, E, logits, st);
+    else
+      sgl::launch_router_ks<32, 32, 8>(xb, wb, T, (int)H, E, logits, st);
+  } else if (T > 256 && H % 64 == 0) {
     if (tiles(64, 128) >= 240)
       sgl::launch_router_lds<64, 128, 4>(xb, wb, T, (int)H, E, logits, st);
     else if (tiles(32, 128) >= 240)

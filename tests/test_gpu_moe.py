@@ -89,6 +89,33 @@ def test_route_topk_exact_ties_go_to_lower_ids(gpu, score_func, use_bias, E, k):
     np.testing.assert_allclose(w.cpu().numpy(), w_ref, rtol=2e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("score_func", ["sigmoid", "softmax"])
+def test_route_topk_score_ties_from_distinct_logits(gpu, score_func):
+    """Distinct logits whose fp32 scores are equal (sigmoid saturates to 1.0
+    above 17.5; softmax underflows to 0 far below the row max): the picks
+    follow the scores, ties to the lower id, as topk on the scores does
+    (model.py:574-579), not the order of the logits."""
+    from sglang_lite_amd import moe as M
+
+    rng = np.random.default_rng(77)
+    T, E, k = 64, 256, 8
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    for t in range(T):
+        if score_func == "sigmoid":  # 12 saturated logits, shuffled so that id order != logit order
+            cols = rng.choice(E, 12, replace=False)
+            logits[t, cols] = rng.uniform(18.0, 30.0, 12).astype(np.float32)
+        else:  # three dominant logits, the rest far enough below to underflow
+            logits[t] = rng.uniform(-70.0, -60.0, E).astype(np.float32)
+            logits[t, rng.choice(E, 3, replace=False)] = [52.0, 51.0, 50.0]
+    scores = OM.route_scores(logits, score_func)
+    top = -np.sort(-scores, axis=1)
+    assert np.all(top[:, k - 1] == top[:, k])  # the k-th pick is tied in every row
+    w_ref, ids_ref = OM.route_topk(logits, k, score_func)
+    w, ids = M.route_topk(to_dev_f32(logits, gpu), k, score_func)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_allclose(w.cpu().numpy(), w_ref, rtol=2e-6, atol=1e-7)
+
+
 def test_route_topk_matches_torch_topk(gpu):
     """Library routine pin: torch.topk on torch.softmax scores (CPU)."""
     from sglang_lite_amd import moe as M
@@ -286,11 +313,16 @@ def _gate_case(rng, T, H, E, scale=None):
     (32, 256, 8, 2, "sigmoid", True),
     (1000, 512, 256, 8, "sqrtsoftplus", False),
     (7, 4096, 256, 8, "softmax", True),
-    (4100, 1024, 256, 8, "sqrtsoftplus", True),  # LDS-staged 32 x 128 tiles, a ragged last tile
+    # 2 x 2 wavefronts over 64-deep stages
+    (4100, 1024, 256, 8, "sqrtsoftplus", True),  # 32 x 128 tiles, a ragged last tile
     (8200, 512, 256, 8, "sqrtsoftplus", False),  # 64 x 128 tiles
+    (8200, 192, 256, 8, "sigmoid", True),  # 64 x 128 tiles, H % 128 == 64
+    (4100, 320, 256, 8, "sigmoid", True),  # 32 x 128 tiles, H % 128 == 64
+    (2050, 320, 256, 8, "sqrtsoftplus", False),  # 32 x 64 tiles (H % 128 == 64)
+    (513, 64, 72, 4, "sigmoid", True),  # 32 x 32 tiles (H % 128 == 64), one stage
+    # K split over the wavefronts, 128-deep stages (also (300, 1024, ...) and (1000, 512, ...) above)
     (2050, 1024, 256, 8, "sigmoid", True),  # 32 x 64 tiles
-    (600, 256, 200, 8, "sqrtsoftplus", True),  # 32 x 32 tiles, E past the last tile, 4 stages
-    (513, 64, 72, 4, "sigmoid", True),  # one 64-deep stage
+    (600, 256, 200, 8, "sqrtsoftplus", True),  # 32 x 32 tiles, E past the last tile, 2 stages
     (400, 96, 64, 4, "softmax", False),  # H % 64 != 0: the register-loaded kernel
 ])
 def test_gate_kernel_matches_oracle(gpu, T, H, E, k, score_func, use_bias):
