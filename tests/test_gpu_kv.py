@@ -63,11 +63,12 @@ def test_pack_layout_a_bit_exact(gpu, dtype, mode, T, monkeypatch):
     np.testing.assert_array_equal(pages2.cpu().numpy(), OK.to_paged_hnd(ref, 64))
 
 
-@pytest.mark.parametrize("page,T", [(16, 100), (48, 97), (40, 90), (64, 128), (128, 300)])
+@pytest.mark.parametrize("page,T", [(16, 100), (48, 97), (40, 90), (64, 128), (128, 300), (7, 30),
+                                    (2, 5)])
 def test_pack_paged_page_sizes_and_strided_rows(gpu, page, T):
-    """Footer pages at several page sizes (multiples of 16 take the
-    16-rows-per-wavefront kernel, 40 the row kernel), a ragged last page, and
-    input rows that are a view of a wider [T, 576] buffer (row stride 576)."""
+    """Footer pages at several page sizes (odd ones among them), a ragged
+    last page, and input rows that are a view of a wider [T, 576] buffer (row
+    stride 576)."""
     from sglang_lite_amd import dsv4_kv_pack as KVP
 
     print(f"paged pack page={page} T={T}", flush=True)
