@@ -3008,14 +3008,27 @@ __global__ __launch_bounds__(splitk::NT) void gemm_splitk_kernel(const GemmArgs 
   const int g4 = lane >> 4, r16 = lane & 15;
   const int64_t M = args.M, N = args.N, K = args.K;
   const int KB = (int)(K / 128);
-  // workgroup -> (column tile t, split s): consecutive workgroups (which the
-  // dispatcher spreads over the XCDs) take consecutive tiles of one split
+  // workgroup -> (row tile mt, split s, column tile t): consecutive
+  // workgroups (which the dispatcher spreads over the XCDs) take consecutive
+  // tiles of one split
   const int n_tiles = (int)(N / BN);
-  const int s = blockIdx.x / n_tiles;
-  const int t = blockIdx.x - s * n_tiles;
+  const int rest = blockIdx.x / n_tiles;
+  const int t = blockIdx.x - rest * n_tiles;
+  const int mt = rest / sk.S;
+  const int s = rest - mt * sk.S;
+  const int64_t m0 = (int64_t)mt * ROWS;
   const int kb0 = s * KS;
   const int nkb = min(KS, KB - kb0);  // >= 1: S = ceil(KB / KS)
   const int64_t n0 = (int64_t)t * BN;
+  // [gate | up] of an expert record: columns past n_split are the up half
+  const bool second = args.bsrc != nullptr && n0 >= args.n_split;
+  const uint8_t* bmat = args.b;
+  const void* sbm = args.sb;
+  if (args.bsrc) {
+    bmat = uniform_ptr(second ? args.bsrc->w_up : args.bsrc->w_gate);
+    sbm = uniform_ptr(second ? args.bsrc->s_up : args.bsrc->s_gate);
+  }
+  const int64_t nl = second ? n0 - args.n_split : n0;
   const int rr = lane >> 3, pc = lane & 7;
 
   // the A slice: one DMA moves rows 8h..8h+7 of K block kl (lane: row
@@ -3031,7 +3044,7 @@ __global__ __launch_bounds__(splitk::NT) void gemm_splitk_kernel(const GemmArgs 
     if (q < NDA) {
       const int kl = q / (ROWS / 8), h8 = q - kl * (ROWS / 8);
       const int r = h8 * 8 + rr;
-      const int64_t row = r < M ? r : M - 1;
+      const int64_t row = m0 + r < M ? m0 + r : M - 1;
       const int kb = kb0 + (kl < nkb ? kl : 0);
       dma16v((uint64_t)(uintptr_t)args.a + (uint64_t)(row * K + (int64_t)kb * 128) +
                  (uint32_t)((pc ^ swz(r & 15)) << 4),
@@ -3050,7 +3063,7 @@ __global__ __launch_bounds__(splitk::NT) void gemm_splitk_kernel(const GemmArgs 
     if (q < NDS) {
       const int i = q * 64 + lane;
       const int r = i / KS, kl = i - r * KS;
-      const int64_t row = r < M ? r : M - 1;
+      const int64_t row = m0 + r < M ? m0 + r : M - 1;
       const int kb = kb0 + (kl < nkb ? kl : 0);
       if (args.sa_e8m0)  // e8m0 scales: the aligned dword holding the byte
         dma4v((uint64_t)(uintptr_t)args.sa + (uint64_t)((row * KB + kb) & ~(int64_t)3),
@@ -3060,19 +3073,19 @@ __global__ __launch_bounds__(splitk::NT) void gemm_splitk_kernel(const GemmArgs 
               __builtin_amdgcn_readfirstlane(sa_lds + (uint32_t)(q * 256)));
     }
   }
-  const int64_t idx0 = (n0 / 128) * KB + kb0;
+  const int64_t idx0 = (nl / 128) * KB + kb0;
   if (wave == NW - 1) {
     const uint32_t sk_lds = __builtin_amdgcn_readfirstlane(lds_u32(sSk));
     if (args.sb_e8m0) {
       const int nd = (int)((idx0 & 3) + nkb + 3) / 4;
       if (lane < nd)
-        dma4v((uint64_t)(uintptr_t)args.sb + (uint64_t)((idx0 & ~(int64_t)3) + 4 * lane), sk_lds);
+        dma4v((uint64_t)(uintptr_t)sbm + (uint64_t)((idx0 & ~(int64_t)3) + 4 * lane), sk_lds);
     } else if (lane < nkb) {
-      dma4v((uint64_t)(uintptr_t)args.sb + (uint64_t)(idx0 + lane) * 4u, sk_lds);
+      dma4v((uint64_t)(uintptr_t)sbm + (uint64_t)(idx0 + lane) * 4u, sk_lds);
     }
   }
   // B: column n0 + 16 wave + r16, K bytes [32 g4, +32) of each block
-  const uint8_t* brow = args.b + (n0 + 16 * wave + r16) * K + 32 * g4;
+  const uint8_t* brow = bmat + (nl + 16 * wave + r16) * K + 32 * g4;
   v8i bf[KS];
 #pragma unroll
   for (int kl = 0; kl < KS; ++kl) bf[kl] = load_frag_global(brow + (int64_t)(kb0 + (kl < nkb ? kl : 0)) * 128);
@@ -3103,7 +3116,7 @@ __global__ __launch_bounds__(splitk::NT) void gemm_splitk_kernel(const GemmArgs 
 #pragma unroll
         for (int mi = 0; mi < TM; ++mi) {
           const int row = 16 * mi + r16;
-          const int src = row < M ? row : (int)M - 1;
+          const int64_t src = m0 + row < M ? m0 + row : M - 1;
           const int sae = (int)((__float_as_uint(sSa[row * KS + kl]) >>
                                  (((uint32_t)(src * KB + kb0 + kl) & 3u) * 8u)) & 0xFFu);
           const v4f p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[mi], bf[kl], vzero, 0, 0, 0, sae, 0,
@@ -3129,7 +3142,7 @@ __global__ __launch_bounds__(splitk::NT) void gemm_splitk_kernel(const GemmArgs 
   for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = 16 * mi + 4 * g4 + r;
+      const int64_t row = m0 + 16 * mi + 4 * g4 + r;
       if (row < M) part[row * N + col] = acc[mi][r];
     }
 }
@@ -3163,10 +3176,20 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 }
 
 template <int KS, int TM>
+int launch_splitk_gemm(GemmArgs& a, int S, float* part, hipStream_t stream) {
+  const SplitKArgs sk{part, S};
+  const int n_tiles = (int)(a.N / splitk::BN);
+  const int m_tiles = (int)ceil_div(a.M, (int64_t)(16 * TM));
+  gemm_splitk_kernel<KS, TM><<<(unsigned)(n_tiles * S * m_tiles), splitk::NT, 0, stream>>>(a, sk);
+  return check_launch("gemm_fp8_splitk");
+}
+
+template <int KS, int TM>
 int launch_splitk_ks(GemmArgs& a, int S, float* part, hipStream_t stream) {
   const SplitKArgs sk{part, S};
   const int n_tiles = (int)(a.N / splitk::BN);
-  gemm_splitk_kernel<KS, TM><<<(unsigned)(n_tiles * S), splitk::NT, 0, stream>>>(a, sk);
+  const int m_tiles = (int)ceil_div(a.M, (int64_t)(16 * TM));
+  gemm_splitk_kernel<KS, TM><<<(unsigned)(n_tiles * S * m_tiles), splitk::NT, 0, stream>>>(a, sk);
   int rc = check_launch("gemm_fp8_splitk");
   if (rc) return rc;
   const int64_t MN = a.M * a.N;
@@ -3237,6 +3260,150 @@ int try_splitk(GemmArgs& a, hipStream_t stream) {
 }
 
 }  // namespace
+
+namespace {
+
+// The shared expert's [gate | up] partials summed in split order (as
+// splitk_reduce_kernel sums them), then the gate/up epilogue of the grouped
+// kernel on each 128-column group: gate and up rounded to bf16, the SwiGLU
+// clamp, h = bf16(silu(gate) * up) (routing weight 1), and the 1x128 requant
+// of h.  16 lanes per (row, group), 8 columns each; 16 groups per workgroup.
+template <int MODE>
+__global__ __launch_bounds__(256) void shared_swiglu_kernel(const float* __restrict__ part, int S,
+                                                            int64_t T, int64_t I,
+                                                            const int32_t* __restrict__ shared_base,
+                                                            float lim, uint8_t* __restrict__ hq,
+                                                            float* __restrict__ hs) {
+  const int64_t NB = I / 128;
+  const int64_t task = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);  // (row, group)
+  const int j = threadIdx.x & 15;
+  const bool live = task < T * NB;  // the tail's 16-lane groups stay for the shuffles
+  const int64_t t = live ? task / NB : 0, g = live ? task - (task / NB) * NB : 0;
+  const int64_t N = 2 * I, MN = T * N;
+  const float* pg = part + t * N + g * 128 + 8 * j;
+  float gs[8], us[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) gs[i] = us[i] = 0.0f;
+  for (int sp = 0; sp < S; ++sp) {
+    const float4 g0 = *reinterpret_cast<const float4*>(pg + sp * MN);
+    const float4 g1 = *reinterpret_cast<const float4*>(pg + sp * MN + 4);
+    const float4 u0 = *reinterpret_cast<const float4*>(pg + sp * MN + I);
+    const float4 u1 = *reinterpret_cast<const float4*>(pg + sp * MN + I + 4);
+    const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      gs[i] = sp ? gs[i] + gv[i] : gv[i];
+      us[i] = sp ? us[i] + uv[i] : uv[i];
+    }
+  }
+  float f[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float gt = bf16_round(gs[i]);
+    float up = bf16_round(us[i]);
+    if (lim > 0.0f) {
+      up = clampf_(up, -lim, lim);
+      gt = gt > lim ? lim : gt;
+    }
+    const float ex = __builtin_amdgcn_exp2f(gt * -1.4426950408889634f);
+    const float silu = gt * __builtin_amdgcn_rcpf(1.0f + ex);
+    f[i] = bits_f32((uint32_t)bf16_bits_exact(silu * up) << 16);
+  }
+  float amax = 0.0f;  // IEEE maximum: a NaN makes the group's scale NaN
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = __builtin_elementwise_maximum(amax, fabsf(f[i]));
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) amax = __builtin_elementwise_maximum(amax, __shfl_xor(amax, o, 64));
+  if (!live) return;
+  const float sf = group_scale(MODE, amax);
+  const int64_t p = (int64_t)*shared_base + t;
+  *reinterpret_cast<uint2*>(hq + p * I + g * 128 + 8 * j) = quant8_e4m3(MODE, f, sf);
+  if (j == 0) hs[p * NB + g] = sf;
+}
+
+// Split plan of the shared gate/up ([gate | up] = N = 2I columns, K = H):
+// 32-row tiles up to T = 32, else 64; about 256 workgroups; at most as many
+// splits as `room` bytes of partials hold.  T <= 128: at T = 256 (128 tiles
+// of the grouped kernel) four splits measured no faster (H = 4096, I = 2048:
+// the partials' traffic takes what the extra workgroups gain), at T = 64 the
+// FP4 decode layer is 14-16 us faster.
+bool shared_split_plan(int64_t T, int64_t H, int64_t I, size_t room, int* tm, int* ks, int* sp) {
+  using namespace splitk;
+  if (T < 1 || T > 128 || (2 * I) % BN != 0 || H % 128 != 0) return false;
+  const int TM = T <= 32 ? 2 : 4;
+  const int64_t m_tiles = ceil_div(T, (int64_t)(16 * TM));
+  const int KB = (int)(H / 128);
+  const int64_t tiles = (2 * I / BN) * m_tiles;
+  const int64_t s_target = tiles >= 256 ? 1 : 256 / tiles;
+  const int64_t s_room = (int64_t)(room / ((size_t)T * (size_t)(2 * I) * 4));
+  int KS = (int)ceil_div((int64_t)KB, std::min<int64_t>(s_target, s_room > 0 ? s_room : 1));
+  KS = (int)std::max<int64_t>(KS, ceil_div((int64_t)KB, (int64_t)SMAX));
+  if (KS > KSMAX) return false;
+  const int S = (int)ceil_div((int64_t)KB, (int64_t)KS);
+  if (S < 2 || (int64_t)S > s_room) return false;
+  *tm = TM;
+  *ks = KS;
+  *sp = S;
+  return true;
+}
+
+template <int TM>
+int launch_shared_splitk(GemmArgs& a, int KS, int S, float* part, hipStream_t stream) {
+  switch (KS) {
+    case 1: return launch_splitk_gemm<1, TM>(a, S, part, stream);
+    case 2: return launch_splitk_gemm<2, TM>(a, S, part, stream);
+    case 3: return launch_splitk_gemm<3, TM>(a, S, part, stream);
+    case 4: return launch_splitk_gemm<4, TM>(a, S, part, stream);
+    case 5: return launch_splitk_gemm<5, TM>(a, S, part, stream);
+    case 6: return launch_splitk_gemm<6, TM>(a, S, part, stream);
+    case 7: return launch_splitk_gemm<7, TM>(a, S, part, stream);
+    default: return launch_splitk_gemm<8, TM>(a, S, part, stream);
+  }
+}
+
+}  // namespace
+
+int launch_shared_gate_up_split(const GemmArgs& sh, void* part, size_t part_bytes,
+                                const int32_t* shared_base, hipStream_t stream) {
+  int TM = 0, KS = 0, S = 0;
+  if (!part || !aligned(part, 16) || sh.wfmt != WF_FP8 ||
+      !shared_split_plan(sh.T, sh.K, sh.N, part_bytes, &TM, &KS, &S))
+    return kSharedNoSplit;
+  GemmArgs a = {};
+  a.a = sh.a;
+  a.sa = sh.sa;
+  a.wfmt = WF_FP8;
+  a.M = sh.T;
+  a.N = 2 * sh.N;
+  a.K = sh.K;
+  a.bsrc = sh.experts;  // the shared expert's record: the kernel reads its pointers
+  a.n_split = sh.N;
+  float* p = reinterpret_cast<float*>(part);
+  const int rc = TM == 2 ? launch_shared_splitk<2>(a, KS, S, p, stream)
+                         : launch_shared_splitk<4>(a, KS, S, p, stream);
+  if (rc) return rc;
+  const int64_t tasks = sh.T * (sh.N / 128);
+  const unsigned g = (unsigned)ceil_div(tasks, (int64_t)16);
+  switch (sh.scale_mode) {
+    case SCALE_TORCH_FP32:
+      shared_swiglu_kernel<SCALE_TORCH_FP32><<<g, 256, 0, stream>>>(p, S, sh.T, sh.N, shared_base,
+                                                                    sh.swiglu_limit, sh.hq, sh.hs);
+      break;
+    case SCALE_TORCH_UE8M0:
+      shared_swiglu_kernel<SCALE_TORCH_UE8M0><<<g, 256, 0, stream>>>(p, S, sh.T, sh.N, shared_base,
+                                                                     sh.swiglu_limit, sh.hq, sh.hs);
+      break;
+    case SCALE_TILELANG_FP32:
+      shared_swiglu_kernel<SCALE_TILELANG_FP32><<<g, 256, 0, stream>>>(p, S, sh.T, sh.N, shared_base,
+                                                                       sh.swiglu_limit, sh.hq, sh.hs);
+      break;
+    default:
+      shared_swiglu_kernel<SCALE_TILELANG_UE8M0><<<g, 256, 0, stream>>>(p, S, sh.T, sh.N, shared_base,
+                                                                        sh.swiglu_limit, sh.hq, sh.hs);
+  }
+  return check_launch("moe_shared_gate_up_split");
+}
 
 size_t dense_fp8_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   int KS = 0, S = 0;

@@ -898,7 +898,9 @@ struct MoeWorkspace {
   int32_t* slot_pos;
   uint8_t* hq;
   float* hs;
-  uint16_t* out;
+  uint16_t* out;      // the down projection's rows; before down runs, the FP4
+                      // layer's shared gate/up split-K partials (same stream)
+  size_t out_bytes;
   int32_t* tile_ctr;  // [4][8] per-XCD tile counters of the gate/up and down GEMMs
                       // (routed + shared, or one launch each)
   size_t bytes;
@@ -925,6 +927,7 @@ MoeWorkspace carve(void* base, int64_t T, int64_t H, int64_t I, int E, int k, in
   w.slot_pos = reinterpret_cast<int32_t*>(take(P * 4));
   w.hq = take(rows * I);
   w.hs = reinterpret_cast<float*>(take(rows * (I / 128) * 4));
+  w.out_bytes = (size_t)(T * (k + has_shared) * H * 2);
   w.out = reinterpret_cast<uint16_t*>(take(T * (k + has_shared) * H * 2));
   w.tile_ctr = reinterpret_cast<int32_t*>(take(kTileCtrs * 4));
   w.bytes = (size_t)off;
@@ -1012,7 +1015,7 @@ int run_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I
                 const int32_t* offsets, const int32_t* sorted_slot, const float* route_w,
                 const sgl_expert_ptrs* experts, int has_shared, int expert_format,
                 float swiglu_limit, int scale_mode, void* hq, float* hs, int* tile_ctr,
-                hipStream_t stream) {
+                hipStream_t stream, void* part = nullptr, size_t part_bytes = 0) {
   int rc = check_moe_shapes("moe_gate_up", T, H, I, E, k, expert_format);
   if (rc) return rc;
   SGL_REQUIRE(scale_mode >= 0 && scale_mode <= 3, "moe_gate_up: bad scale_mode %d", scale_mode);
@@ -1058,6 +1061,14 @@ int run_gate_up(const void* xq, const float* xs, int64_t T, int64_t H, int64_t I
   sh.wfmt = WF_FP8;
   sh.sb_pow2 = pow2w;
   sh.tile_ctr = tile_ctr ? tile_ctr + 8 : nullptr;
+  // at decode sizes the shared expert's weight stream split over K, so about
+  // one workgroup per CU carries it (its tiles alone are 32), in the
+  // caller's spare space; the grouped launch otherwise
+  if (part) {
+    if ((rc = launch_gemm(KIND_GATE_UP, g, g.T * g.k / g.E, stream))) return rc;
+    rc = launch_shared_gate_up_split(sh, part, part_bytes, offsets + E, stream);
+    return rc == kSharedNoSplit ? launch_gemm(KIND_GATE_UP, sh, T, stream) : rc;
+  }
   return run_routed_and_shared(KIND_GATE_UP, g, sh, T, stream);
 }
 
@@ -1285,7 +1296,7 @@ int sgl_moe_forward(const void* x, int64_t T, int64_t H, int64_t I, int E, int k
     return rc;
   if ((rc = sgl::run_gate_up(w.xq, w.xs, T, H, I, E, k, w.offsets, w.sorted_slot, weights, experts,
                              has_shared, expert_format, swiglu_limit, scale_mode, w.hq, w.hs,
-                             w.tile_ctr, st)))
+                             w.tile_ctr, st, w.out, w.out_bytes)))
     return rc;
   if ((rc = sgl::run_down(w.hq, w.hs, T, H, I, E, k, w.offsets, w.sorted_slot, experts, has_shared,
                           expert_format, scale_mode, w.out, w.tile_ctr + 16, st)))
@@ -1325,7 +1336,7 @@ int sgl_moe_forward_local(const void* x, int64_t T, int64_t H, int64_t I, int E,
     return rc;
   if ((rc = sgl::run_gate_up(w.xq, w.xs, T, H, I, E, k, w.offsets, w.sorted_slot, weights, experts,
                              has_shared, expert_format, swiglu_limit, scale_mode, w.hq, w.hs,
-                             w.tile_ctr, st)))
+                             w.tile_ctr, st, w.out, w.out_bytes)))
     return rc;
   if ((rc = sgl::run_down(w.hq, w.hs, T, H, I, E, k, w.offsets, w.sorted_slot, experts, has_shared,
                           expert_format, scale_mode, w.out, w.tile_ctr + 16, st)))

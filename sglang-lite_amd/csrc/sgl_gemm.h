@@ -53,6 +53,11 @@ struct GemmArgs {
   int* tile_ctr;    // moe: 8 zeroed per-XCD tile counters -> dynamic tile order (null: static)
   void* ws;         // dense: the caller's workspace (split-K partials), or null
   size_t ws_bytes;
+  // split-K over the [gate | up] weights of one expert record (device memory,
+  // read by the kernel; the shared gate/up of an FP4 layer): columns [0,
+  // n_split) are w_gate / s_gate, [n_split, N) w_up / s_up at column - n_split
+  const sgl_expert_ptrs* bsrc;
+  int64_t n_split;
 };
 
 int launch_gemm(int kind, GemmArgs& args, int64_t rows_hint, hipStream_t stream);
@@ -60,5 +65,16 @@ int launch_gemm(int kind, GemmArgs& args, int64_t rows_hint, hipStream_t stream)
 // Bytes of workspace the dense FP8 GEMM of this shape uses (its split-K
 // partials; 0 when the shape does not split).  A function of the shape only.
 size_t dense_fp8_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+// The FP8 shared expert's gate/up in an FP4 layer at decode sizes (T <= 128),
+// split over K so that about one workgroup per CU streams its weights: the
+// fp32 partials of [gate | up] go to `part` (at most part_bytes), then the
+// split-ordered sum, SwiGLU and 1x128 requant write hq / hs rows from
+// *shared_base (offsets[E], read on the device).  `sh` is the shared launch's
+// arguments (experts[E], xq / xs, scale mode, SwiGLU limit).  Returns
+// kSharedNoSplit when the shape or the space does not split.
+constexpr int kSharedNoSplit = 1;
+int launch_shared_gate_up_split(const GemmArgs& sh, void* part, size_t part_bytes,
+                                const int32_t* shared_base, hipStream_t stream);
 
 }  // namespace sgl
