@@ -133,17 +133,6 @@ void sparse_attn_kernel(const AttnArgs a) {
       }
   }
 
-  // Q^T B operand: lane (head c32, half g2) of step ks holds
-  // q[h0 + c32][256 dh + 16 ks + 8 g2, +8); the two token halves share it
-  {
-    const int h = min(h0 + c32, a.Hh - 1);
-    const uint16_t* qrow = a.q + ((b * a.M + m) * a.Hh + h) * (int64_t)kD + 256 * dh + 8 * g2;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int ks = 8 * th + k;
-      sQ[hg][dh][ks][lane] = *reinterpret_cast<const uint4*>(qrow + 16 * ks);
-    }
-  }
   v16f acc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -238,6 +227,20 @@ void sparse_attn_kernel(const AttnArgs a) {
   int32_t ids = jb < nblk ? check_id(jb, load_ids(jb)) : -1;
   int32_t ids_next = jb < nblk ? load_ids(jb + 1 < nblk ? jb + 1 : jb) : -1;  // raw (none when K == 0)
   load_rows(ids);
+  // Q^T B operand: lane (head c32, half g2) of step ks holds
+  // q[h0 + c32][256 dh + 16 ks + 8 g2, +8); the two token halves share it.
+  // Loaded after the first rows' gathers are issued, so its memory latency
+  // overlaps theirs instead of preceding the index load (the decode shapes'
+  // start of a workgroup: three round trips before the first block, now two)
+  {
+    const int h = min(h0 + c32, a.Hh - 1);
+    const uint16_t* qrow = a.q + ((b * a.M + m) * a.Hh + h) * (int64_t)kD + 256 * dh + 8 * g2;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int ks = 8 * th + k;
+      sQ[hg][dh][ks][lane] = *reinterpret_cast<const uint4*>(qrow + 16 * ks);
+    }
+  }
   for (int j = jb; j < nblk; ++j) {
     const uint64_t valid = __ballot(ids >= 0);
     __syncthreads();  // the previous block's tile is consumed
