@@ -243,6 +243,90 @@ def test_layer_stages_at_full_size(gpu, experts, T, kind):
     experts.cache.clear()
 
 
+@pytest.mark.parametrize("frag", [False, True])
+def test_fp4_prefill_T8192_stages(gpu, experts, frag):
+    """MXFP4 routed experts (the reference's live format) with the FP8 shared
+    expert at the prefill shape, T = 8192, uniform routing, row-major tiles
+    or the register-fed kernels over fragment-layout copies: the integer
+    stages bit-exact, the one-call layer equal to the stages, the hottest,
+    coldest and a one-row expert's requantized h and down GEMM (on the
+    device's own h) against the oracle, the shared expert's first 256 rows,
+    and the combine exact given the device's rows."""
+    from sglang_lite_amd import kernel as K
+    from sglang_lite_amd import moe as M
+
+    print(f"fp4 prefill T=8192 uniform, frag={frag}", flush=True)
+    rng = np.random.default_rng(8192 + frag)
+    T = 8192
+    g = torch.Generator(device=gpu)
+    g.manual_seed(19)
+    u8t = torch.uint8
+    w13 = torch.randint(0, 256, (E, 2, I, H // 2), dtype=u8t, device=gpu, generator=g)
+    s13 = torch.randint(119, 122, (E, 2, I, H // 32), dtype=u8t, device=gpu, generator=g)
+    w2 = torch.randint(0, 256, (E, H, I // 2), dtype=u8t, device=gpu, generator=g)
+    s2 = torch.randint(119, 122, (E, H, I // 32), dtype=u8t, device=gpu, generator=g)
+    e8 = torch.float8_e8m0fnu
+    ent = [(w13[e, 0], w13[e, 1], w2[e], s13[e, 0].view(e8), s13[e, 1].view(e8), s2[e].view(e8))
+           for e in range(E)]
+    table = M.ExpertTable.build(ent, tuple(experts.table.keep[-6:]), frag_layout=frag)
+    x = bf16_values(rng, (T, H))
+    draw = lambda n: rng.standard_normal((n, E)).astype(np.float32)  # noqa: E731
+    w, ids, w_ref, ids_ref = _route(gpu, _untie(rng, draw(T), draw))
+    xd = to_dev_bf16(x, gpu)
+    xq, xs = K.act_quant(xd)
+    counts, offsets, sorted_slot, slot_pos = M.permute(ids, E)
+    hq, hs = M.gate_up(xq, xs, offsets, sorted_slot, w.reshape(-1), table, K_TOP)
+    out = M.down(hq, hs, offsets, sorted_slot, table, T, K_TOP)
+    y = M.combine(out, ids, True)
+    y_layer = M.moe_forward(xd, ids, w, table)
+    torch.cuda.synchronize()
+    perm = OM.permute(ids_ref, E)
+    for name, dev in (("counts", counts), ("offsets", offsets), ("sorted_slot", sorted_slot),
+                      ("slot_pos", slot_pos)):
+        np.testing.assert_array_equal(dev.cpu().numpy(), perm[name], err_msg=name)
+    np.testing.assert_array_equal(u8(y), u8(y_layer))
+
+    def host(e):
+        return {"fmt": "fp4", "w1": u8(w13[e, 0]), "w3": u8(w13[e, 1]), "w2": u8(w2[e]),
+                "s1": u8(s13[e, 0]), "s3": u8(s13[e, 1]), "s2": u8(s2[e])}
+
+    cnt = perm["counts"]
+    nz = np.nonzero(cnt)[0]
+    sample = {int(nz[np.argmax(cnt[nz])]), int(nz[np.argmin(cnt[nz])])}
+    ones = np.nonzero(cnt == 1)[0]
+    if ones.size:
+        sample.add(int(ones[0]))
+    hq_n, hs_n, out_n = u8(hq), f32(hs), f32(out)
+    for e in sorted(sample):
+        p0, p1 = perm["offsets"][e], perm["offsets"][e + 1]
+        sl = perm["sorted_slot"][p0:p1]
+        tok, top = sl // K_TOP, sl % K_TOP
+        he = host(e)
+        tr = {}
+        ref = OM.expert_forward(x[tok], he, w_ref[tok, top][:, None], trace=tr)
+        assert_requant_close(hq_n[p0:p1], hs_n[p0:p1], tr["hq"], tr["hs"], f"fp4 h expert {e} ({p1 - p0} rows)")
+        assert_gemm_close(out_n[tok, top], F4.fp4_gemm(hq_n[p0:p1], hs_n[p0:p1], he["w2"], he["s2"]),
+                          f"fp4 down expert {e} on the device's h ({p1 - p0} rows)")
+        assert_layer_close(out_n[tok, top], ref, f"fp4 expert {e} vs the oracle's expert")
+    P = T * K_TOP
+    n_sh = 256
+    tr = {}
+    ref = OM.expert_forward(x[:n_sh], experts.host("shared"), None, trace=tr)
+    assert_requant_close(hq_n[P:P + n_sh], hs_n[P:P + n_sh], tr["hq"], tr["hs"], "h shared")
+    exs = experts.host("shared")
+    assert_gemm_close(out_n[:n_sh, K_TOP], OM.fp8_gemm(hq_n[P:P + n_sh], hs_n[P:P + n_sh], exs["w2"],
+                                                        exs["s2"]), "down shared on the device's h")
+    order = np.argsort(ids_ref, axis=1, kind="stable")
+    acc = np.zeros((T, H), np.float32)
+    for jj in range(K_TOP):
+        acc = (acc + np.take_along_axis(out_n[:, :K_TOP], order[:, jj][:, None, None], 1)[:, 0]
+               ).astype(np.float32)
+    acc = (acc + out_n[:, K_TOP]).astype(np.float32)
+    np.testing.assert_array_equal(f32(y).view(np.uint32), Q.bf16_round(acc).view(np.uint32))
+    del table, w13, w2
+    experts.cache.clear()
+
+
 @pytest.mark.parametrize("M_", [1024, 4096])
 def test_dense_gemm_config_shape(gpu, experts, M_):
     """N = 4096, K = 7168: the 128 x 128 (M = 1024) and 128 x 256 (M = 4096)
