@@ -230,8 +230,8 @@ void sparse_attn_kernel(const AttnArgs a) {
   // Q^T B operand: lane (head c32, half g2) of step ks holds
   // q[h0 + c32][256 dh + 16 ks + 8 g2, +8); the two token halves share it.
   // Loaded after the first rows' gathers are issued, so its memory latency
-  // overlaps theirs instead of preceding the index load (the decode shapes'
-  // start of a workgroup: three round trips before the first block, now two)
+  // overlaps theirs: the first block waits for two memory round trips (the
+  // indices, then the rows with Q), not three
   {
     const int h = min(h0 + c32, a.Hh - 1);
     const uint16_t* qrow = a.q + ((b * a.M + m) * a.Hh + h) * (int64_t)kD + 256 * dh + 8 * g2;
