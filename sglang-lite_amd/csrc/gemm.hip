@@ -53,6 +53,10 @@ constexpr int kMaxGroups = 1025;  // 1024 routed experts + shared
 #ifndef SGL_NT_WEIGHTS
 #define SGL_NT_WEIGHTS 1
 #endif
+// MoE tiles of one wavefront row: compute only the 16-row blocks a group fills
+#ifndef SGL_DEAD_SKIP
+#define SGL_DEAD_SKIP 1
+#endif
 
 constexpr int kMaxKB = 128;       // K <= 16384: weight scales of a tile staged in LDS
 
@@ -464,7 +468,7 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
           // loads (same box, T = 64 / 256 / 512: FP8 layer 0.62 / 0.99 /
           // 1.18 ms, FP4 0.43 / 0.68 / 0.85; with nt only for experts that
           // fit in one tile 0.61 / 1.00 / 1.19 and 0.44 / 0.72 / 0.88)
-          if (KIND != KIND_DENSE && BM == 32 && SGL_NT_WEIGHTS)
+          if (KIND != KIND_DENSE && BM <= 64 && SGL_NT_WEIGHTS)
             dma16nt(up_half ? b1 : b0, vo + (uint32_t)st * 128u, sl + (uint32_t)c * 1024u);
           else
             dma16(up_half ? b1 : b0, vo + (uint32_t)st * 128u, sl + (uint32_t)c * 1024u);
@@ -530,14 +534,16 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
         return (int)((raw >> (((uint32_t)(src * KB + st * KS + ks) & 3u) * 8u)) & 0xFFu);
       };
 
-      // a wavefront whose rows all lie past the tile's last row has no work
-      if (computes && (wm * TM) * 16 < rows) {
+      // the MFMAs of the wavefront's first NL 16-row blocks: a tile's rows
+      // past its last are not computed (their outputs are dropped)
+      auto blocks = [&](auto nl_c) __attribute__((always_inline)) {
+        constexpr int NL = decltype(nl_c)::value;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           const uint8_t* tA = stg + ks * (BM * 128);
-          v8i af[TM];
+          v8i af[NL];
 #pragma unroll
-          for (int mi = 0; mi < TM; ++mi) af[mi] = read_frag(tA + (wm * TM + mi) * 16 * 128, fla);
+          for (int mi = 0; mi < NL; ++mi) af[mi] = read_frag(tA + (wm * TM + mi) * 16 * 128, fla);
           if constexpr (!FP4 && LW > 0) {
             // two compute wavefronts share each SIMD (the loaders issue the
             // DMAs), so the MFMAs of one overlap the other's promotion and
@@ -559,9 +565,9 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
             // weight fragment of block nj + 1 is read while the MFMAs of
             // block nj run (two fragment buffers), so no MFMA waits on LDS
             static_assert(C::SA_ROWS == 16, "row-scale slot layout");
-            float sa1[TM];
+            float sa1[NL];
 #pragma unroll
-            for (int mi = 0; mi < TM; ++mi) sa1[mi] = tS[(wm * TM + mi) * 64 + r16];  // fp32 (grouped)
+            for (int mi = 0; mi < NL; ++mi) sa1[mi] = tS[(wm * TM + mi) * 64 + r16];  // fp32 (grouped)
             float sbh[HALVES];
 #pragma unroll
             for (int hv = 0; hv < HALVES; ++hv) sbh[hv] = sSb[KIND == KIND_GATE_UP ? hv : wave_blk][kb];
@@ -569,20 +575,20 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
             bf[0] = read_frag(tB + tile_col(0) * 128, fl);
 #pragma unroll
             for (int hv = 0; hv < HALVES; ++hv) {
-              float ss[TM];
+              float ss[NL];
 #pragma unroll
-              for (int mi = 0; mi < TM; ++mi) ss[mi] = sa1[mi] * sbh[hv];
+              for (int mi = 0; mi < NL; ++mi) ss[mi] = sa1[mi] * sbh[hv];
 #pragma unroll
               for (int nh = 0; nh < TN / HALVES; ++nh) {
                 const int nj = hv * (TN / HALVES) + nh;
                 if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + tile_col(nj + 1) * 128, fl);
-                v4f pr[TM];
+                v4f pr[NL];
 #pragma unroll
-                for (int mi = 0; mi < TM; ++mi)
+                for (int mi = 0; mi < NL; ++mi)
                   pr[mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[nj & 1], af[mi], vzero, 0, 0,
                                                                             0, 0, 0, 0);
 #pragma unroll
-                for (int mi = 0; mi < TM; ++mi)
+                for (int mi = 0; mi < NL; ++mi)
 #pragma unroll
                   for (int r = 0; r < 4; ++r) acc[mi][nj][r] = fmaf(pr[mi][r], ss[mi], acc[mi][nj][r]);
               }
@@ -598,9 +604,9 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
               // 128-column block): the MFMA accumulates in place, no
               // promotion; fp32 weight scales: C += P' sb, which is the
               // promotion's C += P (sa sb) to the bit
-              int sae[TM];
+              int sae[NL];
 #pragma unroll
-              for (int mi = 0; mi < TM; ++mi) sae[mi] = row_exp((wm * TM + mi) * 16 + r16, 0);
+              for (int mi = 0; mi < NL; ++mi) sae[mi] = row_exp((wm * TM + mi) * 16 + r16, 0);
               v8i bf[2];
               bf[0] = read_frag(tB + tile_col(0) * 128, fl);
               if (pow2) {
@@ -609,7 +615,7 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
                 for (int nj = 0; nj < TN; ++nj) {
                   if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + tile_col(nj + 1) * 128, fl);
 #pragma unroll
-                  for (int mi = 0; mi < TM; ++mi)
+                  for (int mi = 0; mi < NL; ++mi)
                     acc[mi][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                         af[mi], bf[nj & 1], acc[mi][nj], 0, 0, 0, sae[mi], 0, sbe);
                 }
@@ -617,22 +623,22 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
 #pragma unroll
                 for (int nj = 0; nj < TN; ++nj) {
                   if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + tile_col(nj + 1) * 128, fl);
-                  v4f pr[TM];
+                  v4f pr[NL];
 #pragma unroll
-                  for (int mi = 0; mi < TM; ++mi)
+                  for (int mi = 0; mi < NL; ++mi)
                     pr[mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[mi], bf[nj & 1], vzero, 0, 0,
                                                                               0, sae[mi], 0, 127);
 #pragma unroll
-                  for (int mi = 0; mi < TM; ++mi)
+                  for (int mi = 0; mi < NL; ++mi)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) acc[mi][nj][r] = fmaf(pr[mi][r], sbv0, acc[mi][nj][r]);
                 }
               }
               continue;
             }
-            float sav[TM][4];
+            float sav[NL][4];
 #pragma unroll
-            for (int mi = 0; mi < TM; ++mi)
+            for (int mi = 0; mi < NL; ++mi)
 #pragma unroll
               for (int r = 0; r < 4; ++r) sav[mi][r] = row_scale((wm * TM + mi) * 16 + 4 * g4 + r, 0);
             // software pipeline: B fragment nj+1 is read while the MFMAs of
@@ -640,31 +646,35 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
             // nj's MFMAs are issued, so neither the LDS latency nor the MFMA
             // latency sits in front of a dependent instruction
             v8i bf[2];
-            v4f pr[2][TM];
+            v4f pr[2][NL];
             bf[0] = read_frag(tB + tile_col(0) * 128, fl);
 #pragma unroll
             for (int nj = 0; nj < TN; ++nj) {
               if (nj + 1 < TN) bf[(nj + 1) & 1] = read_frag(tB + tile_col(nj + 1) * 128, fl);
 #pragma unroll
-              for (int mi = 0; mi < TM; ++mi)
+              for (int mi = 0; mi < NL; ++mi)
                 pr[nj & 1][mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                     af[mi], bf[nj & 1], vzero, 0, 0, 0, 0, 0, 0);
               if (nj > 0) {
                 const float sbv = (KIND == KIND_GATE_UP && nj - 1 >= TN / 2) ? sbv1 : sbv0;
 #pragma unroll
-                for (int mi = 0; mi < TM; ++mi)
+                for (int mi = 0; mi < NL; ++mi) {
+                  // updated as a whole vector, so the accumulators stay in registers
+                  v4f t = acc[mi][nj - 1];
 #pragma unroll
-                  for (int r = 0; r < 4; ++r)
-                    acc[mi][nj - 1][r] =
-                        fmaf(pr[(nj - 1) & 1][mi][r], sav[mi][r] * sbv, acc[mi][nj - 1][r]);
+                  for (int r = 0; r < 4; ++r) t[r] = fmaf(pr[(nj - 1) & 1][mi][r], sav[mi][r] * sbv, t[r]);
+                  acc[mi][nj - 1] = t;
+                }
               }
             }
             const float sbv = (KIND == KIND_GATE_UP && TN - 1 >= TN / 2) ? sbv1 : sbv0;
 #pragma unroll
-            for (int mi = 0; mi < TM; ++mi)
+            for (int mi = 0; mi < NL; ++mi) {
+              v4f t = acc[mi][TN - 1];
 #pragma unroll
-              for (int r = 0; r < 4; ++r)
-                acc[mi][TN - 1][r] = fmaf(pr[(TN - 1) & 1][mi][r], sav[mi][r] * sbv, acc[mi][TN - 1][r]);
+              for (int r = 0; r < 4; ++r) t[r] = fmaf(pr[(TN - 1) & 1][mi][r], sav[mi][r] * sbv, t[r]);
+              acc[mi][TN - 1] = t;
+            }
           } else {
             // fp4 B: lane (r16, g4) of column block nj reads 16 bytes = K
             // [32 g4, 32 g4 + 32) of the step from column tile_col(nj) + r16,
@@ -686,9 +696,9 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
             if constexpr (SAHW) {
               // power-of-two row scales: e8m0 = the fp32 exponent field; both
               // scales are applied inside the MFMA, which accumulates in place
-              int sae[TM];
+              int sae[NL];
 #pragma unroll
-              for (int mi = 0; mi < TM; ++mi) sae[mi] = row_exp((wm * TM + mi) * 16 + r16, ks);
+              for (int mi = 0; mi < NL; ++mi) sae[mi] = row_exp((wm * TM + mi) * 16 + r16, ks);
 #pragma unroll
               for (int nj = 0; nj < TN; ++nj) {
                 if (nj + 1 < TN) {
@@ -696,19 +706,19 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
                   sbb[(nj + 1) & 1] = read_sb(nj + 1);
                 }
 #pragma unroll
-                for (int mi = 0; mi < TM; ++mi)
+                for (int mi = 0; mi < NL; ++mi)
                   acc[mi][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                       af[mi], bf[nj & 1], acc[mi][nj], 0, 4, 0, sae[mi], 0, sbb[nj & 1]);
               }
             } else {
               // fp32 row scales: the weight scales inside the MFMA, the row
               // scale promoted once per 128-deep step as in the fp8 path
-              float sav[TM][4];
+              float sav[NL][4];
 #pragma unroll
-              for (int mi = 0; mi < TM; ++mi)
+              for (int mi = 0; mi < NL; ++mi)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) sav[mi][r] = row_scale((wm * TM + mi) * 16 + 4 * g4 + r, ks);
-              v4f pr[2][TM];
+              v4f pr[2][NL];
 #pragma unroll
               for (int nj = 0; nj < TN; ++nj) {
                 if (nj + 1 < TN) {
@@ -716,25 +726,37 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
                   sbb[(nj + 1) & 1] = read_sb(nj + 1);
                 }
 #pragma unroll
-                for (int mi = 0; mi < TM; ++mi)
+                for (int mi = 0; mi < NL; ++mi)
                   pr[nj & 1][mi] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                       af[mi], bf[nj & 1], vzero, 0, 4, 0, 127, 0, sbb[nj & 1]);
                 if (nj > 0) {
 #pragma unroll
-                  for (int mi = 0; mi < TM; ++mi)
+                  for (int mi = 0; mi < NL; ++mi)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
                       acc[mi][nj - 1][r] = fmaf(pr[(nj - 1) & 1][mi][r], sav[mi][r], acc[mi][nj - 1][r]);
                 }
               }
 #pragma unroll
-              for (int mi = 0; mi < TM; ++mi)
+              for (int mi = 0; mi < NL; ++mi)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                   acc[mi][TN - 1][r] = fmaf(pr[(TN - 1) & 1][mi][r], sav[mi][r], acc[mi][TN - 1][r]);
             }
           }
         }
+      };
+      // a wavefront whose rows all lie past the tile's last row has no work;
+      // with one wavefront row (WM = 1, the decode tiles) a routed group
+      // shorter than the tile computes only the 16-row blocks it fills
+      const int live = rows - wm * TM * 16;
+      if (!computes || live <= 0) return;
+      if constexpr (SGL_DEAD_SKIP && KIND != KIND_DENSE && WM == 1 && TM >= 2) {
+        if (live > (TM / 2) * 16) blocks(std::integral_constant<int, TM>{});
+        else if (TM >= 4 && live > 16) blocks(std::integral_constant<int, (TM >= 4 ? TM / 2 : 1)>{});
+        else blocks(std::integral_constant<int, 1>{});
+      } else {
+        blocks(std::integral_constant<int, TM>{});
       }
     };
 
@@ -3475,6 +3497,13 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
                      : launch_fp4<false>(kind, a, rows_hint, stream);
   }
   const bool big = rows_hint >= 64;
+  // 64-row tiles (a 3-slot ring) from 16 rows per expert on average: the
+  // Zipf head's experts stream their weight slices in half as many tiles,
+  // and the groups shorter than the tile skip the MFMAs of the 16-row blocks
+  // they do not fill (H = 4096, I = 2048, T = 512, same box: 1.157 against
+  // 1.186 ms with 32-row tiles; at T = 64 / 256 the 32-row tiles are faster,
+  // 0.619 / 0.988 against 0.645 / 1.004)
+  const bool tall = !big && rows_hint >= 16;
   // the pipelined prefill kernel: K in [512, 8192] (at least four stages; the
   // tile's weight scales fit its LDS table) and fp32 weight scales
   const bool pipe_ok = SGL_PIPE && a.K >= 512 && a.K <= 128 * pipe::kMaxKBp && !a.sb_e8m0;
@@ -3535,7 +3564,8 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       if (big && pipe_ok)
         return pow2 ? launch_pipe<KIND_GATE_UP, true>(a, stream) : launch_pipe<KIND_GATE_UP, false>(a, stream);
       return big ? launch_cfg<KIND_GATE_UP, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)
-                 : launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 4>(a, stream);
+                 : tall ? launch_cfg<KIND_GATE_UP, 64, 256, 1, 4, 3>(a, stream)
+                        : launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 4>(a, stream);
     default:
       if (shared_narrow) return launch_cfg<KIND_DOWN, 32, 64, 1, 4, 4>(a, stream);
       if (shared_small) return launch_cfg<KIND_DOWN, 32, 256, 1, 4, 4>(a, stream);
@@ -3543,7 +3573,8 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       if (big && pipe_ok)
         return pow2 ? launch_pipe<KIND_DOWN, true>(a, stream) : launch_pipe<KIND_DOWN, false>(a, stream);
       return big ? launch_cfg<KIND_DOWN, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)
-                 : launch_cfg<KIND_DOWN, 32, 256, 1, 4, 4>(a, stream);
+                 : tall ? launch_cfg<KIND_DOWN, 64, 256, 1, 4, 3>(a, stream)
+                        : launch_cfg<KIND_DOWN, 32, 256, 1, 4, 4>(a, stream);
   }
 }
 
