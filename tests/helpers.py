@@ -203,3 +203,21 @@ def assert_requant_close(q_dev: np.ndarray, s_dev: np.ndarray, q_ref: np.ndarray
     assert over == 0, f"{what}: {over} values beyond the requantization bound ({st})"
     assert rel <= REL_L2, f"{what}: rel-L2 {rel:.3e} ({st})"
     return st
+
+
+def ids_with_counts(rng, counts, k):
+    """[T, k] expert ids in which expert e appears exactly counts[e] times, k
+    distinct experts per token (each count at most T), tokens shuffled."""
+    pool = np.repeat(np.arange(len(counts)), counts)
+    assert pool.size % k == 0
+    T = pool.size // k
+    assert max(counts) <= T
+    ids = pool.reshape(k, T).T  # token t: pool[t], pool[t + T], ... (distinct: runs are <= T long)
+    return np.ascontiguousarray(ids[rng.permutation(T)]).astype(np.int32)
+
+
+# group sizes on both sides of every 16-row block edge of a decode tile; 16
+# experts, k = 2: 228 slots (14 rows per expert on average: 32-row tiles) and
+# 674 slots (42 on average: 64-row tiles), plus the shared expert's T rows
+EDGE_COUNTS_32 = [1, 15, 16, 17, 31, 32, 33, 0, 47, 2, 3, 4, 5, 6, 7, 9]
+EDGE_COUNTS_64 = [1, 15, 16, 17, 31, 32, 33, 47, 48, 49, 63, 64, 65, 0, 96, 97]

@@ -201,6 +201,29 @@ def test_moe_forward_fp4_experts_matches_oracle(gpu, T, H, I, E, k, shared, lim,
     assert_gemm_close(f32(y), y_ref, f"moe fp4 T={T} H={H} I={I} E={E} k={k} mode={mode}")
 
 
+@pytest.mark.parametrize("mode", [0, 3])
+def test_moe_fp4_group_sizes_at_block_edges(gpu, mode):
+    """FP4 decode tiles (32 rows) compute only the 16-row blocks a group
+    fills: group sizes 0, 1, 15, 16, 17, 31, 32, 33, 47 ... against the oracle."""
+    from sglang_lite_amd import moe as M
+    from helpers import EDGE_COUNTS_32, ids_with_counts
+
+    rng = np.random.default_rng(1234 + mode)
+    H, I, E, k = 512, 256, len(EDGE_COUNTS_32), 2
+    ids = ids_with_counts(rng, EDGE_COUNTS_32, k)
+    T = ids.shape[0]
+    print(f"moe fp4 block edges T={T} E={E} mode={mode}", flush=True)
+    x = bf16_values(rng, (T, H))
+    w = rng.uniform(0.1, 1.0, (T, k)).astype(np.float32)
+    experts = [OM.make_fp4_expert(rng, H, I) for _ in range(E)]
+    sh = OM.make_expert(rng, H, I)
+    table = fp4_table(experts, sh, gpu)
+    y = M.moe_forward(to_dev_bf16(x, gpu), torch.from_numpy(ids).to(gpu), to_dev_f32(w, gpu), table,
+                      scale_mode=mode)
+    y_ref = OM.moe_forward(x, ids, w, experts, sh, mode=mode)
+    assert_gemm_close(f32(y), y_ref, f"moe fp4 block edges mode={mode}")
+
+
 def test_moe_fp4_stages_match_oracle(gpu):
     """gate_up / down with FP4 routed experts, stage by stage: the routed and
     the shared rows of h, and the expert outputs."""

@@ -7,8 +7,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import (assert_gemm_close, bf16_values, f32, to_dev_bf16, to_dev_f32, to_dev_fp8,
-                     u8)
+from helpers import (EDGE_COUNTS_32, EDGE_COUNTS_64, assert_gemm_close, bf16_values, f32,
+                     ids_with_counts, to_dev_bf16, to_dev_f32, to_dev_fp8, u8)
 from oracle import moe as OM
 from oracle import quant as Q
 
@@ -235,6 +235,27 @@ def test_moe_forward_matches_oracle(gpu, T, H, I, E, k, shared, lim, zipf):
                       table, swiglu_limit=lim)
     y_ref = OM.moe_forward(x, ids, w, experts, sh, swiglu_limit=lim)
     assert_gemm_close(f32(y), y_ref, f"moe T={T} H={H} I={I} E={E} k={k}")
+
+
+@pytest.mark.parametrize("counts", [EDGE_COUNTS_32, EDGE_COUNTS_64], ids=["rows32", "rows64"])
+def test_moe_forward_group_sizes_at_block_edges(gpu, counts):
+    """Decode tiles compute only the 16-row blocks a group fills (one, two or
+    four of them): every group size at a block edge against the oracle."""
+    from sglang_lite_amd import moe as M
+
+    rng = np.random.default_rng(sum(counts))
+    H, I, E, k = 256, 256, len(counts), 2
+    ids = ids_with_counts(rng, counts, k)
+    T = ids.shape[0]
+    print(f"moe block edges T={T} E={E} rows/expert={T * k // E}", flush=True)
+    x = bf16_values(rng, (T, H))
+    w = rng.uniform(0.1, 1.0, (T, k)).astype(np.float32)
+    experts = [OM.make_expert(rng, H, I) for _ in range(E)]
+    sh = OM.make_expert(rng, H, I)
+    table = table_from(experts, sh, gpu)
+    y = M.moe_forward(to_dev_bf16(x, gpu), torch.from_numpy(ids).to(gpu), to_dev_f32(w, gpu), table)
+    y_ref = OM.moe_forward(x, ids, w, experts, sh)
+    assert_gemm_close(f32(y), y_ref, f"moe block edges T={T}")
 
 
 def test_moe_forward_big_rows_tile_path(gpu):
