@@ -468,7 +468,7 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
           // loads (same box, T = 64 / 256 / 512: FP8 layer 0.62 / 0.99 /
           // 1.18 ms, FP4 0.43 / 0.68 / 0.85; with nt only for experts that
           // fit in one tile 0.61 / 1.00 / 1.19 and 0.44 / 0.72 / 0.88)
-          if (KIND != KIND_DENSE && BM <= 64 && SGL_NT_WEIGHTS)
+          if (KIND != KIND_DENSE && BM == 32 && SGL_NT_WEIGHTS)
             dma16nt(up_half ? b1 : b0, vo + (uint32_t)st * 128u, sl + (uint32_t)c * 1024u);
           else
             dma16(up_half ? b1 : b0, vo + (uint32_t)st * 128u, sl + (uint32_t)c * 1024u);
@@ -747,13 +747,12 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
         }
       };
       // a wavefront whose rows all lie past the tile's last row has no work;
-      // with one wavefront row (WM = 1, the decode tiles) a routed group
-      // shorter than the tile computes only the 16-row blocks it fills
+      // in the 32-row decode tiles (one wavefront row) a routed group of at
+      // most 16 rows computes only the first 16-row block
       const int live = rows - wm * TM * 16;
       if (!computes || live <= 0) return;
-      if constexpr (SGL_DEAD_SKIP && KIND != KIND_DENSE && WM == 1 && TM >= 2) {
-        if (live > (TM / 2) * 16) blocks(std::integral_constant<int, TM>{});
-        else if (TM >= 4 && live > 16) blocks(std::integral_constant<int, (TM >= 4 ? TM / 2 : 1)>{});
+      if constexpr (SGL_DEAD_SKIP && KIND != KIND_DENSE && WM == 1 && TM == 2) {
+        if (live > 16) blocks(std::integral_constant<int, 2>{});
         else blocks(std::integral_constant<int, 1>{});
       } else {
         blocks(std::integral_constant<int, TM>{});
@@ -3497,13 +3496,6 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
                      : launch_fp4<false>(kind, a, rows_hint, stream);
   }
   const bool big = rows_hint >= 64;
-  // 64-row tiles (a 3-slot ring) from 16 rows per expert on average: the
-  // Zipf head's experts stream their weight slices in half as many tiles,
-  // and the groups shorter than the tile skip the MFMAs of the 16-row blocks
-  // they do not fill (H = 4096, I = 2048, T = 512, same box: 1.157 against
-  // 1.186 ms with 32-row tiles; at T = 64 / 256 the 32-row tiles are faster,
-  // 0.619 / 0.988 against 0.645 / 1.004)
-  const bool tall = !big && rows_hint >= 16;
   // the pipelined prefill kernel: K in [512, 8192] (at least four stages; the
   // tile's weight scales fit its LDS table) and fp32 weight scales
   const bool pipe_ok = SGL_PIPE && a.K >= 512 && a.K <= 128 * pipe::kMaxKBp && !a.sb_e8m0;
@@ -3564,8 +3556,7 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       if (big && pipe_ok)
         return pow2 ? launch_pipe<KIND_GATE_UP, true>(a, stream) : launch_pipe<KIND_GATE_UP, false>(a, stream);
       return big ? launch_cfg<KIND_GATE_UP, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)
-                 : tall ? launch_cfg<KIND_GATE_UP, 64, 256, 1, 4, 3>(a, stream)
-                        : launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 4>(a, stream);
+                 : launch_cfg<KIND_GATE_UP, 32, 256, 1, 4, 4>(a, stream);
     default:
       if (shared_narrow) return launch_cfg<KIND_DOWN, 32, 64, 1, 4, 4>(a, stream);
       if (shared_small) return launch_cfg<KIND_DOWN, 32, 256, 1, 4, 4>(a, stream);
@@ -3573,8 +3564,7 @@ int launch_gemm(int kind, GemmArgs& a, int64_t rows_hint, hipStream_t stream) {
       if (big && pipe_ok)
         return pow2 ? launch_pipe<KIND_DOWN, true>(a, stream) : launch_pipe<KIND_DOWN, false>(a, stream);
       return big ? launch_cfg<KIND_DOWN, 128, 256, 2, SGL_LWN, 3, WF_FP8, false, SGL_LW>(a, stream)
-                 : tall ? launch_cfg<KIND_DOWN, 64, 256, 1, 4, 3>(a, stream)
-                        : launch_cfg<KIND_DOWN, 32, 256, 1, 4, 4>(a, stream);
+                 : launch_cfg<KIND_DOWN, 32, 256, 1, 4, 4>(a, stream);
   }
 }
 

@@ -216,8 +216,9 @@ def ids_with_counts(rng, counts, k):
     return np.ascontiguousarray(ids[rng.permutation(T)]).astype(np.int32)
 
 
-# group sizes on both sides of every 16-row block edge of a decode tile; 16
-# experts, k = 2: 228 slots (14 rows per expert on average: 32-row tiles) and
-# 674 slots (42 on average: 64-row tiles), plus the shared expert's T rows
-EDGE_COUNTS_32 = [1, 15, 16, 17, 31, 32, 33, 0, 47, 2, 3, 4, 5, 6, 7, 9]
-EDGE_COUNTS_64 = [1, 15, 16, 17, 31, 32, 33, 47, 48, 49, 63, 64, 65, 0, 96, 97]
+# group sizes on both sides of every 16-row block edge of a 32-row decode
+# tile, in a group's only tile and in its last one; 16 experts, k = 2: 228
+# and 674 slots (14 and 42 rows per expert on average), plus the shared
+# expert's T rows
+EDGE_COUNTS_SHORT = [1, 15, 16, 17, 31, 32, 33, 0, 47, 2, 3, 4, 5, 6, 7, 9]
+EDGE_COUNTS_LONG = [1, 15, 16, 17, 31, 32, 33, 47, 48, 49, 63, 64, 65, 0, 96, 97]

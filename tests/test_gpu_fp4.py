@@ -206,11 +206,11 @@ def test_moe_fp4_group_sizes_at_block_edges(gpu, mode):
     """FP4 decode tiles (32 rows) compute only the 16-row blocks a group
     fills: group sizes 0, 1, 15, 16, 17, 31, 32, 33, 47 ... against the oracle."""
     from sglang_lite_amd import moe as M
-    from helpers import EDGE_COUNTS_32, ids_with_counts
+    from helpers import EDGE_COUNTS_SHORT, ids_with_counts
 
     rng = np.random.default_rng(1234 + mode)
-    H, I, E, k = 512, 256, len(EDGE_COUNTS_32), 2
-    ids = ids_with_counts(rng, EDGE_COUNTS_32, k)
+    H, I, E, k = 512, 256, len(EDGE_COUNTS_SHORT), 2
+    ids = ids_with_counts(rng, EDGE_COUNTS_SHORT, k)
     T = ids.shape[0]
     print(f"moe fp4 block edges T={T} E={E} mode={mode}", flush=True)
     x = bf16_values(rng, (T, H))
