@@ -94,7 +94,9 @@ __global__ __launch_bounds__(256) void kv_pack_a_kernel(const uint8_t* __restric
                                                         const PageTable pt) {
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * 4;
-  const int64_t w0 = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  // wave-uniform row index: the paging arithmetic and the row branches run
+  // on scalar registers
+  const int64_t w0 = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int shift = page_shift_of(page);
   for (int64_t tb = w0 * R; tb < rows_total; tb += nwaves * R) {
     float f[R][8];
@@ -133,8 +135,7 @@ __global__ __launch_bounds__(256) void kv_pack_a_kernel(const uint8_t* __restric
       float amax = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) amax = __builtin_elementwise_maximum(amax, fabsf(f[r][i]));
-#pragma unroll
-      for (int o = 4; o > 0; o >>= 1) amax = __builtin_elementwise_maximum(amax, __shfl_xor(amax, o, 64));
+      amax = lane_group_max<8>(amax);
       const float sf = group_scale(MODE, amax);
       const uint32_t sbyte = pow2_to_e8m0(sf);
       if (lane < 56) {

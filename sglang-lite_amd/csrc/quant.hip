@@ -29,13 +29,11 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4& v, float* f) {
   }
 }
 
-// IEEE maximum (v_maximum3_f32) over the group's lanes: a NaN element makes
-// the group's amax NaN, as the reference's amax does
+// IEEE maximum (v_maximum_f32) over the group's lanes, by DPP: a NaN element
+// makes the group's amax NaN, as the reference's amax does
 template <int LPG>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int o = LPG / 2; o > 0; o >>= 1) v = __builtin_elementwise_maximum(v, __shfl_xor(v, o, 64));
-  return v;
+  return lane_group_max<LPG>(v);
 }
 
 // R groups per thread and step (group g, g + sweep, ...), loads first, so R

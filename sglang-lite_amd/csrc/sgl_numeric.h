@@ -12,6 +12,8 @@
 #pragma once
 
 #include <stdint.h>
+
+#include <type_traits>
 #if !defined(__HIPCC__)
 #include <math.h>
 #endif
@@ -225,41 +227,71 @@ SGL_HD uint8_t quant_elem(int mode, float x, float sf, float inv) {
 }
 
 #if defined(__HIPCC__)
+// clampf_(x, -448, 448) in three instructions: the median of three for every
+// non-NaN x (the same value, -0 included), x itself for a NaN
+__device__ __forceinline__ float clamp448(float x) {
+  const float c = __builtin_amdgcn_fmed3f(x, -448.0f, 448.0f);
+  return x != x ? x : c;
+}
+// 1 / sf for the ue8m0 modes' scales: a power of two 2^k (normal, so
+// 2^-k is exact, 2^-127 a subnormal) by ldexp; Inf gives +0 and a NaN itself,
+// as the IEEE division does (a quiet NaN divisor is the quotient)
+__device__ __forceinline__ float pow2_recip(float sf) {
+  const int e = (int)((f32_bits(sf) >> 23) & 0xFFu);
+  const float r = __builtin_amdgcn_ldexpf(1.0f, 127 - e);
+  return e == 255 ? (sf != sf ? sf : 0.0f) : r;
+}
+// The maximum over aligned groups of LANES (2, 4, 8 or 16) lanes by DPP
+// moves, NaN-propagating: after the two quad permutations every lane holds
+// its quad's maximum, the half-row mirror (lane i <-> 7 - i) joins the two
+// quads of 8 lanes and the row mirror (i <-> 15 - i) the two halves of 16
+template <int LANES>
+__device__ __forceinline__ float lane_group_max(float v) {
+  static_assert(LANES == 2 || LANES == 4 || LANES == 8 || LANES == 16, "2 to 16 lanes");
+  auto dpp = [](float x, auto ctrl) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x),
+                                                              decltype(ctrl)::value, 0xF, 0xF, false));
+  };
+  using quad_xor1 = std::integral_constant<int, 0xB1>;  // quad_perm [1, 0, 3, 2]
+  using quad_xor2 = std::integral_constant<int, 0x4E>;  // quad_perm [2, 3, 0, 1]
+  using half_mirror = std::integral_constant<int, 0x141>;
+  using row_mirror = std::integral_constant<int, 0x140>;
+  v = __builtin_elementwise_maximum(v, dpp(v, quad_xor1{}));
+  if constexpr (LANES >= 4) v = __builtin_elementwise_maximum(v, dpp(v, quad_xor2{}));
+  if constexpr (LANES >= 8) v = __builtin_elementwise_maximum(v, dpp(v, half_mirror{}));
+  if constexpr (LANES >= 16) v = __builtin_elementwise_maximum(v, dpp(v, row_mirror{}));
+  return v;
+}
+
 // Eight consecutive elements of one group -> e4m3 bytes (little-endian in
 // .x then .y), bit-identical to quant_elem for every mode.  ue8m0 scales are
 // powers of two (or Inf / NaN), so TileLang-ue8m0 and KV divisions equal the
 // product with the exact reciprocal; only TileLang-fp32 divides.
-__device__ __forceinline__ uint2 quant8_e4m3(int mode, const float* f, float sf) {
-  float y[8];
+template <int N>
+__device__ __forceinline__ void quant_scale(int mode, const float* f, float sf, float* y) {
   if (mode == SCALE_TILELANG_FP32) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = clampf_(f[i] / sf, -448.0f, 448.0f);
+    for (int i = 0; i < N; ++i) y[i] = clamp448(f[i] / sf);
   } else {
-    const float inv = 1.0f / sf;
+    const bool torch_mode = mode == SCALE_TORCH_FP32 || mode == SCALE_TORCH_UE8M0;
+    const float inv = mode == SCALE_TORCH_FP32 ? 1.0f / sf : pow2_recip(sf);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = f[i] * inv;
-    if (mode != SCALE_TORCH_FP32 && mode != SCALE_TORCH_UE8M0) {
+    for (int i = 0; i < N; ++i) y[i] = f[i] * inv;
+    if (!torch_mode) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) y[i] = clampf_(y[i], -448.0f, 448.0f);
+      for (int i = 0; i < N; ++i) y[i] = clamp448(y[i]);
     }
   }
+}
+__device__ __forceinline__ uint2 quant8_e4m3(int mode, const float* f, float sf) {
+  float y[8];
+  quant_scale<8>(mode, f, sf, y);
   return make_uint2(pk4_e4m3_exact(y[0], y[1], y[2], y[3]), pk4_e4m3_exact(y[4], y[5], y[6], y[7]));
 }
 // The same arithmetic for four values (four consecutive e4m3 bytes).
 __device__ __forceinline__ uint32_t quant4_e4m3(int mode, const float* f, float sf) {
   float y[4];
-  if (mode == SCALE_TILELANG_FP32) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) y[i] = clampf_(f[i] / sf, -448.0f, 448.0f);
-  } else {
-    const float inv = 1.0f / sf;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) y[i] = f[i] * inv;
-    if (mode != SCALE_TORCH_FP32 && mode != SCALE_TORCH_UE8M0) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) y[i] = clampf_(y[i], -448.0f, 448.0f);
-    }
-  }
+  quant_scale<4>(mode, f, sf, y);
   return pk4_e4m3_exact(y[0], y[1], y[2], y[3]);
 }
 #endif
