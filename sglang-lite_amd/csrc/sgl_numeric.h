@@ -233,13 +233,18 @@ __device__ __forceinline__ float clamp448(float x) {
   const float c = __builtin_amdgcn_fmed3f(x, -448.0f, 448.0f);
   return x != x ? x : c;
 }
-// 1 / sf for the ue8m0 modes' scales: a power of two 2^k (normal, so
-// 2^-k is exact, 2^-127 a subnormal) by ldexp; Inf gives +0 and a NaN itself,
-// as the IEEE division does (a quiet NaN divisor is the quotient)
+// 1 / sf, equal to the IEEE division, for the ue8m0 modes' scales: a normal
+// power of two +-2^k by ldexp (2^-k is exact, 2^-127 a subnormal), +-0 gives
+// +-Inf (the TileLang formula makes -0 of a NaN group: 2^(129) wraps into the
+// sign bit), +-Inf gives +-0 and a NaN itself (a quiet NaN divisor is the
+// quotient); subnormal scales are not produced by any mode
 __device__ __forceinline__ float pow2_recip(float sf) {
-  const int e = (int)((f32_bits(sf) >> 23) & 0xFFu);
-  const float r = __builtin_amdgcn_ldexpf(1.0f, 127 - e);
-  return e == 255 ? (sf != sf ? sf : 0.0f) : r;
+  const uint32_t u = f32_bits(sf);
+  const uint32_t sign = u & 0x80000000u;
+  const int e = (int)((u >> 23) & 0xFFu);
+  const float r = bits_f32(f32_bits(__builtin_amdgcn_ldexpf(1.0f, 127 - e)) | sign);
+  const float special = e == 0 ? bits_f32(sign | 0x7F800000u) : (sf != sf ? sf : bits_f32(sign));
+  return (e == 0 || e == 255) ? special : r;
 }
 // The maximum over aligned groups of LANES (2, 4, 8 or 16) lanes by DPP
 // moves, NaN-propagating: after the two quad permutations every lane holds

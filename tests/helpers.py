@@ -222,3 +222,29 @@ def ids_with_counts(rng, counts, k):
 # expert's T rows
 EDGE_COUNTS_SHORT = [1, 15, 16, 17, 31, 32, 33, 0, 47, 2, 3, 4, 5, 6, 7, 9]
 EDGE_COUNTS_LONG = [1, 15, 16, 17, 31, 32, 33, 47, 48, 49, 63, 64, 65, 0, 96, 97]
+
+
+def assert_e4m3_equal_nan_signless(got: np.ndarray, ref: np.ndarray, what: str = "e4m3") -> None:
+    """e4m3 bytes equal, except that two NaN codes (S.1111.111) may differ in
+    sign: a NaN's sign is not fixed by the reference's arithmetic (x86 numpy's
+    Inf * 0 is a negative NaN, the GPU's a positive one)."""
+    got = np.asarray(got, np.uint8)
+    ref = np.asarray(ref, np.uint8)
+    both_nan = ((got & 0x7F) == 0x7F) & ((ref & 0x7F) == 0x7F)
+    bad = (got != ref) & ~both_nan
+    assert not bad.any(), f"{what}: {int(bad.sum())} bytes differ, first at {np.argwhere(bad)[:4].tolist()}"
+
+
+def nan_inf_rows(rng, cols: int) -> np.ndarray:
+    """Six bf16-exact rows with NaN / Inf elements: a NaN, +Inf, -Inf, NaN in
+    an all-zero row, +Inf beside NaN in one group, and a plain row."""
+    x = bf16_values(rng, (6, cols))
+    x[0, 3] = np.nan
+    x[1, 70] = np.inf
+    x[2, cols - 56] = -np.inf
+    x[3, :] = 0.0
+    x[3, 129] = np.nan
+    x[4, 10] = np.inf
+    x[4, 11] = np.nan
+    return x
+

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import bf16_values, u8
+from helpers import assert_e4m3_equal_nan_signless, bf16_values, nan_inf_rows, u8
 from oracle import kv as OK
 from oracle import quant as Q
 
@@ -61,6 +61,33 @@ def test_pack_layout_a_bit_exact(gpu, dtype, mode, T, monkeypatch):
     np.testing.assert_array_equal(pages.cpu().numpy(), OK.to_paged_hnd(ref, 64))
     pages2 = KVP.to_paged_hnd(out, 64)
     np.testing.assert_array_equal(pages2.cpu().numpy(), OK.to_paged_hnd(ref, 64))
+
+
+@pytest.mark.parametrize("mode", [4, 3, 1])
+def test_pack_layout_a_nan_and_inf_rows(gpu, mode, monkeypatch):
+    """Rows with NaN / Inf values: scale bytes and RoPE bytes exact, the e4m3
+    bytes exact up to the sign of NaN codes, plain and footer-paged."""
+    from sglang_lite_amd import dsv4_kv_pack as KVP
+
+    monkeypatch.delenv("SGLANG_LITE_AMD_ACT_QUANT", raising=False)
+    x = nan_inf_rows(np.random.default_rng(mode), 512)
+    xt = torch.from_numpy(x).to(torch.bfloat16)
+    rope = xt[:, 448:].contiguous().view(torch.uint8).numpy()
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        ref = OK.pack_layout_a(x, rope, mode)
+    d = xt.to(gpu)
+    for got, want, what in ((KVP.pack_dsv4_kv_bf16(d, act_quant_fn=_quantizer(mode)), ref, "rows"),
+                            (KVP.to_paged_hnd(KVP.pack_dsv4_kv_bf16(d, act_quant_fn=_quantizer(mode)), 64),
+                             OK.to_paged_hnd(ref, 64), "pages")):
+        g = got.cpu().numpy()
+        if what == "pages":
+            g, want = OK.unpage(g, 64)[:6], OK.unpage(want, 64)[:6]
+        assert_e4m3_equal_nan_signless(g[:, :448], want[:, :448], f"layout A mode {mode} {what} e4m3")
+        np.testing.assert_array_equal(g[:, 448:], want[:, 448:])
+    pages = KVP.pack_dsv4_kv_paged(d, 64, act_quant_fn=_quantizer(mode)).cpu().numpy()
+    g, want = OK.unpage(pages, 64)[:6], ref
+    assert_e4m3_equal_nan_signless(g[:, :448], want[:, :448], f"layout A mode {mode} paged e4m3")
+    np.testing.assert_array_equal(g[:, 448:], want[:, 448:])
 
 
 @pytest.mark.parametrize("page,T", [(16, 100), (48, 97), (40, 90), (64, 128), (128, 300), (7, 30),

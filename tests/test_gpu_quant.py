@@ -6,7 +6,8 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import bf16_values, to_dev_bf16, to_dev_f32, u8
+from helpers import (assert_e4m3_equal_nan_signless, bf16_values, nan_inf_rows, to_dev_bf16, to_dev_f32,
+                     u8)
 from oracle import quant as Q
 
 pytestmark = pytest.mark.gpu
@@ -35,6 +36,25 @@ def test_act_quant_bit_exact(gpu, mode, group, shape):
     torch.cuda.synchronize()
     np.testing.assert_array_equal(u8(y), q_ref)
     np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("group", [64, 128])
+def test_act_quant_nan_and_inf_groups(gpu, mode, group):
+    """Groups holding NaN or Inf: the scale (NaN, Inf or the mode's clamp of
+    them) bit-exact, the e4m3 bytes exact up to the sign of NaN codes."""
+    from sglang_lite_amd import kernel as K
+
+    x = nan_inf_rows(np.random.default_rng(mode * 7 + group), 512)
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        q_ref, s_ref = Q.scale_mode_quant(x, mode, group)
+    y, s = K.act_quant(to_dev_bf16(x, gpu), group, None, torch.float32, False, scale_mode=mode)
+    torch.cuda.synchronize()
+    assert_e4m3_equal_nan_signless(u8(y), q_ref, f"act_quant mode {mode} group {group}")
+    s_dev = s.cpu().numpy()
+    both_nan = np.isnan(s_dev) & np.isnan(s_ref)
+    np.testing.assert_array_equal(np.where(both_nan, 0, s_dev.view(np.uint32)),
+                                  np.where(both_nan, 0, s_ref.view(np.uint32)))
 
 
 def test_act_quant_default_formula_is_torch_per_token(gpu):
