@@ -258,7 +258,8 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const uint8_t* __restric
   constexpr int ODIM = LAYOUT == SGL_KV_LAYOUT_A ? A_DIM : B_DIM;
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * 4;
-  const int64_t w0 = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  // wave-uniform row index: output addresses and row checks on scalar registers
+  const int64_t w0 = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int shift = page_shift_of(page);
   // lane r < R: index r of the step starting at rb (clamped into the array)
   auto load_idx = [&](int64_t rb) -> int32_t {
@@ -272,7 +273,7 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const uint8_t* __restric
     bool ok[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int32_t v = __builtin_amdgcn_readfirstlane(__shfl(my_id, r, 64));
+      const int32_t v = __builtin_amdgcn_readlane(my_id, r);
       ok[r] = rb + r < total && v >= 0 && v < n_rows;
       id[r] = ok[r] ? v : 0;
     }
@@ -324,11 +325,21 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const uint8_t* __restric
         continue;
       }
       const bool deq = LAYOUT == SGL_KV_LAYOUT_B || lane < 56;
+      // Products are NaN only from an e4m3 NaN code (S.1111.111) or a NaN
+      // scale (layout A: the 0xFF byte; layout B: NaN bits); a row with
+      // neither in any lane takes the plain conversion, which equals the
+      // NaN-canonicalising one for every other value (one wave-uniform test)
+      const uint32_t t0 = qv[r].x & 0x7F7F7F7Fu, t1 = qv[r].y & 0x7F7F7F7Fu;
+      const bool code_nan = (((t0 + 0x01010101u) | (t1 + 0x01010101u)) & 0x80808080u) != 0u;
+      const bool scale_nan = LAYOUT == SGL_KV_LAYOUT_A ? sraw[r] == 0xFFu : (sraw[r] & 0x7FFFFFFFu) > 0x7F800000u;
+      const bool exact = __ballot(deq && (code_nan || scale_nan)) != 0ull;
       if (deq) {
         float sc;
         if constexpr (LAYOUT == SGL_KV_LAYOUT_A) {
+          // 2^(sb - 127); byte 0 is 2^-127 (0x00400000) and 0xFF the NaN
+          // 0x7FC00000: both take the 0x400000 bit
           const uint32_t sb = sraw[r];
-          sc = sb == 0xFFu ? bits_f32(0x7FC00000u) : (sb == 0 ? bits_f32(0x00400000u) : bits_f32(sb << 23));
+          sc = bits_f32((sb << 23) | (sb == 0u || sb == 0xFFu ? 0x00400000u : 0u));
         } else {
           sc = bits_f32(sraw[r]);
         }
@@ -336,8 +347,13 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const uint8_t* __restric
         unpack4_e4m3(qv[r].x, d);
         unpack4_e4m3(qv[r].y, d + 4);
         uint32_t w[4];
+        if (exact) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = pk2_bf16_exact(d[2 * i] * sc, d[2 * i + 1] * sc);
+          for (int i = 0; i < 4; ++i) w[i] = pk2_bf16_exact(d[2 * i] * sc, d[2 * i + 1] * sc);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) w[i] = pk2_bf16(d[2 * i] * sc, d[2 * i + 1] * sc);
+        }
         *reinterpret_cast<uint4*>(o + lane * 8) = make_uint4(w[0], w[1], w[2], w[3]);
       } else {
         *reinterpret_cast<uint4*>(o + lane * 8) = rope[r];
