@@ -252,6 +252,44 @@ def test_gather_dequant_bit_exact(gpu):
     np.testing.assert_array_equal(got_b.float().cpu().numpy().view(np.uint32), ref_b.view(np.uint32))
 
 
+def test_gather_dequant_rows_with_nan_codes_and_scales(gpu):
+    """Rows holding e4m3 NaN codes or NaN scales (packed from NaN / Inf
+    values, plus one NaN code planted in a finite row) beside plain rows:
+    NaN where the oracle has NaN (the device writes the canonical bf16 NaN),
+    every other value bit-exact, layouts A (plain and footer pages) and B."""
+    from sglang_lite_amd import dsv4_kv_pack as KVP
+
+    rng = np.random.default_rng(24)
+    x = np.concatenate([nan_inf_rows(rng, 576), bf16_values(rng, (58, 576))])
+    xt = torch.from_numpy(x).to(torch.bfloat16)
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        rows_a = OK.pack_layout_a(x[:, :512], xt[:, 448:512].contiguous().view(torch.uint8).numpy(), 4)
+        rows_b = OK.pack_layout_b(x[:, :512], xt[:, 512:].contiguous().view(torch.uint8).numpy())
+    rows_a[7, 100] = 0x7F  # a NaN code in a finite row
+    rows_b[8, 200] = 0xFF
+    idx = rng.integers(0, 64, (4, 96)).astype(np.int32)
+    idx[:, :8] = np.arange(8)
+    idx[1, 8:16] = np.arange(8)
+    d_idx = torch.from_numpy(idx).to(gpu)
+
+    def check(got, ref, what):
+        got = got.float().cpu().numpy()
+        nan = np.isnan(ref)
+        assert nan.any(), what
+        assert np.array_equal(np.isnan(got), nan), f"{what}: NaN positions differ"
+        assert np.all(got.view(np.uint32)[nan] == 0x7FC00000), f"{what}: NaN not canonical"
+        np.testing.assert_array_equal(got.view(np.uint32)[~nan], ref.view(np.uint32)[~nan])
+
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref_a = OK.gather_dequant(rows_a, idx, "A")
+        ref_b = OK.gather_dequant(rows_b, idx, "B")
+    d_rows = torch.from_numpy(rows_a).to(gpu)
+    check(KVP.gather_dequant(d_rows, d_idx, layout="A"), ref_a, "layout A")
+    check(KVP.gather_dequant(KVP.to_paged_hnd(d_rows, 64), d_idx, layout="A", page_size=64), ref_a,
+          "layout A pages")
+    check(KVP.gather_dequant(torch.from_numpy(rows_b).to(gpu), d_idx, layout="B"), ref_b, "layout B")
+
+
 def test_layout_a_dequant_equals_qat_inplace(gpu):
     """Layout A gather = the official QAT quant-dequant (kernel.py:84-91) of the
     NoPE part with the injected act_quant formula."""
