@@ -4,7 +4,8 @@ TEST INFRASTRUCTURE ONLY.  This package restates the reference algorithms
 (ParaTensor/sglang-lite; each function cites the reference file:line it
 follows) in numpy so the HIP kernels can be checked against it.  Only
 ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import it, and only as the checker or the timed CPU baseline.
+``bench.py`` may import it, and only to check results against or as the timed
+CPU baseline.
 The product package (``sglang_lite_amd``) never imports it and has no CPU
 fallback.
 

@@ -7,7 +7,8 @@ routing weight applied before w2, bf16 h, the ascending-expert fp32 combine,
 the shared expert added last -- and nothing but its own output checked it.
 These vectors come from the reference's code for that composition instead.
 
-What runs (this container only; nothing here travels to the GPU box):
+What runs (when the fixtures are generated; the tests read only the
+committed vectors):
 
 * ``engine/vendor/deepseek_infer/model.py`` -- the official ``Gate``,
   ``Expert``, ``MoE`` and ``Linear`` / ``linear`` classes, loaded as module
