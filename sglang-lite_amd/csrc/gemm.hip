@@ -747,8 +747,8 @@ __global__ __launch_bounds__(64 * (WM * WN + LW)) void gemm_fp8_kernel(const Gem
         }
       };
       // a wavefront whose rows all lie past the tile's last row has no work;
-      // in the 32-row decode tiles (one wavefront row) a routed group of at
-      // most 16 rows computes only the first 16-row block
+      // a 32-row decode tile (one wavefront row) that holds at most 16 rows
+      // (a group's last tile) computes only its first 16-row block
       const int live = rows - wm * TM * 16;
       if (!computes || live <= 0) return;
       if constexpr (SGL_DEAD_SKIP && KIND != KIND_DENSE && WM == 1 && TM == 2) {
