@@ -19,6 +19,9 @@ constexpr int B_LAT = 512, B_DIM = 576, B_ROW = 656;
 #ifndef SGL_KV_BLOCKS_PER_CU
 #define SGL_KV_BLOCKS_PER_CU 32
 #endif
+// the layout A pack: 12 blocks per CU (65 536 rows, 64-row pages: 23.7-24.0
+// against 24.6 us with 32; 8: 27.2; the gathers are 2-3 us slower at 12-16)
+constexpr int kPackABlocksPerCU = 12;
 constexpr int kKvRows = SGL_KV_ROWS;  // rows per wavefront step in the pack kernels
 // rows per wavefront step in the gather (measured at 128 x 2048 rows of a
 // 65536-row cache: layout A 87 -> 74 us with 4, layout B best with 1)
@@ -395,10 +398,10 @@ __global__ __launch_bounds__(256) void split_indices_kernel(const IT* __restrict
 }
 
 // 4 wavefronts per block, rows_per_wave rows per wavefront step; at most
-// SGL_KV_BLOCKS_PER_CU blocks per CU, the rest loop.
-unsigned grid_for_rows(int64_t rows, int rows_per_wave = 1) {
+// blocks_per_cu blocks per CU, the rest loop.
+unsigned grid_for_rows(int64_t rows, int rows_per_wave = 1, int blocks_per_cu = SGL_KV_BLOCKS_PER_CU) {
   int64_t blocks = ceil_div(rows, 4 * (int64_t)rows_per_wave);
-  const int64_t cap = (int64_t)device_cu_count() * SGL_KV_BLOCKS_PER_CU;
+  const int64_t cap = (int64_t)device_cu_count() * blocks_per_cu;
   if (blocks > cap) blocks = cap;
   return (unsigned)(blocks < 1 ? 1 : blocks);
 }
@@ -445,7 +448,7 @@ int sgl_kv_pack(const void* kv, int dtype, int64_t T, int64_t ldkv, int layout, 
     SGL_REQUIRE(out && (T == 0 || kv), "kv_pack: null pointer");
     SGL_REQUIRE(sgl::aligned(out, 8) && (T == 0 || (sgl::aligned(kv, 16) && (ldkv * es) % 16 == 0)),
                 "kv_pack: kv rows must be 16-byte aligned, out 8-byte aligned");
-    const unsigned g = sgl::grid_for_rows(rows, sgl::kKvRows);
+    const unsigned g = sgl::grid_for_rows(rows, sgl::kKvRows, sgl::kPackABlocksPerCU);
     if (dtype == SGL_BF16)
       sgl::launch_pack_a<SGL_BF16>(g, st, scale_mode, (const uint8_t*)kv, T, ldkv * es, paged, page_size,
                                    rows, (uint8_t*)out, sgl::PageTable{});
@@ -499,7 +502,7 @@ int sgl_kv_pack_to_pages(const void* kv, int dtype, int64_t T, int64_t ldkv, int
               "kv_pack_to_pages: kv rows must be 16-byte aligned, pool 8-byte aligned");
   uint8_t* slab = (uint8_t*)pool + (int64_t)layer_idx * num_blocks * page_size * sgl::A_ROW;
   const sgl::PageTable pt{block_table, start_pos, num_blocks};
-  const unsigned g = sgl::grid_for_rows(T, sgl::kKvRows);
+  const unsigned g = sgl::grid_for_rows(T, sgl::kKvRows, sgl::kPackABlocksPerCU);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == SGL_BF16)
     sgl::launch_pack_a<SGL_BF16>(g, st, scale_mode, (const uint8_t*)kv, T, ldkv * es, 0, page_size, T, slab, pt);
