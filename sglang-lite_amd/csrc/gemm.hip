@@ -1714,7 +1714,7 @@ __device__ __forceinline__ void store_b64(void* p, uint2 v) {
 #define SGL_RB_DBG 2
 #endif
 namespace rb {
-constexpr int BM = 128, BN = 256;
+constexpr int BM = 128;  // tile rows (the tile columns: 256 NJ, set per launch)
 constexpr int SLOTS = 4;  // LDS slots of 128-deep activation stages
 constexpr int A_BYTES = BM * 128;
 constexpr int kMinKB = 16, kMaxKBr = 64;
