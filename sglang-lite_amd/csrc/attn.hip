@@ -50,6 +50,7 @@ typedef v4s __attribute__((address_space(3))) lds_v4s;
 constexpr int kD = 512;     // head dim: 448 latent + 64 rope
 constexpr int kBlk = 64;    // gathered rows per block
 constexpr int kHG = 64;     // heads per workgroup
+constexpr int kMaxSplits = 8;  // workgroups a query's rows split over, at most
 constexpr int kARow = 584, kAData = 576, kANope = 448;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -398,20 +399,38 @@ __global__ __launch_bounds__(256) void sparse_attn_combine_kernel(const AttnArgs
   const int h = (int)(w % a.Hh);
   const int64_t q = w / a.Hh;  // b * M + m
   const float NEG_INF = -__builtin_huge_valf();
+  // every split's loads are issued before the first is used (at most
+  // kMaxSplits splits), so their latencies overlap instead of adding up;
+  // the maximum and the sums then run in split order as before
+  float msp[kMaxSplits], lsp[kMaxSplits];
+  float4 usp[kMaxSplits], vsp[kMaxSplits];
+#pragma unroll
+  for (int sp = 0; sp < kMaxSplits; ++sp) {
+    if (sp < a.nsplit) {
+      const int64_t r = (q * a.nsplit + sp) * a.Hh + h;
+      msp[sp] = a.ws_ml[r * 2];
+      lsp[sp] = a.ws_ml[r * 2 + 1];
+      const float4* src = reinterpret_cast<const float4*>(a.ws_acc + r * kD + lane * 8);
+      usp[sp] = src[0];
+      vsp[sp] = src[1];
+    }
+  }
   float mx = NEG_INF;
-  for (int sp = 0; sp < a.nsplit; ++sp) mx = fmaxf_(mx, a.ws_ml[((q * a.nsplit + sp) * a.Hh + h) * 2]);
+#pragma unroll
+  for (int sp = 0; sp < kMaxSplits; ++sp)
+    if (sp < a.nsplit) mx = fmaxf_(mx, msp[sp]);
   const float ref = mx == NEG_INF ? 0.0f : mx;
   float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   float l = 0.0f;
-  for (int sp = 0; sp < a.nsplit; ++sp) {
-    const int64_t r = (q * a.nsplit + sp) * a.Hh + h;
-    const float ms = a.ws_ml[r * 2];
-    const float f = __builtin_amdgcn_exp2f(ms - ref);  // 0 for an all-masked split
-    l += a.ws_ml[r * 2 + 1] * f;
-    const float4* src = reinterpret_cast<const float4*>(a.ws_acc + r * kD + lane * 8);
-    const float4 u = src[0], v = src[1];
-    o[0] += u.x * f; o[1] += u.y * f; o[2] += u.z * f; o[3] += u.w * f;
-    o[4] += v.x * f; o[5] += v.y * f; o[6] += v.z * f; o[7] += v.w * f;
+#pragma unroll
+  for (int sp = 0; sp < kMaxSplits; ++sp) {
+    if (sp < a.nsplit) {
+      const float f = __builtin_amdgcn_exp2f(msp[sp] - ref);  // 0 for an all-masked split
+      l += lsp[sp] * f;
+      const float4 u = usp[sp], v = vsp[sp];
+      o[0] += u.x * f; o[1] += u.y * f; o[2] += u.z * f; o[3] += u.w * f;
+      o[4] += v.x * f; o[5] += v.y * f; o[6] += v.z * f; o[7] += v.w * f;
+    }
   }
   const float den = l + __builtin_amdgcn_exp2f(a.sink[h] * kLog2e - ref);
   uint32_t wv[4];
@@ -431,7 +450,7 @@ int attn_splits(int64_t B, int64_t M, int Hh, int64_t K) {
   // that the merge reads back: past 8 splits that traffic costs more than the
   // parallelism gains (8 sequences x 2048 rows: 32 splits 45.7 us, 8 splits
   // 38.3 us, measured)
-  if (ns > 8) ns = 8;
+  if (ns > kMaxSplits) ns = kMaxSplits;
   if (ns <= 1) return 1;
   const int64_t bps = (nblk + ns - 1) / ns;
   return (int)((nblk + bps - 1) / bps);  // no empty split
