@@ -778,13 +778,23 @@ __global__ __launch_bounds__(NT) void combine_kernel(const uint16_t* __restrict_
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-    for (int jj = 0; jj < nv; ++jj) {
-      const uint4 v = ld16_stream(base + (int64_t)ord[jj] * H + col);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    // every row's load is issued before the first is summed (k <= 16), so
+    // their latencies overlap; the sum runs in ascending expert order as
+    // before, the shared row last
+    uint4 rv[16];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[2 * i] += bits_f32(w[i] << 16);
-        acc[2 * i + 1] += bits_f32(w[i] & 0xFFFF0000u);
+    for (int jj = 0; jj < 16; ++jj)
+      if (jj < nv) rv[jj] = ld16_stream(base + (int64_t)ord[jj] * H + col);
+    const uint4 sv = !PARTIAL && has_shared ? ld16_stream(base + (int64_t)k * H + col) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) {
+      if (jj < nv) {
+        const uint32_t w[4] = {rv[jj].x, rv[jj].y, rv[jj].z, rv[jj].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[2 * i] += bits_f32(w[i] << 16);
+          acc[2 * i + 1] += bits_f32(w[i] & 0xFFFF0000u);
+        }
       }
     }
     if constexpr (PARTIAL) {
@@ -793,7 +803,7 @@ __global__ __launch_bounds__(NT) void combine_kernel(const uint16_t* __restrict_
       yo[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
     } else {
       if (has_shared) {
-        const uint4 v = ld16_stream(base + (int64_t)k * H + col);
+        const uint4 v = sv;
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
