@@ -51,12 +51,14 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extra", action="store_true", help="headline prefill line only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--profile-kernels", nargs="?", const="fp8", choices=("fp8", "fp4", "small", "frag", "fp4frag"),
+    ap.add_argument("--profile-kernels", nargs="?", const="fp8",
+                    choices=("fp8", "fp4", "small", "frag", "fp4frag", "attn"),
                     help="for rocprofv3 runs: only 3 prefill steps (fp8: FP8 experts; fp4: FP4 "
                          "routed experts in the ue8m0 scale mode; frag / fp4frag: the same with "
                          "fragment-layout weight copies, then 3 decode steps at T = 64/256/512; "
-                         "small: the short kernels) plus a counter-calibration kernel; prints no "
-                         "JSON")
+                         "small: the short kernels; attn: the sparse attention off packed pages "
+                         "at 128 x 2048 and decode 32 x 640, 5 calls each) plus a "
+                         "counter-calibration kernel; prints no JSON")
     return ap.parse_args()
 
 
@@ -319,6 +321,35 @@ def mfma_ceiling(torch, dev, iters=2000):
         flops = (threads // 64) * iters * 16 * 65536.0
         res[name] = round(flops / a.elapsed_time(b) / 1e9, 1)
     return res
+
+
+def profile_attn(torch, KVP, dev):
+    """The sparse attention of the bench extras, 5 calls per shape, for kernel
+    traces: 128 query tokens x 2048 rows of one 65536-row packed cache, then
+    32 sequences x 640 rows, each of its own 32768-row cache (64 heads)."""
+    from sglang_lite_amd import v4_sparse_mla as SA
+
+    ga = torch.Generator().manual_seed(6)
+    kva = torch.randn(65536, 512, generator=ga).to(torch.bfloat16).to(dev)
+    pages_a = KVP.pack_dsv4_kv_paged(kva, 64).unsqueeze(0)
+    del kva
+    qa = torch.randn(1, 128, 64, 512, generator=ga).to(torch.bfloat16).to(dev)
+    ia = torch.stack([torch.randperm(65536, generator=ga)[:2048] for _ in range(128)]).to(
+        torch.int32).view(1, 128, 2048).to(dev)
+    sink = torch.randn(64, generator=ga).to(dev)
+    for _ in range(5):
+        SA.sparse_attn_packed(qa, pages_a, sink, ia, 512 ** -0.5)
+    torch.cuda.synchronize()
+    del pages_a, qa, ia
+    Bd, NRd, Kd = 32, 32768, 640
+    kvd = torch.randn(Bd * NRd, 512, generator=ga).to(torch.bfloat16).to(dev)
+    pages_d = KVP.pack_dsv4_kv_paged(kvd, 64).view(Bd, NRd // 64, 1, 64, 584)
+    del kvd
+    qd = torch.randn(Bd, 1, 64, 512, generator=ga).to(torch.bfloat16).to(dev)
+    idd = torch.randint(0, NRd, (Bd, 1, Kd), generator=ga).to(torch.int32).to(dev)
+    for _ in range(5):
+        SA.sparse_attn_packed(qd, pages_d, sink, idd, 512 ** -0.5)
+    torch.cuda.synchronize()
 
 
 def profile_small(torch, M, K, table, dev):
@@ -695,6 +726,8 @@ def main():
                     M.moe_forward(xd, ids, w, tf)
         elif args.profile_kernels == "small":
             profile_small(torch, M, K, table, dev)
+        elif args.profile_kernels == "attn":
+            profile_attn(torch, KVP, dev)
         else:
             for _ in range(3):
                 pre.step()
